@@ -1,0 +1,233 @@
+"""Benchmark of the Nori ICL hot path on one MI355X.
+
+Workload (the long-context configuration the headline metric is quoted on): nori-30m
+block dims -- 12 layers, embed 352, 8 heads of width 44 -- one table whose 64 features
+give 33 feature-group tokens, a 65,536-row context and 4 query batches of 1,024 rows.
+
+One step is the whole ICL stage of that job, with inputs resident in HBM:
+  * cache build: every layer's full-precision (fp16, the GPU autocast dtype) context
+    K/V [33, 65536, 2, 8, 44] is quantized to the int8 cache (HIP codec);
+  * 4 query batches x 12 layers of the cached sequence-attention sublayer
+    (layer.py:1945-1953 with forward_with_kv_cache :685-745): RMSNorm of the query
+    tokens (HIP), Q projection (hipBLASLt GEMM), query -> context attention over the
+    int8 cache (HIP, int8 K/V dequantized in registers), output projection and the
+    deepnorm residual.
+value = query rows per second of the step (4,096 rows per step).
+
+The JSON line also carries the roofline of the dominant kernel (attention, bound by
+dense fp16/bf16 MFMA at 2.5 PFLOP/s), measured with HIP events on the launch stream,
+the same for the quantize kernel against 8 TB/s of HBM, and the CPU baseline: the
+oracle's fp32 online-softmax scan (the reference's CPU path, layer.py:777-839) timed on
+the host cores over a bounded sample of the same attention work.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "synthefy-nori_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK = 8.0e12  # B/s
+MFMA_BF16_PEAK = 2.5e15  # FLOP/s, dense
+
+# nori-30m block dims and the 64k-row context configuration
+LAYERS, EMBED, HEADS, HEAD_DIM = 12, 352, 8, 44
+GROUPS = 33  # ceil(64 features / 2 per group) + 1 target token
+CONTEXT_ROWS = 65536
+QUERY_BATCHES, QUERY_ROWS = 4, 1024
+DEEPNORM_ALPHA = LAYERS ** -0.5
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
+    p.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    p.add_argument("--cpu-sample-queries", type=int, default=1024)
+    return p.parse_args()
+
+
+def build_workload(torch, layers, dev):
+    g = torch.Generator(device=dev).manual_seed(2)
+    kv_shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
+    kv = [torch.randn(kv_shape, generator=g, device=dev, dtype=torch.float16) for _ in range(layers)]
+    codes = [torch.empty(kv_shape, dtype=torch.int8, device=dev) for _ in range(layers)]
+    scales = [torch.empty(kv_shape[:-1] + (1,), dtype=torch.float32, device=dev) for _ in range(layers)]
+    wq = [(torch.randn(HEADS * HEAD_DIM, EMBED, generator=g, device=dev) * EMBED ** -0.5).half() for _ in range(layers)]
+    wo = [(torch.randn(HEADS, HEAD_DIM, EMBED, generator=g, device=dev) * 0.02).half() for _ in range(layers)]
+    queries = [torch.randn(GROUPS, QUERY_ROWS, EMBED, generator=g, device=dev, dtype=torch.float16) for _ in range(QUERY_BATCHES)]
+    return kv, codes, scales, wq, wo, queries
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one MI355X: the Nori ICL path shards by table/token group or by "
+            "context rows without changing the per-GPU kernel, and this build runs on a single GPU. "
+            "Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    import nori_amd
+    from nori_amd.kv_cache_scaling import _quantize_into
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    layers = args.layers
+    kv, codes, scales, wq, wo, queries = build_workload(torch, layers, dev)
+    stream = torch.cuda.current_stream(dev)
+    attn_ms: list[float] = []
+    quant_ms: list[float] = []
+
+    def timed(fn, sink):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        r = fn()
+        e1.record(stream)
+        sink.append((e0, e1))
+        return r
+
+    def step(record):
+        qsink, asink = ([], []) if record else (None, None)
+        for layer in range(layers):
+            f = lambda layer=layer: _quantize_into(kv[layer], codes[layer], scales[layer])  # noqa: E731
+            timed(f, qsink) if record else f()
+        outs = []
+        for x in queries:
+            for layer in range(layers):
+                xn = nori_amd.rms_norm(x, EMBED, None, 1e-5)
+                q = torch.nn.functional.linear(xn, wq[layer]).view(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM)
+                f = lambda q=q, layer=layer: nori_amd.icl_attention(q, codes[layer], scales[layer])  # noqa: E731
+                o = timed(f, asink) if record else f()
+                x = x + DEEPNORM_ALPHA * torch.einsum("...hd,hds->...s", o, wo[layer])
+            outs.append(x)
+        return outs, qsink, asink
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    events_q, events_a = [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        _, qs, as_ = step(True)
+        events_q += qs
+        events_a += as_
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    quant_ms = [a.elapsed_time(b) for a, b in events_q]
+    attn_ms = [a.elapsed_time(b) for a, b in events_a]
+
+    rows_per_step = QUERY_BATCHES * QUERY_ROWS
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = rows_per_step * args.steps / elapsed
+
+    attn_flop = 4.0 * GROUPS * HEADS * QUERY_ROWS * CONTEXT_ROWS * HEAD_DIM  # per launch, unpadded D
+    attn_avg_s = sum(attn_ms) / len(attn_ms) / 1e3
+    attn_achieved = attn_flop / attn_avg_s
+    n_elem = GROUPS * CONTEXT_ROWS * 2 * HEADS * HEAD_DIM
+    quant_bytes = n_elem * (2 + 1) + 4 * n_elem // HEAD_DIM  # fp16 in, int8 + fp32 scale out
+    quant_avg_s = sum(quant_ms) / len(quant_ms) / 1e3
+    quant_achieved = quant_bytes / quant_avg_s
+
+    line = {
+        "metric": "query rows/s @ 64k-row int8 ctx; attn % MFMA peak; quant kernel % HBM BW",
+        "value": round(value, 2),
+        "unit": "query rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA (int8 K/V codes, fp32 softmax/accumulate)",
+        "data": "synthetic: random-init nori-30m block weights, N(0,1) fp16 context K/V and query tokens",
+        "config": {
+            "workload": "nori-30m ICL stage: int8 cache build for 12 layers over a 65536-row context "
+            "+ 4 query batches x 1024 rows x 12 cached attention sublayers",
+            "layers": layers, "embed": EMBED, "heads": HEADS, "head_dim": HEAD_DIM,
+            "token_groups": GROUPS, "context_rows": CONTEXT_ROWS,
+            "query_rows_per_step": rows_per_step, "cache": "int8 per-vector absmax (resident)",
+        },
+        "roofline": {
+            "kernel": "icl_attention_kernel<48, int8>",
+            "bound": "mfma",
+            "achieved": round(attn_achieved / 1e12, 2),
+            "peak": MFMA_BF16_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(attn_achieved / MFMA_BF16_PEAK, 4),
+            "traffic": None,
+            "work_per_launch": f"{attn_flop:.4e} FLOP = 4*33*8*1024*65536*44",
+            "avg_launch_ms": round(attn_avg_s * 1e3, 4),
+            "launches": len(attn_ms),
+        },
+        "quant_roofline": {
+            "kernel": "quantize_tile_kernel<f16>",
+            "bound": "hbm",
+            "achieved": round(quant_achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(quant_achieved / HBM_PEAK, 4),
+            "work_per_launch": f"{quant_bytes:.4e} B = n*(2+1) + 4*n/44, n = 33*65536*2*8*44",
+            "avg_launch_ms": round(quant_avg_s * 1e3, 4),
+            "launches": len(quant_ms),
+        },
+    }
+    if args.cpu_baseline == "on":
+        line["cpu_baseline"] = cpu_baseline(torch, codes[0], scales[0], args.cpu_sample_queries, layers)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(torch, codes, scales, n_query, layers):
+    """Time the oracle's fp32 online-softmax scan (the reference's CPU attention) on the host.
+
+    Sample: one of the 33 token groups, ``n_query`` query rows, one layer, over the same
+    65,536-row int8 cache (copied to the host, dequantized per 32k-row block as
+    BlockwiseSeqKV.iter_kv_blocks does). Extrapolated to the step's query rows/s.
+    """
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, n_query, HEADS, HEAD_DIM, generator=g)
+    c = codes[:1].cpu()
+    s = scales[:1].cpu()
+
+    def blocks():
+        step = 32768
+        for a in range(0, CONTEXT_ROWS, step):
+            yield c[:, a : a + step].float() * s[:, a : a + step]
+
+    t0 = time.perf_counter()
+    oa.blockwise_attention_fp32(q, blocks())
+    t = time.perf_counter() - t0
+    # the step runs GROUPS token groups x layers layers x QUERY_BATCHES batches of QUERY_ROWS rows
+    seconds_per_step = t * (QUERY_ROWS / n_query) * GROUPS * layers * QUERY_BATCHES
+    return {
+        "value": round(QUERY_BATCHES * QUERY_ROWS / seconds_per_step, 4),
+        "unit": "query rows/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"1 of {GROUPS} token groups x {n_query} query rows x 1 of {layers} layers over the "
+        f"65536-row int8 cache: {t:.2f} s; fp32 online softmax (oracle.attention.blockwise_attention_fp32, "
+        "layer.py:777-839), extrapolated linearly to the step",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,151 @@
+/*
+ * nori_hip.h -- C ABI of libnori_hip.so, the MI355X (gfx950) kernels of Nori's
+ * in-context-learning (ICL) hot path: the int8 context K/V cache codec, RMSNorm, and
+ * query-row -> context attention over the cached K/V.
+ *
+ * The reference (Synthefy/synthefy-nori) has no FFI: its operators are Python
+ * callables over torch tensors. Each entry point below replaces one of them; the
+ * comment names the reference function (file:line, relative to the reference repo
+ * root) whose semantics it implements. The Python drop-ins that keep the reference's
+ * names and signatures call these through ctypes (synthefy-nori_amd/nori_amd/_native.py).
+ *
+ * Conventions
+ *   - Plain C types only. Device buffers are raw device pointers owned by the
+ *     caller; the library allocates nothing unless a function says otherwise.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the legacy default stream.
+ *     Work is enqueued on it; no entry point synchronises the host.
+ *   - Strides are in ELEMENTS of the buffer they describe; the innermost (head_dim)
+ *     axis is always contiguous.
+ *   - Every entry point returns a nori_status. On failure, nori_last_error() returns
+ *     a thread-local message describing the first problem found.
+ */
+#ifndef NORI_HIP_H
+#define NORI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    NORI_OK = 0,
+    NORI_ERR_INVALID = 1,      /* bad shape/stride/pointer: the reference raises ValueError   */
+    NORI_ERR_RUNTIME = 2,      /* HIP launch/runtime failure: RuntimeError                      */
+    NORI_ERR_UNSUPPORTED = 3,  /* combination not implemented: NotImplementedError              */
+    NORI_ERR_OUT_OF_MEMORY = 4 /* hipErrorOutOfMemory: torch.cuda.OutOfMemoryError upstream     */
+} nori_status;
+
+typedef enum {
+    NORI_F32 = 0,
+    NORI_F16 = 1,
+    NORI_BF16 = 2,
+    NORI_I8 = 3
+} nori_dtype;
+
+/* How `amax / 127.0` is evaluated when the scale is formed (see nori_kv_quantize_int8). */
+typedef enum {
+    NORI_SCALE_DIV_TRUE = 0,  /* IEEE division: torch's CPU kernel                          */
+    NORI_SCALE_DIV_RECIP = 1  /* multiply by fp32 1/127: torch's ROCm/CUDA kernel            */
+} nori_scale_div;
+
+/* Flags of nori_icl_attention. */
+#define NORI_ATTN_MERGE 1u /* merge into running (out fp32, lse) instead of overwriting them */
+
+/* Version of this ABI (bumped on any signature change). */
+int nori_abi_version(void);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* nori_last_error(void);
+
+/*
+ * Symmetric per-vector absmax int8 quantization of K/V head vectors.
+ * Replaces quantize_int8 (src/synthefy_nori/model/kv_cache_scaling.py:29-37):
+ *     scale = t.abs().amax(-1, keepdim=True).clamp_min(1e-12) / 127.0
+ *     codes = clamp(round(t / scale), -127, 127).to(int8);  scales = scale.to(float32)
+ * evaluated with torch's per-op rounding in the source dtype, so codes and scales are
+ * bit-identical to the torch expression on the device `scale_div` names.
+ *
+ * Vectors are addressed two-level, so a slice written into preallocated storage
+ * (BlockwiseSeqKV.from_row_slices, kv_cache_scaling.py:253-303) needs no copy:
+ *   vector (o, i), o < n_outer, i < n_inner, has its d elements at
+ *     src    + o*src_outer_stride    + i*src_inner_stride      (src_dtype)
+ *     codes  + o*codes_outer_stride  + i*codes_inner_stride    (int8)
+ *   and its scale at scales + o*scales_outer_stride + i*scales_inner_stride (fp32).
+ * For a contiguous [BG, N, 2, Hkv, D] cache: n_outer = 1, n_inner = BG*N*2*Hkv,
+ * inner strides d / d / 1.
+ * src_dtype: NORI_F32, NORI_F16 or NORI_BF16. NaN inside a vector yields code 0.
+ */
+int nori_kv_quantize_int8(const void* src, int src_dtype, int64_t n_outer, int64_t n_inner, int32_t d,
+                          int64_t src_outer_stride, int64_t src_inner_stride, int8_t* codes,
+                          int64_t codes_outer_stride, int64_t codes_inner_stride, float* scales,
+                          int64_t scales_outer_stride, int64_t scales_inner_stride, int32_t scale_div,
+                          void* stream);
+
+/*
+ * Dequantization: dst = (float(codes) * scale) rounded to dst_dtype.
+ * Replaces dequantize_int8 (kv_cache_scaling.py:40-41). Same two-level addressing
+ * as nori_kv_quantize_int8, with dst in place of src.
+ */
+int nori_kv_dequantize_int8(const int8_t* codes, const float* scales, int64_t n_outer, int64_t n_inner,
+                            int32_t d, int64_t codes_outer_stride, int64_t codes_inner_stride,
+                            int64_t scales_outer_stride, int64_t scales_inner_stride, void* dst,
+                            int dst_dtype, int64_t dst_outer_stride, int64_t dst_inner_stride,
+                            void* stream);
+
+/*
+ * RMSNorm over rows of `cols` elements: y = x * rsqrt(mean(x^2) + eps) (* weight).
+ * Replaces RMSNorm.forward (src/synthefy_nori/model/layer.py:251-258), native
+ * (F.rms_norm) variant: statistic and product in fp32, one rounding to `dtype`.
+ * weight may be NULL (elementwise_affine=False, the layer norms of layer.py:1346-1349);
+ * otherwise it has `cols` elements of `weight_dtype`.
+ */
+int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
+                  const void* weight, int weight_dtype, float eps, void* y, int64_t y_row_stride,
+                  void* stream);
+
+/*
+ * Query-row -> context attention over a K/V cache:
+ *     out[b, i, h, :] = softmax_j(scale * q[b, i, h, :] . k[b, j, hk, :]) @ v[b, j, hk, :]
+ * with hk = h / (heads / kv_heads) (MQA/GQA broadcast, layer.py:640-649, 956).
+ * Replaces the dense cached attention (MultiheadAttention.compute_attention_by_torch,
+ * layer.py:936-1049), the CPU blockwise online softmax (layer.py:747-839) and the
+ * GPU per-block flex + LSE merge (layer.py:841-934, _flex_attention_with_lse :132-182).
+ *
+ * q      : [bg, nq, heads, d] at q + b*q_bg_stride + i*q_row_stride + h*q_head_stride.
+ * kv     : the cache as the reference lays it out, [bg, nk, 2, kv_heads, d]:
+ *          K of (b, j, hk) at kv + b*kv_bg_stride + j*kv_row_stride + hk*d,
+ *          V at the same place + kv_half_stride.
+ *          kv_dtype NORI_I8: int8 codes with fp32 scales at
+ *            kv_scales + b*sc_bg_stride + j*sc_row_stride + hk (+ sc_half_stride for V),
+ *            dequantized in-kernel (kv_cache_scaling.py:40-41);
+ *          NORI_F16 / NORI_BF16 / NORI_F32: full-precision cache, kv_scales ignored.
+ * scale  : logit scale (1/sqrt(d) when the reference passes none, layer.py:798, 857).
+ * out    : [bg, nq, heads, d] addressed like q, in out_dtype.
+ * lse    : optional natural-log log-sum-exp of the scaled logits, fp32, [bg, heads, nq]
+ *          contiguous (the flex LSE, layer.py:87-93, 123).
+ * flags  : NORI_ATTN_MERGE: `out` (must be NORI_F32) and `lse` (required) hold a
+ *          running normalized output and LSE from earlier key blocks; this call merges
+ *          its keys into them exactly as layer.py:914-920 does (start from lse = -inf,
+ *          out = 0).
+ * workspace / workspace_bytes: device scratch for the split-context schedule; size from
+ *          nori_icl_attention_workspace_size(). May be NULL/0, which disables splitting.
+ * Requires d % 4 == 0, 4 <= d <= 128, heads % kv_heads == 0, nk >= 1.
+ */
+int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                       int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
+                       int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
+                       int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                       int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
+                       void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                       int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace nori_icl_attention uses for these sizes (0 when it never splits). */
+int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NORI_HIP_H */

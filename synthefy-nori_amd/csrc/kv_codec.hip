@@ -1,0 +1,336 @@
+// int8 context K/V cache codec for gfx950: quantize and dequantize head vectors.
+//
+// Semantics (bit-exact): quantize_int8 / dequantize_int8,
+// src/synthefy_nori/model/kv_cache_scaling.py:29-41, evaluated the way torch does it,
+// i.e. every op computed in fp32 and its result rounded to the source dtype T:
+//   m = amax|t|                (exact; NaN propagates)
+//   m = max(m, T(1e-12))       (clamp_min; T(1e-12) is 0 in fp16)
+//   s = T(m / 127)             (CPU: IEEE division; ROCm: m * fp32(1/127))
+//   c = clamp(rint(T(t / s)), -127, 127)   (t/s is an IEEE fp32 quotient, then T-rounded)
+//   scale = float(s)
+// Dequantize: T(float(c) * scale).
+//
+// Schedule. HBM-bound streaming: a workgroup stages a tile of up to 256 vectors that
+// are contiguous in memory into LDS with 128-bit loads (any head width: a 44-element
+// bf16 vector is 88 bytes and not 16-byte aligned on its own, but 256 of them are),
+// each thread then codes one vector out of LDS, the codes go back through LDS and
+// leave with 128-bit stores. Vectors that are not contiguous, or too long for the
+// tile, take a one-thread-per-vector kernel reading global memory directly.
+//
+// The per-element quotient t/s uses one IEEE reciprocal per vector and Markstein's
+// correction q = fma(fma(-q0, s, t), y, q0), q0 = t*y, y = RN(1/s). For 2^-96 <= s <= 2^96
+// it returns the correctly rounded quotient wherever |t/s| >= 1/4 (below that the code is
+// 0 whichever quotient is used); checked for every fp16 and bf16 (t, s) pair and for
+// random fp32 pairs on the CPU by tests/exact_quotient_check.c. Other vectors (zero,
+// tiny, huge, infinite or NaN scale) divide exactly.
+#include "nori_common.h"
+
+namespace {
+
+using namespace nori;
+
+constexpr int kTileThreads = 256;
+constexpr int kMaxTileVectorBytes = 128;  // keeps the tile under 48 KiB of LDS; longer vectors use the direct kernel
+
+template <int DT> struct Storage;
+template <> struct Storage<NORI_F32> { using T = uint32_t; };
+template <> struct Storage<NORI_F16> { using T = uint16_t; };
+template <> struct Storage<NORI_BF16> { using T = uint16_t; };
+
+template <int DT>
+__device__ __forceinline__ float bits_to_f32(typename Storage<DT>::T b) {
+    if constexpr (DT == NORI_F32) return __uint_as_float(b);
+    else if constexpr (DT == NORI_F16) return f16_to_f32(b);
+    else return bf16_to_f32(b);
+}
+
+// |x| as an unsigned key whose integer order is the float order with NaN on top, so an
+// integer max is a NaN-propagating absmax (torch's amax propagates NaN).
+template <int DT>
+__device__ __forceinline__ uint32_t abs_key(typename Storage<DT>::T b) {
+    if constexpr (DT == NORI_F32) return b & 0x7fffffffu;
+    else return (uint32_t)b & 0x7fffu;
+}
+
+struct VectorScale {
+    float s;     // scale in T, widened to fp32
+    float y;     // RN(1/s)
+    bool fast;   // Markstein quotient valid for this vector
+};
+
+template <int DT>
+__device__ __forceinline__ VectorScale make_scale(uint32_t max_key, int scale_div) {
+    const float m = bits_to_f32<DT>((typename Storage<DT>::T)max_key);
+    const float floor_t = round_to<DT>((float)1e-12);  // clamp_min(1e-12) in T
+    const float m2 = (m != m) ? m : fmaxf(m, floor_t);
+    float s;
+    if (scale_div == NORI_SCALE_DIV_RECIP) s = round_to<DT>(m2 * (1.0f / 127.0f));
+    else s = round_to<DT>(m2 / 127.0f);
+    VectorScale vs;
+    vs.s = s;
+    vs.y = 1.0f / s;
+    // Outside [2^-96, 2^96] the residual fma(-q0, s, t) may be subnormal and inexact.
+    vs.fast = s >= 0x1p-96f && s <= 0x1p96f;
+    return vs;
+}
+
+// Code of one element; `t` is finite whenever vs.fast holds (|t| <= amax < inf).
+template <int DT>
+__device__ __forceinline__ int code_of(float t, const VectorScale& vs) {
+    if (vs.fast) {
+        const float q0 = t * vs.y;
+        const float r = fmaf(-q0, vs.s, t);
+        const float q = fmaf(r, vs.y, q0);
+        const float k = rintf(round_to<DT>(q));
+        return (int)__builtin_amdgcn_fmed3f(k, -127.0f, 127.0f);
+    }
+    const float k = rintf(round_to<DT>(t / vs.s));
+    if (k != k) return 0;  // NaN -> 0, the GPU's float->int conversion of NaN
+    return (int)fminf(fmaxf(k, -127.0f), 127.0f);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// Cooperative global -> LDS copy of `nbytes` (a multiple of `elem` bytes).
+__device__ __forceinline__ void copy_in(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g, int nbytes,
+                                        int elem) {
+    const int tid = threadIdx.x;
+    int done = 0;
+    if ((((uintptr_t)g) & 15) == 0) {
+        const int n16 = nbytes >> 4;
+        for (int i = tid; i < n16; i += kTileThreads)
+            reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(g)[i];
+        done = n16 << 4;
+    }
+    if (elem == 4) {
+        for (int i = (done >> 2) + tid; i < (nbytes >> 2); i += kTileThreads)
+            reinterpret_cast<uint32_t*>(lds)[i] = reinterpret_cast<const uint32_t*>(g)[i];
+    } else {
+        for (int i = (done >> 1) + tid; i < (nbytes >> 1); i += kTileThreads)
+            reinterpret_cast<uint16_t*>(lds)[i] = reinterpret_cast<const uint16_t*>(g)[i];
+    }
+}
+
+// Cooperative LDS -> global copy of `nbytes` bytes (any count, any alignment >= 1).
+__device__ __forceinline__ void copy_out(uint8_t* __restrict__ g, const uint8_t* __restrict__ lds, int nbytes) {
+    const int tid = threadIdx.x;
+    int done = 0;
+    if ((((uintptr_t)g) & 15) == 0) {
+        const int n16 = nbytes >> 4;
+        for (int i = tid; i < n16; i += kTileThreads)
+            reinterpret_cast<uint4*>(g)[i] = reinterpret_cast<const uint4*>(lds)[i];
+        done = n16 << 4;
+    }
+    for (int i = done + tid; i < nbytes; i += kTileThreads) g[i] = lds[i];
+}
+
+// ------------------------------------------------------------------ quantize
+template <int DT>
+__global__ void __launch_bounds__(kTileThreads)
+quantize_tile_kernel(const uint8_t* __restrict__ src, int64_t n_inner, int d, int64_t src_outer_bytes,
+                     int8_t* __restrict__ codes, int64_t codes_outer, float* __restrict__ scales,
+                     int64_t scales_outer, int64_t tiles_per_outer, int scale_div) {
+    using S = typename Storage<DT>::T;
+    constexpr int es = sizeof(S);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int64_t tile = blockIdx.x;
+    const int64_t o = tile / tiles_per_outer;
+    const int64_t v0 = (tile - o * tiles_per_outer) * kTileThreads;
+    const int nv = (int)min<int64_t>(kTileThreads, n_inner - v0);
+    const int vec_bytes = d * es;
+    uint8_t* lds_src = lds;
+    uint8_t* lds_codes = lds + ((kTileThreads * vec_bytes + 15) & ~15);
+
+    copy_in(lds_src, src + o * src_outer_bytes + v0 * vec_bytes, nv * vec_bytes, es);
+    __syncthreads();
+
+    const int v = threadIdx.x;
+    if (v < nv) {
+        const S* x = reinterpret_cast<const S*>(lds_src) + (int64_t)v * d;
+        uint32_t mk = 0;
+        for (int i = 0; i < d; ++i) mk = max(mk, abs_key<DT>(x[i]));
+        const VectorScale vs = make_scale<DT>(mk, scale_div);
+        uint8_t* c = lds_codes + v * d;
+        int i = 0;
+        if ((d & 3) == 0) {
+            for (; i < d; i += 4) {
+                const uint32_t w = pack4(code_of<DT>(bits_to_f32<DT>(x[i]), vs), code_of<DT>(bits_to_f32<DT>(x[i + 1]), vs),
+                                         code_of<DT>(bits_to_f32<DT>(x[i + 2]), vs), code_of<DT>(bits_to_f32<DT>(x[i + 3]), vs));
+                *reinterpret_cast<uint32_t*>(c + i) = w;
+            }
+        }
+        for (; i < d; ++i) c[i] = (uint8_t)(int8_t)code_of<DT>(bits_to_f32<DT>(x[i]), vs);
+        scales[o * scales_outer + v0 + v] = vs.s;
+    }
+    __syncthreads();
+    copy_out(reinterpret_cast<uint8_t*>(codes + o * codes_outer + v0 * d), lds_codes, nv * d);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kTileThreads)
+quantize_direct_kernel(const void* __restrict__ src_v, int64_t n_outer, int64_t n_inner, int d,
+                       int64_t src_outer, int64_t src_inner, int8_t* __restrict__ codes, int64_t codes_outer,
+                       int64_t codes_inner, float* __restrict__ scales, int64_t scales_outer,
+                       int64_t scales_inner, int scale_div) {
+    using S = typename Storage<DT>::T;
+    const S* src = reinterpret_cast<const S*>(src_v);
+    const int64_t idx = (int64_t)blockIdx.x * kTileThreads + threadIdx.x;
+    if (idx >= n_outer * n_inner) return;
+    const int64_t o = idx / n_inner, i = idx - o * n_inner;
+    const S* x = src + o * src_outer + i * src_inner;
+    uint32_t mk = 0;
+    for (int e = 0; e < d; ++e) mk = max(mk, abs_key<DT>(x[e]));
+    const VectorScale vs = make_scale<DT>(mk, scale_div);
+    int8_t* c = codes + o * codes_outer + i * codes_inner;
+    for (int e = 0; e < d; ++e) c[e] = (int8_t)code_of<DT>(bits_to_f32<DT>(x[e]), vs);
+    scales[o * scales_outer + i * scales_inner] = vs.s;
+}
+
+// ------------------------------------------------------------------ dequantize
+template <int DT>
+__global__ void __launch_bounds__(kTileThreads)
+dequant_tile_kernel(const int8_t* __restrict__ codes, int64_t n_inner, int d, int64_t codes_outer,
+                    const float* __restrict__ scales, int64_t scales_outer, uint8_t* __restrict__ dst,
+                    int64_t dst_outer_bytes, int64_t tiles_per_outer) {
+    using S = typename Storage<DT>::T;
+    constexpr int es = sizeof(S);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int64_t tile = blockIdx.x;
+    const int64_t o = tile / tiles_per_outer;
+    const int64_t v0 = (tile - o * tiles_per_outer) * kTileThreads;
+    const int nv = (int)min<int64_t>(kTileThreads, n_inner - v0);
+    uint8_t* lds_codes = lds;
+    uint8_t* lds_out = lds + ((kTileThreads * d + 15) & ~15);
+
+    const uint8_t* gc = reinterpret_cast<const uint8_t*>(codes + o * codes_outer + v0 * d);
+    {
+        // codes: 16-byte chunks when aligned, bytes otherwise
+        const int nbytes = nv * d;
+        int done = 0;
+        if ((((uintptr_t)gc) & 15) == 0) {
+            const int n16 = nbytes >> 4;
+            for (int i = threadIdx.x; i < n16; i += kTileThreads)
+                reinterpret_cast<uint4*>(lds_codes)[i] = reinterpret_cast<const uint4*>(gc)[i];
+            done = n16 << 4;
+        }
+        for (int i = done + threadIdx.x; i < nbytes; i += kTileThreads) lds_codes[i] = gc[i];
+    }
+    __syncthreads();
+    const int v = threadIdx.x;
+    if (v < nv) {
+        const float s = scales[o * scales_outer + v0 + v];
+        const int8_t* c = reinterpret_cast<const int8_t*>(lds_codes) + v * d;
+        S* y = reinterpret_cast<S*>(lds_out) + (int64_t)v * d;
+        for (int i = 0; i < d; ++i) {
+            const float f = (float)c[i] * s;
+            if constexpr (DT == NORI_F32) y[i] = __float_as_uint(f);
+            else if constexpr (DT == NORI_F16) y[i] = f32_to_f16(f);
+            else y[i] = f32_to_bf16(f);
+        }
+    }
+    __syncthreads();
+    copy_out(dst + o * dst_outer_bytes + v0 * d * es, lds_out, nv * d * es);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kTileThreads)
+dequant_direct_kernel(const int8_t* __restrict__ codes, int64_t n_outer, int64_t n_inner, int d,
+                      int64_t codes_outer, int64_t codes_inner, const float* __restrict__ scales,
+                      int64_t scales_outer, int64_t scales_inner, void* __restrict__ dst_v, int64_t dst_outer,
+                      int64_t dst_inner) {
+    using S = typename Storage<DT>::T;
+    S* dst = reinterpret_cast<S*>(dst_v);
+    const int64_t idx = (int64_t)blockIdx.x * kTileThreads + threadIdx.x;
+    if (idx >= n_outer * n_inner) return;
+    const int64_t o = idx / n_inner, i = idx - o * n_inner;
+    const float s = scales[o * scales_outer + i * scales_inner];
+    const int8_t* c = codes + o * codes_outer + i * codes_inner;
+    S* y = dst + o * dst_outer + i * dst_inner;
+    for (int e = 0; e < d; ++e) {
+        const float f = (float)c[e] * s;
+        if constexpr (DT == NORI_F32) y[e] = __float_as_uint(f);
+        else if constexpr (DT == NORI_F16) y[e] = f32_to_f16(f);
+        else y[e] = f32_to_bf16(f);
+    }
+}
+
+int check_common(int64_t n_outer, int64_t n_inner, int32_t d) {
+    if (n_outer < 0 || n_inner < 0) return fail(NORI_ERR_INVALID, "negative vector count (%lld x %lld)", (long long)n_outer, (long long)n_inner);
+    if (d <= 0) return fail(NORI_ERR_INVALID, "head width must be positive, got %d", d);
+    return NORI_OK;
+}
+
+}  // namespace
+
+extern "C" int nori_kv_quantize_int8(const void* src, int src_dtype, int64_t n_outer, int64_t n_inner, int32_t d,
+                                     int64_t src_outer_stride, int64_t src_inner_stride, int8_t* codes,
+                                     int64_t codes_outer_stride, int64_t codes_inner_stride, float* scales,
+                                     int64_t scales_outer_stride, int64_t scales_inner_stride, int32_t scale_div,
+                                     void* stream_v) {
+    clear_error();
+    if (int st = check_common(n_outer, n_inner, d)) return st;
+    if (src_dtype != NORI_F32 && src_dtype != NORI_F16 && src_dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "quantize_int8: unsupported source dtype %s", dtype_name(src_dtype));
+    if (scale_div != NORI_SCALE_DIV_TRUE && scale_div != NORI_SCALE_DIV_RECIP)
+        return fail(NORI_ERR_INVALID, "quantize_int8: unknown scale_div %d", scale_div);
+    if (n_outer == 0 || n_inner == 0) return NORI_OK;
+    if (!src || !codes || !scales) return fail(NORI_ERR_INVALID, "quantize_int8: null pointer");
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int es = dtype_size(src_dtype);
+    const bool tiled = src_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1 &&
+                       d * es <= kMaxTileVectorBytes;
+    if (tiled) {
+        const int64_t tiles_per_outer = (n_inner + kTileThreads - 1) / kTileThreads;
+        const int64_t grid = tiles_per_outer * n_outer;
+        const size_t lds = ((size_t)kTileThreads * d * es + 15) / 16 * 16 + (size_t)kTileThreads * d;
+        NORI_DISPATCH_FLOAT(src_dtype, DT,
+            hipLaunchKernelGGL(quantize_tile_kernel<DT>, dim3((unsigned)grid), dim3(kTileThreads), lds, stream,
+                               (const uint8_t*)src, n_inner, d, src_outer_stride * es, codes, codes_outer_stride,
+                               scales, scales_outer_stride, tiles_per_outer, scale_div));
+    } else {
+        const int64_t total = n_outer * n_inner;
+        const int64_t grid = (total + kTileThreads - 1) / kTileThreads;
+        NORI_DISPATCH_FLOAT(src_dtype, DT,
+            hipLaunchKernelGGL(quantize_direct_kernel<DT>, dim3((unsigned)grid), dim3(kTileThreads), 0, stream, src,
+                               n_outer, n_inner, d, src_outer_stride, src_inner_stride, codes, codes_outer_stride,
+                               codes_inner_stride, scales, scales_outer_stride, scales_inner_stride, scale_div));
+    }
+    return launch_status("quantize_int8");
+}
+
+extern "C" int nori_kv_dequantize_int8(const int8_t* codes, const float* scales, int64_t n_outer, int64_t n_inner,
+                                       int32_t d, int64_t codes_outer_stride, int64_t codes_inner_stride,
+                                       int64_t scales_outer_stride, int64_t scales_inner_stride, void* dst,
+                                       int dst_dtype, int64_t dst_outer_stride, int64_t dst_inner_stride,
+                                       void* stream_v) {
+    clear_error();
+    if (int st = check_common(n_outer, n_inner, d)) return st;
+    if (dst_dtype != NORI_F32 && dst_dtype != NORI_F16 && dst_dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "dequantize_int8: unsupported output dtype %s", dtype_name(dst_dtype));
+    if (n_outer == 0 || n_inner == 0) return NORI_OK;
+    if (!codes || !scales || !dst) return fail(NORI_ERR_INVALID, "dequantize_int8: null pointer");
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int es = dtype_size(dst_dtype);
+    const bool tiled = dst_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1 &&
+                       d * es <= kMaxTileVectorBytes;
+    if (tiled) {
+        const int64_t tiles_per_outer = (n_inner + kTileThreads - 1) / kTileThreads;
+        const int64_t grid = tiles_per_outer * n_outer;
+        const size_t lds = ((size_t)kTileThreads * d + 15) / 16 * 16 + (size_t)kTileThreads * d * es;
+        NORI_DISPATCH_FLOAT(dst_dtype, DT,
+            hipLaunchKernelGGL(dequant_tile_kernel<DT>, dim3((unsigned)grid), dim3(kTileThreads), lds, stream, codes,
+                               n_inner, d, codes_outer_stride, scales, scales_outer_stride, (uint8_t*)dst,
+                               dst_outer_stride * es, tiles_per_outer));
+    } else {
+        const int64_t total = n_outer * n_inner;
+        const int64_t grid = (total + kTileThreads - 1) / kTileThreads;
+        NORI_DISPATCH_FLOAT(dst_dtype, DT,
+            hipLaunchKernelGGL(dequant_direct_kernel<DT>, dim3((unsigned)grid), dim3(kTileThreads), 0, stream, codes,
+                               n_outer, n_inner, d, codes_outer_stride, codes_inner_stride, scales,
+                               scales_outer_stride, scales_inner_stride, dst, dst_outer_stride, dst_inner_stride));
+    }
+    return launch_status("dequantize_int8");
+}

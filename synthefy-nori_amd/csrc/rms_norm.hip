@@ -1,0 +1,177 @@
+// RMSNorm for gfx950: y = x * rsqrt(mean(x^2) + eps) (* w), rows of `cols` elements.
+//
+// Semantics: RMSNorm.forward with use_native=True, i.e. torch.nn.functional.rms_norm
+// (src/synthefy_nori/model/layer.py:251-253): the mean of squares and the product are
+// formed in fp32 and the result is rounded once to the input dtype (then multiplied by
+// the weight when one is given).
+//
+// Schedule. HBM-bound: each row is read once and written once. A group of G lanes
+// (G = the power of two covering the row's 16-byte chunks, at most 64) owns one row:
+// every lane loads 16-byte chunks, accumulates x^2 in fp32, the group reduces with
+// lane shuffles, and the same registers are scaled and stored. A 128-wide bf16 row
+// is 16 chunks, so one wavefront normalizes 4 rows per pass. Rows whose length or
+// alignment does not allow 16-byte chunks use an element-wise kernel.
+#include "nori_common.h"
+
+namespace {
+
+using namespace nori;
+
+constexpr int kThreads = 256;
+constexpr int kMaxChunksPerLane = 4;  // rows up to 64*4 chunks = 4 KiB on the chunked path
+
+template <int DT>
+__device__ __forceinline__ void unpack_chunk(const uint4& c, float* f) {
+    if constexpr (DT == NORI_F32) {
+        f[0] = __uint_as_float(c.x); f[1] = __uint_as_float(c.y);
+        f[2] = __uint_as_float(c.z); f[3] = __uint_as_float(c.w);
+    } else {
+        const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (DT == NORI_F16) {
+                f[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffff));
+                f[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
+            } else {
+                f[2 * k] = __uint_as_float(w[k] << 16);
+                f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint4 pack_chunk(const float* f) {
+    uint4 c;
+    if constexpr (DT == NORI_F32) {
+        c.x = __float_as_uint(f[0]); c.y = __float_as_uint(f[1]);
+        c.z = __float_as_uint(f[2]); c.w = __float_as_uint(f[3]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo, hi;
+            if constexpr (DT == NORI_F16) { lo = f32_to_f16(f[2 * k]); hi = f32_to_f16(f[2 * k + 1]); }
+            else { lo = f32_to_bf16(f[2 * k]); hi = f32_to_bf16(f[2 * k + 1]); }
+            w[k] = lo | (hi << 16);
+        }
+        c.x = w[0]; c.y = w[1]; c.z = w[2]; c.w = w[3];
+    }
+    return c;
+}
+
+// G lanes per row; rows_per_block = kThreads / G.
+template <int DT, int WDT, int G>
+__global__ void __launch_bounds__(kThreads)
+rms_norm_chunked_kernel(const uint8_t* __restrict__ x, int64_t rows, int cols, int64_t x_row_bytes,
+                        const void* __restrict__ w, float eps, uint8_t* __restrict__ y, int64_t y_row_bytes) {
+    constexpr int EPC = 16 / (DT == NORI_F32 ? 4 : 2);  // elements per 16-byte chunk
+    const int lane_in_row = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
+    const int nchunks = cols / EPC;
+    const bool active = row < rows;
+    float v[kMaxChunksPerLane][EPC];
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxChunksPerLane; ++k) {
+        const int ch = lane_in_row + k * G;
+        if (active && ch < nchunks) {
+            const uint4 c = *reinterpret_cast<const uint4*>(x + row * x_row_bytes + (int64_t)ch * 16);
+            unpack_chunk<DT>(c, v[k]);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) acc = fmaf(v[k][e], v[k][e], acc);
+        }
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, G);
+    const float inv = rsqrtf(acc / (float)cols + eps);
+#pragma unroll
+    for (int k = 0; k < kMaxChunksPerLane; ++k) {
+        const int ch = lane_in_row + k * G;
+        if (active && ch < nchunks) {
+            float o[EPC];
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+                o[e] = round_to<DT>(v[k][e] * inv);
+                if (w) o[e] = o[e] * load_elem<WDT>(w, (int64_t)ch * EPC + e);
+            }
+            *reinterpret_cast<uint4*>(y + row * y_row_bytes + (int64_t)ch * 16) = pack_chunk<DT>(o);
+        }
+    }
+}
+
+// One wavefront per row, element-wise loads: any width and alignment.
+template <int DT, int WDT>
+__global__ void __launch_bounds__(kThreads)
+rms_norm_elementwise_kernel(const void* __restrict__ x, int64_t rows, int cols, int64_t x_row_stride,
+                            const void* __restrict__ w, float eps, void* __restrict__ y, int64_t y_row_stride) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    float acc = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        const float v = load_elem<DT>(x, row * x_row_stride + c);
+        acc = fmaf(v, v, acc);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const float inv = rsqrtf(acc / (float)cols + eps);
+    for (int c = lane; c < cols; c += 64) {
+        float o = round_to<DT>(load_elem<DT>(x, row * x_row_stride + c) * inv);
+        if (w) o = o * load_elem<WDT>(w, c);
+        store_elem<DT>(y, row * y_row_stride + c, o);
+    }
+}
+
+template <int DT, int WDT>
+int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, float eps, void* y, int64_t ys,
+           hipStream_t stream) {
+    constexpr int es = (DT == NORI_F32) ? 4 : 2;
+    constexpr int EPC = 16 / es;
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ((xs * es) % 16 == 0) &&
+                         ((ys * es) % 16 == 0) && (cols % EPC == 0);
+    const int nchunks = cols / EPC;
+    if (aligned && nchunks <= 64 * kMaxChunksPerLane) {
+        int g = 1;
+        while (g < nchunks && g < 64) g <<= 1;
+        const int rows_per_block = kThreads / g;
+        const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+#define NORI_RMS_CASE(GV)                                                                                     \
+    case GV:                                                                                                   \
+        hipLaunchKernelGGL((rms_norm_chunked_kernel<DT, WDT, GV>), dim3(grid), dim3(kThreads), 0, stream,       \
+                           (const uint8_t*)x, rows, cols, xs * es, w, eps, (uint8_t*)y, ys * es);              \
+        break;
+        switch (g) {
+            NORI_RMS_CASE(1) NORI_RMS_CASE(2) NORI_RMS_CASE(4) NORI_RMS_CASE(8)
+            NORI_RMS_CASE(16) NORI_RMS_CASE(32) NORI_RMS_CASE(64)
+        }
+#undef NORI_RMS_CASE
+    } else {
+        const unsigned grid = (unsigned)((rows + (kThreads / 64) - 1) / (kThreads / 64));
+        hipLaunchKernelGGL((rms_norm_elementwise_kernel<DT, WDT>), dim3(grid), dim3(kThreads), 0, stream, x, rows,
+                           cols, xs, w, eps, y, ys);
+    }
+    return launch_status("rms_norm");
+}
+
+}  // namespace
+
+extern "C" int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
+                             const void* weight, int weight_dtype, float eps, void* y, int64_t y_row_stride,
+                             void* stream_v) {
+    clear_error();
+    if (rows < 0 || cols <= 0) return fail(NORI_ERR_INVALID, "rms_norm: bad shape rows=%lld cols=%d", (long long)rows, cols);
+    if (dtype != NORI_F32 && dtype != NORI_F16 && dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "rms_norm: unsupported dtype %s", dtype_name(dtype));
+    if (weight && weight_dtype != NORI_F32 && weight_dtype != NORI_F16 && weight_dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "rms_norm: unsupported weight dtype %s", dtype_name(weight_dtype));
+    if (rows == 0) return NORI_OK;
+    if (!x || !y) return fail(NORI_ERR_INVALID, "rms_norm: null pointer");
+    if (!weight) weight_dtype = dtype;
+    hipStream_t stream = (hipStream_t)stream_v;
+    int st = NORI_OK;
+    NORI_DISPATCH_FLOAT(dtype, DT,
+        NORI_DISPATCH_FLOAT(weight_dtype, WDT,
+            st = launch<DT, WDT>(x, rows, cols, x_row_stride, weight, eps, y, y_row_stride, stream)));
+    return st;
+}

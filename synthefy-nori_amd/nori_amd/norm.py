@@ -1,0 +1,66 @@
+"""RMSNorm on libnori_hip.so -- drop-in for ``RMSNorm`` (src/synthefy_nori/model/layer.py:233-258)."""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _native as nat
+
+
+def rms_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """x * rsqrt(mean(x^2) + eps) (* weight) over the trailing ``normalized_shape`` axes.
+
+    The native ``F.rms_norm`` semantics (layer.py:253): statistic and product in fp32,
+    one rounding to x's dtype, then the weight multiply.
+    """
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+    normalized_shape = tuple(normalized_shape)
+    if tuple(x.shape[-len(normalized_shape):]) != normalized_shape:
+        raise ValueError(f"input {tuple(x.shape)} does not end in normalized_shape {normalized_shape}")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise NotImplementedError(f"rms_norm takes float32/float16/bfloat16, got {x.dtype}")
+    device = nat.require_device(x, weight)
+    cols = 1
+    for s in normalized_shape:
+        cols *= int(s)
+    x2 = x.reshape(-1, cols)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    y = torch.empty((rows, cols), dtype=x.dtype, device=device)
+    w = None
+    if weight is not None:
+        w = weight.reshape(cols)
+        if not w.is_contiguous():
+            w = w.contiguous()
+    nat.check(
+        nat.lib().nori_rms_norm(
+            x2.data_ptr(), nat.dtype_code(x.dtype), rows, cols, x2.stride(0),
+            nat.ptr(w), nat.dtype_code(w.dtype) if w is not None else nat.NORI_F32, float(eps),
+            y.data_ptr(), y.stride(0), nat.stream_of(device),
+        ),
+        "rms_norm",
+    )
+    return y.reshape(x.shape)
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm with the reference constructor and state dict (layer.py:233-258), computed by HIP."""
+
+    def __init__(self, normalized_shape, eps=1e-5, elementwise_affine=False, device=None, dtype=None):
+        super().__init__()
+        if isinstance(normalized_shape, int):
+            normalized_shape = (normalized_shape,)
+        self.normalized_shape = tuple(normalized_shape)
+        self.eps = eps
+        self.elementwise_affine = elementwise_affine
+        self.use_native = True
+        if elementwise_affine:
+            self.weight = nn.Parameter(torch.ones(self.normalized_shape, device=device, dtype=dtype))
+        else:
+            self.register_parameter("weight", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return rms_norm(x, self.normalized_shape, self.weight, self.eps)

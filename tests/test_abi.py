@@ -1,0 +1,91 @@
+"""The C-ABI library loads and exports every entry point include/nori_hip.h declares.
+
+CPU only: no kernel is launched. Argument checks that fail before any device work are
+exercised too, with the exception types the reference raises for the same mistakes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO_ROOT
+
+HEADER = os.path.join(REPO_ROOT, "include", "nori_hip.h")
+
+
+def declared_symbols() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nori_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_symbols() == sorted(
+        [
+            "nori_abi_version",
+            "nori_last_error",
+            "nori_kv_quantize_int8",
+            "nori_kv_dequantize_int8",
+            "nori_rms_norm",
+            "nori_icl_attention",
+            "nori_icl_attention_workspace_size",
+        ]
+    )
+
+
+def test_library_exports_every_declared_symbol():
+    from nori_amd import _native
+
+    lib = ctypes.CDLL(_native.library_path())
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert set(declared_symbols()) == set(_native.SIGNATURES)
+    assert _native.lib().nori_abi_version() == 1
+
+
+def test_argument_errors_map_to_reference_exceptions():
+    from nori_amd import _native as nat
+
+    lib = nat.lib()
+    # head width 0 -> NORI_ERR_INVALID -> ValueError, before any device call
+    st = lib.nori_kv_quantize_int8(None, nat.NORI_BF16, 1, 1, 0, 0, 0, None, 0, 0, None, 0, 0, 1, None)
+    assert st == nat.NORI_ERR_INVALID
+    assert b"head width" in lib.nori_last_error()
+    with pytest.raises(ValueError):
+        nat.check(st, "quantize_int8")
+    # int8 source is not a float dtype -> NotImplementedError
+    st = lib.nori_kv_quantize_int8(None, nat.NORI_I8, 1, 1, 4, 4, 4, None, 0, 4, None, 0, 1, 1, None)
+    assert st == nat.NORI_ERR_UNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        nat.check(st, "quantize_int8")
+    # attention: heads not divisible by kv heads / odd head width / empty cache
+    args = [None, nat.NORI_BF16, 1, 1, 3, 64, 0, 0, 0, None, nat.NORI_I8, None, 8, 2, 0, 0, 0, 0, 0, 0, 1.0,
+            None, nat.NORI_BF16, 0, 0, 0, None, 0, None, 0, None]
+    assert lib.nori_icl_attention(*args) == nat.NORI_ERR_INVALID
+    args[4], args[13] = 4, 2
+    args[5] = 42
+    assert lib.nori_icl_attention(*args) == nat.NORI_ERR_UNSUPPORTED
+    args[5], args[12] = 64, 0
+    assert lib.nori_icl_attention(*args) == nat.NORI_ERR_INVALID
+    assert b"empty" in lib.nori_last_error()
+    # empty inputs are a no-op, not an error
+    assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
+    assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
+
+
+def test_operators_refuse_cpu_tensors():
+    import torch
+
+    import nori_amd
+
+    t = torch.randn(2, 3, 2, 1, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nori_amd.quantize_int8(t)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nori_amd.rms_norm(torch.randn(4, 8), 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nori_amd.icl_attention(torch.randn(2, 3, 1, 8), t)

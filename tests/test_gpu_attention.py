@@ -1,0 +1,188 @@
+"""GPU parity of query-row -> context attention over the (int8) K/V cache.
+
+Checked against the float64 oracle (oracle/attention.py) evaluated on the exact values
+the cache holds (codes x scales for int8 caches). Tolerance is the reference's bf16
+attention bar, max-abs <= 2e-2 (tests/test_blockwise_context_attention.py:172, 403);
+typical errors are reported in the assertion messages and sit near 1e-3.
+Covers the dense path, GQA/MQA, every supported head width, context lengths that are not
+multiples of the 64-row block, query counts that are not multiples of the 256-row tile,
+the split-context schedule, large logits (lazy max rescaling), the LSE output, the
+running-output merge (layer.py:915-920), and the BlockwiseSeqKV host-streamed and
+resident-int8 paths.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import nori_amd
+from nori_amd import attention as attn
+from nori_amd.kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def make_cache(bg, nk, hkv, d, device, seed, dtype=torch.float16, outliers=True):
+    g = torch.Generator().manual_seed(seed)
+    kv = torch.randn(bg, nk, 2, hkv, d, generator=g)
+    if outliers:
+        ch = torch.randperm(d, generator=g)[: max(1, round(0.02 * d))]
+        kv[..., ch] *= 8.0
+    return kv.to(dtype).to(device)
+
+
+def make_queries(bg, nq, h, d, device, seed, dtype=torch.bfloat16, gain=1.0):
+    g = torch.Generator().manual_seed(seed + 1000)
+    return (torch.randn(bg, nq, h, d, generator=g) * gain).to(dtype).to(device)
+
+
+def reference(q, kv_values, scale=None):
+    """float64 oracle over the values the cache represents: kv_values [BG, N, 2, Hkv, D]."""
+    kvv = kv_values.double().cpu().numpy()
+    out, lse = oa.attention_f64(q.double().cpu().numpy(), kvv[:, :, 0], kvv[:, :, 1], scale)
+    return torch.from_numpy(out), torch.from_numpy(lse)
+
+
+def check(got, exp, tol=TOL):
+    err = (got.double().cpu() - exp).abs()
+    assert err.max().item() <= tol, f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e})"
+
+
+@pytest.mark.parametrize("d", [8, 16, 44, 56, 64, 128])
+@pytest.mark.parametrize("heads,kv_heads", [(2, 2), (4, 1)])
+def test_int8_cache_matches_oracle(cuda, d, heads, kv_heads):
+    bg, nq, nk = 3, 300, 331
+    kv = make_cache(bg, nk, kv_heads, d, cuda, seed=d + heads)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, heads, d, cuda, seed=d)
+    lse = torch.empty(bg, heads, nq, device=cuda)
+    got = nori_amd.icl_attention(q, codes, scales, lse=lse)
+    assert got.dtype == q.dtype and got.shape == q.shape
+    values = codes.double() * scales.double()
+    exp, exp_lse = reference(q, values)
+    check(got, exp)
+    assert (lse.double().cpu() - exp_lse).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_full_precision_cache_matches_oracle(cuda, kv_dtype):
+    kv = make_cache(2, 200, 2, 64, cuda, seed=3, dtype=kv_dtype)
+    q = make_queries(2, 77, 2, 64, cuda, seed=3, dtype=torch.float16)
+    got = nori_amd.icl_attention(q, kv)
+    exp, _ = reference(q, kv)
+    check(got, exp)
+
+
+@pytest.mark.parametrize("nk", [1, 5, 63, 64, 65])
+@pytest.mark.parametrize("nq", [1, 31, 257])
+def test_ragged_lengths(cuda, nk, nq):
+    kv = make_cache(2, nk, 2, 44, cuda, seed=nk)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(2, nq, 2, 44, cuda, seed=nq)
+    got = nori_amd.icl_attention(q, codes, scales)
+    exp, _ = reference(q, codes.double() * scales.double())
+    check(got, exp)
+
+
+def test_split_context_schedule(cuda):
+    # one small (bg, head, query tile) grid over a long context: the kernel splits the
+    # context across workgroups and merges the partial (O, LSE) pairs
+    bg, h, nq, nk, d = 1, 2, 100, 5000, 64
+    assert attn.workspace_bytes(bg, nq, h, d, nk) > 0
+    kv = make_cache(bg, nk, h, d, cuda, seed=11)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, h, d, cuda, seed=11)
+    lse = torch.empty(bg, h, nq, device=cuda)
+    got = nori_amd.icl_attention(q, codes, scales, lse=lse)
+    exp, exp_lse = reference(q, codes.double() * scales.double())
+    check(got, exp)
+    assert (lse.double().cpu() - exp_lse).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("gain", [4.0, 12.0])
+def test_large_logits_exercise_rescaling(cuda, gain):
+    # QASS multiplies queries by ~log(n) (layer.py:433-456): logits of tens of units, where the
+    # running max must move between blocks; the first block is deliberately weak
+    bg, nq, nk, d = 2, 64, 700, 64
+    kv = make_cache(bg, nk, 2, d, cuda, seed=21)
+    kv[:, :64] *= 0.05
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, 2, d, cuda, seed=21, gain=gain)
+    got = nori_amd.icl_attention(q, codes, scales)
+    exp, _ = reference(q, codes.double() * scales.double())
+    check(got, exp)
+
+
+def test_merge_of_two_halves_equals_one_call(cuda):
+    bg, h, nq, nk, d = 2, 4, 50, 300, 56
+    kv = make_cache(bg, nk, 1, d, cuda, seed=31)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, h, d, cuda, seed=31)
+    run = torch.zeros(bg, nq, h, d, device=cuda)
+    lse = torch.full((bg, h, nq), float("-inf"), device=cuda)
+    for a, b in ((0, 130), (130, 300)):
+        nori_amd.icl_attention(q, codes[:, a:b], scales[:, a:b], out=run, lse=lse, merge=True)
+    exp, exp_lse = reference(q, codes.double() * scales.double())
+    check(run, exp)
+    assert (lse.double().cpu() - exp_lse).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("offload", [True, False])
+def test_blockwise_cache_paths(cuda, offload):
+    bg, h, nq, d = 3, 2, 40, 44
+    kv = make_cache(bg, 517, h, d, cuda, seed=41)
+    cache = BlockwiseSeqKV.from_row_slices(
+        (kv[:, a:b] for a, b in ((0, 200), (200, 201), (201, 517))), 1, bg, quantize=True, device=cuda,
+        dtype=kv.dtype, offload=offload, n_rows=517,
+    )
+    dense = ScalableSeqKV(kv, 1, bg, quantize=True, device=cuda)
+    q = make_queries(bg, nq, h, d, cuda, seed=41)
+    got = nori_amd.compute_attention_blockwise(q, cache)
+    payload, scales = dense.device_payload()
+    exp, _ = reference(q, payload.double() * scales.double())
+    check(got, exp)
+    got_dense = nori_amd.attend_dense(q, dense)
+    check(got_dense, exp)
+    if offload:
+        assert cache.max_staged_rows == 316 and cache.resident_gpu_bytes() == 0
+
+
+def test_config2_attention(cuda):
+    # isolated nori-6m ICL block: BG=9, 1024 queries over 4096 int8 context rows, H=2, D=64, bf16
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(9, 1024, 2, 64, generator=g)
+    kv = torch.randn(9, 4096, 2, 2, 64, generator=g)
+    ch = torch.randperm(128, generator=g)[:3]
+    q.view(9, 1024, 128)[..., ch] *= 8.0
+    kv.view(9, 4096, 2, 128)[..., ch] *= 8.0
+    q = q.to(torch.bfloat16).to(cuda)
+    kv = kv.to(torch.bfloat16).to(cuda)
+    codes, scales = nori_amd.quantize_int8(kv)
+    got = nori_amd.icl_attention(q, codes, scales)
+    exp, _ = reference(q, codes.double() * scales.double(), 1 / math.sqrt(64))
+    check(got, exp)
+    # against torch SDPA over the dequantized cache, as the reference's dense path computes it
+    deq = nori_amd.dequantize_int8(codes, scales, torch.bfloat16)
+    k, v = deq.unbind(dim=2)
+    sdpa = torch.nn.functional.scaled_dot_product_attention(
+        q.float().permute(0, 2, 1, 3), k.float().permute(0, 2, 1, 3).contiguous(), v.float().permute(0, 2, 1, 3).contiguous()
+    ).permute(0, 2, 1, 3)
+    assert (got.float() - sdpa).abs().max().item() <= TOL
+
+
+def test_shape_errors(cuda):
+    q = torch.randn(2, 5, 3, 16, device=cuda, dtype=torch.bfloat16)
+    kv = torch.randn(2, 7, 2, 2, 16, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cannot attend"):
+        nori_amd.icl_attention(q, kv)
+    with pytest.raises(ValueError, match="head width"):
+        nori_amd.icl_attention(q[..., :8], torch.randn(2, 7, 2, 3, 16, device=cuda))
+    with pytest.raises(NotImplementedError):
+        nori_amd.icl_attention(torch.randn(2, 5, 2, 6, device=cuda), torch.randn(2, 7, 2, 2, 6, device=cuda))

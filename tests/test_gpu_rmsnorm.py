@@ -1,0 +1,69 @@
+"""GPU parity of RMSNorm (layer.py:233-258) against the oracle and torch's F.rms_norm.
+
+Tolerance: the kernel forms the statistic in fp32 and rounds once to the dtype, so it
+may differ from the float64 oracle and from torch's native kernel by one unit in the
+last place of the output dtype (the reference documents 1 bf16 ulp between its own
+native and decomposed variants, predictor.py:247-250). Per element:
+|got - ref| <= 1 ulp(ref) of the dtype (fp32: 4 ulp, different summation order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import nori_amd
+from oracle import codec
+
+pytestmark = pytest.mark.gpu
+
+ULP_BITS = {torch.float32: 23, torch.float16: 10, torch.bfloat16: 7}
+ULPS = {torch.float32: 4, torch.float16: 1, torch.bfloat16: 1}
+
+
+def ulp(x: torch.Tensor, dtype) -> torch.Tensor:
+    a = x.abs().double().clamp_min(torch.finfo(dtype).tiny)
+    return torch.exp2(torch.floor(torch.log2(a)) - ULP_BITS[dtype])
+
+
+def oracle(x: torch.Tensor, w: torch.Tensor | None, eps: float) -> torch.Tensor:
+    c = x.cpu()
+    if c.dtype == torch.bfloat16:
+        raw = c.view(torch.int16).numpy().view(np.uint16)
+        wr = None if w is None else w.cpu().view(torch.int16).numpy().view(np.uint16)
+        out = codec.rms_norm(raw, wr, "bf16", eps)
+        return torch.from_numpy(out.view(np.int16)).view(torch.bfloat16)
+    name = "f32" if c.dtype == torch.float32 else "f16"
+    out = codec.rms_norm(c.numpy(), None if w is None else w.cpu().numpy(), name, eps)
+    return torch.from_numpy(out)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cols", [44, 64, 128, 352, 560, 100, 3])
+@pytest.mark.parametrize("affine", [False, True])
+def test_rms_norm_within_one_ulp(cuda, dtype, cols, affine):
+    g = torch.Generator(device=cuda).manual_seed(cols)
+    x = (torch.randn(3, 37, cols, generator=g, device=cuda) * 3).to(dtype)
+    w = (torch.rand(cols, generator=g, device=cuda) + 0.5).to(dtype) if affine else None
+    eps = 1e-6 if affine else 1e-5
+    got = nori_amd.rms_norm(x, cols, w, eps)
+    assert got.dtype == dtype and got.shape == x.shape
+    ref = oracle(x, w, eps).to(cuda)
+    tol = ULPS[dtype] * ulp(ref, dtype) * (2 if affine else 1)
+    assert torch.all((got.double() - ref.double()).abs() <= tol)
+    nat = torch.nn.functional.rms_norm(x, (cols,), weight=w, eps=eps)
+    assert torch.all((got.double() - nat.double()).abs() <= 2 * tol)
+
+
+def test_rms_norm_module_and_strided_rows(cuda):
+    m = nori_amd.RMSNorm(128, eps=1e-5).to(cuda)
+    x = torch.randn(2, 300, 9, 128, device=cuda, dtype=torch.bfloat16)
+    y = m(x)
+    ref = torch.nn.functional.rms_norm(x, (128,), eps=1e-5)
+    assert (y.float() - ref.float()).abs().max() <= 2 * 2.0**-7 * ref.float().abs().max()
+    # a non-contiguous row view (the [:, :eval_pos] slices of layer.py) takes the same path
+    xs = x[:, ::3]
+    ys = nori_amd.rms_norm(xs, 128, None, 1e-5)
+    assert torch.equal(ys, m(xs.contiguous()))
+    assert nori_amd.rms_norm(torch.empty(0, 64, device=cuda), 64).shape == (0, 64)

@@ -1,0 +1,80 @@
+"""Host-side logic of the drop-in cache containers that needs no kernel (CPU tensors).
+
+Mirrors the transport and error-behaviour checks of the reference's
+tests/test_kv_cache_scaling.py and tests/test_blockwise_context_attention.py.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nori_amd.kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, _vector_layout, scale_caches
+
+
+def _row_slices(kv, rows):
+    start = 0
+    for width in rows:
+        yield kv[:, start : start + width]
+        start += width
+
+
+def test_scalable_identity_and_offload_without_quantization():
+    kv = torch.randn(2, 50, 2, 4, 8)
+    c = ScalableSeqKV(kv, 2, 5, quantize=False, offload=False, device=torch.device("cpu"))
+    assert c["batch"] == 2 and c["groups"] == 5 and torch.equal(c["kv"], kv)
+    c = ScalableSeqKV(kv, 2, 5, quantize=False, offload=True, device=torch.device("cpu"))
+    assert torch.equal(c["kv"], kv) and c.resident_gpu_bytes() == 0
+    with pytest.raises(KeyError):
+        c["nope"]
+
+
+def test_from_row_slices_reassembles_and_rejects_empty():
+    kv = torch.randn(2, 100, 2, 3, 8)
+    out = ScalableSeqKV.from_row_slices(iter([kv[:, i : i + 32] for i in range(0, 100, 32)]), 2, 3, quantize=False,
+                                        device=torch.device("cpu"), dtype=kv.dtype)
+    assert torch.equal(out["kv"], kv)
+    with pytest.raises(ValueError):
+        ScalableSeqKV.from_row_slices(iter([]), 1, 1, quantize=True, device=torch.device("cpu"), dtype=torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_blockwise_transport_and_full_read_refusal(dtype):
+    kv = torch.randn(2, 11, 2, 3, 4, dtype=dtype)
+    cache = BlockwiseSeqKV.from_row_slices(_row_slices(kv, (3, 5, 3)), 1, 2, quantize=False,
+                                           device=torch.device("cpu"), dtype=dtype)
+    assert torch.equal(torch.cat(list(cache.iter_kv_blocks()), dim=1), kv)
+    assert cache.resident_gpu_bytes() == 0 and cache.host_bytes() == kv.numel() * kv.element_size()
+    assert cache.n_rows == 11 and cache.max_block_rows == 5 and cache.max_staged_rows == 5
+    with pytest.raises(RuntimeError, match="cannot materialize a full layer"):
+        cache["kv"]
+    blocks = list(cache.iter_kv_blocks(block_rows=2))
+    assert max(b.shape[1] for b in blocks) <= 2 and cache.max_staged_rows == 2
+    with pytest.raises(ValueError):
+        list(cache.iter_kv_blocks(block_rows=0))
+
+
+def test_blockwise_resident_requires_int8_and_row_count():
+    kv = torch.randn(1, 4, 2, 1, 4)
+    with pytest.raises(ValueError, match="quantize=True"):
+        BlockwiseSeqKV.from_row_slices(iter([kv]), 1, 1, quantize=False, device=torch.device("cpu"), offload=False, n_rows=4)
+    with pytest.raises(ValueError, match="positive n_rows"):
+        BlockwiseSeqKV.from_row_slices(iter([kv]), 1, 1, quantize=True, device=torch.device("cpu"), offload=False)
+    with pytest.raises(ValueError):
+        BlockwiseSeqKV([], 1, 1, device=torch.device("cpu"), dtype=torch.float32, quantized=False)
+
+
+def test_scale_caches_is_a_noop_when_off():
+    caches = [{"seq_kv": {"kv": torch.randn(1, 10, 2, 2, 4), "batch": 1, "groups": 1}}]
+    assert scale_caches(caches) is caches and isinstance(caches[0]["seq_kv"], dict)
+
+
+def test_vector_layout_collapses_leading_axes():
+    kv = torch.empty(3, 100, 2, 4, 44)
+    assert _vector_layout(kv) == (1, 3 * 100 * 2 * 4, 0, 44)
+    view = kv[:, 10:30]  # a row slice of preallocated storage: two strided levels
+    assert _vector_layout(view) == (3, 20 * 2 * 4, 100 * 2 * 4 * 44, 44)
+    scales = torch.empty(3, 100, 2, 4, 1)[:, 10:30]
+    assert _vector_layout(scales) == (3, 20 * 2 * 4, 100 * 2 * 4, 1)
+    assert _vector_layout(torch.empty(2, 3, 8)[:, :, ::2]) is None  # last axis not contiguous
+    assert _vector_layout(torch.empty(4, 5, 6, 8)[::2, ::2]) is None  # three levels
