@@ -1,0 +1,12 @@
+// Instantiations of the attention kernel for bfloat16 K/V caches (icl_attention_kernel.h).
+#include "icl_attention_kernel.h"
+
+namespace nori {
+namespace attn {
+
+int launch_bf16(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+    return launch_dtype<NORI_BF16>(dp, ones, nw, a, stream);
+}
+
+}  // namespace attn
+}  // namespace nori

@@ -1,0 +1,12 @@
+// Instantiations of the attention kernel for float32 K/V caches (icl_attention_kernel.h).
+#include "icl_attention_kernel.h"
+
+namespace nori {
+namespace attn {
+
+int launch_f32(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+    return launch_dtype<NORI_F32>(dp, ones, nw, a, stream);
+}
+
+}  // namespace attn
+}  // namespace nori

@@ -1,0 +1,521 @@
+// Query-row -> context attention kernel for gfx950 (device template; the host entry point
+// and the launch dispatch live in icl_attention.hip, the explicit instantiations in
+// icl_attention_<cache dtype>.hip).
+//
+// Semantics: out[b, i, h] = softmax_j(scale * q[b, i, h] . k[b, j, hk]) @ v[b, j, hk] with
+// hk = h / (heads / kv_heads), plus the natural-log LSE of the scaled logits: the dense cached
+// attention (layer.py:936-1049), the CPU online-softmax scan (layer.py:777-839) and the GPU
+// flex block + exact LSE merge (layer.py:841-934) of the reference, with the int8
+// dequantization of kv_cache_scaling.py:40-41 folded into the tile loads.
+//
+// Schedule. A workgroup of NW wavefronts owns NW*32 query rows of one (b, h) and one
+// context range, scanned in blocks of 64 keys.
+//   * Q lives in registers as f16 MFMA operands for the whole scan.
+//   * K/V blocks are software pipelined: while the wavefronts compute on block i from one
+//     LDS buffer, each thread holds its share of block i+1's raw cache words (issued before
+//     the compute, consumed after it) and converts them into the other buffer, so one
+//     barrier per block separates the two and the HBM latency hides under the MFMA work.
+//       K: int8 codes -> exact f16 integers (v_perm builds 1024+u, one packed add removes
+//          the bias); the row's scale times scale*log2(e) goes to an fp32 table, so the
+//          logit MFMA is exact in the codes and the scale is applied in fp32.
+//       V: codes -> fp32 * row scale -> f16 (RN), i.e. exactly the fp16 value the
+//          reference's dequantization produces; stored transposed ([d][key]) with keys
+//          permuted inside each 16-key group so the probabilities leave the logit MFMA in
+//          the operand order of the PV MFMA (no cross-lane moves).
+//   * Per wavefront and block: S^T = K Q^T (v_mfma_f32_32x32x16_f16, 32 keys x 32 queries per
+//     tile), x = s*kfac - m (one fma), online softmax in base 2 with lazy rescaling (the
+//     running max only moves when a block exceeds it by 2^8), P rounded to f16, and
+//     O^T += V^T P^T (v_mfma_f32_32x32x16_f16).
+//   * The softmax denominator comes out of the PV MFMA: when the head width leaves a padding
+//     row in the last 32-row tile of V^T, that row holds ones and accumulates sum_j p_j for
+//     free; only head widths that are multiples of 32 sum P on the VALU.
+//   * Workgroups are renumbered so that the query tiles and heads that read the same cache
+//     rows are dealt to the same XCD (the hardware deals workgroups round-robin over the 8
+//     XCDs), so each cache line comes from HBM once per XCD and is then served by its L2.
+#pragma once
+
+#include <math.h>
+
+#include "nori_common.h"
+
+namespace nori {
+namespace attn {
+
+constexpr int KB = 64;   // context rows (keys) per block
+constexpr int QPW = 32;  // query rows per wavefront
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleSlack = 8.0f;  // log2 units a block may exceed the running max by
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Args {
+    const void* q; int q_dtype; int64_t nq; int heads; int d;
+    int64_t q_bg, q_row, q_head;
+    const void* kv; const float* kvs; int64_t nk; int hgroup;
+    int64_t kv_bg, kv_row, kv_half, sc_bg, sc_row, sc_half;
+    float scale_log2;  // logit scale * log2(e)
+    void* out; int out_dtype; int64_t o_bg, o_row, o_head;
+    float* lse; uint32_t flags;
+    int64_t bg; int nqt; int nsplit; int64_t keys_per_split;
+    float* part_o; float* part_lse;  // [nsplit][bg][heads][nq][d], [nsplit][bg][heads][nq]
+    int64_t nunits;
+};
+
+// 4 int8 codes -> two f16x2 holding the same integers (exact): v_perm builds the f16 bit
+// patterns of 1024 + (c + 128), one packed add subtracts 1152.
+__device__ __forceinline__ void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) + bias);
+}
+
+// 4 int8 codes times an fp32 scale -> two f16x2, each product rounded to fp32 then to f16
+// (RN), the value of (q.float() * scale).to(float16). fma((c + 128), s, -128 s) is the
+// product c*s rounded once, since both terms are exact inside the fma. (float)(byte)
+// compiles to v_cvt_f32_ubyteN.
+__device__ __forceinline__ void codes_scaled_to_f16(uint32_t w, float s, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const float off = -128.0f * s;
+    const float v0 = pin_f32(fmaf((float)(u & 0xffu), s, off));
+    const float v1 = pin_f32(fmaf((float)((u >> 8) & 0xffu), s, off));
+    const float v2 = pin_f32(fmaf((float)((u >> 16) & 0xffu), s, off));
+    const float v3 = pin_f32(fmaf((float)((u >> 24) & 0xffu), s, off));
+    lo = __builtin_bit_cast(uint32_t, f16x2{(_Float16)v0, (_Float16)v1});
+    hi = __builtin_bit_cast(uint32_t, f16x2{(_Float16)v2, (_Float16)v3});
+}
+
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+    if (dt == NORI_F32) return reinterpret_cast<const float*>(p)[i];
+    if (dt == NORI_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v) {
+    if (dt == NORI_F32) reinterpret_cast<float*>(p)[i] = v;
+    else if (dt == NORI_F16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+    else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// Merge a normalized partial (o, lse) into the running fp32 output/LSE (layer.py:915-920).
+__device__ __forceinline__ void merge_weights(float lse_old, float lse_part, float& w_old, float& w_new,
+                                              float& lse_out) {
+    const float mx = fmaxf(lse_old, lse_part);
+    if (mx == -INFINITY) { w_old = 0.f; w_new = 0.f; lse_out = -INFINITY; return; }
+    lse_out = mx + log1pf(expf(-fabsf(lse_old - lse_part)));
+    w_old = expf(lse_old - lse_out);
+    w_new = expf(lse_part - lse_out);
+}
+
+// Raw cache words of one staging unit (4 key rows x 4 head elements of K or V).
+template <int KVT> struct Raw;
+template <> struct Raw<NORI_I8> { uint32_t w[4]; float s[4]; };
+template <> struct Raw<NORI_F16> { u32x2 w[4]; };
+template <> struct Raw<NORI_BF16> { u32x2 w[4]; };
+template <> struct Raw<NORI_F32> { u32x4 w[4]; };
+
+template <int DP, bool ONES>
+struct Geometry {
+    static_assert(DP % 16 == 0 && DP >= 16 && DP <= 128, "padded head width");
+    static constexpr int DV = (DP + 31) / 32 * 32;  // PV output rows (MFMA M granule)
+    static constexpr int KSTEPS = DP / 16;          // logit MFMA k-steps
+    static constexpr int VTILES = DV / 32;
+    static constexpr int DQMAX = DP / 4;            // 4-element quads per padded head vector
+    static constexpr int KPITCH = DP + 8;           // f16 per K row in LDS (+16 B: conflict-free b128 reads)
+    static constexpr int VPITCH = KB + 8;           // f16 per V^T row in LDS
+    static constexpr int KBUF = KB * KPITCH;
+    static constexpr int VBUF = DV * VPITCH;
+};
+
+// Register budget: narrow heads keep 4 wavefronts per SIMD (two 8-wave workgroups per CU).
+template <int DP, int NW>
+struct WavesPerEU { static constexpr int value = (NW == 8 && DP <= 48) ? 4 : 1; };
+
+template <int DP, int KVT, bool ONES, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
+icl_attention_kernel(const Args a) {
+    using G = Geometry<DP, ONES>;
+    constexpr int THREADS = NW * 64;
+    constexpr int UNITS = 2 * 16 * G::DQMAX;
+    constexpr int NU = (UNITS + THREADS - 1) / THREADS;  // staging units per thread (upper bound)
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2 * G::KBUF];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2 * G::VBUF];
+    __shared__ __attribute__((aligned(16))) float kfac[2 * KB];
+
+    // ---- work item, XCD-aware: the hardware deals workgroup i to XCD i % 8; give each XCD
+    // a contiguous range of work items (query tiles fastest, then heads, then context splits,
+    // then table-groups), so the workgroups an XCD runs together read the same cache rows.
+    const int64_t nb = a.nunits;
+    const int64_t xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    const int64_t per = nb / 8, extra = nb % 8;
+    const int64_t work = xcd * per + min<int64_t>(xcd, extra) + local;
+    const int qt = (int)(work % a.nqt);
+    int64_t rest = work / a.nqt;
+    const int h = (int)(rest % a.heads);
+    rest /= a.heads;
+    const int split = (int)(rest % a.nsplit);
+    const int64_t b = rest / a.nsplit;
+    const int hk = h / a.hgroup;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int64_t qi = (int64_t)qt * (NW * QPW) + wave * QPW + l32;
+    const int64_t k_begin = (int64_t)split * a.keys_per_split;
+    const int64_t k_end = min<int64_t>(a.nk, k_begin + a.keys_per_split);
+    const int nblk = (int)((k_end - k_begin + KB - 1) / KB);
+    const int d = a.d;
+    const int dqv = d >> 2;
+
+    // ---- constant LDS: K columns [d, DP) and V^T rows [d, DV) of both buffers are never
+    // staged; they stay zero, except the ones row (last V^T row) that sums P.
+    for (int i = tid; i < 2 * KB * (G::DQMAX - dqv); i += THREADS) {
+        const int bufsel = i / (KB * (G::DQMAX - dqv));
+        const int r = i % (KB * (G::DQMAX - dqv));
+        const int row = r / (G::DQMAX - dqv), dq = dqv + r % (G::DQMAX - dqv);
+        *reinterpret_cast<u32x2*>(&Ks[bufsel * G::KBUF + row * G::KPITCH + 4 * dq]) = u32x2{0u, 0u};
+    }
+    for (int i = tid; i < 2 * (G::DV - d) * KB; i += THREADS) {
+        const int bufsel = i / ((G::DV - d) * KB);
+        const int r = i % ((G::DV - d) * KB);
+        const int row = d + r / KB, col = r % KB;
+        Vt[bufsel * G::VBUF + row * G::VPITCH + col] = (ONES && row == G::DV - 1) ? (_Float16)1.0f : (_Float16)0.0f;
+    }
+
+    // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7]
+    f16x8 qf[G::KSTEPS];
+    {
+        const bool qok = qi < a.nq;
+        const int64_t qbase = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head;
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int dd = 16 * ks + 8 * hh + j;
+                qf[ks][j] = (qok && dd < d) ? (_Float16)load_as_f32(a.q, a.q_dtype, qbase + dd) : (_Float16)0.0f;
+            }
+        }
+    }
+
+    // ---- staging plan of this thread: unit u covers rows 4rq..4rq+3 and elements 4dq..4dq+3
+    // of K (kvsel 0; consecutive threads take consecutive dq, so loads are contiguous) or of V
+    // (kvsel 1; consecutive threads take consecutive rq, so the transposed LDS writes of a
+    // wavefront land in distinct banks). Loads go through one buffer descriptor per block
+    // based at the block's first row (a row holds K then V of every head, so valid rows end
+    // at nvalid*row_bytes): per-lane offsets are 32-bit and rows past the end of the context
+    // range fall outside the descriptor and read as zero. The same holds for the scales.
+    constexpr int kv_es = (KVT == NORI_F32) ? 4 : (KVT == NORI_I8 ? 1 : 2);
+    const uint32_t row_bytes = (uint32_t)(a.kv_row * kv_es);
+    const uint32_t srow_bytes = (uint32_t)(a.sc_row * 4);
+    uint32_t u_off[NU], u_soff[NU], u_lds[NU];
+    bool u_v[NU], u_on[NU], u_dq0[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        const int idx = tid + u * THREADS;
+        const int nk_units = 16 * dqv;
+        int rq, dq;
+        u_on[u] = idx < 2 * nk_units;
+        u_v[u] = idx >= nk_units;
+        if (!u_v[u]) { rq = idx / dqv; dq = idx - rq * dqv; }
+        else { const int v = idx - nk_units; rq = v & 15; dq = v >> 4; }
+        if (!u_on[u]) { rq = 0; dq = 0; }
+        u_dq0[u] = dq == 0;
+        u_off[u] = 4 * rq * row_bytes + (uint32_t)(((u_v[u] ? a.kv_half : 0) + hk * d + 4 * dq) * kv_es);
+        u_soff[u] = 4 * rq * srow_bytes + (uint32_t)(((u_v[u] ? a.sc_half : 0) + hk) * 4);
+        // LDS element offset of the unit's first write in a buffer
+        if (!u_v[u]) u_lds[u] = (uint32_t)(4 * rq * G::KPITCH + 4 * dq);
+        else u_lds[u] = (uint32_t)(4 * dq * G::VPITCH + 16 * (rq >> 2) + 4 * (((rq & 1) << 1) | ((rq >> 1) & 1)));
+    }
+    const char* kv_bg_base = reinterpret_cast<const char*>(a.kv) + b * a.kv_bg * kv_es;
+    const char* sc_bg_base = reinterpret_cast<const char*>(a.kvs) + b * a.sc_bg * 4;
+
+    auto load_block = [&](int64_t kb, Raw<KVT> (&raw)[NU]) {
+        const uint32_t nvalid = (uint32_t)min<int64_t>(KB, k_end - kb);
+        const __amdgpu_buffer_rsrc_t rkv = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kv_bg_base + kb * a.kv_row * kv_es), 0, (int)(nvalid * row_bytes), 0x00020000);
+        __amdgpu_buffer_rsrc_t rsc = rkv;
+        if constexpr (KVT == NORI_I8)
+            rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(sc_bg_base + kb * a.sc_row * 4), 0, (int)(nvalid * srow_bytes),
+                                                    0x00020000);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            if (!u_on[u]) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t off = u_off[u] + i * row_bytes;
+                if constexpr (KVT == NORI_I8) {
+                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b32(rkv, off, 0, 0);
+                    raw[u].s[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, u_soff[u] + i * srow_bytes, 0, 0));
+                } else if constexpr (KVT == NORI_F32) {
+                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b128(rkv, off, 0, 0);
+                } else {
+                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b64(rkv, off, 0, 0);
+                }
+            }
+        }
+    };
+
+    auto store_block = [&](int bufsel, const Raw<KVT> (&raw)[NU]) {
+        _Float16* Kd = Ks + bufsel * G::KBUF;
+        _Float16* Vd = Vt + bufsel * G::VBUF;
+        float* kf = kfac + bufsel * KB;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            if (!u_on[u]) continue;
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (KVT == NORI_I8) {
+                    if (!u_v[u]) codes_to_f16(raw[u].w[i], lo[i], hi[i]);
+                    else codes_scaled_to_f16(raw[u].w[i], raw[u].s[i], lo[i], hi[i]);
+                } else if constexpr (KVT == NORI_F16) {
+                    lo[i] = raw[u].w[i].x; hi[i] = raw[u].w[i].y;
+                } else if constexpr (KVT == NORI_BF16) {
+                    const u32x2 v = raw[u].w[i];
+                    lo[i] = pack_f16(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u));
+                    hi[i] = pack_f16(__uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+                } else {
+                    const u32x4 v = raw[u].w[i];
+                    lo[i] = pack_f16(__uint_as_float(v.x), __uint_as_float(v.y));
+                    hi[i] = pack_f16(__uint_as_float(v.z), __uint_as_float(v.w));
+                }
+            }
+            if (!u_v[u]) {
+                _Float16* dst = Kd + u_lds[u];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x2*>(dst + i * G::KPITCH) = u32x2{lo[i], hi[i]};
+                if (u_dq0[u]) {
+                    const int r0 = (int)(u_lds[u] / G::KPITCH);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float f = a.scale_log2;
+                        if constexpr (KVT == NORI_I8) f = raw[u].s[i] * a.scale_log2;
+                        kf[r0 + i] = f;
+                    }
+                }
+            } else {
+                // transpose the 4x4 (row, d) block; rows of a 16-key group go to columns with
+                // bits 2 and 3 of the key index swapped (the PV operand order)
+                _Float16* dst = Vd + u_lds[u];
+                *reinterpret_cast<u32x2*>(dst + 0 * G::VPITCH) =
+                    u32x2{__builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u), __builtin_amdgcn_perm(lo[3], lo[2], 0x05040100u)};
+                *reinterpret_cast<u32x2*>(dst + 1 * G::VPITCH) =
+                    u32x2{__builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u), __builtin_amdgcn_perm(lo[3], lo[2], 0x07060302u)};
+                *reinterpret_cast<u32x2*>(dst + 2 * G::VPITCH) =
+                    u32x2{__builtin_amdgcn_perm(hi[1], hi[0], 0x05040100u), __builtin_amdgcn_perm(hi[3], hi[2], 0x05040100u)};
+                *reinterpret_cast<u32x2*>(dst + 3 * G::VPITCH) =
+                    u32x2{__builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u), __builtin_amdgcn_perm(hi[3], hi[2], 0x07060302u)};
+            }
+        }
+    };
+
+    f32x16 o[G::VTILES];
+#pragma unroll
+    for (int vt = 0; vt < G::VTILES; ++vt) o[vt] = f32x16{};
+    float m_run = 0.0f;  // running max (log2 units)
+    float l_run = 0.0f;  // this lane's share of the denominator (VALU-summed head widths only)
+
+    {
+        Raw<KVT> raw[NU];
+        load_block(k_begin, raw);
+        store_block(0, raw);
+    }
+    __syncthreads();
+
+    for (int blk = 0; blk < nblk; ++blk) {
+        const int64_t kb = k_begin + (int64_t)blk * KB;
+        const int cur = blk & 1;
+        const bool more = blk + 1 < nblk;
+        Raw<KVT> raw[NU];
+        if (more) load_block(kb + KB, raw);  // in flight during the compute below
+
+        const _Float16* Kc = Ks + cur * G::KBUF;
+        const _Float16* Vc = Vt + cur * G::VBUF;
+        const float* kf = kfac + cur * KB;
+
+        // ---------------- logits S^T[32 keys x 32 queries] for the two 32-key halves
+        f32x16 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                const f16x8 kfr = *reinterpret_cast<const f16x8*>(&Kc[(32 * t + l32) * G::KPITCH + 16 * ks + 8 * hh]);
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qf[ks], s[t], 0, 0, 0);
+            }
+        }
+        // lane holds keys 32t + 8g + 4hh + i (g, i in 0..3) of query qi
+        float x[2][16];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 f = *reinterpret_cast<const f32x4*>(&kf[32 * t + 8 * g + 4 * hh]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[t][4 * g + i] = fmaf(s[t][4 * g + i], f[i], -m_run);
+            }
+        if (kb + KB > k_end) {  // the last block of a context range may be partial
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (kb + 32 * t + 8 * g + 4 * hh + i >= k_end) x[t][4 * g + i] = -INFINITY;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) bm = __builtin_fmaxf(bm, __builtin_fmaxf(x[t][r], x[t][r + 1]));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const bool first = blk == 0;
+        if (first || __any(bm > kRescaleSlack)) {
+            // anchor the running max on the first block; afterwards move it up where a block
+            // overshoots it (rare: the max settles within the first few blocks)
+            const float shift = first ? bm : fmaxf(bm, 0.0f);
+            if (!first) {
+                const float alpha = __builtin_amdgcn_exp2f(-shift);
+                l_run *= alpha;
+#pragma unroll
+                for (int vt = 0; vt < G::VTILES; ++vt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[vt][r] *= alpha;
+            }
+            m_run += shift;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) x[t][r] -= shift;
+        }
+        // ---------------- probabilities (f16, RN) and PV
+        f16x8 pf[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(x[c >> 1][8 * (c & 1) + j]);
+                const float p1 = __builtin_amdgcn_exp2f(x[c >> 1][8 * (c & 1) + j + 1]);
+                const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
+                if constexpr (!ONES) {
+                    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+                    l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
+                }
+                pf[c][j] = pp[0];
+                pf[c][j + 1] = pp[1];
+            }
+        }
+#pragma unroll
+        for (int vt = 0; vt < G::VTILES; ++vt) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vc[(32 * vt + l32) * G::VPITCH + 16 * c + 8 * hh]);
+                o[vt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[vt], 0, 0, 0);
+            }
+        }
+        if (more) store_block(cur ^ 1, raw);
+        __syncthreads();
+    }
+
+    // ---------------- epilogue
+    float l_tot;
+    if constexpr (ONES) {
+        // O^T row DV-1 (tile VTILES-1, g = 3, i = 3) sits in the upper half-wave
+        const float mine = o[G::VTILES - 1][15];
+        const float other = __shfl_xor(mine, 32);
+        l_tot = hh ? mine : other;
+    } else {
+        l_tot = l_run + __shfl_xor(l_run, 32);
+    }
+    if (qi >= a.nq) return;
+    const float inv = 1.0f / l_tot;
+    const float lse_part = (m_run + __log2f(l_tot)) * kLn2;
+    if (a.nsplit > 1) {
+        const int64_t prow = ((split * a.bg + b) * a.heads + h) * a.nq + qi;
+        float* po = a.part_o + prow * d;
+#pragma unroll
+        for (int vt = 0; vt < G::VTILES; ++vt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d0 = 32 * vt + 8 * g + 4 * hh;
+                if (d0 < d)
+                    *reinterpret_cast<f32x4*>(po + d0) =
+                        f32x4{o[vt][4 * g] * inv, o[vt][4 * g + 1] * inv, o[vt][4 * g + 2] * inv, o[vt][4 * g + 3] * inv};
+            }
+        if (hh == 0) a.part_lse[prow] = lse_part;
+        return;
+    }
+    const int64_t obase = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head;
+    const int64_t lse_idx = (b * a.heads + h) * a.nq + qi;
+    const bool merge = a.flags & NORI_ATTN_MERGE;
+    float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
+    if (merge) merge_weights(a.lse[lse_idx], lse_part, w_old, w_new, lse_out);
+#pragma unroll
+    for (int vt = 0; vt < G::VTILES; ++vt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * vt + 8 * g + 4 * hh;
+            if (d0 < d) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = o[vt][4 * g + i] * inv;
+                    if (merge) v = reinterpret_cast<const float*>(a.out)[obase + d0 + i] * w_old + v * w_new;
+                    store_from_f32(a.out, a.out_dtype, obase + d0 + i, v);
+                }
+            }
+        }
+    if (a.lse && hh == 0) a.lse[lse_idx] = lse_out;
+}
+
+// Launches the kernel instantiation for (cache dtype KVT, dp, ones, nw) over a.nunits
+// workgroups. Each icl_attention_<dtype>.hip instantiates one KVT (parallel builds).
+template <int KVT, int DP, bool ONES>
+int launch_shape(int nw, const Args& a, hipStream_t stream) {
+    const dim3 grid((unsigned)a.nunits);
+    if (nw == 8) hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 8>), grid, dim3(8 * 64), 0, stream, a);
+    else hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 2>), grid, dim3(2 * 64), 0, stream, a);
+    return NORI_OK;
+}
+
+template <int KVT>
+int launch_dtype(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+    switch (dp) {
+        case 16: return launch_shape<KVT, 16, true>(nw, a, stream);
+        case 32: return ones ? launch_shape<KVT, 32, true>(nw, a, stream) : launch_shape<KVT, 32, false>(nw, a, stream);
+        case 48: return launch_shape<KVT, 48, true>(nw, a, stream);
+        case 64: return ones ? launch_shape<KVT, 64, true>(nw, a, stream) : launch_shape<KVT, 64, false>(nw, a, stream);
+        case 80: return launch_shape<KVT, 80, true>(nw, a, stream);
+        case 96: return ones ? launch_shape<KVT, 96, true>(nw, a, stream) : launch_shape<KVT, 96, false>(nw, a, stream);
+        case 112: return launch_shape<KVT, 112, true>(nw, a, stream);
+        case 128: return ones ? launch_shape<KVT, 128, true>(nw, a, stream) : launch_shape<KVT, 128, false>(nw, a, stream);
+        default: return fail(NORI_ERR_UNSUPPORTED, "icl_attention: no kernel for padded head width %d", dp);
+    }
+}
+
+int launch_i8(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
+int launch_f16(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
+int launch_bf16(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
+int launch_f32(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
+
+inline int launch_kvt(int kv_dtype, int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+    switch (kv_dtype) {
+        case NORI_I8: return launch_i8(dp, ones, nw, a, stream);
+        case NORI_F16: return launch_f16(dp, ones, nw, a, stream);
+        case NORI_BF16: return launch_bf16(dp, ones, nw, a, stream);
+        case NORI_F32: return launch_f32(dp, ones, nw, a, stream);
+        default: return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported cache dtype %s", dtype_name(kv_dtype));
+    }
+}
+
+// Workgroups of the int8-cache kernel for (dp, ones, nw) that fit on one CU at once.
+int resident_workgroups(int dp, bool ones, int nw);
+
+}  // namespace attn
+}  // namespace nori

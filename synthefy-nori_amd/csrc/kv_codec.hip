@@ -25,6 +25,10 @@
 // tiny, huge, infinite or NaN scale) divide exactly.
 #include "nori_common.h"
 
+// torch rounds the result of every op separately; no multiply-add is fused here unless
+// the source writes fmaf. (Narrowing conversions are kept apart by pin_f32.)
+#pragma clang fp contract(off)
+
 namespace {
 
 using namespace nori;

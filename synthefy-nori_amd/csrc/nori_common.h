@@ -47,15 +47,23 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // which is what torch's .to(dtype) and its per-op result rounding do.
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// Hides an fp32 value from instruction selection. The backend otherwise folds a multiply
+// (or fma) followed by a narrowing to fp16 into one v_fma_mixlo_f16, which rounds the exact
+// product straight to fp16; torch rounds it to fp32 first and then to fp16.
+__device__ __forceinline__ float pin_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    __bf16 h = (__bf16)f;
+    __bf16 h = (__bf16)pin_f32(f);
     return __builtin_bit_cast(uint16_t, h);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
-    _Float16 h = (_Float16)f;
+    _Float16 h = (_Float16)pin_f32(f);
     return __builtin_bit_cast(uint16_t, h);
 }
 

@@ -13,6 +13,10 @@
 // alignment does not allow 16-byte chunks use an element-wise kernel.
 #include "nori_common.h"
 
+// torch rounds the result of every op separately; no multiply-add is fused here unless
+// the source writes fmaf. (Narrowing conversions are kept apart by pin_f32.)
+#pragma clang fp contract(off)
+
 namespace {
 
 using namespace nori;

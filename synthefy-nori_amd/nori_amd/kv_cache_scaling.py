@@ -68,6 +68,24 @@ def _source_layout(t: torch.Tensor) -> tuple[torch.Tensor, tuple[int, int, int, 
     return t, layout
 
 
+def _split_strides(layout: tuple[int, int, int, int] | None, n_outer: int, n_inner: int) -> tuple[int, int] | None:
+    """(outer, inner) strides addressing ``layout``'s vectors as an ``n_outer`` x ``n_inner`` grid.
+
+    A single-level layout (vectors at k * inner) takes any split of its count; a two-level
+    one only its own. None when the vectors cannot be addressed that way.
+    """
+    if layout is None:
+        return None
+    lo, li, so, si = layout
+    if lo * li != n_outer * n_inner:
+        return None
+    if (lo, li) == (n_outer, n_inner):
+        return so, si
+    if lo == 1:
+        return n_inner * si, si
+    return None
+
+
 def _quantize_into(src: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor) -> None:
     """Quantize ``src`` (float, last axis = head vector) into preallocated ``codes``/``scales`` views."""
     device = nat.require_device(src, codes, scales)
@@ -78,21 +96,28 @@ def _quantize_into(src: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor)
     if src.numel() == 0:
         return
     src, (so, si, sos, sis) = _source_layout(src)
-    c_layout = _vector_layout(codes)
-    s_layout = _vector_layout(scales)
-    if c_layout is None or s_layout is None or c_layout[:2] != (so, si) or s_layout[:2] != (so, si):
-        # the destinations do not share the source's vector grouping: go through fresh buffers
+    c_str = _split_strides(_vector_layout(codes), so, si)
+    s_str = _split_strides(_vector_layout(scales), so, si)
+    if c_str is None or s_str is None:
+        # the destinations cannot be addressed with the source's vector grid: code into
+        # contiguous buffers (always addressable) and copy
         tmp_c = torch.empty(src.shape, dtype=torch.int8, device=device)
         tmp_s = torch.empty(tuple(src.shape[:-1]) + (1,), dtype=torch.float32, device=device)
-        _quantize_into(src, tmp_c, tmp_s)
+        _launch_quantize(src, (so, si, sos, sis), tmp_c, _split_strides(_vector_layout(tmp_c), so, si),
+                         tmp_s, _split_strides(_vector_layout(tmp_s), so, si), device)
         codes.copy_(tmp_c)
         scales.copy_(tmp_s)
         return
+    _launch_quantize(src, (so, si, sos, sis), codes, c_str, scales, s_str, device)
+
+
+def _launch_quantize(src, src_layout, codes, c_str, scales, s_str, device) -> None:
+    so, si, sos, sis = src_layout
     nat.check(
         nat.lib().nori_kv_quantize_int8(
             src.data_ptr(), nat.dtype_code(src.dtype), so, si, src.shape[-1], sos, sis,
-            codes.data_ptr(), c_layout[2], c_layout[3],
-            scales.data_ptr(), s_layout[2], s_layout[3],
+            codes.data_ptr(), c_str[0], c_str[1],
+            scales.data_ptr(), s_str[0], s_str[1],
             nat.SCALE_DIV_RECIP, nat.stream_of(device),
         ),
         "quantize_int8",
@@ -105,21 +130,24 @@ def _dequantize_into(q: torch.Tensor, scale: torch.Tensor, out: torch.Tensor) ->
         return
     q, (qo, qi, qos, qis) = _source_layout(q)
     scale, s_layout = _source_layout(scale)
-    _, _, sos, sis = s_layout
-    o_layout = _vector_layout(out)
-    if o_layout is None or o_layout[:2] != (qo, qi) or s_layout[:2] != (qo, qi):
-        q, scale = q.contiguous(), scale.contiguous()
-        tmp = torch.empty(q.shape, dtype=out.dtype, device=device)
-        _dequantize_into(q, scale, tmp)
-        out.copy_(tmp)
-        return
+    s_str = _split_strides(s_layout, qo, qi)
+    o_str = _split_strides(_vector_layout(out), qo, qi)
+    if s_str is None:
+        scale = scale.contiguous()
+        s_str = _split_strides(_vector_layout(scale), qo, qi)
+    target = out
+    if o_str is None:
+        target = torch.empty(q.shape, dtype=out.dtype, device=device)
+        o_str = _split_strides(_vector_layout(target), qo, qi)
     nat.check(
         nat.lib().nori_kv_dequantize_int8(
-            q.data_ptr(), scale.data_ptr(), qo, qi, q.shape[-1], qos, qis, sos, sis,
-            out.data_ptr(), nat.dtype_code(out.dtype), o_layout[2], o_layout[3], nat.stream_of(device),
+            q.data_ptr(), scale.data_ptr(), qo, qi, q.shape[-1], qos, qis, s_str[0], s_str[1],
+            target.data_ptr(), nat.dtype_code(out.dtype), o_str[0], o_str[1], nat.stream_of(device),
         ),
         "dequantize_int8",
     )
+    if target is not out:
+        out.copy_(target)
 
 
 # ----------------------------------------------------------------------------- codec

@@ -2,8 +2,9 @@
 
 Checked against the float64 oracle (oracle/attention.py) evaluated on the exact values
 the cache holds (codes x scales for int8 caches). Tolerance is the reference's bf16
-attention bar, max-abs <= 2e-2 (tests/test_blockwise_context_attention.py:172, 403);
-typical errors are reported in the assertion messages and sit near 1e-3.
+attention bar, assert_close(rtol=2e-2, atol=2e-2), i.e. |got - exp| <= 2e-2 + 2e-2*|exp|
+(tests/test_blockwise_context_attention.py:172, 403); the assertion messages report the
+max and mean absolute errors, which sit near 1e-3.
 Covers the dense path, GQA/MQA, every supported head width, context lengths that are not
 multiples of the 64-row block, query counts that are not multiples of the 256-row tile,
 the split-context schedule, large logits (lazy max rescaling), the LSE output, the
@@ -51,8 +52,16 @@ def reference(q, kv_values, scale=None):
 
 
 def check(got, exp, tol=TOL):
+    """|got - exp| <= tol + tol * |exp| elementwise: torch.testing.assert_close(rtol=tol, atol=tol),
+    the criterion of the reference's own bf16 attention tests."""
+    exp = exp.double()
     err = (got.double().cpu() - exp).abs()
-    assert err.max().item() <= tol, f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e})"
+    bound = tol + tol * exp.abs()
+    worst = int(torch.argmax(err - bound))
+    assert bool((err <= bound).all()), (
+        f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e}); worst excess at flat index {worst}: "
+        f"got {got.double().cpu().flatten()[worst].item():.5f} vs {exp.flatten()[worst].item():.5f}"
+    )
 
 
 @pytest.mark.parametrize("d", [8, 16, 44, 56, 64, 128])
@@ -168,13 +177,15 @@ def test_config2_attention(cuda):
     got = nori_amd.icl_attention(q, codes, scales)
     exp, _ = reference(q, codes.double() * scales.double(), 1 / math.sqrt(64))
     check(got, exp)
-    # against torch SDPA over the dequantized cache, as the reference's dense path computes it
-    deq = nori_amd.dequantize_int8(codes, scales, torch.bfloat16)
+    # against torch SDPA over the fp32-dequantized cache: the reference's dense path as it runs
+    # on the CPU (fp32 cache dtype). With x8 outlier channels in both Q and K the logits reach
+    # ~200, where a bf16 dequantization alone moves outputs by O(1); fp32 keeps the check sharp.
+    deq = nori_amd.dequantize_int8(codes, scales, torch.float32).cpu()
     k, v = deq.unbind(dim=2)
     sdpa = torch.nn.functional.scaled_dot_product_attention(
-        q.float().permute(0, 2, 1, 3), k.float().permute(0, 2, 1, 3).contiguous(), v.float().permute(0, 2, 1, 3).contiguous()
+        q.cpu().float().permute(0, 2, 1, 3), k.permute(0, 2, 1, 3).contiguous(), v.permute(0, 2, 1, 3).contiguous()
     ).permute(0, 2, 1, 3)
-    assert (got.float() - sdpa).abs().max().item() <= TOL
+    check(got, sdpa.double())
 
 
 def test_shape_errors(cuda):

@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from nori_amd.kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, _vector_layout, scale_caches
+from nori_amd.kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, _split_strides, _vector_layout, scale_caches
 
 
 def _row_slices(kv, rows):
@@ -78,3 +78,25 @@ def test_vector_layout_collapses_leading_axes():
     assert _vector_layout(scales) == (3, 20 * 2 * 4, 100 * 2 * 4, 1)
     assert _vector_layout(torch.empty(2, 3, 8)[:, :, ::2]) is None  # last axis not contiguous
     assert _vector_layout(torch.empty(4, 5, 6, 8)[::2, ::2]) is None  # three levels
+
+
+def test_split_strides_addresses_contiguous_outputs_of_a_sliced_source():
+    # a row slice of a cache is two-level (3 x 800 vectors); the fresh contiguous codes and
+    # scales that quantize_int8 allocates for it are single-level and must take that split
+    src = torch.empty(3, 517, 2, 2, 44)[:, 0:200]
+    so, si, sos, sis = _vector_layout(src)
+    assert (so, si) == (3, 800)
+    codes = torch.empty(src.shape, dtype=torch.int8)
+    scales = torch.empty(tuple(src.shape[:-1]) + (1,))
+    assert _split_strides(_vector_layout(codes), so, si) == (800 * 44, 44)
+    assert _split_strides(_vector_layout(scales), so, si) == (800, 1)
+    # element addresses agree with torch's own indexing
+    o, i = 2, 517
+    assert codes[o].reshape(-1, 44)[i].data_ptr() - codes.data_ptr() == o * 800 * 44 + i * 44
+    # a two-level destination only takes its own split; mismatched counts are refused
+    view = torch.empty(3, 517, 2, 2, 44)[:, 100:300]
+    assert _split_strides(_vector_layout(view), 3, 800) == (517 * 4 * 44, 44)
+    assert _split_strides(_vector_layout(view), 1, 2400) is None
+    assert _split_strides(_vector_layout(codes), 4, 600) == (600 * 44, 44)
+    assert _split_strides(_vector_layout(codes), 4, 601) is None
+    assert _split_strides(None, 1, 1) is None
