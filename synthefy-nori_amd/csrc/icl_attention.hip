@@ -74,7 +74,7 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     Plan p;
     p.dp = (d + 15) / 16 * 16;
     p.ones = (d % 32) != 0;
-    p.nw = nq > 96 ? 8 : 2;
+    p.nw = (nq > 256 && p.dp <= 48) ? 16 : (nq > 96 ? 8 : 2);
     p.nqt = (int)((nq + p.nw * QPW - 1) / (p.nw * QPW));
     const int64_t nkb = (nk + KB - 1) / KB;
     const int64_t base = bg * heads * (int64_t)p.nqt;

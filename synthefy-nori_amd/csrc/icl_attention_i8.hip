@@ -14,6 +14,12 @@ template <int DP, bool ONES>
 int occupancy(int nw) {
     int n = 0;
     hipError_t e;
+    if constexpr (DP <= 48) {
+        if (nw == 16) {
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 16>, 16 * 64, 0);
+            return e == hipSuccess ? n : 1;
+        }
+    }
     if (nw == 8) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 8>, 8 * 64, 0);
     else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 2>, 2 * 64, 0);
     return e == hipSuccess ? n : 1;
@@ -23,8 +29,8 @@ int occupancy(int nw) {
 
 int resident_workgroups(int dp, bool ones, int nw) {
     // cached per shape: the answer depends only on the compiled kernel and the device
-    static int cache[8][2][2] = {};
-    const int di = dp / 16 - 1, oi = ones ? 1 : 0, ni = nw == 8 ? 1 : 0;
+    static int cache[8][2][3] = {};
+    const int di = dp / 16 - 1, oi = ones ? 1 : 0, ni = nw == 16 ? 2 : (nw == 8 ? 1 : 0);
     if (di < 0 || di > 7) return 1;
     int& slot = cache[di][oi][ni];
     if (slot == 0) {

@@ -18,8 +18,8 @@
 //       K: int8 codes -> exact f16 integers (v_perm builds 1024+u, one packed add removes
 //          the bias); the row's scale times scale*log2(e) goes to an fp32 table, so the
 //          logit MFMA is exact in the codes and the scale is applied in fp32.
-//       V: codes -> fp32 * row scale -> f16 (RN), i.e. exactly the fp16 value the
-//          reference's dequantization produces; stored transposed ([d][key]) with keys
+//       V: exact f16 codes times the f16 row scale (one packed multiply, RN): the fp16
+//          value the reference's dequantization produces; stored transposed ([d][key]) with keys
 //          permuted inside each 16-key group so the probabilities leave the logit MFMA in
 //          the operand order of the PV MFMA (no cross-lane moves).
 //   * Per wavefront and block: S^T = K Q^T (v_mfma_f32_32x32x16_f16, 32 keys x 32 queries per
@@ -74,19 +74,40 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t&
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) + bias);
 }
 
-// 4 int8 codes times an fp32 scale -> two f16x2, each product rounded to fp32 then to f16
-// (RN), the value of (q.float() * scale).to(float16). fma((c + 128), s, -128 s) is the
-// product c*s rounded once, since both terms are exact inside the fma. (float)(byte)
-// compiles to v_cvt_f32_ubyteN.
+// 4 int8 codes times a row scale -> two f16x2: exact f16 code integers times the scale
+// rounded to f16, one packed multiply (RN). For caches built from fp16 or bf16 tensors the
+// scale is an fp16/bf16 value, exactly representable in f16, so this is the value of
+// (q.float() * scale).to(float16), the reference's fp16 dequantization, bit for bit; an
+// fp32-built cache picks up one extra f16 rounding of its scale (2^-11 relative).
 __device__ __forceinline__ void codes_scaled_to_f16(uint32_t w, float s, uint32_t& lo, uint32_t& hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const float off = -128.0f * s;
-    const float v0 = pin_f32(fmaf((float)(u & 0xffu), s, off));
-    const float v1 = pin_f32(fmaf((float)((u >> 8) & 0xffu), s, off));
-    const float v2 = pin_f32(fmaf((float)((u >> 16) & 0xffu), s, off));
-    const float v3 = pin_f32(fmaf((float)((u >> 24) & 0xffu), s, off));
-    lo = __builtin_bit_cast(uint32_t, f16x2{(_Float16)v0, (_Float16)v1});
-    hi = __builtin_bit_cast(uint32_t, f16x2{(_Float16)v2, (_Float16)v3});
+    codes_to_f16(w, lo, hi);
+    const _Float16 sh = (_Float16)s;
+    const f16x2 s2 = {sh, sh};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) * s2);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) * s2);
+}
+
+// v_max3_f32 / v_max_f32 without the NaN-quieting copies the compiler puts in front of
+// fmaxf operands (the logits are MFMA results; NaN inputs give NaN outputs either way).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+__device__ __forceinline__ float max2f(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// Value of lane l ^ 32 (the other half-wave), via v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ float other_half(float v) {
+    // the swap trades lanes 32-63 of the first operand with lanes 0-31 of the second: r[0]
+    // holds lanes 0-31 of v in both halves, r[1] lanes 32-63. fi=true reads the partner lane
+    // even where the compiler has masked it off (a select around the call may do that).
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+    return __uint_as_float((__lane_id() < 32) ? r[1] : r[0]);
 }
 
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
@@ -137,7 +158,7 @@ struct Geometry {
 
 // Register budget: narrow heads keep 4 wavefronts per SIMD (two 8-wave workgroups per CU).
 template <int DP, int NW>
-struct WavesPerEU { static constexpr int value = (NW == 8 && DP <= 48) ? 4 : 1; };
+struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 48)) ? 4 : 1; };
 
 template <int DP, int KVT, bool ONES, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
@@ -370,12 +391,19 @@ icl_attention_kernel(const Args a) {
                     for (int i = 0; i < 4; ++i)
                         if (kb + 32 * t + 8 * g + 4 * hh + i >= k_end) x[t][4 * g + i] = -INFINITY;
         }
-        float bm = -INFINITY;
+        float ma = max3f(x[0][0], x[0][1], x[0][2]);
+        float mb = max3f(x[1][0], x[1][1], x[1][2]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) bm = __builtin_fmaxf(bm, __builtin_fmaxf(x[t][r], x[t][r + 1]));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        for (int r = 3; r < 15; r += 2) {
+            ma = max3f(ma, x[0][r], x[0][r + 1]);
+            mb = max3f(mb, x[1][r], x[1][r + 1]);
+        }
+        float bm = max3f(ma, mb, max2f(x[0][15], x[1][15]));
+        {
+            // both halves of the swap together hold lanes l and l ^ 32 in every lane
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), true, false);
+            bm = max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+        }
         const bool first = blk == 0;
         if (first || __any(bm > kRescaleSlack)) {
             // anchor the running max on the first block; afterwards move it up where a block
@@ -429,10 +457,10 @@ icl_attention_kernel(const Args a) {
     if constexpr (ONES) {
         // O^T row DV-1 (tile VTILES-1, g = 3, i = 3) sits in the upper half-wave
         const float mine = o[G::VTILES - 1][15];
-        const float other = __shfl_xor(mine, 32);
-        l_tot = hh ? mine : other;
+        const float theirs = other_half(mine);
+        l_tot = hh ? mine : theirs;
     } else {
-        l_tot = l_run + __shfl_xor(l_run, 32);
+        l_tot = l_run + other_half(l_run);
     }
     if (qi >= a.nq) return;
     const float inv = 1.0f / l_tot;
@@ -479,6 +507,12 @@ icl_attention_kernel(const Args a) {
 template <int KVT, int DP, bool ONES>
 int launch_shape(int nw, const Args& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.nunits);
+    if constexpr (DP <= 48) {
+        if (nw == 16) {
+            hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 16>), grid, dim3(16 * 64), 0, stream, a);
+            return NORI_OK;
+        }
+    }
     if (nw == 8) hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 8>), grid, dim3(8 * 64), 0, stream, a);
     else hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 2>), grid, dim3(2 * 64), 0, stream, a);
     return NORI_OK;
