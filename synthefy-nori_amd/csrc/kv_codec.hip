@@ -23,6 +23,8 @@
 // 0 whichever quotient is used); checked for every fp16 and bf16 (t, s) pair and for
 // random fp32 pairs on the CPU by tests/exact_quotient_check.c. Other vectors (zero,
 // tiny, huge, infinite or NaN scale) divide exactly.
+#include <algorithm>
+
 #include "nori_common.h"
 
 // torch rounds the result of every op separately; no multiply-add is fused here unless
@@ -193,6 +195,222 @@ quantize_direct_kernel(const void* __restrict__ src_v, int64_t n_outer, int64_t 
     scales[o * scales_outer + i * scales_inner] = vs.s;
 }
 
+// ------------------------------------------------------------------ quantize, wave path
+// One wavefront codes 64 consecutive head vectors (a "chunk") of one outer index: it pulls
+// the chunk's bytes with coalesced 16-byte loads into its own LDS region, each lane then
+// reads its vector with 8/16-byte LDS reads, codes it in registers (width D known at
+// compile time, so nothing is indexed dynamically), writes the codes back to the region
+// and the wave stores them with 16-byte stores. No workgroup barrier: the region is
+// private to the wave and LDS operations of a wave complete in order.
+//
+// Fast-path codes: with q the exact quotient RN(t/s) (Markstein, above), the code is
+// rint(RN_T(q)). For fp16 that is one packed add: RN16(q) + 1536 in fp16 rounds to an
+// integer half-to-even (the fp16 spacing in [1024, 2048) is 1), and the low byte of
+// 1536 + k is k in two's complement. fp32 and bf16 do the same with 1.5 * 2^23 in fp32.
+// |t| <= amax bounds |t/s| by 127 * (1 + 2^-11) for fp16 and fp32 sources, so only bf16
+// (scale rounded to 8 bits) needs the clamp; vectors outside the fast domain (zero, tiny,
+// huge, inf, NaN) take code_of().
+//
+// Lanes exchange data through the region, which the compiler would otherwise treat as
+// private to each lane and reorder freely: wave_sync() orders the phases.
+constexpr int kChunk = 64;
+constexpr int kWaveWaves = 4;
+
+// Orders LDS accesses of the lanes of one wavefront: a compiler fence scoped to the wave
+// (the hardware already executes a wave's LDS operations in order).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack_codes_fast(const float (&q)[4]) {
+    if constexpr (DT == NORI_F16) {
+        const f16x2 magic = {(_Float16)1536.0f, (_Float16)1536.0f};
+        const f16x2 h01 = f16x2{(_Float16)pin_f32(q[0]), (_Float16)pin_f32(q[1])} + magic;
+        const f16x2 h23 = f16x2{(_Float16)pin_f32(q[2]), (_Float16)pin_f32(q[3])} + magic;
+        return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
+    } else {
+        // bf16 rounding of q can reach 127.5 (its spacing there is 0.5), which rounds to 128:
+        // clamp in the shifted domain, where every value is an exact integer
+        constexpr float kMagic = 12582912.0f;
+        uint32_t k[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = round_to<DT>(q[i]) + kMagic;
+            if constexpr (DT == NORI_BF16) v = __builtin_amdgcn_fmed3f(v, kMagic - 127.0f, kMagic + 127.0f);
+            k[i] = __float_as_uint(v);
+        }
+        return (k[0] & 0xffu) | ((k[1] & 0xffu) << 8) | ((k[2] & 0xffu) << 16) | (k[3] << 24);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float elem_of(const uint32_t* x, int e) {
+    if constexpr (DT == NORI_F32) return __uint_as_float(x[e]);
+    else {
+        const uint32_t w = x[e >> 1];
+        const uint16_t b = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+        return bits_to_f32<DT>(b);
+    }
+}
+
+template <int DT, int D>
+__global__ void __launch_bounds__(kWaveWaves * 64)
+quantize_wave_kernel(const uint8_t* __restrict__ src, int64_t n_outer, int64_t n_inner, int64_t src_outer_bytes,
+                     uint8_t* __restrict__ codes, int64_t codes_outer, float* __restrict__ scales, int64_t scales_outer,
+                     int64_t chunks_per_outer, int scale_div) {
+    using S = typename Storage<DT>::T;
+    constexpr int es = sizeof(S);
+    constexpr int VB = D * es;            // bytes per source vector (a multiple of 8)
+    constexpr int XW = VB / 4;            // source dwords per vector
+    constexpr int CB = kChunk * VB;       // source bytes per chunk (a multiple of 16)
+    constexpr int WPL = (CB / 16 + 63) / 64;  // 16-byte words per lane
+    constexpr int OB = kChunk * D;        // code bytes per chunk (a multiple of 16)
+    constexpr int OPL = (OB / 16 + 63) / 64;
+    static_assert(D % 4 == 0 && VB % 8 == 0 && CB % 16 == 0 && OB % 16 == 0, "vector width");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kWaveWaves][CB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint8_t* region = lds[wave];
+    const int64_t total = n_outer * chunks_per_outer;
+
+    for (int64_t ch = (int64_t)blockIdx.x * kWaveWaves + wave; ch < total; ch += (int64_t)gridDim.x * kWaveWaves) {
+        const int64_t o = ch / chunks_per_outer;
+        const int64_t v0 = (ch - o * chunks_per_outer) * kChunk;
+        const int nv = (int)min<int64_t>(kChunk, n_inner - v0);
+        const uint8_t* g = src + o * src_outer_bytes + v0 * VB;
+        const int nbytes = nv * VB;
+
+        // ---- chunk -> LDS (whole 16-byte words; the last word of a ragged tail per element)
+        u32x4v w[WPL];
+#pragma unroll
+        for (int k = 0; k < WPL; ++k) {
+            const int idx = lane + 64 * k;
+            if (16 * idx + 16 <= nbytes) {
+                w[k] = *reinterpret_cast<const u32x4v*>(g + 16 * idx);
+            } else {
+                w[k] = u32x4v{0u, 0u, 0u, 0u};
+                if (16 * idx < nbytes) {
+                    S tmp[16 / es];
+#pragma unroll
+                    for (int e = 0; e < 16 / es; ++e)
+                        tmp[e] = (16 * idx + e * es < nbytes) ? reinterpret_cast<const S*>(g + 16 * idx)[e] : (S)0;
+                    w[k] = __builtin_bit_cast(u32x4v, tmp);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < WPL; ++k) {
+            const int idx = lane + 64 * k;
+            if (16 * idx < CB) *reinterpret_cast<u32x4v*>(region + 16 * idx) = w[k];
+        }
+        wave_sync();
+
+        // ---- this lane's vector
+        uint32_t x[XW];
+#pragma unroll
+        for (int j = 0; j < XW; j += 2) {
+            const u32x2v v = *reinterpret_cast<const u32x2v*>(region + lane * VB + 4 * j);
+            x[j] = v.x;
+            x[j + 1] = v.y;
+        }
+        uint32_t mk;
+        if constexpr (DT == NORI_F32) {
+            mk = 0;
+#pragma unroll
+            for (int j = 0; j < XW; ++j) mk = max(mk, x[j] & 0x7fffffffu);
+        } else {
+            u16x2 m2 = {0, 0};
+#pragma unroll
+            for (int j = 0; j < XW; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, x[j] & 0x7fff7fffu));
+            mk = max((uint32_t)m2.x, (uint32_t)m2.y);
+        }
+        const VectorScale vs = make_scale<DT>(mk, scale_div);
+        uint32_t c[D / 4];
+        if (vs.fast) {
+#pragma unroll
+            for (int j = 0; j < D / 4; ++j) {
+                float q[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float t = elem_of<DT>(x, 4 * j + i);
+                    const float q0 = t * vs.y;
+                    const float r = fmaf(-q0, vs.s, t);
+                    q[i] = fmaf(r, vs.y, q0);
+                }
+                c[j] = pack_codes_fast<DT>(q);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < D / 4; ++j)
+                c[j] = pack4(code_of<DT>(elem_of<DT>(x, 4 * j), vs), code_of<DT>(elem_of<DT>(x, 4 * j + 1), vs),
+                             code_of<DT>(elem_of<DT>(x, 4 * j + 2), vs), code_of<DT>(elem_of<DT>(x, 4 * j + 3), vs));
+        }
+
+        // ---- codes -> LDS, once every lane has read its vector
+        wave_sync();
+#pragma unroll
+        for (int j = 0; j < D / 4; ++j) *reinterpret_cast<uint32_t*>(region + lane * D + 4 * j) = c[j];
+        wave_sync();
+        if (lane < nv) scales[o * scales_outer + v0 + lane] = vs.s;
+        uint8_t* gc = codes + o * codes_outer + v0 * D;
+        const int cbytes = nv * D;
+#pragma unroll
+        for (int k = 0; k < OPL; ++k) {
+            const int idx = lane + 64 * k;
+            if (16 * idx >= OB) continue;
+            const u32x4v cw = *reinterpret_cast<const u32x4v*>(region + 16 * idx);
+            if (16 * idx + 16 <= cbytes) {
+                *reinterpret_cast<u32x4v*>(gc + 16 * idx) = cw;
+            } else if (16 * idx < cbytes) {
+                const uint8_t* cb = reinterpret_cast<const uint8_t*>(&cw);
+                for (int e = 0; e < 16 && 16 * idx + e < cbytes; ++e) gc[16 * idx + e] = cb[e];
+            }
+        }
+        wave_sync();  // the next chunk overwrites the region
+    }
+}
+
+// Launches the wave path when the width has an instantiation and the layout allows 16-byte
+// transfers; returns false otherwise (the caller then uses the tile or direct kernel).
+template <int DT>
+bool launch_quantize_wave(const void* src, int64_t n_outer, int64_t n_inner, int d, int64_t src_outer_bytes,
+                          int8_t* codes, int64_t codes_outer, float* scales, int64_t scales_outer, int scale_div,
+                          hipStream_t stream) {
+    if ((uintptr_t)src % 16 || (uintptr_t)codes % 16 || (n_outer > 1 && (src_outer_bytes % 16 || codes_outer % 16)))
+        return false;
+    // four waves' chunks must fit the 64 KiB of LDS a workgroup may address
+    if ((int64_t)kWaveWaves * kChunk * d * dtype_size(DT) > 65536) return false;
+    const int64_t cpo = (n_inner + kChunk - 1) / kChunk;
+    const int64_t chunks = cpo * n_outer;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    // enough waves to keep HBM busy, few enough that each walks several chunks
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>((chunks + kWaveWaves - 1) / kWaveWaves, (int64_t)cus * 8));
+#define NORI_QW(DV)                                                                                           \
+    case DV:                                                                                                  \
+        hipLaunchKernelGGL((quantize_wave_kernel<DT, DV>), dim3((unsigned)grid), dim3(kWaveWaves * 64), 0, stream, \
+                           (const uint8_t*)src, n_outer, n_inner, src_outer_bytes, (uint8_t*)codes, codes_outer,   \
+                           scales, scales_outer, cpo, scale_div);                                              \
+        return true;
+    switch (d) {
+        NORI_QW(16) NORI_QW(32) NORI_QW(44) NORI_QW(48) NORI_QW(56) NORI_QW(64)
+        default: break;
+    }
+    if constexpr (DT != NORI_F32) {
+        switch (d) {
+            NORI_QW(96) NORI_QW(128)
+            default: break;
+        }
+    }
+    return false;
+#undef NORI_QW
+}
+
 // ------------------------------------------------------------------ dequantize
 template <int DT>
 __global__ void __launch_bounds__(kTileThreads)
@@ -284,8 +502,15 @@ extern "C" int nori_kv_quantize_int8(const void* src, int src_dtype, int64_t n_o
     if (!src || !codes || !scales) return fail(NORI_ERR_INVALID, "quantize_int8: null pointer");
     hipStream_t stream = (hipStream_t)stream_v;
     const int es = dtype_size(src_dtype);
-    const bool tiled = src_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1 &&
-                       d * es <= kMaxTileVectorBytes;
+    const bool contiguous = src_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1;
+    if (contiguous) {
+        bool done = false;
+        NORI_DISPATCH_FLOAT(src_dtype, DT,
+            done = launch_quantize_wave<DT>(src, n_outer, n_inner, d, src_outer_stride * es, codes, codes_outer_stride,
+                                            scales, scales_outer_stride, scale_div, stream));
+        if (done) return launch_status("quantize_int8");
+    }
+    const bool tiled = contiguous && d * es <= kMaxTileVectorBytes;
     if (tiled) {
         const int64_t tiles_per_outer = (n_inner + kTileThreads - 1) / kTileThreads;
         const int64_t grid = tiles_per_outer * n_outer;
