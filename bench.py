@@ -15,18 +15,21 @@ One step is the whole ICL stage of that job, with inputs resident in HBM:
 value = query rows per second of the step (4,096 rows per step).
 
 The JSON line also carries the roofline of the dominant kernel (attention, bound by
-dense fp16/bf16 MFMA at 2.5 PFLOP/s), measured with HIP events on the launch stream,
-the same for the quantize kernel against 8 TB/s of HBM, and the CPU baseline: the
-oracle's fp32 online-softmax scan (the reference's CPU path, layer.py:777-839) timed on
-the host cores over a bounded sample of the same attention work.
+dense fp16/bf16 MFMA at 2.5 PFLOP/s), measured with HIP events on the launch stream
+around each attention call (its kernel and, when the context is split, the merge of
+the partials), the same for the quantize kernel against 8 TB/s of HBM, the HBM traffic
+per launch measured by rocprofv3 counters (profiles/traffic_nori30m_64k.md, when
+present), and the CPU baseline: the oracle (quantizer in C, attention as the
+reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
+bounded sample of the same work.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
+import re
 import sys
 import time
 
@@ -37,6 +40,7 @@ for _p in (ROOT, os.path.join(ROOT, "synthefy-nori_amd")):
 
 HBM_PEAK = 8.0e12  # B/s
 MFMA_BF16_PEAK = 2.5e15  # FLOP/s, dense
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_nori30m_64k.md")
 
 # nori-30m block dims and the 64k-row context configuration
 LAYERS, EMBED, HEADS, HEAD_DIM = 12, 352, 8, 44
@@ -53,8 +57,32 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
     p.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
-    p.add_argument("--cpu-sample-queries", type=int, default=1024)
+    p.add_argument("--cpu-sample-queries", type=int, default=512, help="query rows of the CPU attention sample")
+    p.add_argument(
+        "--probe-traffic", action="store_true",
+        help="run a 1 GiB device copy (counter calibration), one quantize and one attention launch of the "
+        "workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
+    )
     return p.parse_args()
+
+
+def probe_traffic(torch, dev):
+    import nori_amd
+    from nori_amd.kv_cache_scaling import _quantize_into
+
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    g = torch.Generator(device=dev).manual_seed(2)
+    kv = torch.randn((GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    codes = torch.empty(kv.shape, dtype=torch.int8, device=dev)
+    scales = torch.empty(kv.shape[:-1] + (1,), dtype=torch.float32, device=dev)
+    q = torch.randn((GROUPS, QUERY_ROWS, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    for _ in range(2):
+        b.copy_(a)
+        _quantize_into(kv, codes, scales)
+        nori_amd.icl_attention(q, codes, scales)
+    torch.cuda.synchronize()
+    print("traffic probe: 2 x (1 GiB copy, quantize, attention) done", flush=True)
 
 
 def build_workload(torch, layers, dev):
@@ -67,6 +95,20 @@ def build_workload(torch, layers, dev):
     wo = [(torch.randn(HEADS, HEAD_DIM, EMBED, generator=g, device=dev) * 0.02).half() for _ in range(layers)]
     queries = [torch.randn(GROUPS, QUERY_ROWS, EMBED, generator=g, device=dev, dtype=torch.float16) for _ in range(QUERY_BATCHES)]
     return kv, codes, scales, wq, wo, queries
+
+
+def measured_traffic():
+    """HBM bytes per launch of the attention and quantize kernels from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None, None
+    found = {}
+    for name in ("attention", "quantize"):
+        m = re.search(rf"^traffic_bytes_{name}\s*=\s*([0-9.eE+]+)", text, re.M)
+        found[name] = float(m.group(1)) if m else None
+    return found["attention"], found["quantize"]
 
 
 def main():
@@ -82,15 +124,19 @@ def main():
     import torch
 
     import nori_amd
+    from nori_amd import attention as attn
     from nori_amd.kv_cache_scaling import _quantize_into
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.probe_traffic:
+        probe_traffic(torch, dev)
+        return
     layers = args.layers
     kv, codes, scales, wq, wo, queries = build_workload(torch, layers, dev)
+    ws_bytes = attn.workspace_bytes(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM, CONTEXT_ROWS)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
-    attn_ms: list[float] = []
-    quant_ms: list[float] = []
 
     def timed(fn, sink):
         e0 = torch.cuda.Event(enable_timing=True)
@@ -111,7 +157,7 @@ def main():
             for layer in range(layers):
                 xn = nori_amd.rms_norm(x, EMBED, None, 1e-5)
                 q = torch.nn.functional.linear(xn, wq[layer]).view(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM)
-                f = lambda q=q, layer=layer: nori_amd.icl_attention(q, codes[layer], scales[layer])  # noqa: E731
+                f = lambda q=q, layer=layer: nori_amd.icl_attention(q, codes[layer], scales[layer], workspace=workspace)  # noqa: E731
                 o = timed(f, asink) if record else f()
                 x = x + DEEPNORM_ALPHA * torch.einsum("...hd,hds->...s", o, wo[layer])
             outs.append(x)
@@ -142,6 +188,7 @@ def main():
     quant_bytes = n_elem * (2 + 1) + 4 * n_elem // HEAD_DIM  # fp16 in, int8 + fp32 scale out
     quant_avg_s = sum(quant_ms) / len(quant_ms) / 1e3
     quant_achieved = quant_bytes / quant_avg_s
+    attn_traffic, quant_traffic = measured_traffic()
 
     line = {
         "metric": "query rows/s @ 64k-row int8 ctx; attn % MFMA peak; quant kernel % HBM BW",
@@ -164,49 +211,61 @@ def main():
             "query_rows_per_step": rows_per_step, "cache": "int8 per-vector absmax (resident)",
         },
         "roofline": {
-            "kernel": "icl_attention_kernel<48, int8, ones, 8 waves>",
+            "kernel": "icl_attention_kernel<48, int8, ones, 16 waves> (+ combine_splits_kernel)",
             "bound": "mfma",
             "achieved": round(attn_achieved / 1e12, 2),
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(attn_achieved / MFMA_BF16_PEAK, 4),
-            "traffic": None,
+            "traffic": attn_traffic,
             "work_per_launch": f"{attn_flop:.4e} FLOP = 4*33*8*1024*65536*44",
             "avg_launch_ms": round(attn_avg_s * 1e3, 4),
             "launches": len(attn_ms),
         },
         "quant_roofline": {
-            "kernel": "quantize_tile_kernel<f16>",
+            "kernel": "quantize_wave_kernel<f16, 44>",
             "bound": "hbm",
             "achieved": round(quant_achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(quant_achieved / HBM_PEAK, 4),
+            "traffic": quant_traffic,
             "work_per_launch": f"{quant_bytes:.4e} B = n*(2+1) + 4*n/44, n = 33*65536*2*8*44",
             "avg_launch_ms": round(quant_avg_s * 1e3, 4),
             "launches": len(quant_ms),
         },
     }
     if args.cpu_baseline == "on":
-        line["cpu_baseline"] = cpu_baseline(torch, codes[0], scales[0], args.cpu_sample_queries, layers)
+        line["cpu_baseline"] = cpu_baseline(torch, kv[0], codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(torch, codes, scales, n_query, layers):
-    """Time the oracle's fp32 online-softmax scan (the reference's CPU attention) on the host.
+def cpu_baseline(torch, kv, codes, scales, n_query, layers):
+    """Time the oracle on the host: the reference's CPU path for the same step.
 
-    Sample: one of the 33 token groups, ``n_query`` query rows, one layer, over the same
-    65,536-row int8 cache (copied to the host, dequantized per 32k-row block as
-    BlockwiseSeqKV.iter_kv_blocks does). Extrapolated to the step's query rows/s.
+    Sample (about 10 s): the quantizer (oracle C restatement, one thread) over 2 of the 33
+    token groups of one layer's fp16 cache, and the attention (the reference's fp32
+    online-softmax scan over 32k-row blocks dequantized as BlockwiseSeqKV.iter_kv_blocks
+    does, torch on all host cores) for all 33 token groups x ``n_query`` query rows of one
+    layer. Both scale linearly in their sizes; the step is 12 layers x (quantize + 4
+    batches x 1024 query rows of attention).
     """
     from oracle import attention as oa
+    from oracle import codec
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    # quantize: 2 token groups of one layer, fp16 source, GPU scale mode
+    qgroups = 2
+    src = kv[:qgroups].cpu().numpy()
+    t0 = time.perf_counter()
+    codec.quantize_int8(src, "f16", codec.DIV_RECIP)
+    t_quant = (time.perf_counter() - t0) * GROUPS / qgroups
+    # attention: every token group, n_query rows, one layer
     g = torch.Generator().manual_seed(5)
-    q = torch.randn(1, n_query, HEADS, HEAD_DIM, generator=g)
-    c = codes[:1].cpu()
-    s = scales[:1].cpu()
+    q = torch.randn(GROUPS, n_query, HEADS, HEAD_DIM, generator=g)
+    c = codes.cpu()
+    s = scales.cpu()
 
     def blocks():
         step = 32768
@@ -215,17 +274,19 @@ def cpu_baseline(torch, codes, scales, n_query, layers):
 
     t0 = time.perf_counter()
     oa.blockwise_attention_fp32(q, blocks())
-    t = time.perf_counter() - t0
-    # the step runs GROUPS token groups x layers layers x QUERY_BATCHES batches of QUERY_ROWS rows
-    seconds_per_step = t * (QUERY_ROWS / n_query) * GROUPS * layers * QUERY_BATCHES
+    t_attn = (time.perf_counter() - t0) * QUERY_ROWS / n_query
+    seconds_per_step = layers * (t_quant + QUERY_BATCHES * t_attn)
     return {
         "value": round(QUERY_BATCHES * QUERY_ROWS / seconds_per_step, 4),
         "unit": "query rows/s",
-        "cores": torch.get_num_threads(),
+        "cores": cores,
         "kind": "port",
-        "sample": f"1 of {GROUPS} token groups x {n_query} query rows x 1 of {layers} layers over the "
-        f"65536-row int8 cache: {t:.2f} s; fp32 online softmax (oracle.attention.blockwise_attention_fp32, "
-        "layer.py:777-839), extrapolated linearly to the step",
+        "sample": f"quantize: oracle C restatement (1 thread) over {qgroups} of {GROUPS} token groups of one layer, "
+        f"{t_quant * qgroups / GROUPS:.2f} s; attention: fp32 online softmax (oracle.attention."
+        f"blockwise_attention_fp32, layer.py:777-839; torch, {cores} threads) over {GROUPS} token groups x "
+        f"{n_query} query rows x 1 layer against the 65536-row int8 cache, {t_attn * n_query / QUERY_ROWS:.2f} s; "
+        f"extrapolated linearly to {layers} layers x (quantize + {QUERY_BATCHES} x {QUERY_ROWS} query rows) = "
+        f"{seconds_per_step:.0f} s per step",
     }
 
 

@@ -47,6 +47,7 @@ def icl_attention(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     merge: bool = False,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """softmax(scale * q k^T) v for every (bg, query, head); returns ``out`` ([BG, Q, H, D]).
 
@@ -55,6 +56,8 @@ def icl_attention(
     lse: optional fp32 [BG, H, Q] natural-log LSE output.
     merge: treat ``out`` (fp32) and ``lse`` as a running output/LSE of earlier key
     blocks and fold this block in (layer.py:915-920).
+    workspace: optional uint8 device buffer of at least ``workspace_bytes(...)`` bytes for
+    the split-context partials; allocated per call when omitted.
     """
     if q.dim() != 4:
         raise ValueError(f"query must be [BG, Q, H, D], got {tuple(q.shape)}")
@@ -96,7 +99,10 @@ def icl_attention(
     if scale is None:
         scale = 1.0 / math.sqrt(float(d))
     ws_bytes = workspace_bytes(bg, nq, heads, d, nk)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+    elif workspace.device != device or workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor on the query's device")
     kvb, kvr, kvh = _kv_strides(kv)
     scb = scr = sch = 0
     if kv_scales is not None:
