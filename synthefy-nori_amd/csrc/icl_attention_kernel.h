@@ -197,32 +197,35 @@ icl_attention_kernel(const Args a) {
 
     // ---- constant LDS: K columns [d, DP) and V^T rows [d, DV) of both buffers are never
     // staged; they stay zero, except the ones row (last V^T row) that sums P.
-    for (int i = tid; i < 2 * KB * (G::DQMAX - dqv); i += THREADS) {
-        const int bufsel = i / (KB * (G::DQMAX - dqv));
-        const int r = i % (KB * (G::DQMAX - dqv));
-        const int row = r / (G::DQMAX - dqv), dq = dqv + r % (G::DQMAX - dqv);
-        *reinterpret_cast<u32x2*>(&Ks[bufsel * G::KBUF + row * G::KPITCH + 4 * dq]) = u32x2{0u, 0u};
-    }
-    for (int i = tid; i < 2 * (G::DV - d) * KB; i += THREADS) {
-        const int bufsel = i / ((G::DV - d) * KB);
-        const int r = i % ((G::DV - d) * KB);
-        const int row = d + r / KB, col = r % KB;
-        Vt[bufsel * G::VBUF + row * G::VPITCH + col] = (ONES && row == G::DV - 1) ? (_Float16)1.0f : (_Float16)0.0f;
+    for (int row = tid; row < 2 * KB; row += THREADS)
+        for (int dq = dqv; dq < G::DQMAX; ++dq)
+            *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + 4 * dq]) = u32x2{0u, 0u};
+    for (int e = tid; e < 2 * G::DV * KB; e += THREADS) {
+        const int row = (e / KB) % G::DV;  // compile-time divisors
+        if (row >= d)
+            Vt[(e / (G::DV * KB)) * G::VBUF + row * G::VPITCH + e % KB] =
+                (ONES && row == G::DV - 1) ? (_Float16)1.0f : (_Float16)0.0f;
     }
 
-    // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7]
+    // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7]; the
+    // dtype branch is uniform and taken once, outside the element loops
     f16x8 qf[G::KSTEPS];
     {
         const bool qok = qi < a.nq;
         const int64_t qbase = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head;
+        auto fill = [&](auto load) {
 #pragma unroll
-        for (int ks = 0; ks < G::KSTEPS; ++ks) {
+            for (int ks = 0; ks < G::KSTEPS; ++ks) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int dd = 16 * ks + 8 * hh + j;
-                qf[ks][j] = (qok && dd < d) ? (_Float16)load_as_f32(a.q, a.q_dtype, qbase + dd) : (_Float16)0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    const int dd = 16 * ks + 8 * hh + j;
+                    qf[ks][j] = (qok && dd < d) ? (_Float16)load(qbase + dd) : (_Float16)0.0f;
+                }
             }
-        }
+        };
+        if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+        else if (a.q_dtype == NORI_BF16) fill([&](int64_t i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+        else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
     }
 
     // ---- staging plan of this thread: unit u covers rows 4rq..4rq+3 and elements 4dq..4dq+3
