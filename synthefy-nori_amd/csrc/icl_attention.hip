@@ -59,7 +59,7 @@ int device_cu_count() {
 
 struct Plan {
     int dp;        // head width padded to the logit MFMA granule (16)
-    bool ones;     // the softmax denominator comes out of the PV MFMA
+    int mode;      // how logits and the denominator are formed (attn::Mode)
     int nw;        // wavefronts per workgroup (32 query rows each)
     int nqt;       // query tiles per (b, h)
     int nsplit;    // context ranges per (b, h, query tile)
@@ -73,12 +73,13 @@ struct Plan {
 Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     Plan p;
     p.dp = (d + 15) / 16 * 16;
-    p.ones = (d % 32) != 0;
+    p.mode = mode_for(d);
     p.nw = (nq > 256 && p.dp <= 48) ? 16 : (nq > 96 ? 8 : 2);
     p.nqt = (int)((nq + p.nw * QPW - 1) / (p.nw * QPW));
+    const int KB = block_keys(p.nw);
     const int64_t nkb = (nk + KB - 1) / KB;
     const int64_t base = bg * heads * (int64_t)p.nqt;
-    const int64_t slots = (int64_t)device_cu_count() * std::max(1, resident_workgroups(p.dp, p.ones, p.nw));
+    const int64_t slots = (int64_t)device_cu_count() * std::max(1, resident_workgroups(p.dp, p.mode, p.nw));
     // seconds per 64-key block of one workgroup at ~40 % of the dense MFMA peak shared by all slots
     const double t_blk = (double)p.nw * QPW * KB * p.dp * 4.0 / (1.0e15 / (double)slots);
     const double t_partial = (double)bg * heads * nq * (d + 1) * 8.0 / 5.0e12;  // write + read one range's partials
@@ -139,15 +140,15 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     if (kv_dtype == NORI_I8 && !kv_scales) return fail(NORI_ERR_INVALID, "icl_attention: int8 cache without scales");
     if (bg == 0 || nq == 0) return NORI_OK;
     if (!q || !kv || !out) return fail(NORI_ERR_INVALID, "icl_attention: null pointer");
-    // cache rows are read 4 elements at a time, through 32-bit offsets within a block of 64
-    // rows, and a row must hold its K then V heads (the [.., N, 2, Hkv, D] cache layout)
+    // cache rows are read 4 elements at a time, through 32-bit offsets within a block of up
+    // to 128 rows, and a row must hold its K then V heads (the [.., N, 2, Hkv, D] cache layout)
     const int es = dtype_size(kv_dtype);
     if (((uintptr_t)kv) % (4 * es) || kv_row_stride % 4 || kv_bg_stride % 4 || kv_half_stride % 4)
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: cache rows must start on 4-element boundaries");
     if (kv_half_stride < (int64_t)kv_heads * d || kv_row_stride < kv_half_stride + (int64_t)kv_heads * d ||
-        (double)KB * kv_row_stride * es >= 2147483647.0)
+        (double)block_keys(16) * kv_row_stride * es >= 2147483647.0)
         return fail(NORI_ERR_UNSUPPORTED,
-                    "icl_attention: cache rows must be [K heads | V heads] within one row stride of < 32 MiB");
+                    "icl_attention: cache rows must be [K heads | V heads] within one row stride of < 16 MiB");
     if (kv_dtype == NORI_I8 && (sc_half_stride < kv_heads || sc_row_stride < sc_half_stride + kv_heads))
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: scale rows must be [K heads | V heads] within one row stride");
 
@@ -169,6 +170,7 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     if (need > 0 && (!workspace || workspace_bytes_given < need)) {
         // no (or too little) scratch: one range per work item
         args.nsplit = 1;
+        const int KB = block_keys(plan.nw);
         args.keys_per_split = (nk + KB - 1) / KB * KB;
     }
     args.part_o = args.nsplit > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
@@ -177,7 +179,7 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     if (args.nunits * plan.nw * 64 > 0xffffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: grid too large");
 
     hipStream_t stream = (hipStream_t)stream_v;
-    int st = launch_kvt(kv_dtype, plan.dp, plan.ones, plan.nw, args, stream);
+    int st = launch_kvt(kv_dtype, plan.dp, plan.mode, plan.nw, args, stream);
     if (st != NORI_OK) return st;
     if ((st = launch_status("icl_attention")) != NORI_OK) return st;
     if (args.nsplit > 1) {

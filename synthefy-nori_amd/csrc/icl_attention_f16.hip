@@ -4,8 +4,8 @@
 namespace nori {
 namespace attn {
 
-int launch_f16(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
-    return launch_dtype<NORI_F16>(dp, ones, nw, a, stream);
+int launch_f16(int dp, int mode, int nw, const Args& a, hipStream_t stream) {
+    return launch_dtype<NORI_F16>(dp, mode, nw, a, stream);
 }
 
 }  // namespace attn

@@ -4,8 +4,8 @@
 namespace nori {
 namespace attn {
 
-int launch_f32(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
-    return launch_dtype<NORI_F32>(dp, ones, nw, a, stream);
+int launch_f32(int dp, int mode, int nw, const Args& a, hipStream_t stream) {
+    return launch_dtype<NORI_F32>(dp, mode, nw, a, stream);
 }
 
 }  // namespace attn

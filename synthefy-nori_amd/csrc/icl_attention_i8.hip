@@ -4,45 +4,50 @@
 namespace nori {
 namespace attn {
 
-int launch_i8(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
-    return launch_dtype<NORI_I8>(dp, ones, nw, a, stream);
+int launch_i8(int dp, int mode, int nw, const Args& a, hipStream_t stream) {
+    return launch_dtype<NORI_I8>(dp, mode, nw, a, stream);
 }
 
 namespace {
 
-template <int DP, bool ONES>
+template <int DP, int MODE>
 int occupancy(int nw) {
     int n = 0;
     hipError_t e;
     if constexpr (DP <= 48) {
         if (nw == 16) {
-            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 16>, 16 * 64, 0);
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 16>, 16 * 64, 0);
             return e == hipSuccess ? n : 1;
         }
     }
-    if (nw == 8) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 8>, 8 * 64, 0);
-    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, ONES, 2>, 2 * 64, 0);
+    if (nw == 8) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 8>, 8 * 64, 0);
+    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 2>, 2 * 64, 0);
     return e == hipSuccess ? n : 1;
+}
+
+template <int DP, int OTHER>
+int occupancy_of(int mode, int nw) {
+    return mode == kFold ? occupancy<DP, kFold>(nw) : occupancy<DP, OTHER>(nw);
 }
 
 }  // namespace
 
-int resident_workgroups(int dp, bool ones, int nw) {
+int resident_workgroups(int dp, int mode, int nw) {
     // cached per shape: the answer depends only on the compiled kernel and the device
-    static int cache[8][2][3] = {};
-    const int di = dp / 16 - 1, oi = ones ? 1 : 0, ni = nw == 16 ? 2 : (nw == 8 ? 1 : 0);
-    if (di < 0 || di > 7) return 1;
-    int& slot = cache[di][oi][ni];
+    static int cache[8][3][3] = {};
+    const int di = dp / 16 - 1, ni = nw == 16 ? 2 : (nw == 8 ? 1 : 0);
+    if (di < 0 || di > 7 || mode < 0 || mode > 2) return 1;
+    int& slot = cache[di][mode][ni];
     if (slot == 0) {
         switch (dp) {
-            case 16: slot = occupancy<16, true>(nw); break;
-            case 32: slot = ones ? occupancy<32, true>(nw) : occupancy<32, false>(nw); break;
-            case 48: slot = occupancy<48, true>(nw); break;
-            case 64: slot = ones ? occupancy<64, true>(nw) : occupancy<64, false>(nw); break;
-            case 80: slot = occupancy<80, true>(nw); break;
-            case 96: slot = ones ? occupancy<96, true>(nw) : occupancy<96, false>(nw); break;
-            case 112: slot = occupancy<112, true>(nw); break;
-            default: slot = ones ? occupancy<128, true>(nw) : occupancy<128, false>(nw); break;
+            case 16: slot = occupancy_of<16, kOnes>(mode, nw); break;
+            case 32: slot = occupancy_of<32, kValu>(mode, nw); break;
+            case 48: slot = occupancy_of<48, kOnes>(mode, nw); break;
+            case 64: slot = occupancy_of<64, kValu>(mode, nw); break;
+            case 80: slot = occupancy_of<80, kOnes>(mode, nw); break;
+            case 96: slot = occupancy_of<96, kValu>(mode, nw); break;
+            case 112: slot = occupancy_of<112, kOnes>(mode, nw); break;
+            default: slot = occupancy_of<128, kValu>(mode, nw); break;
         }
         if (slot <= 0) slot = 1;
     }

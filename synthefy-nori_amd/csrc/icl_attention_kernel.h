@@ -41,7 +41,9 @@
 namespace nori {
 namespace attn {
 
-constexpr int KB = 64;   // context rows (keys) per block
+// Context rows (keys) per block, the unit of staging and of the one barrier per block:
+// 128 for 16-wave workgroups (a barrier over 16 wavefronts is the costlier one), 64 otherwise.
+constexpr int block_keys(int nw) { return nw == 16 ? 128 : 64; }
 constexpr int QPW = 32;  // query rows per wavefront
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -87,11 +89,23 @@ __device__ __forceinline__ void codes_scaled_to_f16(uint32_t w, float s, uint32_
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) * s2);
 }
 
-// v_max3_f32 / v_max_f32 without the NaN-quieting copies the compiler puts in front of
-// fmaxf operands (the logits are MFMA results; NaN inputs give NaN outputs either way).
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+// Max of 16 values as a depth-3 tree of v_max3_f32, without the NaN-quieting copies the
+// compiler puts in front of fmaxf operands (the inputs are MFMA results; NaN inputs give NaN
+// outputs either way), in one asm block (the compiler follows every asm statement with a
+// hazard nop; one block pays it once).
+__device__ __forceinline__ float max16f(const float (&x)[16]) {
+    float r, t0, t1, t2, t3;
+    asm("v_max3_f32 %1, %5, %6, %7\n\t"
+        "v_max3_f32 %2, %8, %9, %10\n\t"
+        "v_max3_f32 %3, %11, %12, %13\n\t"
+        "v_max3_f32 %4, %14, %15, %16\n\t"
+        "v_max3_f32 %0, %17, %18, %19\n\t"
+        "v_max3_f32 %1, %1, %2, %20\n\t"
+        "v_max3_f32 %0, %0, %3, %4\n\t"
+        "v_max_f32 %0, %0, %1"
+        : "=&v"(r), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]),
+          "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
     return r;
 }
 
@@ -143,9 +157,27 @@ template <> struct Raw<NORI_F16> { u32x2 w[4]; };
 template <> struct Raw<NORI_BF16> { u32x2 w[4]; };
 template <> struct Raw<NORI_F32> { u32x4 w[4]; };
 
-template <int DP, bool ONES>
+// How a kernel forms the logits and the softmax denominator for head width d, padded width DP.
+enum Mode : int {
+    // d < DP. K column d holds ones and the Q fragment carries -m (the running max) there,
+    // so the logit MFMA returns s - m in log2 units with no VALU work: Q is prescaled by
+    // scale*log2(e) and K rows are dequantized with their scales, the f16 value of the
+    // reference's dequantization. The padding row of V^T holds ones and sums P.
+    kFold = 0,
+    // d = DP < DV: x = s * kfac - m on the VALU from exact f16 K codes and an fp32 per-key
+    // factor (scale * scale*log2(e)); the padding row of V^T sums P.
+    kOnes = 1,
+    // d = DP = DV: as kOnes, with the denominator summed on the VALU.
+    kValu = 2,
+};
+
+constexpr int mode_for(int d) { return d % 16 != 0 ? kFold : (d % 32 != 0 ? kOnes : kValu); }
+
+template <int DP, bool ONES, int NW>
 struct Geometry {
     static_assert(DP % 16 == 0 && DP >= 16 && DP <= 128, "padded head width");
+    static constexpr int KB = block_keys(NW);
+    static constexpr int SPB = KB / 32;             // 32-key steps per block
     static constexpr int DV = (DP + 31) / 32 * 32;  // PV output rows (MFMA M granule)
     static constexpr int KSTEPS = DP / 16;          // logit MFMA k-steps
     static constexpr int VTILES = DV / 32;
@@ -154,22 +186,31 @@ struct Geometry {
     static constexpr int VPITCH = KB + 8;           // f16 per V^T row in LDS
     static constexpr int KBUF = KB * KPITCH;
     static constexpr int VBUF = DV * VPITCH;
+    // LDS buffers in the K/V ring: three let a block be staged while the previous block's V
+    // and the next block's K are both being read (one barrier per block); wide heads, whose
+    // buffers are large, use two and a second barrier. The budget keeps two 8-wave
+    // workgroups on a CU (a 16-wave workgroup has the CU to itself).
+    static constexpr int BUF_BYTES = (KBUF + VBUF) * 2 + KB * 4;
+    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : 64) * 1024 ? 3 : 2;
 };
 
 // Register budget: narrow heads keep 4 wavefronts per SIMD (two 8-wave workgroups per CU).
 template <int DP, int NW>
 struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 48)) ? 4 : 1; };
 
-template <int DP, int KVT, bool ONES, int NW>
+template <int DP, int KVT, int MODE, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
 icl_attention_kernel(const Args a) {
-    using G = Geometry<DP, ONES>;
+    constexpr bool ONES = MODE != kValu;
+    constexpr bool FOLD = MODE == kFold;
+    using G = Geometry<DP, ONES, NW>;
+    constexpr int KB = G::KB;
     constexpr int THREADS = NW * 64;
-    constexpr int UNITS = 2 * 16 * G::DQMAX;
+    constexpr int UNITS = 2 * (KB / 4) * G::DQMAX;
     constexpr int NU = (UNITS + THREADS - 1) / THREADS;  // staging units per thread (upper bound)
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[2 * G::KBUF];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[2 * G::VBUF];
-    __shared__ __attribute__((aligned(16))) float kfac[2 * KB];
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[G::NBUF * G::KBUF];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[G::NBUF * G::VBUF];
+    __shared__ __attribute__((aligned(16))) float kfac[FOLD ? 4 : G::NBUF * KB];
 
     // ---- work item, XCD-aware: the hardware deals workgroup i to XCD i % 8; give each XCD
     // a contiguous range of work items (query tiles fastest, then heads, then context splits,
@@ -195,22 +236,27 @@ icl_attention_kernel(const Args a) {
     const int d = a.d;
     const int dqv = d >> 2;
 
-    // ---- constant LDS: K columns [d, DP) and V^T rows [d, DV) of both buffers are never
-    // staged; they stay zero, except the ones row (last V^T row) that sums P.
-    for (int row = tid; row < 2 * KB; row += THREADS)
+    // ---- constant LDS: K columns [d, DP) and V^T rows [d, DV) of every buffer are never
+    // staged; they stay zero, except K column d when the logit offset is folded into the
+    // MFMA (d is a multiple of 4, so it opens quad d/4) and the ones row (last V^T row)
+    // that sums P.
+    for (int row = tid; row < G::NBUF * KB; row += THREADS)
         for (int dq = dqv; dq < G::DQMAX; ++dq)
-            *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + 4 * dq]) = u32x2{0u, 0u};
-    for (int e = tid; e < 2 * G::DV * KB; e += THREADS) {
+            *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + 4 * dq]) =
+                u32x2{(FOLD && dq == dqv) ? 0x3c00u : 0u, 0u};
+    for (int e = tid; e < G::NBUF * G::DV * KB; e += THREADS) {
         const int row = (e / KB) % G::DV;  // compile-time divisors
         if (row >= d)
             Vt[(e / (G::DV * KB)) * G::VBUF + row * G::VPITCH + e % KB] =
                 (ONES && row == G::DV - 1) ? (_Float16)1.0f : (_Float16)0.0f;
     }
 
-    // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7]; the
-    // dtype branch is uniform and taken once, outside the element loops
+    // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7], times
+    // scale*log2(e) when the logit offset is folded (element d then carries -m, 0 until the
+    // first step sets it); the dtype branch is uniform and taken once, outside the loops
     f16x8 qf[G::KSTEPS];
     {
+        const float qmul = FOLD ? a.scale_log2 : 1.0f;
         const bool qok = qi < a.nq;
         const int64_t qbase = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head;
         auto fill = [&](auto load) {
@@ -219,7 +265,7 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int dd = 16 * ks + 8 * hh + j;
-                    qf[ks][j] = (qok && dd < d) ? (_Float16)load(qbase + dd) : (_Float16)0.0f;
+                    qf[ks][j] = (qok && dd < d) ? (_Float16)(load(qbase + dd) * qmul) : (_Float16)0.0f;
                 }
             }
         };
@@ -243,12 +289,12 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
         const int idx = tid + u * THREADS;
-        const int nk_units = 16 * dqv;
+        const int nk_units = (KB / 4) * dqv;
         int rq, dq;
         u_on[u] = idx < 2 * nk_units;
         u_v[u] = idx >= nk_units;
         if (!u_v[u]) { rq = idx / dqv; dq = idx - rq * dqv; }
-        else { const int v = idx - nk_units; rq = v & 15; dq = v >> 4; }
+        else { const int v = idx - nk_units; rq = v % (KB / 4); dq = v / (KB / 4); }
         if (!u_on[u]) { rq = 0; dq = 0; }
         u_dq0[u] = dq == 0;
         u_off[u] = 4 * rq * row_bytes + (uint32_t)(((u_v[u] ? a.kv_half : 0) + hk * d + 4 * dq) * kv_es);
@@ -297,7 +343,7 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if constexpr (KVT == NORI_I8) {
-                    if (!u_v[u]) codes_to_f16(raw[u].w[i], lo[i], hi[i]);
+                    if (!FOLD && !u_v[u]) codes_to_f16(raw[u].w[i], lo[i], hi[i]);
                     else codes_scaled_to_f16(raw[u].w[i], raw[u].s[i], lo[i], hi[i]);
                 } else if constexpr (KVT == NORI_F16) {
                     lo[i] = raw[u].w[i].x; hi[i] = raw[u].w[i].y;
@@ -315,7 +361,7 @@ icl_attention_kernel(const Args a) {
                 _Float16* dst = Kd + u_lds[u];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x2*>(dst + i * G::KPITCH) = u32x2{lo[i], hi[i]};
-                if (u_dq0[u]) {
+                if (!FOLD && u_dq0[u]) {
                     const int r0 = (int)(u_lds[u] / G::KPITCH);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -346,72 +392,55 @@ icl_attention_kernel(const Args a) {
     float m_run = 0.0f;  // running max (log2 units)
     float l_run = 0.0f;  // this lane's share of the denominator (VALU-summed head widths only)
 
-    {
-        Raw<KVT> raw[NU];
-        load_block(k_begin, raw);
-        store_block(0, raw);
-    }
-    __syncthreads();
-
-    for (int blk = 0; blk < nblk; ++blk) {
-        const int64_t kb = k_begin + (int64_t)blk * KB;
-        const int cur = blk & 1;
-        const bool more = blk + 1 < nblk;
-        Raw<KVT> raw[NU];
-        if (more) load_block(kb + KB, raw);  // in flight during the compute below
-
-        const _Float16* Kc = Ks + cur * G::KBUF;
-        const _Float16* Vc = Vt + cur * G::VBUF;
-        const float* kf = kfac + cur * KB;
-
-        // ---------------- logits S^T[32 keys x 32 queries] for the two 32-key halves
-        f32x16 s[2];
+    // S^T[32 keys x 32 queries] of the 32 K rows at Kh (lane: keys 8g + 4hh + i, query qi)
+    auto logits = [&](const _Float16* Kh) {
+        f32x16 acc = f32x16{};
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                const f16x8 kfr = *reinterpret_cast<const f16x8*>(&Kc[(32 * t + l32) * G::KPITCH + 16 * ks + 8 * hh]);
-                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qf[ks], s[t], 0, 0, 0);
-            }
+        for (int ks = 0; ks < G::KSTEPS; ++ks) {
+            const f16x8 kfr = *reinterpret_cast<const f16x8*>(&Kh[l32 * G::KPITCH + 16 * ks + 8 * hh]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qf[ks], acc, 0, 0, 0);
         }
-        // lane holds keys 32t + 8g + 4hh + i (g, i in 0..3) of query qi
-        float x[2][16];
+        return acc;
+    };
+
+    // Online softmax of one 32-key step whose first key is kstep (logits s, per-key factors
+    // kf[0..32), V^T columns Vh[.][0..32)), then O^T += V^T P^T. s_next holds the following
+    // step's logits, already in flight; with the offset folded into the MFMA they carry the
+    // running max they were issued with and follow it when it moves.
+    auto softmax_pv = [&](const f32x16& s, f32x16& s_next, const float* kf, const _Float16* Vh, int64_t kstep,
+                          bool first) {
+        float x[16];
+        if constexpr (FOLD) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int r = 0; r < 16; ++r) x[r] = s[r];
+        } else {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const f32x4 f = *reinterpret_cast<const f32x4*>(&kf[32 * t + 8 * g + 4 * hh]);
+                const f32x4 f = *reinterpret_cast<const f32x4*>(&kf[8 * g + 4 * hh]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[t][4 * g + i] = fmaf(s[t][4 * g + i], f[i], -m_run);
+                for (int i = 0; i < 4; ++i) x[4 * g + i] = fmaf(s[4 * g + i], f[i], -m_run);
             }
-        if (kb + KB > k_end) {  // the last block of a context range may be partial
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (kb + 32 * t + 8 * g + 4 * hh + i >= k_end) x[t][4 * g + i] = -INFINITY;
         }
-        float ma = max3f(x[0][0], x[0][1], x[0][2]);
-        float mb = max3f(x[1][0], x[1][1], x[1][2]);
+        if (kstep + 32 > k_end) {  // the last step of a context range may be partial
 #pragma unroll
-        for (int r = 3; r < 15; r += 2) {
-            ma = max3f(ma, x[0][r], x[0][r + 1]);
-            mb = max3f(mb, x[1][r], x[1][r + 1]);
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (kstep + 8 * g + 4 * hh + i >= k_end) x[4 * g + i] = -INFINITY;
         }
-        float bm = max3f(ma, mb, max2f(x[0][15], x[1][15]));
+        float bm = max16f(x);
         {
             // both halves of the swap together hold lanes l and l ^ 32 in every lane
             const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), true, false);
             bm = max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
         }
-        const bool first = blk == 0;
         if (first || __any(bm > kRescaleSlack)) {
-            // anchor the running max on the first block; afterwards move it up where a block
-            // overshoots it (rare: the max settles within the first few blocks)
-            const float shift = first ? bm : fmaxf(bm, 0.0f);
+            // anchor the running max on the first step (its first key is valid for every
+            // query); afterwards move it up where a step overshoots it (rare: the max settles
+            // within the first few blocks). A folded max is an f16 value (the Q fragment
+            // carries it), so the shift is the exact difference of two f16 values.
+            float shift = first ? bm : fmaxf(bm, 0.0f);
+            if constexpr (FOLD) shift = (float)(_Float16)(m_run + shift) - m_run;
             if (!first) {
                 const float alpha = __builtin_amdgcn_exp2f(-shift);
                 l_run *= alpha;
@@ -422,18 +451,25 @@ icl_attention_kernel(const Args a) {
             }
             m_run += shift;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int r = 0; r < 16; ++r) x[r] -= shift;
+            if constexpr (FOLD) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) x[t][r] -= shift;
+                for (int r = 0; r < 16; ++r) s_next[r] -= shift;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (16 * ks + 8 * hh + j == d) qf[ks][j] = (_Float16)(-m_run);
+            }
         }
-        // ---------------- probabilities (f16, RN) and PV
-        f16x8 pf[4];
+        // probabilities (f16, RN); pf[c] holds keys 16c + 8hh + 0..7 in the PV operand order
+        f16x8 pf[2];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 2; ++c) {
 #pragma unroll
             for (int j = 0; j < 8; j += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(x[c >> 1][8 * (c & 1) + j]);
-                const float p1 = __builtin_amdgcn_exp2f(x[c >> 1][8 * (c & 1) + j + 1]);
+                const float p0 = __builtin_amdgcn_exp2f(x[8 * c + j]);
+                const float p1 = __builtin_amdgcn_exp2f(x[8 * c + j + 1]);
                 const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
                 if constexpr (!ONES) {
                     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
@@ -446,13 +482,67 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
         for (int vt = 0; vt < G::VTILES; ++vt) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vc[(32 * vt + l32) * G::VPITCH + 16 * c + 8 * hh]);
+            for (int c = 0; c < 2; ++c) {
+                const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vh[(32 * vt + l32) * G::VPITCH + 16 * c + 8 * hh]);
                 o[vt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[vt], 0, 0, 0);
             }
         }
-        if (more) store_block(cur ^ 1, raw);
-        __syncthreads();
+    };
+
+    // Software pipeline over 32-key steps: each step issues the logit MFMAs of the following
+    // step before its own softmax, so every wavefront always holds MFMA work that is
+    // independent of the VALU work in front of it. Blocks are staged into the LDS ring ahead
+    // of use from raw words loaded one block before that.
+    //   * three buffers: block i+2 is staged while block i is computed (after its first
+    //     step) and one barrier closes each block, so the staging overlaps the compute of
+    //     the other wavefronts;
+    //   * two buffers (wide heads): block i+1 is staged before the last step of block i,
+    //     fenced by a barrier on each side.
+    Raw<KVT> raw[NU];
+    load_block(k_begin, raw);
+    store_block(0, raw);
+    constexpr int AHEAD = G::NBUF >= 3 ? 2 : 1;
+    if constexpr (AHEAD == 2) {
+        if (nblk > 1) {
+            load_block(k_begin + KB, raw);
+            store_block(1, raw);
+        }
+    }
+    if (nblk > AHEAD) load_block(k_begin + AHEAD * KB, raw);
+    __syncthreads();
+    f32x16 s_cur = logits(Ks);
+
+    for (int blk = 0; blk < nblk; ++blk) {
+        const int64_t kb = k_begin + (int64_t)blk * KB;
+        const int cur = blk % G::NBUF, nxt = (blk + 1) % G::NBUF;
+        const _Float16* Kc = Ks + cur * G::KBUF;
+        const _Float16* Vc = Vt + cur * G::VBUF;
+        const float* kf = kfac + (FOLD ? 0 : cur * KB);
+#pragma unroll
+        for (int st = 0; st < G::SPB; ++st) {
+            if constexpr (AHEAD == 1) {
+                if (st == G::SPB - 1) {
+                    __syncthreads();  // every wavefront is done with block blk-1, the target buffer
+                    if (blk + 1 < nblk) {
+                        store_block(nxt, raw);
+                        if (blk + 2 < nblk) load_block(kb + 2 * KB, raw);  // lands during the next block
+                    }
+                    __syncthreads();
+                }
+            }
+            // logits of the following step in flight: the next 32 rows of this block, or the
+            // first 32 rows of the next block (a stale buffer after the last block, unused)
+            f32x16 s_next = logits(st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Ks + nxt * G::KBUF);
+            softmax_pv(s_cur, s_next, kf + (FOLD ? 0 : 32 * st), Vc + 32 * st, kb + 32 * st, blk == 0 && st == 0);
+            s_cur = s_next;
+            if constexpr (AHEAD == 2) {
+                if (st == 0 && blk + 2 < nblk) {
+                    store_block((blk + 2) % G::NBUF, raw);
+                    if (blk + 3 < nblk) load_block(kb + 3 * KB, raw);  // lands during the next block
+                }
+            }
+        }
+        if constexpr (AHEAD == 2) __syncthreads();
     }
 
     // ---------------- epilogue
@@ -507,52 +597,55 @@ icl_attention_kernel(const Args a) {
 
 // Launches the kernel instantiation for (cache dtype KVT, dp, ones, nw) over a.nunits
 // workgroups. Each icl_attention_<dtype>.hip instantiates one KVT (parallel builds).
-template <int KVT, int DP, bool ONES>
+template <int KVT, int DP, int MODE>
 int launch_shape(int nw, const Args& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.nunits);
     if constexpr (DP <= 48) {
         if (nw == 16) {
-            hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 16>), grid, dim3(16 * 64), 0, stream, a);
+            hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 16>), grid, dim3(16 * 64), 0, stream, a);
             return NORI_OK;
         }
     }
-    if (nw == 8) hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 8>), grid, dim3(8 * 64), 0, stream, a);
-    else hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, ONES, 2>), grid, dim3(2 * 64), 0, stream, a);
+    if (nw == 8) hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 8>), grid, dim3(8 * 64), 0, stream, a);
+    else hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 2>), grid, dim3(2 * 64), 0, stream, a);
     return NORI_OK;
 }
 
+// Padded head width DP has two kernels: kFold for d < DP, and kOnes (DP % 32 = 16) or kValu
+// (DP % 32 = 0) for d = DP.
 template <int KVT>
-int launch_dtype(int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+int launch_dtype(int dp, int mode, int nw, const Args& a, hipStream_t stream) {
+    const bool fold = mode == kFold;
     switch (dp) {
-        case 16: return launch_shape<KVT, 16, true>(nw, a, stream);
-        case 32: return ones ? launch_shape<KVT, 32, true>(nw, a, stream) : launch_shape<KVT, 32, false>(nw, a, stream);
-        case 48: return launch_shape<KVT, 48, true>(nw, a, stream);
-        case 64: return ones ? launch_shape<KVT, 64, true>(nw, a, stream) : launch_shape<KVT, 64, false>(nw, a, stream);
-        case 80: return launch_shape<KVT, 80, true>(nw, a, stream);
-        case 96: return ones ? launch_shape<KVT, 96, true>(nw, a, stream) : launch_shape<KVT, 96, false>(nw, a, stream);
-        case 112: return launch_shape<KVT, 112, true>(nw, a, stream);
-        case 128: return ones ? launch_shape<KVT, 128, true>(nw, a, stream) : launch_shape<KVT, 128, false>(nw, a, stream);
+        case 16: return fold ? launch_shape<KVT, 16, kFold>(nw, a, stream) : launch_shape<KVT, 16, kOnes>(nw, a, stream);
+        case 32: return fold ? launch_shape<KVT, 32, kFold>(nw, a, stream) : launch_shape<KVT, 32, kValu>(nw, a, stream);
+        case 48: return fold ? launch_shape<KVT, 48, kFold>(nw, a, stream) : launch_shape<KVT, 48, kOnes>(nw, a, stream);
+        case 64: return fold ? launch_shape<KVT, 64, kFold>(nw, a, stream) : launch_shape<KVT, 64, kValu>(nw, a, stream);
+        case 80: return fold ? launch_shape<KVT, 80, kFold>(nw, a, stream) : launch_shape<KVT, 80, kOnes>(nw, a, stream);
+        case 96: return fold ? launch_shape<KVT, 96, kFold>(nw, a, stream) : launch_shape<KVT, 96, kValu>(nw, a, stream);
+        case 112: return fold ? launch_shape<KVT, 112, kFold>(nw, a, stream) : launch_shape<KVT, 112, kOnes>(nw, a, stream);
+        case 128: return fold ? launch_shape<KVT, 128, kFold>(nw, a, stream) : launch_shape<KVT, 128, kValu>(nw, a, stream);
         default: return fail(NORI_ERR_UNSUPPORTED, "icl_attention: no kernel for padded head width %d", dp);
     }
 }
 
-int launch_i8(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
-int launch_f16(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
-int launch_bf16(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
-int launch_f32(int dp, bool ones, int nw, const Args& a, hipStream_t stream);
+int launch_i8(int dp, int mode, int nw, const Args& a, hipStream_t stream);
+int launch_f16(int dp, int mode, int nw, const Args& a, hipStream_t stream);
+int launch_bf16(int dp, int mode, int nw, const Args& a, hipStream_t stream);
+int launch_f32(int dp, int mode, int nw, const Args& a, hipStream_t stream);
 
-inline int launch_kvt(int kv_dtype, int dp, bool ones, int nw, const Args& a, hipStream_t stream) {
+inline int launch_kvt(int kv_dtype, int dp, int mode, int nw, const Args& a, hipStream_t stream) {
     switch (kv_dtype) {
-        case NORI_I8: return launch_i8(dp, ones, nw, a, stream);
-        case NORI_F16: return launch_f16(dp, ones, nw, a, stream);
-        case NORI_BF16: return launch_bf16(dp, ones, nw, a, stream);
-        case NORI_F32: return launch_f32(dp, ones, nw, a, stream);
+        case NORI_I8: return launch_i8(dp, mode, nw, a, stream);
+        case NORI_F16: return launch_f16(dp, mode, nw, a, stream);
+        case NORI_BF16: return launch_bf16(dp, mode, nw, a, stream);
+        case NORI_F32: return launch_f32(dp, mode, nw, a, stream);
         default: return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported cache dtype %s", dtype_name(kv_dtype));
     }
 }
 
-// Workgroups of the int8-cache kernel for (dp, ones, nw) that fit on one CU at once.
-int resident_workgroups(int dp, bool ones, int nw);
+// Workgroups of the int8-cache kernel for (dp, mode, nw) that fit on one CU at once.
+int resident_workgroups(int dp, int mode, int nw);
 
 }  // namespace attn
 }  // namespace nori
