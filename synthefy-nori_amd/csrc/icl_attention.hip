@@ -12,31 +12,36 @@ namespace {
 using namespace nori;
 using namespace nori::attn;
 
-// Merges nsplit partial (O, LSE) pairs -- and the running output when merging -- into the
-// final output. One thread per (b, h, query, 4-element quad of the head vector).
+// Merges the nsplit partial (O, LSE) pairs of every tail unit's rows -- and the running
+// output when merging -- into the final output. One thread per (tail unit, row of its query
+// tile, 4-element quad of the head vector).
 __global__ void __launch_bounds__(256)
 combine_splits_kernel(const Args a) {
     const int dqv = a.d >> 2;
+    const int64_t ntail = a.nunits - a.n_whole;
+    const int64_t prows = ntail * a.qrows;  // partial rows per context range
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t rows = a.bg * a.heads * a.nq;
-    if (idx >= rows * dqv) return;
-    const int64_t row = idx / dqv;
-    const int dq = (int)(idx - row * dqv);
-    const int64_t qi = row % a.nq;
-    const int64_t bh = row / a.nq;
-    const int h = (int)(bh % a.heads);
-    const int64_t b = bh / a.heads;
+    if (idx >= prows * dqv) return;
+    const int64_t prow = idx / dqv;
+    const int dq = (int)(idx - prow * dqv);
+    const int64_t unit = a.n_whole + prow / a.qrows;
+    const int qt = (int)(unit % a.nqt);
+    const int h = (int)((unit / a.nqt) % a.heads);
+    const int64_t b = unit / a.nqt / a.heads;
+    const int64_t qi = (int64_t)qt * a.qrows + prow % a.qrows;
+    if (qi >= a.nq) return;
     float mx = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) mx = fmaxf(mx, a.part_lse[s * rows + row]);
+    for (int s = 0; s < a.nsplit; ++s) mx = fmaxf(mx, a.part_lse[s * prows + prow]);
     float sum = 0.f;
-    for (int s = 0; s < a.nsplit; ++s) sum += expf(a.part_lse[s * rows + row] - mx);
+    for (int s = 0; s < a.nsplit; ++s) sum += expf(a.part_lse[s * prows + prow] - mx);
     const float lse_part = mx + logf(sum);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < a.nsplit; ++s) {
-        const float w = expf(a.part_lse[s * rows + row] - lse_part);
-        const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + (s * rows + row) * a.d + 4 * dq);
+        const float w = expf(a.part_lse[s * prows + prow] - lse_part);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + (s * prows + prow) * a.d + 4 * dq);
         acc += w * v;
     }
+    const int64_t row = (b * a.heads + h) * a.nq + qi;
     const bool merge = a.flags & NORI_ATTN_MERGE;
     float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
     if (merge) merge_weights(a.lse[row], lse_part, w_old, w_new, lse_out);
@@ -58,42 +63,50 @@ int device_cu_count() {
 }
 
 struct Plan {
-    int dp;        // head width padded to the logit MFMA granule (16)
-    int mode;      // how logits and the denominator are formed (attn::Mode)
-    int nw;        // wavefronts per workgroup (32 query rows each)
-    int nqt;       // query tiles per (b, h)
-    int nsplit;    // context ranges per (b, h, query tile)
-    int64_t kps;   // keys per context range (a multiple of the 64-key block)
+    int dp;          // head width padded to the logit MFMA granule (16)
+    int mode;        // how logits and the denominator are formed (attn::Mode)
+    int nw;          // wavefronts per workgroup (32 query rows each)
+    int nqt;         // query tiles per (b, h)
+    int64_t nunits;  // (b, h, query tile) work units
+    int64_t n_whole; // units that scan the whole context in one workgroup
+    int nsplit;      // context ranges per tail unit (1: no split)
+    int64_t kps;     // keys per context range (a multiple of the block)
 };
 
-// Chooses the tile shape and how many ranges the context is split into. Work items are
-// (b, h, query tile, range); a range adds a partial output that a second kernel merges.
-// Splitting is worth it while it evens out the last round of workgroups (and feeds small
-// grids), and stops paying once the partials' HBM traffic outweighs the rounds it saves.
+// Chooses the tile shape and the schedule. Units fill the resident workgroup slots of the
+// device round after round; only the units of the last, partly filled round (the tail) are
+// split, into context ranges that spread them over the slots the full rounds leave idle, and a
+// second kernel merges their partials. A split is taken when the rounds it saves outweigh
+// the partials' HBM traffic.
 Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     Plan p;
     p.dp = (d + 15) / 16 * 16;
     p.mode = mode_for(d);
-    p.nw = (nq > 256 && p.dp <= 48) ? 16 : (nq > 96 ? 8 : 2);
+    p.nw = (nq > 256 && has_16_waves(p.dp, p.mode)) ? 16 : (nq > 96 ? 8 : 2);
     p.nqt = (int)((nq + p.nw * QPW - 1) / (p.nw * QPW));
+    p.nunits = bg * heads * (int64_t)p.nqt;
     const int KB = block_keys(p.nw);
     const int64_t nkb = (nk + KB - 1) / KB;
-    const int64_t base = bg * heads * (int64_t)p.nqt;
     const int64_t slots = (int64_t)device_cu_count() * std::max(1, resident_workgroups(p.dp, p.mode, p.nw));
-    // seconds per 64-key block of one workgroup at ~40 % of the dense MFMA peak shared by all slots
+    const int64_t full = p.nunits / slots, tail = p.nunits % slots;
+    // seconds per block of one workgroup at ~40 % of the dense MFMA peak shared by all slots
     const double t_blk = (double)p.nw * QPW * KB * p.dp * 4.0 / (1.0e15 / (double)slots);
-    const double t_partial = (double)bg * heads * nq * (d + 1) * 8.0 / 5.0e12;  // write + read one range's partials
-    const int64_t max_split = std::max<int64_t>(1, std::min<int64_t>(64, nkb / 4));
-    double best = 1e300;
+    // write + read of one context range's partials of the tail units
+    const double t_partial = (double)tail * p.nw * QPW * (d + 1) * 8.0 / 5.0e12;
+    p.n_whole = p.nunits;
     p.nsplit = 1;
     p.kps = nkb * KB;
-    for (int64_t ns = 1; ns <= max_split; ++ns) {
+    if (tail == 0) return p;
+    double best = (double)(full + 1) * nkb * t_blk;
+    const int64_t max_split = std::max<int64_t>(1, std::min<int64_t>(64, nkb / 4));
+    for (int64_t ns = 2; ns <= max_split; ++ns) {
         const int64_t blocks = (nkb + ns - 1) / ns;
         const int64_t ns_eff = (nkb + blocks - 1) / blocks;
-        const int64_t rounds = (base * ns_eff + slots - 1) / slots;
-        const double cost = (double)rounds * blocks * t_blk + (ns_eff > 1 ? ns_eff * t_partial + 5e-6 : 0.0);
+        const int64_t tail_rounds = (tail * ns_eff + slots - 1) / slots;
+        const double cost = (double)(full * nkb + tail_rounds * blocks) * t_blk + ns_eff * t_partial + 5e-6;
         if (cost < best * 0.995) {
             best = cost;
+            p.n_whole = full * slots;
             p.nsplit = (int)ns_eff;
             p.kps = blocks * KB;
         }
@@ -101,16 +114,16 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     return p;
 }
 
-int64_t workspace_bytes(const Plan& p, int64_t bg, int64_t nq, int heads, int d) {
+int64_t workspace_bytes(const Plan& p, int d) {
     if (p.nsplit <= 1) return 0;
-    return (int64_t)p.nsplit * bg * heads * nq * (d + 1) * (int64_t)sizeof(float);
+    return (int64_t)p.nsplit * (p.nunits - p.n_whole) * p.nw * QPW * (d + 1) * (int64_t)sizeof(float);
 }
 
 }  // namespace
 
 extern "C" int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk) {
     if (bg <= 0 || nq <= 0 || heads <= 0 || d < 4 || d > 128 || d % 4 || nk <= 0) return 0;
-    return workspace_bytes(make_plan(bg, nq, heads, d, nk), bg, nq, heads, d);
+    return workspace_bytes(make_plan(bg, nq, heads, d, nk), d);
 }
 
 extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
@@ -164,26 +177,29 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     args.o_head = out_head_stride; args.lse = lse; args.flags = flags;
     args.bg = bg;
     args.nqt = plan.nqt;
+    args.qrows = plan.nw * QPW;
+    args.nunits = plan.nunits;
+    args.n_whole = plan.n_whole;
     args.nsplit = plan.nsplit;
     args.keys_per_split = plan.kps;
-    const int64_t need = workspace_bytes(plan, bg, nq, heads, d);
+    const int64_t need = workspace_bytes(plan, d);
     if (need > 0 && (!workspace || workspace_bytes_given < need)) {
-        // no (or too little) scratch: one range per work item
+        // no (or too little) scratch: every unit scans the whole context
+        args.n_whole = plan.nunits;
         args.nsplit = 1;
-        const int KB = block_keys(plan.nw);
-        args.keys_per_split = (nk + KB - 1) / KB * KB;
     }
+    args.grid = args.n_whole + (args.nunits - args.n_whole) * args.nsplit;
+    const int64_t prows = (args.nunits - args.n_whole) * args.qrows;
     args.part_o = args.nsplit > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
-    args.part_lse = args.nsplit > 1 ? reinterpret_cast<float*>(workspace) + (int64_t)args.nsplit * bg * heads * nq * d : nullptr;
-    args.nunits = bg * heads * (int64_t)args.nqt * args.nsplit;
-    if (args.nunits * plan.nw * 64 > 0xffffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: grid too large");
+    args.part_lse = args.nsplit > 1 ? reinterpret_cast<float*>(workspace) + (int64_t)args.nsplit * prows * d : nullptr;
+    if (args.grid * plan.nw * 64 > 0xffffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: grid too large");
 
     hipStream_t stream = (hipStream_t)stream_v;
     int st = launch_kvt(kv_dtype, plan.dp, plan.mode, plan.nw, args, stream);
     if (st != NORI_OK) return st;
     if ((st = launch_status("icl_attention")) != NORI_OK) return st;
     if (args.nsplit > 1) {
-        const int64_t threads = bg * heads * nq * (d / 4);
+        const int64_t threads = (args.nunits - args.n_whole) * args.qrows * (d / 4);
         hipLaunchKernelGGL(combine_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, args);
         return launch_status("icl_attention combine");
     }

@@ -14,7 +14,7 @@ template <int DP, int MODE>
 int occupancy(int nw) {
     int n = 0;
     hipError_t e;
-    if constexpr (DP <= 48) {
+    if constexpr (has_16_waves(DP, MODE)) {
         if (nw == 16) {
             e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 16>, 16 * 64, 0);
             return e == hipSuccess ? n : 1;

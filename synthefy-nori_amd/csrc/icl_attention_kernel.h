@@ -60,9 +60,13 @@ struct Args {
     float scale_log2;  // logit scale * log2(e)
     void* out; int out_dtype; int64_t o_bg, o_row, o_head;
     float* lse; uint32_t flags;
-    int64_t bg; int nqt; int nsplit; int64_t keys_per_split;
-    float* part_o; float* part_lse;  // [nsplit][bg][heads][nq][d], [nsplit][bg][heads][nq]
-    int64_t nunits;
+    // Work items are (b, h, query tile) units, numbered with the query tile fastest. Units
+    // [0, n_whole) scan the whole context; each of the tail units [n_whole, nunits) is split
+    // into nsplit ranges of keys_per_split keys whose partial (O, LSE) pairs a second kernel
+    // merges. grid = n_whole + (nunits - n_whole) * nsplit workgroups.
+    int64_t bg; int nqt; int qrows; int nsplit; int64_t keys_per_split;
+    int64_t nunits, n_whole, grid;
+    float* part_o; float* part_lse;  // [nsplit][tail unit][qrows][d], [nsplit][tail unit][qrows]
 };
 
 // 4 int8 codes -> two f16x2 holding the same integers (exact): v_perm builds the f16 bit
@@ -194,6 +198,10 @@ struct Geometry {
     static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : 64) * 1024 ? 3 : 2;
 };
 
+// Shapes with a 16-wave workgroup: narrow heads, where 32 query rows per wavefront fit in
+// 128 VGPRs (4 wavefronts per SIMD) with the pipelined logits in flight.
+constexpr bool has_16_waves(int dp, int mode) { return dp <= 32 || (dp == 48 && mode == kFold); }
+
 // Register budget: narrow heads keep 4 wavefronts per SIMD (two 8-wave workgroups per CU).
 template <int DP, int NW>
 struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 48)) ? 4 : 1; };
@@ -212,26 +220,36 @@ icl_attention_kernel(const Args a) {
     __shared__ __attribute__((aligned(16))) _Float16 Vt[G::NBUF * G::VBUF];
     __shared__ __attribute__((aligned(16))) float kfac[FOLD ? 4 : G::NBUF * KB];
 
-    // ---- work item, XCD-aware: the hardware deals workgroup i to XCD i % 8; give each XCD
-    // a contiguous range of work items (query tiles fastest, then heads, then context splits,
-    // then table-groups), so the workgroups an XCD runs together read the same cache rows.
-    const int64_t nb = a.nunits;
-    const int64_t xcd = blockIdx.x % 8, local = blockIdx.x / 8;
-    const int64_t per = nb / 8, extra = nb % 8;
-    const int64_t work = xcd * per + min<int64_t>(xcd, extra) + local;
-    const int qt = (int)(work % a.nqt);
-    int64_t rest = work / a.nqt;
-    const int h = (int)(rest % a.heads);
-    rest /= a.heads;
-    const int split = (int)(rest % a.nsplit);
-    const int64_t b = rest / a.nsplit;
+    // ---- work item, XCD-aware: the hardware deals workgroup i to XCD i % 8; within each phase
+    // (whole units, then tail ranges) give each XCD a contiguous range of items, so the
+    // workgroups an XCD runs together read the same cache rows (the query tiles of one
+    // (b, h), and with a split context the same key range of both tiles).
+    int64_t unit;
+    int split = -1;  // context range of a tail unit; -1 for a whole unit
+    {
+        const bool tail = (int64_t)blockIdx.x >= a.n_whole;
+        const int64_t base = tail ? a.n_whole : 0;
+        const int64_t n = tail ? a.grid - a.n_whole : a.n_whole;
+        const int64_t g = (int64_t)blockIdx.x - base;
+        const int64_t xcd = g % 8, local = g / 8, per = n / 8, extra = n % 8;
+        const int64_t t = xcd * per + min<int64_t>(xcd, extra) + local;
+        if (!tail) {
+            unit = t;
+        } else {
+            unit = a.n_whole + t / a.nsplit;
+            split = (int)(t % a.nsplit);
+        }
+    }
+    const int qt = (int)(unit % a.nqt);
+    const int h = (int)((unit / a.nqt) % a.heads);
+    const int64_t b = unit / a.nqt / a.heads;
     const int hk = h / a.hgroup;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int64_t qi = (int64_t)qt * (NW * QPW) + wave * QPW + l32;
-    const int64_t k_begin = (int64_t)split * a.keys_per_split;
-    const int64_t k_end = min<int64_t>(a.nk, k_begin + a.keys_per_split);
+    const int64_t k_begin = split < 0 ? 0 : (int64_t)split * a.keys_per_split;
+    const int64_t k_end = split < 0 ? a.nk : min<int64_t>(a.nk, k_begin + a.keys_per_split);
     const int nblk = (int)((k_end - k_begin + KB - 1) / KB);
     const int d = a.d;
     const int dqv = d >> 2;
@@ -558,8 +576,8 @@ icl_attention_kernel(const Args a) {
     if (qi >= a.nq) return;
     const float inv = 1.0f / l_tot;
     const float lse_part = (m_run + __log2f(l_tot)) * kLn2;
-    if (a.nsplit > 1) {
-        const int64_t prow = ((split * a.bg + b) * a.heads + h) * a.nq + qi;
+    if (split >= 0) {
+        const int64_t prow = (split * (a.nunits - a.n_whole) + (unit - a.n_whole)) * a.qrows + (qi - (int64_t)qt * a.qrows);
         float* po = a.part_o + prow * d;
 #pragma unroll
         for (int vt = 0; vt < G::VTILES; ++vt)
@@ -595,12 +613,12 @@ icl_attention_kernel(const Args a) {
     if (a.lse && hh == 0) a.lse[lse_idx] = lse_out;
 }
 
-// Launches the kernel instantiation for (cache dtype KVT, dp, ones, nw) over a.nunits
+// Launches the kernel instantiation for (cache dtype KVT, dp, mode, nw) over a.grid
 // workgroups. Each icl_attention_<dtype>.hip instantiates one KVT (parallel builds).
 template <int KVT, int DP, int MODE>
 int launch_shape(int nw, const Args& a, hipStream_t stream) {
-    const dim3 grid((unsigned)a.nunits);
-    if constexpr (DP <= 48) {
+    const dim3 grid((unsigned)a.grid);
+    if constexpr (has_16_waves(DP, MODE)) {
         if (nw == 16) {
             hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 16>), grid, dim3(16 * 64), 0, stream, a);
             return NORI_OK;

@@ -133,6 +133,46 @@ def test_split_context_schedule(cuda):
     assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, 1)).all()
 
 
+def test_tail_split_matches_whole_units(cuda):
+    # 33 groups x 8 heads x 2 query tiles = 528 work units on 256 slots: two full rounds run
+    # whole, the 16 units of the third round (group 32, query tiles fastest) are split over
+    # the idle slots and merged by the second kernel. Called through the C ABI twice -- with
+    # the workspace (tail split) and without (every unit whole): the whole units are computed
+    # identically by both calls, and group 32 matches the oracle either way.
+    from nori_amd import _native as nat
+
+    bg, h, nq, nk, d = 33, 8, 1024, 4096, 44
+    ws = attn.workspace_bytes(bg, nq, h, d, nk)
+    assert ws > 0
+    kv = make_cache(bg, nk, h, d, cuda, seed=41)
+    codes, scales = nori_amd.quantize_int8(kv)
+    del kv
+    q = make_queries(bg, nq, h, d, cuda, seed=41, dtype=torch.float32)
+    workspace = torch.empty(ws, dtype=torch.uint8, device=cuda)
+    results = []
+    for buf, nbytes in ((workspace, ws), (None, 0)):
+        out = torch.empty_like(q)
+        lse = torch.empty(bg, h, nq, device=cuda)
+        nat.check(
+            nat.lib().nori_icl_attention(
+                q.data_ptr(), nat.dtype_code(q.dtype), bg, nq, h, d, q.stride(0), q.stride(1), q.stride(2),
+                codes.data_ptr(), nat.dtype_code(codes.dtype), scales.data_ptr(), nk, h,
+                codes.stride(0), codes.stride(1), codes.stride(2), scales.stride(0), scales.stride(1), scales.stride(2),
+                1.0 / math.sqrt(d), out.data_ptr(), nat.dtype_code(out.dtype), out.stride(0), out.stride(1),
+                out.stride(2), lse.data_ptr(), 0, nat.ptr(buf), nbytes, nat.stream_of(cuda),
+            ),
+            "icl_attention",
+        )
+        results.append((out, lse))
+    (o_split, l_split), (o_whole, l_whole) = results
+    assert torch.equal(o_split[:32], o_whole[:32]) and torch.equal(l_split[:32], l_whole[:32])
+    values = (codes[32:].double() * scales[32:].double()).cpu()
+    exp, exp_lse = reference(q[32:], values)
+    for o, lse in ((o_split, l_split), (o_whole, l_whole)):
+        check(o[32:], exp)
+        assert ((lse[32:].double().cpu() - exp_lse).abs().numpy() <= lse_bound(q[32:], values, 1)).all()
+
+
 @pytest.mark.parametrize("d", [44, 64])
 @pytest.mark.parametrize("gain", [4.0, 12.0])
 def test_large_logits_exercise_rescaling(cuda, gain, d):
