@@ -211,7 +211,7 @@ def main():
             "query_rows_per_step": rows_per_step, "cache": "int8 per-vector absmax (resident)",
         },
         "roofline": {
-            "kernel": "icl_attention_kernel<48, int8, ones, 16 waves> (+ combine_splits_kernel)",
+            "kernel": "icl_attention_kernel<48, int8, fold, 16 waves> (+ combine_splits_kernel)",
             "bound": "mfma",
             "achieved": round(attn_achieved / 1e12, 2),
             "peak": MFMA_BF16_PEAK / 1e12,
