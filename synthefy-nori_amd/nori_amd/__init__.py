@@ -3,17 +3,23 @@
 Drop-in operators for the reference's context-cache path (Synthefy/synthefy-nori):
 the int8 K/V cache codec and cache containers (``kv_cache_scaling``), query-row ->
 context attention over the cached K/V (``attention``) and RMSNorm (``norm``), all
-computed by hand-written gfx950 kernels in libnori_hip.so, and the per-layer cache build
-and cached apply built on them (``layer``).
+computed by hand-written gfx950 kernels in libnori_hip.so, the per-layer cache build
+and cached apply built on them (``layer``), and the context-cache API around the layer
+stack -- ``FeaturesTransformer.build_context_cache`` / ``apply_context_cache`` with the
+input encoders (``transformer``, ``encoders``).
 """
 
-from . import _native, layer
+from . import _native, encoders, layer, transformer
 from .attention import attend_dense, compute_attention_blockwise, icl_attention
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, dequantize_int8, quantize_int8, scale_caches
 from .norm import RMSNorm, rms_norm
+from .transformer import ContextCache, FeaturesTransformer
 
 __all__ = [
     "BlockwiseSeqKV",
+    "ContextCache",
+    "FeaturesTransformer",
+    "encoders",
     "layer",
     "RMSNorm",
     "ScalableSeqKV",
@@ -24,4 +30,5 @@ __all__ = [
     "quantize_int8",
     "rms_norm",
     "scale_caches",
+    "transformer",
 ]
