@@ -7,8 +7,11 @@ for the parts of the ICL stage that run per layer:
 * ``MultiheadAttention``: ``project_kv_cache`` (:651-683), ``forward_with_kv_cache``
   (:685-745), the separate-Q/KV ``forward`` used by the context self-attention (:1062-1162),
   QASS query scaling (:316-456) and the logN / learnable temperature (:555-583);
-* ``EncoderBaseLayer``: ``forward_train_cache`` (:1771-1913) and ``forward_test_with_cache``
-  (:1915-1967) for the ``smf`` and ``fmfmsm`` layer layouts;
+* ``EncoderBaseLayer``: ``forward_train_cache`` (:1771-1913) -- whole-context, row-bounded
+  (``_forward_train_cache_memsaving`` :1694-1769) and host-streamed
+  (``_forward_train_cache_streaming`` :1574-1692, ``_project_kv_cache_rowchunked``
+  :1482-1572) -- and ``forward_test_with_cache`` (:1915-1967) for the ``smf`` and ``fmfmsm``
+  layer layouts;
 * ``LayerStack``: ``build_train_cache`` / ``forward_test_with_cache`` (:2058-2108).
 
 Every sequence attention -- the context self-attention of the cache build and the
@@ -497,6 +500,155 @@ class EncoderBaseLayer(nn.Module):
         raise NotImplementedError("Cached inference currently supports layer_arch='fmfmsm' and 'smf'")
 
     # -------------------------------------------------------------- cache build / apply
+    def _project_kv_cache_rowchunked(
+        self, attn_mod, x_kv_src, copy_kv, row_chunk, *, norm=None, offload=False, quantize=False, device=None,
+        streaming=False,
+    ):
+        """``attn_mod``'s K/V cache of ``x_kv_src`` [B, N, G, E], projected ``row_chunk`` rows at a
+        time (reference layer.py:1482-1572).
+
+        Each projected slice is folded into the cache as it is produced -- quantized by the HIP
+        codec straight into its rows, and/or moved to the host -- so neither the full-N
+        projection nor a full-precision copy of the whole cache is ever resident. Returns a
+        ``BlockwiseSeqKV`` when streaming, a ``ScalableSeqKV`` when quantizing or offloading,
+        else the plain ``{"kv", "batch", "groups"}`` dict.
+        """
+        n_rows = x_kv_src.shape[1]
+        batch, groups = x_kv_src.shape[0], x_kv_src.shape[2]
+        compute_device = torch.device(device) if device is not None else attn_mod.qkv_proj_weight.device
+
+        def row_slices():
+            for r0 in range(0, n_rows, row_chunk):
+                rows = x_kv_src[:, r0 : min(r0 + row_chunk, n_rows)]
+                if rows.device != compute_device:
+                    rows = rows.to(compute_device)
+                if norm is not None:
+                    rows = norm(rows)
+                projected = attn_mod.project_kv_cache(rows.transpose(1, 2), copy_first_head_kv=copy_kv)["kv"]
+                del rows
+                yield projected
+                del projected
+
+        if streaming:
+            return BlockwiseSeqKV.from_row_slices(
+                row_slices(), batch, groups, quantize=quantize, device=compute_device, dtype=x_kv_src.dtype,
+                offload=offload, n_rows=n_rows,
+            )
+        if not (quantize or offload):
+            return {"kv": torch.cat(list(row_slices()), dim=1), "batch": batch, "groups": groups}
+        return ScalableSeqKV.from_row_slices(
+            row_slices(), batch, groups, quantize=quantize, offload=offload, device=compute_device, dtype=x_kv_src.dtype
+        )
+
+    def _seq_attention_rows(self, rows, seq_attn, seq_norm, cache):
+        """The sequence-attention sublayer for a block of context rows attending to the whole
+        context through ``cache``: pre-norm residual or post-norm (layer.py:1676-1689, 1752-1765)."""
+        if self.pre_norm:
+            attn = seq_attn.forward_with_kv_cache(seq_norm(rows).transpose(1, 2), cache)[0].transpose(1, 2)
+            return self._residual_add(rows, attn)
+        attn = seq_attn.forward_with_kv_cache(rows.transpose(1, 2), cache)[0].transpose(1, 2)
+        return seq_norm(attn + rows)
+
+    def _forward_train_cache_memsaving(
+        self, x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, row_chunk, quantize,
+        offload, device,
+    ):
+        """Row-bounded cache build (reference layer.py:1694-1769). Only the self-attention K/V is
+        full-N and resident; the per-row steps, the self-attention queries and the stored cross
+        cache run ``row_chunk`` rows at a time, writing back into ``x_train`` in place."""
+        seq_attn_train = self.sequence_attentions[index1]
+        seq_attn_test = self.sequence_attentions[index2]
+        seq_norm = self.layer_norms[seq_step]
+        n_rows = x_train.shape[1]
+
+        def run_rows(rows, steps):
+            for step in steps:
+                rows = self._run_non_sequence_step(rows, step_idx=step, feature_atten_mask=feature_atten_mask,
+                                                   eval_pos=rows.shape[1])
+            return rows
+
+        if pre_steps:
+            for r0 in range(0, n_rows, row_chunk):
+                sl = slice(r0, min(r0 + row_chunk, n_rows))
+                x_train[:, sl] = run_rows(x_train[:, sl], pre_steps)
+        norm = seq_norm if self.pre_norm else None
+        train_cache = self._project_kv_cache_rowchunked(
+            seq_attn_train, x_train, self.self_share_all_kv_heads, row_chunk, norm=norm, device=device
+        )
+        test_cache = self._project_kv_cache_rowchunked(
+            seq_attn_test, x_train, self.cross_share_all_kv_heads, row_chunk, norm=norm, device=device,
+            quantize=quantize, offload=offload,
+        )
+        for r0 in range(0, n_rows, row_chunk):
+            sl = slice(r0, min(r0 + row_chunk, n_rows))
+            rows = self._seq_attention_rows(x_train[:, sl], seq_attn_train, seq_norm, train_cache)
+            x_train[:, sl] = run_rows(rows, post_steps)
+        del train_cache
+        return x_train, {"seq_kv": test_cache}
+
+    def _forward_train_cache_streaming(
+        self, x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, row_chunk, quantize,
+        device, *, cross_cache_offload=True,
+    ):
+        """One context layer with only ``row_chunk``-row tensors on the device (reference
+        layer.py:1574-1692).
+
+        The layer input/output and the self-attention K/V stay on the host; each row block is
+        staged for its row-local work, and the self-attention scans the host K/V blocks with the
+        HIP kernel's exact LSE merge (one launch per staged block). The reusable cross cache
+        is offloaded too, or -- the hybrid resident-int8 prefill -- quantized straight into one
+        preallocated device payload.
+        """
+        compute_device = torch.device(device) if device is not None else next(self.parameters()).device
+        if feature_atten_mask is not None:
+            raise NotImplementedError(
+                "stream_context does not yet support feature_atten_mask; staging a full mask would violate the "
+                "bounded-GPU-memory contract"
+            )
+        if x_train.device.type != "cpu":
+            raise ValueError(
+                "stream_context requires CPU-resident context activations; the predictor must not upload the full "
+                "training matrix"
+            )
+        seq_attn_train = self.sequence_attentions[index1]
+        seq_attn_test = self.sequence_attentions[index2]
+        seq_norm = self.layer_norms[seq_step]
+        n_rows = x_train.shape[1]
+
+        def write_host(source, transform):
+            if n_rows <= 0:
+                raise ValueError("stream_context received an empty context")
+            for r0 in range(0, n_rows, row_chunk):
+                sl = slice(r0, min(r0 + row_chunk, n_rows))
+                staged = transform(source[:, sl].to(compute_device))
+                source[:, sl].copy_(staged.detach().to("cpu"))
+                del staged
+            return source
+
+        def run_rows(rows, steps):
+            for step in steps:
+                rows = self._run_non_sequence_step(rows, step_idx=step, feature_atten_mask=feature_atten_mask,
+                                                   eval_pos=rows.shape[1])
+            return rows
+
+        # every row must reach the sequence-attention input before any K/V is projected
+        prepared = write_host(x_train, lambda rows: run_rows(rows, pre_steps)) if pre_steps else x_train
+        del x_train
+        norm = seq_norm if self.pre_norm else None
+        # the self-attention K/V stays full precision; only the cross cache follows cache_dtype
+        train_cache = self._project_kv_cache_rowchunked(
+            seq_attn_train, prepared, self.self_share_all_kv_heads, row_chunk, norm=norm, device=compute_device,
+            quantize=False, offload=True, streaming=True,
+        )
+        test_cache = self._project_kv_cache_rowchunked(
+            seq_attn_test, prepared, self.cross_share_all_kv_heads, row_chunk, norm=norm, device=compute_device,
+            quantize=quantize, offload=cross_cache_offload, streaming=True,
+        )
+        output = write_host(
+            prepared, lambda rows: run_rows(self._seq_attention_rows(rows, seq_attn_train, seq_norm, train_cache), post_steps)
+        )
+        return output, {"seq_kv": test_cache}
+
     def forward_train_cache(
         self,
         x_train: torch.Tensor,
@@ -512,16 +664,40 @@ class EncoderBaseLayer(nn.Module):
 
         The context self-attention runs on the HIP kernel over the projected full-precision
         K/V; the cross cache for the query rows is projected from the same normalized input
-        (or from the self-attention output for serial attention).
+        (or from the self-attention output for serial attention). ``fit_row_chunk`` selects the
+        row-bounded build, ``stream_context`` / ``_hybrid_resident_int8_prefill`` the host-streamed
+        one (non-serial attention only, as in the reference).
         """
         pre_steps, seq_step, post_steps, seq_index = self._cache_steps()
-        if fit_row_chunk or stream_context or _hybrid_resident_int8_prefill:
-            raise NotImplementedError(
-                "row-chunked and streamed context builds (context_row_chunk / stream_context) are not supported "
-                "by this build yet; build the whole context at once"
-            )
         index1 = seq_index * 2 if self.seq_attn_isolated else seq_index
         index2 = index1 + 1 if self.seq_attn_isolated else index1
+        bounded_prefill = stream_context or _hybrid_resident_int8_prefill
+        if (fit_row_chunk or bounded_prefill) and self.seq_attn_serial:
+            requested = "stream_context" if stream_context else "context_row_chunk"
+            raise NotImplementedError(
+                f"{requested} is not supported for serial sequence attention: the serial variant's test cache reads "
+                "the self-attention output, so the bounded build needs a different two-pass schedule"
+            )
+        if bounded_prefill:
+            if not fit_row_chunk:
+                requested = "stream_context" if stream_context else "hybrid resident INT8 prefill"
+                raise ValueError(f"{requested} requires a concrete context_row_chunk")
+            if stream_context and not offload_kv_cache:
+                raise ValueError("stream_context requires offload_kv_cache=True")
+            if _hybrid_resident_int8_prefill and (stream_context or offload_kv_cache or not quantize_kv_cache):
+                raise ValueError(
+                    "hybrid resident INT8 prefill requires stream_context=False, offload_kv_cache=False, and "
+                    "quantize_kv_cache=True"
+                )
+            return self._forward_train_cache_streaming(
+                x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, fit_row_chunk,
+                quantize_kv_cache, device, cross_cache_offload=not _hybrid_resident_int8_prefill,
+            )
+        if fit_row_chunk:
+            return self._forward_train_cache_memsaving(
+                x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, fit_row_chunk,
+                quantize_kv_cache, offload_kv_cache, device,
+            )
         eval_pos = x_train.shape[1]
         for step in pre_steps:
             x_train = self._run_non_sequence_step(x_train, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)

@@ -53,6 +53,17 @@ CTX_VARIANTS = {
 }
 
 
+# Bounded cache builds and the cache dtypes each is run with: row-chunked (fit_row_chunk), host
+# streamed (stream_context, host-offloaded caches) and the hybrid resident-int8 prefill.
+ROW_CHUNK = 32
+BOUNDED_BUILDS = (("rowchunk", (False, True)), ("stream", (False, True)), ("hybrid", (True,)))
+BOUNDED_KWARGS = {
+    "rowchunk": {},
+    "stream": dict(stream_context=True, offload_kv_cache=True),
+    "hybrid": dict(_hybrid_resident_int8_prefill=True),
+}
+
+
 def ctx_config(v):
     return dict(
         preprocess_config_x=dict(
@@ -181,6 +192,17 @@ def main():
                     if quant:
                         put(p, f"codes{i}", skv._q)
                         put(p, f"scales{i}", skv._scale)
+            # the bounded builds (layer.py:1482-1769): 100 context rows in chunks of 32, the last
+            # one ragged; row-chunked (memsaving), host-streamed, and the hybrid resident-int8 prefill
+            for mode, quants in BOUNDED_BUILDS:
+                for quant in quants:
+                    kwargs = dict(quantize_kv_cache=quant, fit_row_chunk=ROW_CHUNK, device=torch.device("cpu"))
+                    kwargs.update(BOUNDED_KWARGS[mode])
+                    xt_out, caches = stack.build_train_cache(x_train.clone(), **kwargs)
+                    y = stack.forward_test_with_cache(x_test.clone(), caches)
+                    sfx = "int8" if quant else "fp"
+                    put(p, f"train_out_{mode}_{sfx}", xt_out)
+                    put(p, f"test_out_{mode}_{sfx}", y)
         for k, v in stack.state_dict().items():
             put(p, "w." + k, v)
         put(p, "x_train", x_train)
@@ -241,6 +263,19 @@ def main():
                 put(p, f"norm_{k}", t)
             put(p, "nan_mean", ctx.nan_mean)
             put(p, "valid_feature_num", ctx.valid_feature_num)
+            # the bounded context builds (transformer.py:1169-1301 for the streamed ones), applied
+            # in query chunks of 16
+            for mode, quants in BOUNDED_BUILDS:
+                for quant in quants:
+                    cache_dtype = "int8" if quant else "bf16"
+                    kwargs = dict(fit_row_chunk=ROW_CHUNK)
+                    if mode == "stream":
+                        kwargs.update(stream_context=True, offload_kv_cache=True)
+                    elif mode == "hybrid":
+                        kwargs.update(_hybrid_resident_int8_prefill=True)
+                    ctx = model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], cache_dtype=cache_dtype, **kwargs)
+                    pred = model.apply_context_cache(x[:, n_ctx:], ctx, row_chunk_size=16)
+                    put(p, f"pred_{mode}_{cache_dtype}", pred)
         for k, t in model.state_dict().items():
             put(p, "w." + k, t)
         put(p, "x", x)

@@ -146,11 +146,16 @@ def test_query_rows_use_the_frozen_context_statistics(gold):
     torch.testing.assert_close(q["data"], whole["data"][:, n_ctx:], rtol=0, atol=0, equal_nan=True)
 
 
-def test_unsupported_levers_raise(gold):
+def test_unsupported_and_invalid_levers_raise(gold):
     model = make_model(gold, "a")
     x, y, n_ctx = table(gold, "a")
-    with pytest.raises(NotImplementedError, match="streamed context"):
-        model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], stream_context=True, offload_kv_cache=True, fit_row_chunk=32)
+    with pytest.raises(ValueError, match="requires a concrete context_row_chunk"):
+        model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], stream_context=True, offload_kv_cache=True)
+    with pytest.raises(ValueError, match="hybrid resident INT8 prefill requires"):
+        model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], _hybrid_resident_int8_prefill=True, fit_row_chunk=32)
+    with pytest.raises(ValueError, match="requires CPU x_train"):
+        model.build_context_cache(x[:, :n_ctx].to("meta"), y[:, :n_ctx], stream_context=True, offload_kv_cache=True,
+                                  fit_row_chunk=32)
     with pytest.raises(ValueError, match="stream_context requires offload_kv_cache"):
         model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], stream_context=True, fit_row_chunk=32)
     with pytest.raises(ValueError, match="concrete cache_dtype"):
@@ -236,3 +241,35 @@ def test_forward_cached_regression_and_chunked_apply_agree(gold, cuda):
     # chunks change only the query count of each attention launch (same per-row arithmetic
     # up to the kernel's per-launch schedule)
     torch.testing.assert_close(chunked, whole, rtol=1e-4, atol=1e-4)
+
+
+# the bounded builds (tests/golden/make_golden.py): row-chunked, host-streamed and hybrid
+# resident-int8 context builds in chunks of 32 context rows, applied in query chunks of 16
+ROW_CHUNK = 32
+BOUNDED = [("rowchunk", "bf16"), ("rowchunk", "int8"), ("stream", "bf16"), ("stream", "int8"), ("hybrid", "int8")]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tag", ["a", "b"])
+@pytest.mark.parametrize("mode,cache_dtype", BOUNDED)
+def test_bounded_context_builds_match_reference(gold, cuda, tag, mode, cache_dtype):
+    model = make_model(gold, tag, cuda)
+    streamed = mode != "rowchunk"
+    # the streamed builds and their apply keep the raw tables on the host
+    x, y, n_ctx = table(gold, tag, "cpu" if streamed else cuda)
+    kwargs = dict(fit_row_chunk=ROW_CHUNK)
+    if mode == "stream":
+        kwargs.update(stream_context=True, offload_kv_cache=True)
+    elif mode == "hybrid":
+        kwargs.update(_hybrid_resident_int8_prefill=True)
+    with torch.inference_mode():
+        ctx = model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], cache_dtype=cache_dtype, **kwargs)
+        pred = model.apply_context_cache(x[:, n_ctx:], ctx, row_chunk_size=16)
+    assert ctx.eval_pos == n_ctx and len(ctx.caches) == 2
+    if streamed:
+        # the query target embedding is drawn once from the context mean; the context targets
+        # are not kept
+        assert ctx.query_y_embedding is not None and ctx.y_train.shape[1] == 0
+        for c in ctx.caches:
+            assert c["seq_kv"].offloaded == (mode == "stream")
+    check(pred, gold[f"ctx_{tag}/pred_{mode}_{cache_dtype}"])

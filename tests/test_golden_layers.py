@@ -96,11 +96,26 @@ def test_layer_stack_takes_the_reference_state_dict(gold, tag):
     stack.load_state_dict(weights(gold, tag), strict=True)
 
 
-def test_unsupported_build_levers_raise_instead_of_being_ignored(gold):
+def test_bounded_build_levers_are_validated_as_the_reference_does(gold):
+    """layer.py:1822-1855: the streamed builds need a row cap, host offload (streaming) or a
+    resident int8 cache (hybrid), and serial attention refuses every bounded build."""
     stack = make_stack(gold, "stack")
     x = torch.from_numpy(gold["stack/x_train"])
-    with pytest.raises(NotImplementedError, match="context_row_chunk"):
-        stack.build_train_cache(x, fit_row_chunk=32)
+    with pytest.raises(ValueError, match="context_row_chunk"):
+        stack.build_train_cache(x.clone(), stream_context=True, offload_kv_cache=True)
+    with pytest.raises(ValueError, match="offload_kv_cache=True"):
+        stack.build_train_cache(x.clone(), stream_context=True, fit_row_chunk=32)
+    with pytest.raises(ValueError, match="hybrid resident INT8 prefill requires"):
+        stack.build_train_cache(x.clone(), _hybrid_resident_int8_prefill=True, fit_row_chunk=32)
+    with pytest.raises(ValueError, match="CPU-resident"):
+        stack.layers[0].forward_train_cache(
+            x.clone().to("meta"), fit_row_chunk=32, stream_context=True, offload_kv_cache=True
+        )
+    serial = make_stack(gold, "stack")
+    for layer in serial.layers:
+        layer.seq_attn_serial = True
+    with pytest.raises(NotImplementedError, match="serial sequence attention"):
+        serial.build_train_cache(x.clone(), fit_row_chunk=32)
 
 
 # ------------------------------------------------------------------------------- GPU
@@ -162,3 +177,45 @@ def test_layer_stack_cache_build_and_apply_match_reference(gold, cuda, tag, quan
             assert np.abs(d).max() <= 1 and np.mean(d != 0) < 0.01
         test_out = stack.forward_test_with_cache(x_test, caches)
         check(test_out, gold[f"{tag}/test_out_{sfx}"])
+
+
+# the bounded builds: the reference's own row-chunked / streamed / hybrid outputs (100 context
+# rows in chunks of 32, tests/golden/make_golden.py)
+ROW_CHUNK = 32
+BOUNDED = [("rowchunk", False), ("rowchunk", True), ("stream", False), ("stream", True), ("hybrid", True)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tag", ["stack", "stack_mqa"])
+@pytest.mark.parametrize("mode,quant", BOUNDED)
+def test_bounded_layer_stack_builds_match_reference(gold, cuda, tag, mode, quant):
+    stack = make_stack(gold, tag)
+    stack.load_state_dict(weights(gold, tag), strict=True)
+    stack = stack.to(cuda)
+    streamed = mode != "rowchunk"
+    # the streamed builds read the context rows from host memory and stage a row chunk at a time
+    x_train = torch.from_numpy(gold[f"{tag}/x_train"]).clone()
+    if not streamed:
+        x_train = x_train.to(cuda)
+    x_test = torch.from_numpy(gold[f"{tag}/x_test"]).to(cuda)
+    kwargs = dict(quantize_kv_cache=quant, fit_row_chunk=ROW_CHUNK, device=cuda)
+    if mode == "stream":
+        kwargs.update(stream_context=True, offload_kv_cache=True)
+    elif mode == "hybrid":
+        kwargs.update(_hybrid_resident_int8_prefill=True)
+    sfx = "int8" if quant else "fp"
+    with torch.inference_mode():
+        train_out, caches = stack.build_train_cache(x_train, **kwargs)
+        assert train_out.device.type == ("cpu" if streamed else "cuda")
+        check(train_out, gold[f"{tag}/train_out_{mode}_{sfx}"])
+        for c in caches:
+            skv = c["seq_kv"]
+            if mode == "rowchunk":
+                assert isinstance(skv, ScalableSeqKV if quant else dict)
+            else:
+                assert isinstance(skv, BlockwiseSeqKV) and skv.quantized == quant
+                # streamed caches live on the host; the hybrid one is one resident int8 payload
+                assert skv.offloaded == (mode == "stream")
+                assert (skv.resident_payload() is not None) == (mode == "hybrid")
+        test_out = stack.forward_test_with_cache(x_test, caches)
+        check(test_out, gold[f"{tag}/test_out_{mode}_{sfx}"])
