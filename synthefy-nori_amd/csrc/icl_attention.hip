@@ -142,6 +142,9 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     if (d < 4 || d > 128 || d % 4)
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: head width %d is not a multiple of 4 in [4, 128]", d);
     if (nk <= 0) return fail(NORI_ERR_INVALID, "icl_attention: empty K/V cache");
+    if (nk > 2147483647LL - 1024)
+        return fail(NORI_ERR_UNSUPPORTED, "icl_attention: %lld context rows exceed the 2^31 - 1024 rows of one launch",
+                    (long long)nk);
     if (q_dtype != NORI_F32 && q_dtype != NORI_F16 && q_dtype != NORI_BF16)
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported query dtype %s", dtype_name(q_dtype));
     if (out_dtype != NORI_F32 && out_dtype != NORI_F16 && out_dtype != NORI_BF16)

@@ -34,19 +34,19 @@ int occupancy_of(int mode, int nw) {
 
 int resident_workgroups(int dp, int mode, int nw) {
     // cached per shape: the answer depends only on the compiled kernel and the device
-    static int cache[8][3][3] = {};
+    static int cache[8][2][3] = {};
     const int di = dp / 16 - 1, ni = nw == 16 ? 2 : (nw == 8 ? 1 : 0);
-    if (di < 0 || di > 7 || mode < 0 || mode > 2) return 1;
+    if (di < 0 || di > 7 || mode < 0 || mode > 1) return 1;
     int& slot = cache[di][mode][ni];
     if (slot == 0) {
         switch (dp) {
-            case 16: slot = occupancy_of<16, kOnes>(mode, nw); break;
+            case 16: slot = occupancy_of<16, kValu>(mode, nw); break;
             case 32: slot = occupancy_of<32, kValu>(mode, nw); break;
-            case 48: slot = occupancy_of<48, kOnes>(mode, nw); break;
+            case 48: slot = occupancy_of<48, kValu>(mode, nw); break;
             case 64: slot = occupancy_of<64, kValu>(mode, nw); break;
-            case 80: slot = occupancy_of<80, kOnes>(mode, nw); break;
+            case 80: slot = occupancy_of<80, kValu>(mode, nw); break;
             case 96: slot = occupancy_of<96, kValu>(mode, nw); break;
-            case 112: slot = occupancy_of<112, kOnes>(mode, nw); break;
+            case 112: slot = occupancy_of<112, kValu>(mode, nw); break;
             default: slot = occupancy_of<128, kValu>(mode, nw); break;
         }
         if (slot <= 0) slot = 1;

@@ -9,26 +9,27 @@
 // dequantization of kv_cache_scaling.py:40-41 folded into the tile loads.
 //
 // Schedule. A workgroup of NW wavefronts owns NW*32 query rows of one (b, h) and one
-// context range, scanned in blocks of 64 keys.
+// context range, scanned in blocks of KB keys.
 //   * Q lives in registers as f16 MFMA operands for the whole scan.
-//   * K/V blocks are software pipelined: while the wavefronts compute on block i from one
-//     LDS buffer, each thread holds its share of block i+1's raw cache words (issued before
-//     the compute, consumed after it) and converts them into the other buffer, so one
-//     barrier per block separates the two and the HBM latency hides under the MFMA work.
-//       K: int8 codes -> exact f16 integers (v_perm builds 1024+u, one packed add removes
-//          the bias); the row's scale times scale*log2(e) goes to an fp32 table, so the
-//          logit MFMA is exact in the codes and the scale is applied in fp32.
-//       V: exact f16 codes times the f16 row scale (one packed multiply, RN): the fp16
-//          value the reference's dequantization produces; stored transposed ([d][key]) with keys
-//          permuted inside each 16-key group so the probabilities leave the logit MFMA in
-//          the operand order of the PV MFMA (no cross-lane moves).
-//   * Per wavefront and block: S^T = K Q^T (v_mfma_f32_32x32x16_f16, 32 keys x 32 queries per
-//     tile), x = s*kfac - m (one fma), online softmax in base 2 with lazy rescaling (the
-//     running max only moves when a block exceeds it by 2^8), P rounded to f16, and
-//     O^T += V^T P^T (v_mfma_f32_32x32x16_f16).
-//   * The softmax denominator comes out of the PV MFMA: when the head width leaves a padding
-//     row in the last 32-row tile of V^T, that row holds ones and accumulates sum_j p_j for
-//     free; only head widths that are multiples of 32 sum P on the VALU.
+//   * K/V blocks are staged into an LDS ring, both row-major ([key][d], f16), two blocks
+//     ahead of use, from raw cache words loaded one block before that. A staging lane owns 16
+//     consecutive elements of one row of K or V: one 16-byte load of int8 codes, an exact
+//     int8 -> f16 conversion (v_perm builds 1024+u, one packed add removes the bias), the row
+//     scale applied by one packed multiply, and two 16-byte LDS writes. The (chunk, K|V) of a
+//     lane is uniform over its wavefront, and the staging wavefronts are spread evenly over
+//     the four SIMDs.
+//   * Per wavefront and 32-key step: S^T = K Q^T (v_mfma_f32_32x32x16_f16, 32 keys x 32
+//     queries), online softmax in base 2 with lazy rescaling (the running max only moves when
+//     a step exceeds it by 2^8), P rounded to f16, then O^T += V^T P^T on
+//     v_mfma_f32_16x16x32_f16 (16 head elements x 16 queries per tile, so V pads only to the
+//     next multiple of 16). Four v_permlane16_swap turn the probabilities of the logit tile
+//     into the two 16-query B operands; V^T operands come straight from the row-major V tile
+//     through ds_read_b64_tr_b16, whose per-lane row addresses put the keys in the order the
+//     swapped probabilities hold them.
+//   * When the head width is not a multiple of 16 the padding carries the rest of the
+//     softmax: K column d holds ones and the Q fragment -m (the running max), so the logit
+//     MFMA returns s - m in log2 units, and the last V column holds ones, so the PV MFMA
+//     accumulates the denominator sum_j p_j in its last output row.
 //   * Workgroups are renumbered so that the query tiles and heads that read the same cache
 //     rows are dealt to the same XCD (the hardware deals workgroups round-robin over the 8
 //     XCDs), so each cache line comes from HBM once per XCD and is then served by its L2.
@@ -47,10 +48,32 @@ constexpr int block_keys(int nw) { return nw == 16 ? 128 : 64; }
 constexpr int QPW = 32;  // query rows per wavefront
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kRescaleSlack = 8.0f;  // log2 units a block may exceed the running max by
+constexpr float kRescaleSlack = 8.0f;  // log2 units a step may exceed the running max by
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// LDS (address space 3) views: constant offsets from an LDS pointer fold into the DS
+// instructions' offset field, so a step's operand reads share one address register
+typedef __attribute__((address_space(3))) _Float16 lds_f16;
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// An LDS pointer the optimizer cannot take apart: the per-block operand bases pass through
+// this, so every read of a step is base + constant (without it, loop strength reduction
+// rebuilds each read's address from separate per-read terms on the VALU).
+__device__ __forceinline__ const lds_f16* opaque_lds(const lds_f16* p) {
+    uint32_t a = (uint32_t)(uintptr_t)p;
+    asm("" : "+v"(a));
+    return (const lds_f16*)(uintptr_t)a;
+}
+
+// ds_read_b64_tr_b16 at an LDS address (8-byte aligned)
+__device__ __forceinline__ f16x4 read_tr16(const lds_f16* p) {
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
 
 struct Args {
     const void* q; int q_dtype; int64_t nq; int heads; int d;
@@ -80,17 +103,14 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t&
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) + bias);
 }
 
-// 4 int8 codes times a row scale -> two f16x2: exact f16 code integers times the scale
-// rounded to f16, one packed multiply (RN). For caches built from fp16 or bf16 tensors the
-// scale is an fp16/bf16 value, exactly representable in f16, so this is the value of
-// (q.float() * scale).to(float16), the reference's fp16 dequantization, bit for bit; an
-// fp32-built cache picks up one extra f16 rounding of its scale (2^-11 relative).
-__device__ __forceinline__ void codes_scaled_to_f16(uint32_t w, float s, uint32_t& lo, uint32_t& hi) {
-    codes_to_f16(w, lo, hi);
-    const _Float16 sh = (_Float16)s;
-    const f16x2 s2 = {sh, sh};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) * s2);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) * s2);
+// Two f16x2 words times an f16 scale, one packed multiply each (RN). For caches built from
+// fp16 or bf16 tensors the scale is an fp16/bf16 value, exactly representable in f16, so
+// code * scale is the value of (q.float() * scale).to(float16), the reference's fp16
+// dequantization, bit for bit; an fp32-built cache picks up one extra f16 rounding of its
+// scale (2^-11 relative).
+__device__ __forceinline__ uint32_t scale_f16x2(uint32_t w, _Float16 s) {
+    const f16x2 s2 = {s, s};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w) * s2);
 }
 
 // Max of 16 values as a depth-3 tree of v_max3_f32, without the NaN-quieting copies the
@@ -128,6 +148,11 @@ __device__ __forceinline__ float other_half(float v) {
     return __uint_as_float((__lane_id() < 32) ? r[1] : r[0]);
 }
 
+// Value of lane `src` (all lanes active).
+__device__ __forceinline__ float lane_value(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
 }
@@ -154,42 +179,69 @@ __device__ __forceinline__ void merge_weights(float lse_old, float lse_part, flo
     w_new = expf(lse_part - lse_out);
 }
 
-// Raw cache words of one staging unit (4 key rows x 4 head elements of K or V).
-template <int KVT> struct Raw;
-template <> struct Raw<NORI_I8> { uint32_t w[4]; float s[4]; };
-template <> struct Raw<NORI_F16> { u32x2 w[4]; };
-template <> struct Raw<NORI_BF16> { u32x2 w[4]; };
-template <> struct Raw<NORI_F32> { u32x4 w[4]; };
+constexpr int elem_size(int kvt) { return kvt == NORI_F32 ? 4 : (kvt == NORI_I8 ? 1 : 2); }
+
+// Raw cache words of one staging unit: 16 consecutive elements of one row of K or V (and,
+// for int8 codes, the row's scale).
+template <int KVT>
+struct Raw {
+    uint32_t w[4 * elem_size(KVT)];
+    float s;
+};
+
+// nbytes (a multiple of 4, at most 4 * NWORDS, uniform over the wavefront) raw bytes at byte
+// offset `off` of a buffer, in 16/12/8/4-byte loads; the words past nbytes are zero.
+template <int NWORDS>
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, uint32_t off, int nbytes, uint32_t (&w)[NWORDS]) {
+#pragma unroll
+    for (int p = 0; p < NWORDS / 4; ++p) {
+        const int left = nbytes - 16 * p;
+        const uint32_t o = off + 16 * p;
+        if (left >= 16) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+            w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+        } else if (left == 12) {
+            const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, o, 0, 0);
+            w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = 0u;
+        } else if (left == 8) {
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
+            w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = 0u; w[4 * p + 3] = 0u;
+        } else if (left == 4) {
+            w[4 * p] = __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0);
+            w[4 * p + 1] = 0u; w[4 * p + 2] = 0u; w[4 * p + 3] = 0u;
+        } else {
+            w[4 * p] = 0u; w[4 * p + 1] = 0u; w[4 * p + 2] = 0u; w[4 * p + 3] = 0u;
+        }
+    }
+}
 
 // How a kernel forms the logits and the softmax denominator for head width d, padded width DP.
 enum Mode : int {
-    // d < DP. K column d holds ones and the Q fragment carries -m (the running max) there,
-    // so the logit MFMA returns s - m in log2 units with no VALU work: Q is prescaled by
-    // scale*log2(e) and K rows are dequantized with their scales, the f16 value of the
-    // reference's dequantization. The padding row of V^T holds ones and sums P.
+    // d < DP (d not a multiple of 16). K column d holds ones and the Q fragment carries -m
+    // (the running max) there, so the logit MFMA returns s - m in log2 units with no VALU
+    // work: Q is prescaled by scale*log2(e) and K rows are dequantized with their scales, the
+    // f16 value of the reference's dequantization. The last V column holds ones and sums P.
     kFold = 0,
-    // d = DP < DV: x = s * kfac - m on the VALU from exact f16 K codes and an fp32 per-key
-    // factor (scale * scale*log2(e)); the padding row of V^T sums P.
-    kOnes = 1,
-    // d = DP = DV: as kOnes, with the denominator summed on the VALU.
-    kValu = 2,
+    // d = DP: x = s * kfac - m on the VALU from exact f16 K codes and an fp32 per-key factor
+    // (scale * scale*log2(e)); the denominator is summed on the VALU.
+    kValu = 1,
 };
 
-constexpr int mode_for(int d) { return d % 16 != 0 ? kFold : (d % 32 != 0 ? kOnes : kValu); }
+constexpr int mode_for(int d) { return d % 16 != 0 ? kFold : kValu; }
 
-template <int DP, bool ONES, int NW>
+template <int DP, int NW>
 struct Geometry {
     static_assert(DP % 16 == 0 && DP >= 16 && DP <= 128, "padded head width");
     static constexpr int KB = block_keys(NW);
-    static constexpr int SPB = KB / 32;             // 32-key steps per block
-    static constexpr int DV = (DP + 31) / 32 * 32;  // PV output rows (MFMA M granule)
-    static constexpr int KSTEPS = DP / 16;          // logit MFMA k-steps
-    static constexpr int VTILES = DV / 32;
-    static constexpr int DQMAX = DP / 4;            // 4-element quads per padded head vector
-    static constexpr int KPITCH = DP + 8;           // f16 per K row in LDS (+16 B: conflict-free b128 reads)
-    static constexpr int VPITCH = KB + 8;           // f16 per V^T row in LDS
+    static constexpr int SPB = KB / 32;        // 32-key steps per block
+    static constexpr int KSTEPS = DP / 16;     // logit MFMA k-steps
+    static constexpr int VT = DP / 16;         // 16-row tiles of O^T (PV output)
+    static constexpr int KPITCH = DP + 8;      // f16 per K row in LDS (+16 B: conflict-free b128 reads)
+    // f16 per V row: the transposed reads of a 16-lane group take 32 bytes from each of 4
+    // rows, which land in distinct banks when the row stride is an odd multiple of 32 bytes
+    static constexpr int VPITCH = DP % 32 == 0 ? DP + 16 : DP;
     static constexpr int KBUF = KB * KPITCH;
-    static constexpr int VBUF = DV * VPITCH;
+    static constexpr int VBUF = KB * VPITCH;
     // LDS buffers in the K/V ring: three let a block be staged while the previous block's V
     // and the next block's K are both being read (one barrier per block); wide heads, whose
     // buffers are large, use two and a second barrier. The budget keeps two 8-wave
@@ -209,16 +261,15 @@ struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 
 template <int DP, int KVT, int MODE, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
 icl_attention_kernel(const Args a) {
-    constexpr bool ONES = MODE != kValu;
     constexpr bool FOLD = MODE == kFold;
-    using G = Geometry<DP, ONES, NW>;
+    using G = Geometry<DP, NW>;
     constexpr int KB = G::KB;
     constexpr int THREADS = NW * 64;
-    constexpr int UNITS = 2 * (KB / 4) * G::DQMAX;
-    constexpr int NU = (UNITS + THREADS - 1) / THREADS;  // staging units per thread (upper bound)
+    constexpr int ES = elem_size(KVT);
+    constexpr int NU = (2 * KB * (DP / 16) + THREADS - 1) / THREADS;  // staging units per thread (upper bound)
     __shared__ __attribute__((aligned(16))) _Float16 Ks[G::NBUF * G::KBUF];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[G::NBUF * G::VBUF];
-    __shared__ __attribute__((aligned(16))) float kfac[FOLD ? 4 : G::NBUF * KB];
+    __shared__ __attribute__((aligned(16))) _Float16 Vs[G::NBUF * G::VBUF];
+    __shared__ __attribute__((aligned(16))) float kfac[(FOLD || KVT != NORI_I8) ? 4 : G::NBUF * KB];
 
     // ---- work item, XCD-aware: the hardware deals workgroup i to XCD i % 8; within each phase
     // (whole units, then tail ranges) give each XCD a contiguous range of items, so the
@@ -250,23 +301,24 @@ icl_attention_kernel(const Args a) {
     const int64_t qi = (int64_t)qt * (NW * QPW) + wave * QPW + l32;
     const int64_t k_begin = split < 0 ? 0 : (int64_t)split * a.keys_per_split;
     const int64_t k_end = split < 0 ? a.nk : min<int64_t>(a.nk, k_begin + a.keys_per_split);
-    const int nblk = (int)((k_end - k_begin + KB - 1) / KB);
+    // keys in this context range (< 2^31, checked on the host), kept in a scalar register so
+    // the per-step "partial step" test is a scalar branch
+    const int klen = __builtin_amdgcn_readfirstlane((int)(k_end - k_begin));
+    const int nblk = (klen + KB - 1) / KB;
     const int d = a.d;
-    const int dqv = d >> 2;
 
-    // ---- constant LDS: K columns [d, DP) and V^T rows [d, DV) of every buffer are never
-    // staged; they stay zero, except K column d when the logit offset is folded into the
-    // MFMA (d is a multiple of 4, so it opens quad d/4) and the ones row (last V^T row)
-    // that sums P.
-    for (int row = tid; row < G::NBUF * KB; row += THREADS)
-        for (int dq = dqv; dq < G::DQMAX; ++dq)
-            *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + 4 * dq]) =
-                u32x2{(FOLD && dq == dqv) ? 0x3c00u : 0u, 0u};
-    for (int e = tid; e < G::NBUF * G::DV * KB; e += THREADS) {
-        const int row = (e / KB) % G::DV;  // compile-time divisors
-        if (row >= d)
-            Vt[(e / (G::DV * KB)) * G::VBUF + row * G::VPITCH + e % KB] =
-                (ONES && row == G::DV - 1) ? (_Float16)1.0f : (_Float16)0.0f;
+    // ---- constant LDS: K columns [d, DP) and V columns [d, DP) of every buffer are never
+    // staged; they stay zero, except, when the logit offset and the denominator are folded
+    // into the MFMAs, K column d (ones: d is a multiple of 4, so it opens quad d/4) and the
+    // last V column (ones).
+    for (int e = tid; e < G::NBUF * KB * (DP / 4); e += THREADS) {
+        const int row = e / (DP / 4), col = 4 * (e % (DP / 4));  // compile-time divisors
+        if (col >= d) {
+            *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + col]) =
+                u32x2{(FOLD && col == d) ? 0x3c00u : 0u, 0u};
+            *reinterpret_cast<u32x2*>(&Vs[(row / KB) * G::VBUF + (row % KB) * G::VPITCH + col]) =
+                u32x2{0u, (FOLD && col == DP - 4) ? 0x3c000000u : 0u};
+        }
     }
 
     // ---- Q fragment (B operand of S^T = K Q^T): lane holds q[qi][16ks + 8hh + 0..7], times
@@ -292,140 +344,132 @@ icl_attention_kernel(const Args a) {
         else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
     }
 
-    // ---- staging plan of this thread: unit u covers rows 4rq..4rq+3 and elements 4dq..4dq+3
-    // of K (kvsel 0; consecutive threads take consecutive dq, so loads are contiguous) or of V
-    // (kvsel 1; consecutive threads take consecutive rq, so the transposed LDS writes of a
-    // wavefront land in distinct banks). Loads go through one buffer descriptor per block
-    // based at the block's first row (a row holds K then V of every head, so valid rows end
-    // at nvalid*row_bytes): per-lane offsets are 32-bit and rows past the end of the context
-    // range fall outside the descriptor and read as zero. The same holds for the scales.
-    constexpr int kv_es = (KVT == NORI_F32) ? 4 : (KVT == NORI_I8 ? 1 : 2);
-    const uint32_t row_bytes = (uint32_t)(a.kv_row * kv_es);
+    // ---- staging plan of this thread. Unit idx = tid + u * THREADS covers elements
+    // [16c, 16c + n) of row idx % KB of K (half 0) or V (half 1), with (c, half) = idx / KB
+    // split as c = group / 2, half = group % 2: KB is a multiple of 64, so (c, half) -- and the
+    // load width n = min(16, d - 16c) -- are uniform over a wavefront. Loads go through one
+    // buffer descriptor per block based at the block's first row (a row holds K then V of every
+    // head, so valid rows end at nvalid*row_bytes): per-lane offsets are 32-bit and rows past
+    // the end of the context range fall outside the descriptor and read as zero. The same
+    // holds for the scales.
+    const uint32_t row_bytes = (uint32_t)(a.kv_row * ES);
     const uint32_t srow_bytes = (uint32_t)(a.sc_row * 4);
+    const int nch = (d + 15) >> 4;  // 16-element chunks per head vector
+    const int wave_first = __builtin_amdgcn_readfirstlane(wave * 64);
     uint32_t u_off[NU], u_soff[NU], u_lds[NU];
-    bool u_v[NU], u_on[NU], u_dq0[NU];
+    int u_nel[NU];  // elements of the unit (0: no unit), uniform over the wavefront
+    bool u_v[NU], u_c0[NU];
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-        const int idx = tid + u * THREADS;
-        const int nk_units = (KB / 4) * dqv;
-        int rq, dq;
-        u_on[u] = idx < 2 * nk_units;
-        u_v[u] = idx >= nk_units;
-        if (!u_v[u]) { rq = idx / dqv; dq = idx - rq * dqv; }
-        else { const int v = idx - nk_units; rq = v % (KB / 4); dq = v / (KB / 4); }
-        if (!u_on[u]) { rq = 0; dq = 0; }
-        u_dq0[u] = dq == 0;
-        u_off[u] = 4 * rq * row_bytes + (uint32_t)(((u_v[u] ? a.kv_half : 0) + hk * d + 4 * dq) * kv_es);
-        u_soff[u] = 4 * rq * srow_bytes + (uint32_t)(((u_v[u] ? a.sc_half : 0) + hk) * 4);
-        // LDS element offset of the unit's first write in a buffer
-        if (!u_v[u]) u_lds[u] = (uint32_t)(4 * rq * G::KPITCH + 4 * dq);
-        else u_lds[u] = (uint32_t)(4 * dq * G::VPITCH + 16 * (rq >> 2) + 4 * (((rq & 1) << 1) | ((rq >> 1) & 1)));
+        const int first = wave_first + u * THREADS;  // unit of lane 0
+        const int group = first / KB;                // uniform
+        const int row = first % KB + lane;
+        const int half = group & 1, c = group >> 1;
+        u_nel[u] = c < nch ? min(16, d - 16 * c) : 0;
+        u_v[u] = half != 0;
+        u_c0[u] = c == 0;
+        u_off[u] = row * row_bytes + (uint32_t)(((half ? a.kv_half : 0) + hk * d + 16 * c) * ES);
+        u_soff[u] = row * srow_bytes + (uint32_t)(((half ? a.sc_half : 0) + hk) * 4);
+        u_lds[u] = (uint32_t)(row * (half ? G::VPITCH : G::KPITCH) + 16 * c);
     }
-    const char* kv_bg_base = reinterpret_cast<const char*>(a.kv) + b * a.kv_bg * kv_es;
+    const char* kv_bg_base = reinterpret_cast<const char*>(a.kv) + b * a.kv_bg * ES;
     const char* sc_bg_base = reinterpret_cast<const char*>(a.kvs) + b * a.sc_bg * 4;
 
     auto load_block = [&](int64_t kb, Raw<KVT> (&raw)[NU]) {
         const uint32_t nvalid = (uint32_t)min<int64_t>(KB, k_end - kb);
         const __amdgpu_buffer_rsrc_t rkv = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(kv_bg_base + kb * a.kv_row * kv_es), 0, (int)(nvalid * row_bytes), 0x00020000);
+            (void*)(kv_bg_base + kb * a.kv_row * ES), 0, (int)(nvalid * row_bytes), 0x00020000);
         __amdgpu_buffer_rsrc_t rsc = rkv;
         if constexpr (KVT == NORI_I8)
             rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(sc_bg_base + kb * a.sc_row * 4), 0, (int)(nvalid * srow_bytes),
                                                     0x00020000);
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
-            if (!u_on[u]) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t off = u_off[u] + i * row_bytes;
-                if constexpr (KVT == NORI_I8) {
-                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b32(rkv, off, 0, 0);
-                    raw[u].s[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, u_soff[u] + i * srow_bytes, 0, 0));
-                } else if constexpr (KVT == NORI_F32) {
-                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b128(rkv, off, 0, 0);
-                } else {
-                    raw[u].w[i] = __builtin_amdgcn_raw_buffer_load_b64(rkv, off, 0, 0);
-                }
-            }
+            if (u_nel[u] == 0) continue;
+            load_words(rkv, u_off[u], u_nel[u] * ES, raw[u].w);
+            if constexpr (KVT == NORI_I8) raw[u].s = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, u_soff[u], 0, 0));
         }
     };
 
     auto store_block = [&](int bufsel, const Raw<KVT> (&raw)[NU]) {
-        _Float16* Kd = Ks + bufsel * G::KBUF;
-        _Float16* Vd = Vt + bufsel * G::VBUF;
-        float* kf = kfac + bufsel * KB;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
-            if (!u_on[u]) continue;
-            uint32_t lo[4], hi[4];
+            const int n = u_nel[u];
+            if (n == 0) continue;
+            // 16 f16 of the unit, as 8 words
+            uint32_t f[8];
+            if constexpr (KVT == NORI_I8) {
+                const bool scaled = FOLD || u_v[u];
+                const _Float16 sh = (_Float16)raw[u].s;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (KVT == NORI_I8) {
-                    if (!FOLD && !u_v[u]) codes_to_f16(raw[u].w[i], lo[i], hi[i]);
-                    else codes_scaled_to_f16(raw[u].w[i], raw[u].s[i], lo[i], hi[i]);
-                } else if constexpr (KVT == NORI_F16) {
-                    lo[i] = raw[u].w[i].x; hi[i] = raw[u].w[i].y;
-                } else if constexpr (KVT == NORI_BF16) {
-                    const u32x2 v = raw[u].w[i];
-                    lo[i] = pack_f16(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u));
-                    hi[i] = pack_f16(__uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
-                } else {
-                    const u32x4 v = raw[u].w[i];
-                    lo[i] = pack_f16(__uint_as_float(v.x), __uint_as_float(v.y));
-                    hi[i] = pack_f16(__uint_as_float(v.z), __uint_as_float(v.w));
-                }
-            }
-            if (!u_v[u]) {
-                _Float16* dst = Kd + u_lds[u];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x2*>(dst + i * G::KPITCH) = u32x2{lo[i], hi[i]};
-                if (!FOLD && u_dq0[u]) {
-                    const int r0 = (int)(u_lds[u] / G::KPITCH);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float f = a.scale_log2;
-                        if constexpr (KVT == NORI_I8) f = raw[u].s[i] * a.scale_log2;
-                        kf[r0 + i] = f;
+                for (int i = 0; i < 4; ++i) {
+                    codes_to_f16(raw[u].w[i], f[2 * i], f[2 * i + 1]);
+                    if (scaled) {
+                        f[2 * i] = scale_f16x2(f[2 * i], sh);
+                        f[2 * i + 1] = scale_f16x2(f[2 * i + 1], sh);
                     }
                 }
+                if (!FOLD && !u_v[u] && u_c0[u]) kfac[bufsel * KB + (int)(u_lds[u] / G::KPITCH)] = raw[u].s * a.scale_log2;
+            } else if constexpr (KVT == NORI_F16) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] = raw[u].w[i];
+            } else if constexpr (KVT == NORI_BF16) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t v = raw[u].w[i];
+                    f[i] = pack_f16(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u));
+                }
             } else {
-                // transpose the 4x4 (row, d) block; rows of a 16-key group go to columns with
-                // bits 2 and 3 of the key index swapped (the PV operand order)
-                _Float16* dst = Vd + u_lds[u];
-                *reinterpret_cast<u32x2*>(dst + 0 * G::VPITCH) =
-                    u32x2{__builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u), __builtin_amdgcn_perm(lo[3], lo[2], 0x05040100u)};
-                *reinterpret_cast<u32x2*>(dst + 1 * G::VPITCH) =
-                    u32x2{__builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u), __builtin_amdgcn_perm(lo[3], lo[2], 0x07060302u)};
-                *reinterpret_cast<u32x2*>(dst + 2 * G::VPITCH) =
-                    u32x2{__builtin_amdgcn_perm(hi[1], hi[0], 0x05040100u), __builtin_amdgcn_perm(hi[3], hi[2], 0x05040100u)};
-                *reinterpret_cast<u32x2*>(dst + 3 * G::VPITCH) =
-                    u32x2{__builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u), __builtin_amdgcn_perm(hi[3], hi[2], 0x07060302u)};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] = pack_f16(__uint_as_float(raw[u].w[2 * i]), __uint_as_float(raw[u].w[2 * i + 1]));
             }
+            _Float16* dst = (u_v[u] ? Vs + bufsel * G::VBUF : Ks + bufsel * G::KBUF) + u_lds[u];
+            // n f16 (a multiple of 4, uniform over the wavefront): 16-byte and 8-byte writes
+            if (n >= 8) *reinterpret_cast<u32x4*>(dst) = u32x4{f[0], f[1], f[2], f[3]};
+            else *reinterpret_cast<u32x2*>(dst) = u32x2{f[0], f[1]};
+            if (n == 16) *reinterpret_cast<u32x4*>(dst + 8) = u32x4{f[4], f[5], f[6], f[7]};
+            else if (n == 12) *reinterpret_cast<u32x2*>(dst + 8) = u32x2{f[4], f[5]};
         }
     };
 
-    f32x16 o[G::VTILES];
+    // O^T accumulators: tile (t, qb) holds rows 16t + 4*(lane/16) + 0..3 of query 16qb + lane%16
+    f32x4 o[G::VT][2];
 #pragma unroll
-    for (int vt = 0; vt < G::VTILES; ++vt) o[vt] = f32x16{};
-    float m_run = 0.0f;  // running max (log2 units)
+    for (int t = 0; t < G::VT; ++t) o[t][0] = o[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = 0.0f;  // running max (log2 units) of query l32
     float l_run = 0.0f;  // this lane's share of the denominator (VALU-summed head widths only)
 
-    // S^T[32 keys x 32 queries] of the 32 K rows at Kh (lane: keys 8g + 4hh + i, query qi)
-    auto logits = [&](const _Float16* Kh) {
+    // S^T[32 keys x 32 queries] of the 32 K rows whose first row is at this lane's Kl - its own
+    // row offset (lane: keys 8g + 4hh + i, query qi)
+    const int k_lane = l32 * G::KPITCH + 8 * hh;  // this lane's A-operand element in a 32-row step
+    auto logits = [&](const lds_f16* Kl) {
         f32x16 acc = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < G::KSTEPS; ++ks) {
-            const f16x8 kfr = *reinterpret_cast<const f16x8*>(&Kh[l32 * G::KPITCH + 16 * ks + 8 * hh]);
+            const f16x8 kfr = *reinterpret_cast<const lds_f16x8*>(Kl + 16 * ks);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qf[ks], acc, 0, 0, 0);
         }
         return acc;
     };
 
-    // Online softmax of one 32-key step whose first key is kstep (logits s, per-key factors
-    // kf[0..32), V^T columns Vh[.][0..32)), then O^T += V^T P^T. s_next holds the following
-    // step's logits, already in flight; with the offset folded into the MFMA they carry the
-    // running max they were issued with and follow it when it moves.
-    auto softmax_pv = [&](const f32x16& s, f32x16& s_next, const float* kf, const _Float16* Vh, int64_t kstep,
+    // Row offset (in f16 elements, within a 32-key step of a V buffer) of this lane's
+    // transposed V^T reads. ds_read_b64_tr_b16 gives lane i of each 16-lane group g element
+    // i % 4 of the 8 bytes read by lanes 16g + i/4 + 4j (j = 0..3), so a lane reading 4
+    // consecutive head elements of key row R(g, t) makes lane i receive V[keys][16T + i]: the
+    // A operand of the 16x16x32 PV MFMA, with its k-slot 8g + j holding key
+    // sigma(g, j) = 16(g%2) + 4(g/2) + 8(j/4) + j%4 -- the key the swapped probability
+    // registers hold in that slot. The second read (slots 4..7) is 8 key rows further.
+    const int vg = lane >> 4, vt = lane & 15;
+    const int v_lane = (16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) * G::VPITCH + 4 * (vt & 3);
+    const lds_f16* const KsL = (const lds_f16*)Ks;
+    const lds_f16* const VsL = (const lds_f16*)Vs;
+
+    // Online softmax of one 32-key step whose first key is kstep (relative to the range start)
+    // (logits s, per-key factors kf[0..32), this lane's V operand address Vl in the step), then
+    // O^T += V^T P^T. s_next holds the following step's logits, already in flight; with the
+    // offset folded into the MFMA they carry the running max they were issued with and follow
+    // it when it moves.
+    auto softmax_pv = [&](const f32x16& s, f32x16& s_next, const float* kf, const lds_f16* Vl, int kstep,
                           bool first) {
         float x[16];
         if constexpr (FOLD) {
@@ -434,25 +478,29 @@ icl_attention_kernel(const Args a) {
         } else {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const f32x4 f = *reinterpret_cast<const f32x4*>(&kf[8 * g + 4 * hh]);
+                f32x4 f;
+                if constexpr (KVT == NORI_I8) f = *reinterpret_cast<const f32x4*>(&kf[8 * g + 4 * hh]);
+                else f = f32x4{a.scale_log2, a.scale_log2, a.scale_log2, a.scale_log2};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) x[4 * g + i] = fmaf(s[4 * g + i], f[i], -m_run);
             }
         }
-        if (kstep + 32 > k_end) {  // the last step of a context range may be partial
+        if (kstep + 32 > klen) {  // the last step of a context range may be partial
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (kstep + 8 * g + 4 * hh + i >= k_end) x[4 * g + i] = -INFINITY;
+                    if (kstep + 8 * g + 4 * hh + i >= klen) x[4 * g + i] = -INFINITY;
         }
+        // the lane's max over its 16 keys decides whether any query of the wavefront must move
+        // its running max; only then is the per-query max (both half-waves) formed
         float bm = max16f(x);
-        {
-            // both halves of the swap together hold lanes l and l ^ 32 in every lane
-            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), true, false);
-            bm = max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
-        }
         if (first || __any(bm > kRescaleSlack)) {
+            {
+                // both halves of the swap together hold lanes l and l ^ 32 in every lane
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), true, false);
+                bm = max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+            }
             // anchor the running max on the first step (its first key is valid for every
             // query); afterwards move it up where a step overshoots it (rare: the max settles
             // within the first few blocks). A folded max is an f16 value (the Q fragment
@@ -462,10 +510,14 @@ icl_attention_kernel(const Args a) {
             if (!first) {
                 const float alpha = __builtin_amdgcn_exp2f(-shift);
                 l_run *= alpha;
+                // alpha of query lane%16 (query block 0) and 16 + lane%16 (block 1)
+                const auto ab = __builtin_amdgcn_permlane16_swap(__float_as_uint(alpha), __float_as_uint(alpha), false, false);
+                const float a0 = __uint_as_float(ab[0]), a1 = __uint_as_float(ab[1]);
 #pragma unroll
-                for (int vt = 0; vt < G::VTILES; ++vt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[vt][r] *= alpha;
+                for (int t = 0; t < G::VT; ++t) {
+                    o[t][0] *= a0;
+                    o[t][1] *= a1;
+                }
             }
             m_run += shift;
 #pragma unroll
@@ -480,30 +532,37 @@ icl_attention_kernel(const Args a) {
                         if (16 * ks + 8 * hh + j == d) qf[ks][j] = (_Float16)(-m_run);
             }
         }
-        // probabilities (f16, RN); pf[c] holds keys 16c + 8hh + 0..7 in the PV operand order
-        f16x8 pf[2];
+        // probabilities (f16, RN): word t of pw holds x[2t], x[2t + 1] (keys 8(t/2) + 4hh + 2(t%2) + 0..1)
+        uint32_t pw[8];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(x[8 * c + j]);
-                const float p1 = __builtin_amdgcn_exp2f(x[8 * c + j + 1]);
-                const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
-                if constexpr (!ONES) {
-                    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-                    l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
-                }
-                pf[c][j] = pp[0];
-                pf[c][j + 1] = pp[1];
+        for (int t = 0; t < 8; ++t) {
+            const float p0 = __builtin_amdgcn_exp2f(x[2 * t]);
+            const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1]);
+            const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
+            if constexpr (!FOLD) {
+                const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+                l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
             }
+            pw[t] = __builtin_bit_cast(uint32_t, pp);
         }
+        // B operands of the two 16-query blocks: swapping words t and t + 4 between 16-lane
+        // rows gives block 0 (queries 0-15) and block 1 (queries 16-31) their 32 keys each
+        u32x4 pa, pb;
 #pragma unroll
-        for (int vt = 0; vt < G::VTILES; ++vt) {
+        for (int t = 0; t < 4; ++t) {
+            const auto r = __builtin_amdgcn_permlane16_swap(pw[t], pw[t + 4], false, false);
+            pa[t] = r[0];
+            pb[t] = r[1];
+        }
+        const f16x8 p0 = __builtin_bit_cast(f16x8, pa);
+        const f16x8 p1 = __builtin_bit_cast(f16x8, pb);
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vh[(32 * vt + l32) * G::VPITCH + 16 * c + 8 * hh]);
-                o[vt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[vt], 0, 0, 0);
-            }
+        for (int t = 0; t < G::VT; ++t) {
+            const f16x4 lo = read_tr16(Vl + 16 * t);
+            const f16x4 hi = read_tr16(Vl + 8 * G::VPITCH + 16 * t);
+            const f16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            o[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p0, o[t][0], 0, 0, 0);
+            o[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p1, o[t][1], 0, 0, 0);
         }
     };
 
@@ -528,14 +587,17 @@ icl_attention_kernel(const Args a) {
     }
     if (nblk > AHEAD) load_block(k_begin + AHEAD * KB, raw);
     __syncthreads();
-    f32x16 s_cur = logits(Ks);
+    f32x16 s_cur = logits(KsL + k_lane);
 
     for (int blk = 0; blk < nblk; ++blk) {
         const int64_t kb = k_begin + (int64_t)blk * KB;
         const int cur = blk % G::NBUF, nxt = (blk + 1) % G::NBUF;
-        const _Float16* Kc = Ks + cur * G::KBUF;
-        const _Float16* Vc = Vt + cur * G::VBUF;
-        const float* kf = kfac + (FOLD ? 0 : cur * KB);
+        // this lane's operand addresses in the current and next buffers; every step of the
+        // block reads at constant offsets from them
+        const lds_f16* Kc = opaque_lds(KsL + cur * G::KBUF + k_lane);
+        const lds_f16* Kn = opaque_lds(KsL + nxt * G::KBUF + k_lane);
+        const lds_f16* Vc = opaque_lds(VsL + cur * G::VBUF + v_lane);
+        const float* kf = kfac + ((FOLD || KVT != NORI_I8) ? 0 : cur * KB);
 #pragma unroll
         for (int st = 0; st < G::SPB; ++st) {
             if constexpr (AHEAD == 1) {
@@ -550,8 +612,9 @@ icl_attention_kernel(const Args a) {
             }
             // logits of the following step in flight: the next 32 rows of this block, or the
             // first 32 rows of the next block (a stale buffer after the last block, unused)
-            f32x16 s_next = logits(st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Ks + nxt * G::KBUF);
-            softmax_pv(s_cur, s_next, kf + (FOLD ? 0 : 32 * st), Vc + 32 * st, kb + 32 * st, blk == 0 && st == 0);
+            f32x16 s_next = logits(st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn);
+            softmax_pv(s_cur, s_next, kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH,
+                       blk * KB + 32 * st, blk == 0 && st == 0);
             s_cur = s_next;
             if constexpr (AHEAD == 2) {
                 if (st == 0 && blk + 2 < nblk) {
@@ -563,54 +626,57 @@ icl_attention_kernel(const Args a) {
         if constexpr (AHEAD == 2) __syncthreads();
     }
 
-    // ---------------- epilogue
-    float l_tot;
-    if constexpr (ONES) {
-        // O^T row DV-1 (tile VTILES-1, g = 3, i = 3) sits in the upper half-wave
-        const float mine = o[G::VTILES - 1][15];
-        const float theirs = other_half(mine);
-        l_tot = hh ? mine : theirs;
+    // ---------------- epilogue: per query, its denominator and running max in the O^T layout
+    // (lane holds query 16qb + lane%16)
+    float l_q[2], m_q[2];
+    if constexpr (FOLD) {
+        // the ones column sums P into O^T row DP-1: tile VT-1, element 3 of lanes 48-63
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) l_q[qb] = lane_value(o[G::VT - 1][qb][3], 48 + (lane & 15));
     } else {
-        l_tot = l_run + other_half(l_run);
-    }
-    if (qi >= a.nq) return;
-    const float inv = 1.0f / l_tot;
-    const float lse_part = (m_run + __log2f(l_tot)) * kLn2;
-    if (split >= 0) {
-        const int64_t prow = (split * (a.nunits - a.n_whole) + (unit - a.n_whole)) * a.qrows + (qi - (int64_t)qt * a.qrows);
-        float* po = a.part_o + prow * d;
+        const float l_tot = l_run + other_half(l_run);
 #pragma unroll
-        for (int vt = 0; vt < G::VTILES; ++vt)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = 32 * vt + 8 * g + 4 * hh;
-                if (d0 < d)
-                    *reinterpret_cast<f32x4*>(po + d0) =
-                        f32x4{o[vt][4 * g] * inv, o[vt][4 * g + 1] * inv, o[vt][4 * g + 2] * inv, o[vt][4 * g + 3] * inv};
-            }
-        if (hh == 0) a.part_lse[prow] = lse_part;
-        return;
+        for (int qb = 0; qb < 2; ++qb) l_q[qb] = lane_value(l_tot, 16 * qb + (lane & 15));
     }
-    const int64_t obase = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head;
-    const int64_t lse_idx = (b * a.heads + h) * a.nq + qi;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) m_q[qb] = lane_value(m_run, 16 * qb + (lane & 15));
     const bool merge = a.flags & NORI_ATTN_MERGE;
-    float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
-    if (merge) merge_weights(a.lse[lse_idx], lse_part, w_old, w_new, lse_out);
 #pragma unroll
-    for (int vt = 0; vt < G::VTILES; ++vt)
+    for (int qb = 0; qb < 2; ++qb) {
+        const int64_t qo = (int64_t)qt * (NW * QPW) + wave * QPW + 16 * qb + (lane & 15);
+        if (qo >= a.nq) continue;
+        const float inv = 1.0f / l_q[qb];
+        const float lse_part = (m_q[qb] + __log2f(l_q[qb])) * kLn2;
+        if (split >= 0) {
+            const int64_t prow =
+                (split * (a.nunits - a.n_whole) + (unit - a.n_whole)) * a.qrows + (qo - (int64_t)qt * a.qrows);
+            float* po = a.part_o + prow * d;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * vt + 8 * g + 4 * hh;
+            for (int t = 0; t < G::VT; ++t) {
+                const int d0 = 16 * t + 4 * (lane >> 4);
+                if (d0 < d) *reinterpret_cast<f32x4*>(po + d0) = o[t][qb] * inv;
+            }
+            if ((lane >> 4) == 0) a.part_lse[prow] = lse_part;
+            continue;
+        }
+        const int64_t obase = b * a.o_bg + qo * a.o_row + (int64_t)h * a.o_head;
+        const int64_t lse_idx = (b * a.heads + h) * a.nq + qo;
+        float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
+        if (merge) merge_weights(a.lse[lse_idx], lse_part, w_old, w_new, lse_out);
+#pragma unroll
+        for (int t = 0; t < G::VT; ++t) {
+            const int d0 = 16 * t + 4 * (lane >> 4);
             if (d0 < d) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = o[vt][4 * g + i] * inv;
+                    float v = o[t][qb][i] * inv;
                     if (merge) v = reinterpret_cast<const float*>(a.out)[obase + d0 + i] * w_old + v * w_new;
                     store_from_f32(a.out, a.out_dtype, obase + d0 + i, v);
                 }
             }
         }
-    if (a.lse && hh == 0) a.lse[lse_idx] = lse_out;
+        if (a.lse && (lane >> 4) == 0) a.lse[lse_idx] = lse_out;
+    }
 }
 
 // Launches the kernel instantiation for (cache dtype KVT, dp, mode, nw) over a.grid
@@ -629,19 +695,18 @@ int launch_shape(int nw, const Args& a, hipStream_t stream) {
     return NORI_OK;
 }
 
-// Padded head width DP has two kernels: kFold for d < DP, and kOnes (DP % 32 = 16) or kValu
-// (DP % 32 = 0) for d = DP.
+// Padded head width DP has two kernels: kFold for d < DP and kValu for d = DP.
 template <int KVT>
 int launch_dtype(int dp, int mode, int nw, const Args& a, hipStream_t stream) {
     const bool fold = mode == kFold;
     switch (dp) {
-        case 16: return fold ? launch_shape<KVT, 16, kFold>(nw, a, stream) : launch_shape<KVT, 16, kOnes>(nw, a, stream);
+        case 16: return fold ? launch_shape<KVT, 16, kFold>(nw, a, stream) : launch_shape<KVT, 16, kValu>(nw, a, stream);
         case 32: return fold ? launch_shape<KVT, 32, kFold>(nw, a, stream) : launch_shape<KVT, 32, kValu>(nw, a, stream);
-        case 48: return fold ? launch_shape<KVT, 48, kFold>(nw, a, stream) : launch_shape<KVT, 48, kOnes>(nw, a, stream);
+        case 48: return fold ? launch_shape<KVT, 48, kFold>(nw, a, stream) : launch_shape<KVT, 48, kValu>(nw, a, stream);
         case 64: return fold ? launch_shape<KVT, 64, kFold>(nw, a, stream) : launch_shape<KVT, 64, kValu>(nw, a, stream);
-        case 80: return fold ? launch_shape<KVT, 80, kFold>(nw, a, stream) : launch_shape<KVT, 80, kOnes>(nw, a, stream);
+        case 80: return fold ? launch_shape<KVT, 80, kFold>(nw, a, stream) : launch_shape<KVT, 80, kValu>(nw, a, stream);
         case 96: return fold ? launch_shape<KVT, 96, kFold>(nw, a, stream) : launch_shape<KVT, 96, kValu>(nw, a, stream);
-        case 112: return fold ? launch_shape<KVT, 112, kFold>(nw, a, stream) : launch_shape<KVT, 112, kOnes>(nw, a, stream);
+        case 112: return fold ? launch_shape<KVT, 112, kFold>(nw, a, stream) : launch_shape<KVT, 112, kValu>(nw, a, stream);
         case 128: return fold ? launch_shape<KVT, 128, kFold>(nw, a, stream) : launch_shape<KVT, 128, kValu>(nw, a, stream);
         default: return fail(NORI_ERR_UNSUPPORTED, "icl_attention: no kernel for padded head width %d", dp);
     }
