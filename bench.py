@@ -60,15 +60,15 @@ def parse_args():
     p.add_argument("--cpu-sample-queries", type=int, default=512, help="query rows of the CPU attention sample")
     p.add_argument(
         "--probe-traffic", action="store_true",
-        help="run a 1 GiB device copy (counter calibration), one quantize and one attention launch of the "
-        "workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
+        help="run a 1 GiB device copy (counter calibration), one quantize, one attention and one dequantize "
+        "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
     )
     return p.parse_args()
 
 
 def probe_traffic(torch, dev):
     import nori_amd
-    from nori_amd.kv_cache_scaling import _quantize_into
+    from nori_amd.kv_cache_scaling import _dequantize_into, _quantize_into
 
     a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
@@ -77,12 +77,14 @@ def probe_traffic(torch, dev):
     codes = torch.empty(kv.shape, dtype=torch.int8, device=dev)
     scales = torch.empty(kv.shape[:-1] + (1,), dtype=torch.float32, device=dev)
     q = torch.randn((GROUPS, QUERY_ROWS, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(kv)
     for _ in range(2):
         b.copy_(a)
         _quantize_into(kv, codes, scales)
         nori_amd.icl_attention(q, codes, scales)
+        _dequantize_into(codes, scales, out)
     torch.cuda.synchronize()
-    print("traffic probe: 2 x (1 GiB copy, quantize, attention) done", flush=True)
+    print("traffic probe: 2 x (1 GiB copy, quantize, attention, dequantize) done", flush=True)
 
 
 def build_workload(torch, layers, dev):
@@ -103,12 +105,12 @@ def measured_traffic():
     try:
         text = open(TRAFFIC_SUMMARY).read()
     except OSError:
-        return None, None
+        return None, None, None
     found = {}
-    for name in ("attention", "quantize"):
+    for name in ("attention", "quantize", "dequantize"):
         m = re.search(rf"^traffic_bytes_{name}\s*=\s*([0-9.eE+]+)", text, re.M)
         found[name] = float(m.group(1)) if m else None
-    return found["attention"], found["quantize"]
+    return found["attention"], found["quantize"], found["dequantize"]
 
 
 def main():
@@ -125,7 +127,7 @@ def main():
 
     import nori_amd
     from nori_amd import attention as attn
-    from nori_amd.kv_cache_scaling import _quantize_into
+    from nori_amd.kv_cache_scaling import _dequantize_into, _quantize_into
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -177,6 +179,17 @@ def main():
     quant_ms = [a.elapsed_time(b) for a, b in events_q]
     attn_ms = [a.elapsed_time(b) for a, b in events_a]
 
+    # dequantization (the full-precision read of a ScalableSeqKV, kv_cache_scaling.py:40-41,
+    # 78-90) is not on the step's path -- attention reads the codes -- so it is timed on its
+    # own, outside the step: one layer's cache back to fp16, HIP events around each launch
+    dq_out = torch.empty_like(kv[0])
+    dq_events = []
+    for i in range(6):
+        f = lambda: _dequantize_into(codes[0], scales[0], dq_out)  # noqa: E731
+        timed(f, dq_events) if i else f()
+    torch.cuda.synchronize()
+    dequant_ms = [a.elapsed_time(b) for a, b in dq_events]
+
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
     value = rows_per_step * args.steps / elapsed
@@ -188,7 +201,9 @@ def main():
     quant_bytes = n_elem * (2 + 1) + 4 * n_elem // HEAD_DIM  # fp16 in, int8 + fp32 scale out
     quant_avg_s = sum(quant_ms) / len(quant_ms) / 1e3
     quant_achieved = quant_bytes / quant_avg_s
-    attn_traffic, quant_traffic = measured_traffic()
+    dequant_avg_s = sum(dequant_ms) / len(dequant_ms) / 1e3
+    dequant_achieved = quant_bytes / dequant_avg_s  # int8 + fp32 scale in, fp16 out: the same bytes
+    attn_traffic, quant_traffic, dequant_traffic = measured_traffic()
 
     line = {
         "metric": "query rows/s @ 64k-row int8 ctx; attn % MFMA peak; quant kernel % HBM BW",
@@ -233,6 +248,18 @@ def main():
             "work_per_launch": f"{quant_bytes:.4e} B = n*(2+1) + 4*n/44, n = 33*65536*2*8*44",
             "avg_launch_ms": round(quant_avg_s * 1e3, 4),
             "launches": len(quant_ms),
+        },
+        "dequant_roofline": {
+            "kernel": "dequantize kernel, int8 + fp32 scale -> fp16",
+            "bound": "hbm",
+            "achieved": round(dequant_achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(dequant_achieved / HBM_PEAK, 4),
+            "traffic": dequant_traffic,
+            "work_per_launch": f"{quant_bytes:.4e} B = n*(1+2) + 4*n/44, n = 33*65536*2*8*44",
+            "avg_launch_ms": round(dequant_avg_s * 1e3, 4),
+            "launches": len(dequant_ms),
         },
     }
     if args.cpu_baseline == "on":

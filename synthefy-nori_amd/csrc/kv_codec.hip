@@ -457,6 +457,56 @@ dequant_tile_kernel(const int8_t* __restrict__ codes, int64_t n_inner, int d, in
     copy_out(dst + o * dst_outer_bytes + v0 * d * es, lds_out, nv * d * es);
 }
 
+// Contiguous slabs of vectors (head width d >= 16): thread t of a slab converts the 16 codes
+// [16t, 16t + 16) -- one 16-byte load -- which belong to at most two vectors, so it needs at
+// most two scales, and writes 16 output elements with 16-byte stores. The product is formed in
+// fp32 and rounded once to the output dtype: (q.float() * scale).to(dtype).
+template <int DT>
+__global__ void __launch_bounds__(kTileThreads)
+dequant_flat_kernel(const int8_t* __restrict__ codes, int64_t n_outer, int64_t n_inner, int d, int64_t codes_outer,
+                    const float* __restrict__ scales, int64_t scales_outer, uint8_t* __restrict__ dst,
+                    int64_t dst_outer_bytes, int64_t chunks_per_outer) {
+    using S = typename Storage<DT>::T;
+    constexpr int es = sizeof(S);
+    const int64_t gid = (int64_t)blockIdx.x * kTileThreads + threadIdx.x;
+    const int64_t o = gid / chunks_per_outer;
+    const int64_t t = gid - o * chunks_per_outer;
+    const int64_t n_elem = n_inner * d;
+    const int64_t e0 = 16 * t;
+    if (o >= n_outer || e0 >= n_elem) return;
+    const int8_t* c = codes + o * codes_outer;
+    const float* sc = scales + o * scales_outer;
+    S* y = reinterpret_cast<S*>(dst + o * dst_outer_bytes);
+    const int64_t v0 = e0 / d;
+    const int split = (int)min<int64_t>(16, (v0 + 1) * d - e0);  // elements of vector v0 in the chunk
+    const float s0 = sc[v0];
+    if (e0 + 16 <= n_elem) {
+        const float s1 = split < 16 ? sc[v0 + 1] : s0;
+        const uint4 w = *reinterpret_cast<const uint4*>(c + e0);
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+        S out[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int code = (int)(int8_t)(words[i >> 2] >> (8 * (i & 3)));
+            const float f = (float)code * (i < split ? s0 : s1);
+            if constexpr (DT == NORI_F32) out[i] = __float_as_uint(f);
+            else if constexpr (DT == NORI_F16) out[i] = f32_to_f16(f);
+            else out[i] = f32_to_bf16(f);
+        }
+        uint4* yo = reinterpret_cast<uint4*>(y + e0);
+#pragma unroll
+        for (int k = 0; k < 16 * es / 16; ++k) yo[k] = reinterpret_cast<const uint4*>(out)[k];
+    } else {
+        // the slab's last, partial chunk
+        for (int64_t e = e0; e < n_elem; ++e) {
+            const float f = (float)c[e] * sc[e / d];
+            if constexpr (DT == NORI_F32) y[e] = __float_as_uint(f);
+            else if constexpr (DT == NORI_F16) y[e] = f32_to_f16(f);
+            else y[e] = f32_to_bf16(f);
+        }
+    }
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kTileThreads)
 dequant_direct_kernel(const int8_t* __restrict__ codes, int64_t n_outer, int64_t n_inner, int d,
@@ -543,8 +593,21 @@ extern "C" int nori_kv_dequantize_int8(const int8_t* codes, const float* scales,
     if (!codes || !scales || !dst) return fail(NORI_ERR_INVALID, "dequantize_int8: null pointer");
     hipStream_t stream = (hipStream_t)stream_v;
     const int es = dtype_size(dst_dtype);
-    const bool tiled = dst_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1 &&
-                       d * es <= kMaxTileVectorBytes;
+    const bool contiguous = dst_inner_stride == d && codes_inner_stride == d && scales_inner_stride == 1;
+    // 16-byte code loads and output stores from slab bases
+    const bool flat = contiguous && d >= 16 && ((uintptr_t)codes % 16) == 0 && (codes_outer_stride % 16) == 0 &&
+                      ((uintptr_t)dst % 16) == 0 && ((dst_outer_stride * es) % 16) == 0;
+    if (flat) {
+        const int64_t chunks_per_outer = (n_inner * d + 15) / 16;
+        const int64_t blocks = (chunks_per_outer * n_outer + kTileThreads - 1) / kTileThreads;
+        if (blocks > 0x7fffffffLL) return fail(NORI_ERR_UNSUPPORTED, "dequantize_int8: cache too large for one launch");
+        NORI_DISPATCH_FLOAT(dst_dtype, DT,
+            hipLaunchKernelGGL(dequant_flat_kernel<DT>, dim3((unsigned)blocks), dim3(kTileThreads), 0, stream, codes,
+                               n_outer, n_inner, d, codes_outer_stride, scales, scales_outer_stride, (uint8_t*)dst,
+                               dst_outer_stride * es, chunks_per_outer));
+        return launch_status("dequantize_int8");
+    }
+    const bool tiled = contiguous && d * es <= kMaxTileVectorBytes;
     if (tiled) {
         const int64_t tiles_per_outer = (n_inner + kTileThreads - 1) / kTileThreads;
         const int64_t grid = tiles_per_outer * n_outer;

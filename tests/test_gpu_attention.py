@@ -190,6 +190,29 @@ def test_large_logits_exercise_rescaling(cuda, gain, d):
     check(got, exp)
 
 
+@pytest.mark.parametrize("d,nq", [(44, 600), (52, 200), (44, 64)])
+def test_key_norm_ramp_moves_the_max_late(cuda, d, nq):
+    # Key magnitudes grow 20x along the context, so blocks early in the scan satisfy the
+    # per-block logit bound (|q| max|k| - m <= slack: the per-step max test is skipped) while
+    # later blocks must move the running max by more than the slack, several times. A bound
+    # that were too small would let probabilities past the slack through unrescaled. Logits
+    # stay within what f16 Q and K resolve at the 2e-2 bar (|q| ~ 3 per element). Shapes: the
+    # 16-wave kernel (d = 44, 600 queries), the 8-wave one (d = 52), the 2-wave one.
+    bg, h, nk = 2, 2, 3000
+    kv = make_cache(bg, nk, h, d, cuda, seed=41)
+    ramp = torch.linspace(0.05, 1.0, nk, device=cuda).view(1, nk, 1, 1, 1)
+    kv = (kv.float() * ramp).to(kv.dtype)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, h, d, cuda, seed=41, gain=3.0)
+    lse = torch.empty(bg, h, nq, device=cuda)
+    got = nori_amd.icl_attention(q, codes, scales, lse=lse)
+    values = codes.double() * scales.double()
+    exp, exp_lse = reference(q, values)
+    check(got, exp)
+    assert torch.isfinite(lse).all()
+    assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, 1)).all()
+
+
 def test_merge_of_two_halves_equals_one_call(cuda):
     bg, h, nq, nk, d = 2, 4, 50, 300, 56
     kv = make_cache(bg, nk, 1, d, cuda, seed=31)

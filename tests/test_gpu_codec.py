@@ -113,6 +113,21 @@ def test_dequantize_bit_exact(cuda, dtype):
     assert np.array_equal(raw.view(np.uint8), exp.view(np.uint8))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 7, 2, 1, 20), (3, 33, 2, 2, 16), (2, 50, 2, 8, 44), (1, 9, 2, 3, 56), (2, 5, 2, 1, 128), (1, 11, 2, 2, 8)])
+def test_dequantize_widths_and_row_slices(cuda, dtype, shape):
+    # every head width class of the dequantizer (16-byte chunks that straddle two vectors, a
+    # partial last chunk, widths below one chunk), whole tensors and row-slice views (two-level
+    # addressing with an outer stride), against torch's own expression on the same device
+    t = outlier_cache(shape, torch.float32, cuda, seed=shape[-1])
+    q, s = torch_reference(t)
+    got = nori_amd.dequantize_int8(q, s, dtype)
+    assert torch.equal(got.cpu(), (q.float() * s).to(dtype).cpu())
+    rows = slice(1, shape[1] - 1) if shape[1] > 2 else slice(0, shape[1])
+    got_rows = nori_amd.dequantize_int8(q[:, rows], s[:, rows], dtype)
+    assert torch.equal(got_rows.cpu(), (q[:, rows].float() * s[:, rows]).to(dtype).cpu())
+
+
 def test_row_slices_into_preallocated_storage_equal_whole_tensor(cuda):
     # reference tests/test_blockwise_context_attention.py:31-61 and test_kv_cache_scaling.py:60-78
     kv = outlier_cache((3, 257, 2, 4, 44), torch.float16, cuda, seed=9)
