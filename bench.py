@@ -59,6 +59,11 @@ def parse_args():
     p.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     p.add_argument("--cpu-sample-queries", type=int, default=512, help="query rows of the CPU attention sample")
     p.add_argument(
+        "--streamed", action="store_true",
+        help="measure the host-streamed long-context path instead: one layer's int8 cache in pinned host "
+        "blocks, one 1024-row query batch, block copies overlapped with attention vs serialized",
+    )
+    p.add_argument(
         "--probe-traffic", action="store_true",
         help="run a 1 GiB device copy (counter calibration), one quantize, one attention and one dequantize "
         "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
@@ -85,6 +90,58 @@ def probe_traffic(torch, dev):
         _dequantize_into(codes, scales, out)
     torch.cuda.synchronize()
     print("traffic probe: 2 x (1 GiB copy, quantize, attention, dequantize) done", flush=True)
+
+
+def streamed(torch, dev, args, block_rows=8192):
+    """Host-streamed long-context attention (BlockwiseSeqKV offloaded, layer.py:841-934): the
+    PCIe-inclusive rate. The layer's int8 cache lives in pinned host blocks of block_rows rows;
+    each query batch stages every block to the device. Prints one JSON line."""
+    import nori_amd
+    from nori_amd import attention as attn
+    from nori_amd.kv_cache_scaling import BlockwiseSeqKV
+
+    g = torch.Generator(device=dev).manual_seed(2)
+    kv = torch.randn((GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    cache = BlockwiseSeqKV.from_row_slices(
+        (kv[:, a : a + block_rows] for a in range(0, CONTEXT_ROWS, block_rows)), 1, GROUPS, quantize=True,
+        device=dev, dtype=kv.dtype, offload=True,
+    )
+    del kv
+    q = torch.randn((GROUPS, QUERY_ROWS, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    host_bytes = cache.host_bytes()
+
+    def serialized():
+        out = torch.zeros((GROUPS, QUERY_ROWS, HEADS, HEAD_DIM), dtype=torch.float32, device=dev)
+        lse = torch.full((GROUPS, HEADS, QUERY_ROWS), float("-inf"), dtype=torch.float32, device=dev)
+        for payload, scales in cache.iter_payload_blocks():
+            nori_amd.icl_attention(q, payload, scales, out=out, lse=lse, merge=True)
+        return out
+
+    def overlapped():
+        return attn.compute_attention_blockwise(q, cache)
+
+    results = {}
+    for name, fn in (("serialized", serialized), ("overlapped", overlapped)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / args.steps
+        results[name] = {
+            "ms_per_query_batch": round(sec * 1e3, 3),
+            "query_rows_per_s": round(QUERY_ROWS / sec, 1),
+            "h2d_GBps": round(host_bytes / sec / 1e9, 2),
+        }
+    print(json.dumps({
+        "streamed": {
+            "workload": f"one nori-30m layer, {CONTEXT_ROWS}-row int8 context in pinned host blocks of {block_rows} "
+            f"rows, {QUERY_ROWS} query rows x {GROUPS} token groups x {HEADS} heads",
+            "host_bytes_per_query_batch": host_bytes,
+            **results,
+        }
+    }), flush=True)
 
 
 def build_workload(torch, layers, dev):
@@ -133,6 +190,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.probe_traffic:
         probe_traffic(torch, dev)
+        return
+    if args.streamed:
+        streamed(torch, dev, args)
         return
     layers = args.layers
     kv, codes, scales, wq, wo, queries = build_workload(torch, layers, dev)

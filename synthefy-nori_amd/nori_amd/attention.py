@@ -148,8 +148,68 @@ def compute_attention_blockwise(q: torch.Tensor, kv_cache: BlockwiseSeqKV, *, sd
         return icl_attention(q, payload, scales, scale=scale)
     running_output = torch.zeros((batch_groups, n_query, n_heads, head_dim), dtype=torch.float32, device=q.device)
     running_lse = torch.full((batch_groups, n_heads, n_query), float("-inf"), dtype=torch.float32, device=q.device)
-    for payload, scales in kv_cache.iter_payload_blocks():
+    _streamed_scan(q, kv_cache, scale, running_output, running_lse)
+    return running_output.to(q.dtype)
+
+
+_COPY_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _copy_stream(device: torch.device) -> torch.cuda.Stream:
+    """One host-to-device staging stream per device, at the default priority."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _COPY_STREAMS:
+        _COPY_STREAMS[idx] = torch.cuda.Stream(device=device)
+    return _COPY_STREAMS[idx]
+
+
+def _streamed_scan(q, kv_cache: BlockwiseSeqKV, scale: float, running_output, running_lse) -> None:
+    """Scan the host blocks of an offloaded cache with the copy of block i+1 overlapping the
+    attention over block i (layer.py:841-934 stages and computes each block in turn).
+
+    Blocks are copied on a staging stream into two device slots sized for the largest block;
+    the compute stream waits for a block's copy, and the staging stream waits for the compute
+    on a slot before overwriting it. Host blocks built from device slices are pinned, so the
+    copies run asynchronously; from pageable memory they are synchronous and merely correct.
+    """
+    device = q.device
+    compute = torch.cuda.current_stream(device)
+    copier = _copy_stream(device)
+    blocks = kv_cache.host_blocks()
+    kv_cache.max_staged_rows = 0
+    if not blocks:
+        return
+    batch_groups = q.shape[0]
+    first_payload, first_scale = blocks[0]
+    row_elems = math.prod(first_payload.shape[2:])
+    cap = batch_groups * kv_cache.max_block_rows * row_elems
+    slots = [torch.empty(cap, dtype=first_payload.dtype, device=device) for _ in range(2)]
+    scale_slots = None
+    if first_scale is not None:
+        scale_cap = batch_groups * kv_cache.max_block_rows * math.prod(first_scale.shape[2:])
+        scale_slots = [torch.empty(scale_cap, dtype=torch.float32, device=device) for _ in range(2)]
+    for t in slots + (scale_slots or []):
+        t.record_stream(copier)  # used on the staging stream as well
+    released: list[torch.cuda.Event | None] = [None, None]
+    copier.wait_stream(compute)  # queries, outputs and slots exist before the first copy
+    for i, (payload, stored_scale) in enumerate(blocks):
         if payload.ndim != 5 or payload.shape[0] != batch_groups:
             raise ValueError(f"streamed K/V block must be [BG, K, 2, Hkv, D], got {tuple(payload.shape)}")
-        icl_attention(q, payload, scales, scale=scale, out=running_output, lse=running_lse, merge=True)
-    return running_output.to(q.dtype)
+        j = i % 2
+        with torch.cuda.stream(copier):
+            if released[j] is not None:
+                copier.wait_event(released[j])
+            staged = slots[j][: payload.numel()].view(payload.shape)
+            staged.copy_(payload, non_blocking=True)
+            staged_scale = None
+            if stored_scale is not None:
+                staged_scale = scale_slots[j][: stored_scale.numel()].view(stored_scale.shape)
+                staged_scale.copy_(stored_scale, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(copier)
+        compute.wait_event(ready)
+        kv_cache.max_staged_rows = max(kv_cache.max_staged_rows, int(payload.shape[1]))
+        icl_attention(q, staged, staged_scale, scale=scale, out=running_output, lse=running_lse, merge=True)
+        done = torch.cuda.Event()
+        done.record(compute)
+        released[j] = done

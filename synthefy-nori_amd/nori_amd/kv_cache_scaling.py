@@ -464,6 +464,13 @@ class BlockwiseSeqKV:
         """Yield (payload, scale-or-None) blocks on the compute device without dequantizing."""
         yield from self._staged_blocks(block_rows)
 
+    def host_blocks(self) -> list[tuple[torch.Tensor, torch.Tensor | None]]:
+        """The stored (payload, scale-or-None) blocks of a host-offloaded cache, in row order: the
+        source of the overlapped streamed scan, which stages them itself."""
+        if not self.offloaded:
+            raise RuntimeError("host_blocks() is for host-offloaded caches; use resident_payload()")
+        return list(self._blocks)
+
     def resident_payload(self) -> tuple[torch.Tensor, torch.Tensor] | None:
         """The whole resident int8 payload and scales, when the cache is device resident."""
         if self.offloaded or self._storage is None:

@@ -248,6 +248,36 @@ def test_blockwise_cache_paths(cuda, offload):
         assert cache.max_staged_rows == 316 and cache.resident_gpu_bytes() == 0
 
 
+@pytest.mark.parametrize("quantize", [True, False])
+def test_streamed_scan_overlaps_many_blocks(cuda, quantize):
+    # 13 host blocks (the last ragged) through the two staging slots: block i+1 is copied on the
+    # staging stream while block i is attended; every slot is reused several times. The merged
+    # result equals one launch over the same cache up to fp32 merge rounding, and a second scan
+    # of the same cache gives the same bits.
+    bg, h, nq, d, rows = 2, 2, 300, 44, 256
+    nk = 12 * rows + 77
+    kv = make_cache(bg, nk, h, d, cuda, seed=43)
+    bounds = [(a, min(a + rows, nk)) for a in range(0, nk, rows)]
+    cache = BlockwiseSeqKV.from_row_slices(
+        (kv[:, a:b] for a, b in bounds), 1, bg, quantize=quantize, device=cuda, dtype=kv.dtype, offload=True,
+    )
+    assert len(cache.host_blocks()) == len(bounds) == 13 and cache.resident_gpu_bytes() == 0
+    q = make_queries(bg, nq, h, d, cuda, seed=43)
+    got = nori_amd.compute_attention_blockwise(q, cache)
+    again = nori_amd.compute_attention_blockwise(q, cache)
+    assert torch.equal(got, again) and cache.max_staged_rows == rows
+    if quantize:
+        codes, scales = nori_amd.quantize_int8(kv)
+        whole = nori_amd.icl_attention(q, codes, scales)
+        values = codes.double() * scales.double()
+    else:
+        whole = nori_amd.icl_attention(q, kv)
+        values = kv
+    torch.testing.assert_close(got.float(), whole.float(), rtol=1e-2, atol=2e-3)
+    exp, _ = reference(q, values)
+    check(got, exp)
+
+
 def test_config2_attention(cuda):
     # isolated nori-6m ICL block: BG=9, 1024 queries over 4096 int8 context rows, H=2, D=64, bf16
     g = torch.Generator().manual_seed(1)
