@@ -141,6 +141,35 @@ int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32
                        int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/*
+ * Fused context-cache write: K/V projection of context rows straight into the int8 cache.
+ * Replaces MultiheadAttention.project_kv_cache (src/synthefy_nori/model/layer.py:651-683)
+ * followed by quantize_int8 (kv_cache_scaling.py:29-37) on the GPU's autocast path, with the
+ * layer's RMSNorm (layer.py:251-253, without an elementwise weight) optionally applied first:
+ *     xn = norm ? T(x * rsqrt(mean(x^2) + eps)) : x          (T = x_dtype)
+ *     kv[r, j*d + e] = f16( f16(xn[r]) . f16(weight[j*d + e]) )  (fp32 accumulation)
+ *     codes, scales = quantize_int8(kv) with T = fp16 and the scale formed per `scale_div`
+ * Rows sit on a two-level grid, row (o, i) for o < n_outer, i < n_inner (a row slice of a
+ * [BG, N, ...] cache, or activations read group by group, in one call):
+ * x      : embed elements at x + o*x_outer_stride + i*x_row_stride (elements), x_dtype
+ *          NORI_F32 / NORI_F16 / NORI_BF16;
+ * weight : [2*kv_heads*d, embed] at weight + k*w_row_stride (K heads, then V heads: the
+ *          reference's qkv_proj_weight[1:] viewed as [2*H*D, E], or its first head for a
+ *          shared-head cache);
+ * codes  : [2, kv_heads, d] int8 at codes + o*codes_outer_stride + i*codes_row_stride (bytes);
+ * scales : [2, kv_heads] fp32 at scales + o*scales_outer_stride + i*scales_row_stride (floats).
+ * Rows of x and weight must be 16-byte aligned and a whole number of 16-byte chunks; code
+ * rows 4-byte aligned; d a multiple of 4 (at most 256). The fp16 K/V are never written.
+ * The projection's fp32 sums run in MFMA order, not the library GEMM's, so a K/V value can
+ * differ from torch's fp16 F.linear in its last bit and its code by one.
+ */
+int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t n_outer, int64_t n_inner, int32_t embed,
+                                  int64_t x_outer_stride, int64_t x_row_stride, int32_t norm, float eps,
+                                  const void* weight, int weight_dtype, int64_t w_row_stride, int32_t kv_heads,
+                                  int32_t d, int8_t* codes, int64_t codes_outer_stride, int64_t codes_row_stride,
+                                  float* scales, int64_t scales_outer_stride, int64_t scales_row_stride,
+                                  int32_t scale_div, void* stream);
+
 /* Bytes of workspace nori_icl_attention uses for these sizes (0 when it never splits). */
 int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk);
 

@@ -26,6 +26,7 @@
 #include <algorithm>
 
 #include "nori_common.h"
+#include "quant_common.h"
 
 // torch rounds the result of every op separately; no multiply-add is fused here unless
 // the source writes fmaf. (Narrowing conversions are kept apart by pin_f32.)
@@ -34,71 +35,10 @@
 namespace {
 
 using namespace nori;
+using namespace nori::quant;
 
 constexpr int kTileThreads = 256;
 constexpr int kMaxTileVectorBytes = 128;  // keeps the tile under 48 KiB of LDS; longer vectors use the direct kernel
-
-template <int DT> struct Storage;
-template <> struct Storage<NORI_F32> { using T = uint32_t; };
-template <> struct Storage<NORI_F16> { using T = uint16_t; };
-template <> struct Storage<NORI_BF16> { using T = uint16_t; };
-
-template <int DT>
-__device__ __forceinline__ float bits_to_f32(typename Storage<DT>::T b) {
-    if constexpr (DT == NORI_F32) return __uint_as_float(b);
-    else if constexpr (DT == NORI_F16) return f16_to_f32(b);
-    else return bf16_to_f32(b);
-}
-
-// |x| as an unsigned key whose integer order is the float order with NaN on top, so an
-// integer max is a NaN-propagating absmax (torch's amax propagates NaN).
-template <int DT>
-__device__ __forceinline__ uint32_t abs_key(typename Storage<DT>::T b) {
-    if constexpr (DT == NORI_F32) return b & 0x7fffffffu;
-    else return (uint32_t)b & 0x7fffu;
-}
-
-struct VectorScale {
-    float s;     // scale in T, widened to fp32
-    float y;     // RN(1/s)
-    bool fast;   // Markstein quotient valid for this vector
-};
-
-template <int DT>
-__device__ __forceinline__ VectorScale make_scale(uint32_t max_key, int scale_div) {
-    const float m = bits_to_f32<DT>((typename Storage<DT>::T)max_key);
-    const float floor_t = round_to<DT>((float)1e-12);  // clamp_min(1e-12) in T
-    const float m2 = (m != m) ? m : fmaxf(m, floor_t);
-    float s;
-    if (scale_div == NORI_SCALE_DIV_RECIP) s = round_to<DT>(m2 * (1.0f / 127.0f));
-    else s = round_to<DT>(m2 / 127.0f);
-    VectorScale vs;
-    vs.s = s;
-    vs.y = 1.0f / s;
-    // Outside [2^-96, 2^96] the residual fma(-q0, s, t) may be subnormal and inexact.
-    vs.fast = s >= 0x1p-96f && s <= 0x1p96f;
-    return vs;
-}
-
-// Code of one element; `t` is finite whenever vs.fast holds (|t| <= amax < inf).
-template <int DT>
-__device__ __forceinline__ int code_of(float t, const VectorScale& vs) {
-    if (vs.fast) {
-        const float q0 = t * vs.y;
-        const float r = fmaf(-q0, vs.s, t);
-        const float q = fmaf(r, vs.y, q0);
-        const float k = rintf(round_to<DT>(q));
-        return (int)__builtin_amdgcn_fmed3f(k, -127.0f, 127.0f);
-    }
-    const float k = rintf(round_to<DT>(t / vs.s));
-    if (k != k) return 0;  // NaN -> 0, the GPU's float->int conversion of NaN
-    return (int)fminf(fmaxf(k, -127.0f), 127.0f);
-}
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-           ((uint32_t)(d & 0xff) << 24);
-}
 
 // Cooperative global -> LDS copy of `nbytes` (a multiple of `elem` bytes).
 __device__ __forceinline__ void copy_in(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g, int nbytes,

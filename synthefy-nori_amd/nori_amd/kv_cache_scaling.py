@@ -166,6 +166,20 @@ def quantize_int8(t: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return codes, scale
 
 
+def _quantize_slice(kv_slice) -> tuple[torch.Tensor, torch.Tensor]:
+    """Codes and scales of a projected row slice, or of a ``FusedKVRows`` slice that is projected
+    and quantized by one kernel (nori_amd.kv_project)."""
+    if isinstance(kv_slice, torch.Tensor):
+        return quantize_int8(kv_slice)
+    return kv_slice.quantize()
+
+
+def _projected(kv_slice) -> torch.Tensor:
+    if isinstance(kv_slice, torch.Tensor):
+        return kv_slice
+    raise TypeError("a fused projection slice only builds an int8 cache (quantize=True)")
+
+
 def dequantize_int8(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """(q.float() * scale).to(dtype) -- reference kv_cache_scaling.py:40-41."""
     if dtype not in (torch.float32, torch.float16, torch.bfloat16):
@@ -270,11 +284,11 @@ class ScalableSeqKV:
             if device is None:
                 device = kv_slice.device
             if quantize:
-                q, scale = quantize_int8(kv_slice)
+                q, scale = _quantize_slice(kv_slice)
                 q_parts.append(q if store is None else q.to(store))
                 scale_parts.append(scale if store is None else scale.to(store))
             else:
-                kv_parts.append(kv_slice if store is None else kv_slice.to(store))
+                kv_parts.append(_projected(kv_slice) if store is None else _projected(kv_slice).to(store))
         if not (q_parts or kv_parts):
             raise ValueError("from_row_slices got no slices; nothing to cache")
 
@@ -399,7 +413,10 @@ class BlockwiseSeqKV:
                     raise ValueError(f"row slices exceed declared n_rows={n_rows}")
                 payload_view = payload_storage[:, offset:end]
                 scale_view = scale_storage[:, offset:end]
-                _quantize_into(kv_slice.to(target_device), payload_view, scale_view)
+                if isinstance(kv_slice, torch.Tensor):
+                    _quantize_into(kv_slice.to(target_device), payload_view, scale_view)
+                else:
+                    kv_slice.quantize_into(payload_view, scale_view)
                 blocks.append((payload_view, scale_view))
                 offset = end
 
@@ -426,11 +443,11 @@ class BlockwiseSeqKV:
             if dtype is None:
                 dtype = kv_slice.dtype
             if quantize:
-                payload, scale = quantize_int8(kv_slice)
+                payload, scale = _quantize_slice(kv_slice)
                 blocks.append((_to_host(payload), _to_host(scale)))
                 del payload, scale
             else:
-                blocks.append((_to_host(kv_slice.detach()), None))
+                blocks.append((_to_host(_projected(kv_slice).detach()), None))
             del kv_slice
         if dtype is None:
             raise ValueError("from_row_slices got no slices; nothing to cache")

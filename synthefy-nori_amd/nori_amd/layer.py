@@ -35,6 +35,7 @@ import torch.nn as nn
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .attention import attend_dense, compute_attention_blockwise, icl_attention
+from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
 from .norm import RMSNorm
 
@@ -132,6 +133,30 @@ class MLP(nn.Module):
 
     def forward(self, x):
         return self.mlp(x)
+
+
+def _fused_cache_write(attn_mod, norm, copy_kv: bool, device: torch.device):
+    """(weight, kv_heads, head_dim, norm_eps) for writing ``attn_mod``'s int8 cache rows with
+    ``kv_project.project_quantize_kv``, or None where that kernel does not compute what the
+    separate steps would: it needs the fp16 autocast of GPU inference (the projection's
+    dtype) and a row norm that is absent or an RMSNorm without an elementwise weight.
+    """
+    if not kv_project.fp16_autocast(device) or attn_mod.qkv_combined:
+        return None
+    embed = attn_mod.embed_dim
+    if norm is None:
+        eps = None
+    elif isinstance(norm, RMSNorm) and norm.weight is None and tuple(norm.normalized_shape) == (embed,):
+        eps = float(norm.eps)
+    else:
+        return None
+    w = attn_mod.qkv_proj_weight[1:]  # [2, H, D, E]
+    if copy_kv:
+        # the shared-head cache projects with the first head only (layer.py:667-675)
+        weight, heads = w[:, :1].reshape(2 * attn_mod.head_dim, embed).contiguous(), 1
+    else:
+        weight, heads = w.reshape(2 * attn_mod.num_heads * attn_mod.head_dim, embed), attn_mod.num_heads
+    return weight, heads, attn_mod.head_dim, eps
 
 
 class MultiheadAttention(nn.Module):
@@ -516,12 +541,18 @@ class EncoderBaseLayer(nn.Module):
         n_rows = x_kv_src.shape[1]
         batch, groups = x_kv_src.shape[0], x_kv_src.shape[2]
         compute_device = torch.device(device) if device is not None else attn_mod.qkv_proj_weight.device
+        fused = _fused_cache_write(attn_mod, norm, copy_kv, compute_device) if quantize else None
 
         def row_slices():
             for r0 in range(0, n_rows, row_chunk):
                 rows = x_kv_src[:, r0 : min(r0 + row_chunk, n_rows)]
                 if rows.device != compute_device:
                     rows = rows.to(compute_device)
+                if fused is not None and kv_project.fusable(rows, fused[0], attn_mod.head_dim):
+                    # norm, projection and quantizer in one kernel; the fp16 K/V never reach HBM
+                    yield kv_project.FusedKVRows(rows.transpose(1, 2), *fused)
+                    del rows
+                    continue
                 if norm is not None:
                     rows = norm(rows)
                 projected = attn_mod.project_kv_cache(rows.transpose(1, 2), copy_first_head_kv=copy_kv)["kv"]

@@ -33,6 +33,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_rms_norm",
             "nori_icl_attention",
             "nori_icl_attention_workspace_size",
+            "nori_kv_project_quantize_int8",
         ]
     )
 
@@ -72,6 +73,21 @@ def test_argument_errors_map_to_reference_exceptions():
     args[5], args[12] = 64, 0
     assert lib.nori_icl_attention(*args) == nat.NORI_ERR_INVALID
     assert b"empty" in lib.nori_last_error()
+    # fused projection + quantize: bad shape, head width not a multiple of 4, unknown dtype
+    proj = [None, nat.NORI_F32, 1, 8, 64, 0, 64, 0, 0.0, None, nat.NORI_F32, 64, 2, 16,
+            None, 0, 64, None, 0, 4, nat.SCALE_DIV_RECIP, None]
+    bad = list(proj); bad[13] = 0
+    assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_ERR_INVALID
+    bad = list(proj); bad[13] = 18
+    assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"head width" in lib.nori_last_error()
+    bad = list(proj); bad[1] = nat.NORI_I8
+    assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(proj); bad[20] = 7
+    assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_ERR_INVALID
+    bad = list(proj); bad[2] = 0
+    assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_kv_project_quantize_int8(*proj) == nat.NORI_ERR_INVALID  # null pointers
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
@@ -89,3 +105,16 @@ def test_operators_refuse_cpu_tensors():
         nori_amd.rms_norm(torch.randn(4, 8), 8)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         nori_amd.icl_attention(torch.randn(2, 3, 1, 8), t)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        nori_amd.project_quantize_kv(torch.randn(5, 32), torch.randn(64, 32), 2, 16)
+
+
+def test_fused_projection_shape_errors():
+    import torch
+
+    import nori_amd
+
+    with pytest.raises(ValueError, match="weight"):
+        nori_amd.project_quantize_kv(torch.randn(5, 32), torch.randn(60, 32), 2, 16)
+    with pytest.raises(ValueError, match="embed width"):
+        nori_amd.project_quantize_kv(torch.randn(5, 48), torch.randn(64, 32), 2, 16)
