@@ -19,7 +19,8 @@ dense fp16/bf16 MFMA at 2.5 PFLOP/s), measured with HIP events on the launch str
 around each attention call (its kernel and, when the context is split, the merge of
 the partials), the same for the quantize kernel against 8 TB/s of HBM, the HBM traffic
 per launch measured by rocprofv3 counters (profiles/traffic_nori30m_64k.md, when
-present), and the CPU baseline: the oracle (quantizer in C, attention as the
+present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes) of one
+layer against the unfused sequence it replaces, and the CPU baseline: the oracle (quantizer in C, attention as the
 reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
 bounded sample of the same work.
 """
@@ -67,6 +68,11 @@ def parse_args():
         "--probe-traffic", action="store_true",
         help="run a 1 GiB device copy (counter calibration), one quantize, one attention and one dequantize "
         "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
+    )
+    p.add_argument(
+        "--cache-write", action="store_true",
+        help="measure only the fused context-cache write of one layer against the unfused sequence "
+        "(also the command its rocprofv3 trace and counters are taken with)",
     )
     return p.parse_args()
 
@@ -156,6 +162,63 @@ def build_workload(torch, layers, dev):
     return kv, codes, scales, wq, wo, queries
 
 
+def cache_write(torch, dev, codes, scales, reps=5):
+    """One layer's cross-cache write at this workload, from the layer's fp32 context rows
+    [1, 65536, 33, 352]: the fused path (operand-row pass + projection/quantizer kernel,
+    nori_amd.project_quantize_kv) against the unfused one it replaces (HIP RMSNorm, torch's
+    fp16-autocast F.linear, HIP quantizer), each timed with HIP events on the launch stream.
+    Both write `codes` / `scales` [33, 65536, 2, 8, 44]."""
+    import nori_amd
+    from nori_amd.kv_cache_scaling import _quantize_into
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(1, CONTEXT_ROWS, GROUPS, EMBED, generator=g, device=dev)
+    w = torch.randn(2 * HEADS * HEAD_DIM, EMBED, generator=g, device=dev) * EMBED ** -0.5
+    xt = x.transpose(1, 2)
+    out = (codes.view(1, GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM), scales.view(1, GROUPS, CONTEXT_ROWS, 2, HEADS, 1))
+    stream = torch.cuda.current_stream(dev)
+
+    def fused():
+        nori_amd.project_quantize_kv(xt, w, HEADS, HEAD_DIM, norm_eps=1e-5, out=out)
+
+    def unfused():
+        xn = nori_amd.rms_norm(x, EMBED, None, 1e-5)
+        with torch.autocast("cuda", dtype=torch.float16):
+            kv = torch.nn.functional.linear(xn.transpose(1, 2).reshape(GROUPS, CONTEXT_ROWS, EMBED), w)
+        _quantize_into(kv.view(GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM), codes, scales)
+
+    def avg_ms(fn):
+        fn()
+        ev = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            ev.append((e0, e1))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / reps
+
+    fused_ms, unfused_ms = avg_ms(fused), avg_ms(unfused)
+    rows = GROUPS * CONTEXT_ROWS
+    n_kv = rows * 2 * HEADS * HEAD_DIM
+    # algorithmic HBM bytes of the fused pair: x read, f16 operand rows written and read,
+    # codes + scales written
+    fused_bytes = rows * EMBED * 4 + 2 * rows * EMBED * 2 + n_kv + 4 * rows * 2 * HEADS
+    del x, xt
+    return {
+        "what": "one layer's int8 cross-cache write from fp32 context rows: RMSNorm -> K/V projection "
+        "(fp16 operands, fp32 sums) -> exact int8 quantizer, 33 x 65536 rows, embed 352 -> 2 x 8 x 44",
+        "fused_ms": round(fused_ms, 4),
+        "unfused_ms": round(unfused_ms, 4),
+        "speedup": round(unfused_ms / fused_ms, 3),
+        "fused_algorithmic_bytes": fused_bytes,
+        "fused_GBps": round(fused_bytes / fused_ms / 1e6, 1),
+        "fused_TFLOPs": round(2.0 * rows * EMBED * 2 * HEADS * HEAD_DIM / fused_ms / 1e9, 1),
+    }
+
+
 def measured_traffic():
     """HBM bytes per launch of the attention and quantize kernels from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -190,6 +253,12 @@ def main():
     torch.cuda.set_device(dev)
     if args.probe_traffic:
         probe_traffic(torch, dev)
+        return
+    if args.cache_write:
+        shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
+        codes = torch.empty(shape, dtype=torch.int8, device=dev)
+        scales = torch.empty(shape[:-1] + (1,), dtype=torch.float32, device=dev)
+        print(json.dumps(cache_write(torch, dev, codes, scales)), flush=True)
         return
     if args.streamed:
         streamed(torch, dev, args)
@@ -249,6 +318,8 @@ def main():
         timed(f, dq_events) if i else f()
     torch.cuda.synchronize()
     dequant_ms = [a.elapsed_time(b) for a, b in dq_events]
+    del dq_out
+    write = cache_write(torch, dev, codes[0], scales[0])
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -322,6 +393,7 @@ def main():
             "launches": len(dequant_ms),
         },
     }
+    line["cache_write"] = write
     if args.cpu_baseline == "on":
         line["cpu_baseline"] = cpu_baseline(torch, kv[0], codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)

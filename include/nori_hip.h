@@ -159,7 +159,9 @@ int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32
  * codes  : [2, kv_heads, d] int8 at codes + o*codes_outer_stride + i*codes_row_stride (bytes);
  * scales : [2, kv_heads] fp32 at scales + o*scales_outer_stride + i*scales_row_stride (floats).
  * Rows of x and weight must be 16-byte aligned and a whole number of 16-byte chunks; code
- * rows 4-byte aligned; d a multiple of 4 (at most 256). The fp16 K/V are never written.
+ * rows 4-byte aligned; d a multiple of 4 up to 128; embed at most 1024. The fp16 K/V are never
+ * written.
+ * workspace: see nori_kv_project_quantize_int8_workspace_size.
  * The projection's fp32 sums run in MFMA order, not the library GEMM's, so a K/V value can
  * differ from torch's fp16 F.linear in its last bit and its code by one.
  */
@@ -168,7 +170,13 @@ int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t n_outer, i
                                   const void* weight, int weight_dtype, int64_t w_row_stride, int32_t kv_heads,
                                   int32_t d, int8_t* codes, int64_t codes_outer_stride, int64_t codes_row_stride,
                                   float* scales, int64_t scales_outer_stride, int64_t scales_row_stride,
-                                  int32_t scale_div, void* stream);
+                                  int32_t scale_div, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of (16-byte aligned) workspace nori_kv_project_quantize_int8 needs: the f16 operand
+ * rows, n_outer*n_inner rows of embed rounded up to 32 -- 0 when x is used as it is (fp16, no
+ * norm, embed a multiple of 32). Written and read within the call's stream order. */
+int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_outer, int64_t n_inner, int32_t embed,
+                                                     int32_t norm);
 
 /* Bytes of workspace nori_icl_attention uses for these sizes (0 when it never splits). */
 int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk);

@@ -8,18 +8,23 @@
 //                                                          autocast path: f16 operands, fp32
 //                                                          accumulation, one rounding)
 //   codes, scale = quantize_int8(kv)  in f16             (kv_cache_scaling.py:29-37, exact)
-// so the fp16 K/V of the layer never exist in HBM: the projection is rounded in LDS and
-// quantized there.
+// The fp16 K/V never exist in memory: each projected head vector is rounded and quantized in
+// registers.
 //
-// Schedule. Persistent workgroups of 4 wavefronts. A workgroup owns a group of `hg` cache
-// heads: their weight rows, each padded to a multiple of 16 with zero rows, stay in LDS as f16
-// for the whole launch; it walks row blocks of 64 context rows. Per block, the x tile is
-// loaded (and normalized) into LDS as f16; each wavefront projects 16 rows onto the group's
-// heads with v_mfma_f32_16x16x32_f16 (the embed width in steps of 32), rounds its 16 x (hg*dp)
-// results to f16 into its own LDS tile, and quantizes its 16*hg head vectors from there
-// (lanes split each vector; the absmax is exchanged with lane shuffles), staging the codes in
-// LDS for coalesced stores. Workgroups are numbered so the head groups of one row block sit
-// on one XCD and share its L2 for the x rows.
+// Two kernels.
+// * operand rows (unless x is already f16 operands: f16, no norm, embed a multiple of 32):
+//   one wavefront per row normalizes it and writes f16(xn) to a workspace row padded with
+//   zeros to a multiple of 32 -- the cast the autocast path makes before its GEMM, with the
+//   norm folded in.
+// * projection + quantizer: persistent workgroups of 4 wavefronts, two per CU. A workgroup
+//   owns a group of `hg` cache heads: their weight rows, each head padded with zero rows to
+//   16 * MT, stay in LDS as f16 for the whole launch. It walks blocks of 4 * 16 * NR rows;
+//   each wavefront loads its 16 * NR operand rows straight into v_mfma_f32_16x16x32_f16 B
+//   operands (lane n + 16*(k/8) holds row n, elements 8*(k/8)..+8 of every 32-wide step).
+//   Per head, the MFMAs compute the transposed projection W_j . x^T, whose result layout gives
+//   every lane four consecutive K/V columns of one row: the head's absmax is a per-lane max and
+//   two shuffles, and the four codes leave as one 32-bit store. Workgroups are numbered so the
+//   head groups of one row block sit on one XCD and share its L2 for the operand rows.
 #include <math.h>
 
 #include <algorithm>
@@ -36,100 +41,195 @@ using namespace nori::quant;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kBM = 64;             // context rows per block (16 per wavefront)
-constexpr int kRowThreads = kThreads / kBM;  // threads that load one x row
+constexpr int kWgPerCu = 2;  // resident workgroups per CU when the weight tile fits half the LDS
+constexpr size_t kLds = 160 * 1024;
+constexpr int kPrepWaves = 4;
 
-// Rows are addressed on a two-level grid, row r = o * n_inner + i (o < n_outer, i < n_inner):
-// x at o * x_outer + i * x_row elements, codes at o * codes_outer + i * codes_row bytes, scales at
-// o * scales_outer + i * scales_row floats -- so a slice of rows of a [BG, N, ...] cache, or the
-// rows of a [N, G, E] activation read group by group, is one launch.
-struct ProjArgs {
-    const void* x; int64_t rows, n_inner; int embed; int64_t x_outer, x_row;  // x rows of embed elements
+// Rows are addressed on a two-level grid, row r = o * n_inner + i (o < n_outer, i < n_inner).
+struct Grid {
+    int64_t rows, n_inner;
+};
+
+__device__ __forceinline__ uint4 load16(const void* base, int64_t byte_off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(base) + byte_off);
+}
+
+// the elements of one raw 16-byte chunk of dtype DT as f32 (4 for fp32, 8 for 16-bit types)
+template <int DT>
+__device__ __forceinline__ void unpack(const uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == NORI_F32) {
+            f[k] = __uint_as_float(w[k]);
+        } else if constexpr (DT == NORI_F16) {
+            f[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffff));
+            f[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
+        } else {
+            f[2 * k] = __uint_as_float(w[k] << 16);
+            f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        }
+    }
+}
+
+template <int DT> constexpr int chunk_elems() { return DT == NORI_F32 ? 4 : 8; }
+
+// ------------------------------------------------------------------ operand rows
+struct PrepArgs {
+    const void* x; Grid grid; int embed; int64_t x_outer, x_row;  // x strides in elements
     int norm; float eps;
-    const void* w; int64_t w_stride;                            // W [2*kv_heads*d, embed]
+    _Float16* ws; int pitch;  // workspace rows of `pitch` f16 (32 * steps), dense
+};
+
+// One wavefront per row, kPrepRows rows at a time (their loads in flight together), rows in
+// contiguous runs per wavefront. Lane l holds 16-byte chunks l, l + 64, ... (at most 4: embed
+// <= 1024); the statistic is a wavefront reduction.
+constexpr int kPrepRows = 4;
+
+template <int DT>
+__global__ void __launch_bounds__(kPrepWaves * 64) prep_rows_kernel(const PrepArgs a) {
+    constexpr int EPC = chunk_elems<DT>();
+    constexpr int ES = DT == NORI_F32 ? 4 : 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * kPrepWaves;
+    const int64_t w = (int64_t)blockIdx.x * kPrepWaves + (threadIdx.x >> 6);
+    const int64_t per = (a.grid.rows + nw - 1) / nw;
+    const int64_t r_begin = w * per, r_end = std::min<int64_t>(a.grid.rows, r_begin + per);
+    if (r_begin >= r_end) return;
+    int64_t o = r_begin / a.grid.n_inner, i = r_begin - o * a.grid.n_inner;
+    const int nch = a.embed / EPC;
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += kPrepRows) {
+        uint4 v[kPrepRows][4];
+#pragma unroll
+        for (int q = 0; q < kPrepRows; ++q) {
+            const bool row_in = r0 + q < r_end;
+            const int64_t base = (o * a.x_outer + i * a.x_row) * ES;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = lane + 64 * j;
+                v[q][j] = row_in && c < nch ? load16(a.x, base + (int64_t)c * 16) : uint4{0u, 0u, 0u, 0u};
+            }
+            if (++i == a.grid.n_inner) { i = 0; ++o; }
+        }
+        float inv[kPrepRows];
+#pragma unroll
+        for (int q = 0; q < kPrepRows; ++q) {
+            inv[q] = 1.0f;
+            if (a.norm) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float f[EPC];
+                    unpack<DT>(v[q][j], f);
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) acc = fmaf(f[e], f[e], acc);
+                }
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+                inv[q] = rsqrtf(acc / (float)a.embed + a.eps);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kPrepRows; ++q) {
+            if (r0 + q >= r_end) break;
+            _Float16* dst = a.ws + (r0 + q) * a.pitch;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = lane + 64 * j;
+                if (c < nch) {
+                    float f[EPC];
+                    unpack<DT>(v[q][j], f);
+                    _Float16 h[EPC];
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e)
+                        h[e] = (_Float16)pin_f32(a.norm ? round_to<DT>(f[e] * inv[q]) : f[e]);
+                    if constexpr (EPC == 8) {
+                        *reinterpret_cast<f16x8*>(dst + c * EPC) = f16x8{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+                    } else {
+                        *reinterpret_cast<uint2*>(dst + c * EPC) =
+                            uint2{(uint32_t)__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
+                                  (uint32_t)__builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16)};
+                    }
+                }
+            }
+            // zeros from embed to the padded width, in 4-element pieces (embed is a multiple of 4)
+            for (int u = a.embed / 4 + lane; u < a.pitch / 4; u += 64) *reinterpret_cast<uint2*>(dst + 4 * u) = uint2{0u, 0u};
+        }
+    }
+}
+
+// ------------------------------------------------------------------ projection + quantizer
+struct ProjArgs {
+    const _Float16* xs; Grid grid; int64_t xs_outer, xs_row;  // f16 operand rows (elements)
+    const void* w; int wdt; int64_t w_stride;  // W [2*kv_heads*d, embed], row stride in elements
+    int embed;
     int nheads;  // 2 * kv_heads cache head vectors per row
-    int d, dp;   // head width, padded to 16
+    int d, dp;   // head width, padded with zero rows to the kernel's 16 * MT
     int hg;      // heads per group (the last group may hold fewer)
     int ngroups;
-    int ep, xp;  // embed padded to 32, LDS row pitch of the x and W tiles (f16 elements)
-    int8_t* codes; int64_t codes_outer, codes_row;  // codes: nheads*d bytes per row
+    int ksteps;  // operand steps of 32 elements in a row (its f16 row holds zeros past embed)
+    int xp;      // LDS pitch of the weight rows (f16 elements): 32 * KS + 8
+    int8_t* codes; int64_t codes_outer, codes_row;    // codes: nheads*d bytes per row
     float* scales; int64_t scales_outer, scales_row;  // scales: nheads floats per row
     int scale_div;
+    int bm;           // rows per block
     int64_t nblocks;  // row blocks
     int streams;      // workgroups per head group
 };
 
-// elements of one 16-byte chunk of dtype DT, as f32
-template <int DT>
-__device__ __forceinline__ void load_chunk(const void* base, int64_t elem, float* f) {
-    if constexpr (DT == NORI_F32) {
-        const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + elem);
-        f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
-    } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + elem);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+// Weight rows c < hg*dp of the group (zero rows in each head's padding and past the last head)
+// into the LDS tile as f16, zero-padded to the pitch. Loaded once per workgroup, eight 16-byte
+// chunks per thread in flight at a time.
+template <int WDT>
+__device__ __forceinline__ void load_weights(const ProjArgs& a, _Float16* wt, int head0, int ghe, int tid) {
+    constexpr int EPC = chunk_elems<WDT>();
+    constexpr int ES = WDT == NORI_F32 ? 4 : 2;
+    constexpr int kRowThreads = 4;
+    const int lr = tid / kRowThreads, lq = tid % kRowThreads;
+    const int nch = a.embed / EPC, pch = (a.xp - 8) / EPC;
+    for (int c = lr; c < a.hg * a.dp; c += kThreads / kRowThreads) {
+        const int hh = c / a.dp, e = c % a.dp;
+        const bool valid = hh < ghe && e < a.d;
+        const int64_t base = ((int64_t)(head0 + hh) * a.d + e) * a.w_stride * ES;
+        for (int j0 = lq; j0 < pch; j0 += kRowThreads * 8) {
+            uint4 v[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if constexpr (DT == NORI_F16) {
-                f[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffff));
-                f[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
-            } else {
-                f[2 * k] = __uint_as_float(w[k] << 16);
-                f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            for (int u = 0; u < 8; ++u) {
+                const int j = j0 + kRowThreads * u;
+                v[u] = (valid && j < nch) ? load16(a.w, base + (int64_t)j * 16) : uint4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int j = j0 + kRowThreads * u;
+                if (j < pch) {
+                    float f[EPC];
+                    unpack<WDT>(v[u], f);
+                    _Float16* dst = wt + c * a.xp + j * EPC;
+#pragma unroll
+                    for (int q = 0; q < EPC; ++q) dst[q] = (_Float16)f[q];
+                }
             }
         }
     }
 }
 
-// The row of `embed` elements at element offset `base` into an LDS row of f16, zero-padded to
-// `ep` (all zeros when !valid), optionally RMS-normalized (rounded to DT first, as RMSNorm
-// returns DT). The kRowThreads threads of a row split its 16-byte chunks and reduce the
-// statistic together.
-template <int DT>
-__device__ __forceinline__ void load_row(const void* src, int64_t base, bool valid, int embed, int ep, bool norm,
-                                         float eps, _Float16* dst, int q) {
-    constexpr int EPC = DT == NORI_F32 ? 4 : 8;  // elements per 16-byte chunk
-    const int nchunks = embed / EPC;
-    float acc = 0.0f;
-    if (norm) {
-        for (int c = q; c < nchunks; c += kRowThreads) {
-            float f[EPC];
-            if (valid) load_chunk<DT>(src, base + (int64_t)c * EPC, f);
-            else for (int e = 0; e < EPC; ++e) f[e] = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) acc = fmaf(f[e], f[e], acc);
-        }
-#pragma unroll
-        for (int off = kRowThreads / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kRowThreads);
-    }
-    const float inv = norm ? rsqrtf(acc / (float)embed + eps) : 1.0f;
-    for (int c = q; c < ep / EPC; c += kRowThreads) {
-        float f[EPC];
-        if (valid && c < nchunks) load_chunk<DT>(src, base + (int64_t)c * EPC, f);
-        else for (int e = 0; e < EPC; ++e) f[e] = 0.0f;
-        _Float16 h[EPC];
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) h[e] = (_Float16)pin_f32(norm ? round_to<DT>(f[e] * inv) : f[e]);
-        if constexpr (EPC == 8) {
-            *reinterpret_cast<f16x8*>(dst + c * EPC) = f16x8{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
-        } else {
-            *reinterpret_cast<f16x2*>(dst + c * EPC) = f16x2{h[0], h[1]};
-            *reinterpret_cast<f16x2*>(dst + c * EPC + 2) = f16x2{h[2], h[3]};
-        }
+// Row r0 + off on the two-level grid, given (o0, i0) of r0; off < 256.
+__device__ __forceinline__ void row_coords(int64_t o0, int64_t i0, int off, int64_t n_inner, int64_t& o,
+                                           int64_t& i) {
+    i = i0 + off;
+    o = o0;
+    if (n_inner >= 256) {
+        if (i >= n_inner) { i -= n_inner; ++o; }
+    } else {
+        const uint32_t q = (uint32_t)i / (uint32_t)n_inner;  // i < n_inner + 256 < 512
+        o += q;
+        i -= (int64_t)q * n_inner;
     }
 }
 
-template <int XDT, int WDT, int NT>
+template <int NR, int KS, int MT>
 __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const ProjArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int64_t row_x[kBM], row_c[kBM], row_s[kBM];  // this block's row offsets (-1: past the end)
-    // LDS: x tile [kBM][xp] f16 | W group [hg*dp][xp] f16 | per-wave f16 results [kBM][hg*dp] |
-    //      per-wave codes [kBM][hg*d]
-    const int gc = a.hg * a.dp;  // group columns (padded)
-    _Float16* xt = reinterpret_cast<_Float16*>(smem);
-    _Float16* wt = xt + kBM * a.xp;
-    _Float16* kvt = wt + gc * a.xp;
-    int8_t* ct = reinterpret_cast<int8_t*>(kvt + kBM * gc);
+    extern __shared__ __attribute__((aligned(16))) _Float16 wt[];  // [hg*dp][xp]
 
     // work: XCD-aware numbering, the head groups of a stream consecutive within one XCD
     const int nwg = (int)gridDim.x;
@@ -141,93 +241,103 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
     const int ghe = min(a.hg, a.nheads - head0);  // heads in this group
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int lr = tid / kRowThreads, lq = tid % kRowThreads;
+    const int g = lane >> 4;  // result lanes hold columns 4g..4g+3 of each 16-column tile
 
-    // weight rows of the group, zero rows in the padding of each head and past the last head
-    for (int c = lr; c < gc; c += kBM) {
-        const int hh = c / a.dp, e = c % a.dp;
-        const bool valid = hh < ghe && e < a.d;
-        load_row<WDT>(a.w, ((int64_t)(head0 + hh) * a.d + e) * a.w_stride, valid, a.embed, a.ep, false, 0.0f,
-                      wt + c * a.xp, lq);
-    }
+    if (a.wdt == NORI_F32) load_weights<NORI_F32>(a, wt, head0, ghe, tid);
+    else if (a.wdt == NORI_F16) load_weights<NORI_F16>(a, wt, head0, ghe, tid);
+    else load_weights<NORI_BF16>(a, wt, head0, ghe, tid);
+    __syncthreads();
 
-    _Float16* kv_w = kvt + wave * 16 * gc;  // this wavefront's 16 rows of results
-    int8_t* ct_w = ct + wave * 16 * (a.hg * a.d);
-    const int ksteps = a.ep / 32;
+    const _Float16* wa = wt + (lane & 15) * a.xp + 8 * g;  // A operand rows of tile 0 of head 0
     for (int64_t rb = stream; rb < a.nblocks; rb += a.streams) {
-        const int64_t r0 = rb * kBM;
-        __syncthreads();  // the previous block's tiles and offsets are no longer read; W is loaded
-        if (tid < kBM) {
-            const int64_t r = r0 + tid;
-            const int64_t o = r / a.n_inner, i = r - o * a.n_inner;
-            const bool in = r < a.rows;
-            row_x[tid] = in ? o * a.x_outer + i * a.x_row : -1;
-            row_c[tid] = in ? o * a.codes_outer + i * a.codes_row : -1;
-            row_s[tid] = in ? o * a.scales_outer + i * a.scales_row : -1;
-        }
-        __syncthreads();
-        const int64_t xoff = row_x[lr];
-        load_row<XDT>(a.x, xoff, xoff >= 0, a.embed, a.ep, a.norm != 0, a.eps, xt + lr * a.xp, lq);
-        __syncthreads();
+        const int64_t r0 = rb * a.bm;
+        const int64_t o0 = r0 / a.grid.n_inner, i0 = r0 - o0 * a.grid.n_inner;
 
-        // ---- projection: 16 rows x gc columns per wavefront
-        f32x4 acc[NT];
+        // ---- operand rows of this wavefront -> B operands; their code and scale row offsets.
+        // Lanes of rows past the last read the last row and store nothing.
+        f16x8 xf[NR][KS];
+        int64_t c_off[NR], s_off[NR];
 #pragma unroll
-        for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const _Float16* xa = xt + (wave * 16 + (lane & 15)) * a.xp + 8 * (lane >> 4);
-        const _Float16* wb = wt + (lane & 15) * a.xp + 8 * (lane >> 4);
-        for (int ks = 0; ks < ksteps; ++ks) {
-            const f16x8 av = *reinterpret_cast<const f16x8*>(xa + 32 * ks);
+        for (int nt = 0; nt < NR; ++nt) {
+            const int off0 = (wave * NR + nt) * 16 + (lane & 15);
+            const bool valid = r0 + off0 < a.grid.rows;
+            int64_t o, i;
+            row_coords(o0, i0, valid ? off0 : (int)(a.grid.rows - 1 - r0), a.grid.n_inner, o, i);
+            const _Float16* xrow = a.xs + o * a.xs_outer + i * a.xs_row + 8 * g;
+            c_off[nt] = valid ? o * a.codes_outer + i * a.codes_row : -1;
+            s_off[nt] = valid ? o * a.scales_outer + i * a.scales_row : -1;
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                if (16 * n < gc) {
-                    const f16x8 bv = *reinterpret_cast<const f16x8*>(wb + 16 * n * a.xp + 32 * ks);
-                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[n], 0, 0, 0);
+            for (int ks = 0; ks < KS; ++ks)
+                xf[nt][ks] = ks < a.ksteps ? *reinterpret_cast<const f16x8*>(xrow + 32 * ks) : f16x8{};
+        }
+
+        for (int hh = 0; hh < ghe; ++hh) {
+            // ---- projection of the head: MT column tiles x NR row tiles
+            f32x4 acc[MT][NR];
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int nt = 0; nt < NR; ++nt) acc[m][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const _Float16* wh = wa + hh * a.dp * a.xp;
+            // all KS steps and MT tiles: past `ksteps`, and in each head's padding rows, the
+            // operands are zero, so the MFMA chain has no branch
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(wh + 16 * m * a.xp + 32 * ks);
+#pragma unroll
+                    for (int nt = 0; nt < NR; ++nt)
+                        acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xf[nt][ks], acc[m][nt], 0, 0, 0);
                 }
             }
-        }
-        // f16 results: lane holds column 16n + lane%16 of rows 4*(lane/16) + i
+            // operand reads two steps ahead of the MFMAs that use them
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * MT, 0);
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            if (16 * n < gc) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    kv_w[(4 * (lane >> 4) + i) * gc + 16 * n + (lane & 15)] = (_Float16)pin_f32(acc[n][i]);
+            for (int ks = 0; ks < KS; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, MT * NR, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, MT, 0);
             }
-        }
-        __syncthreads();  // results visible across the lanes that quantize them
 
-        // ---- quantize the wavefront's 16 * ghe head vectors: lpv lanes per vector
-        const int nvec = 16 * ghe;
-        const int lpv = nvec >= 64 ? 1 : (nvec >= 32 ? 2 : (nvec >= 16 ? 4 : 4));
-        const int epl = (a.d + lpv - 1) / lpv;  // elements per lane
-        for (int v0 = 0; v0 < nvec; v0 += 64 / lpv) {
-            const int v = v0 + lane / lpv, part = lane % lpv;
-            const bool on = v < nvec;
-            const int row = on ? v % 16 : 0, hh = on ? v / 16 : 0;
-            const int e0 = part * epl, e1 = min(a.d, e0 + epl);
-            const uint16_t* src = reinterpret_cast<const uint16_t*>(kv_w) + row * gc + hh * a.dp;
-            uint32_t key = 0;
-            if (on)
-                for (int e = e0; e < e1; ++e) key = max(key, abs_key<NORI_F16>(src[e]));
-            for (int off = 1; off < lpv; off <<= 1) key = max(key, (uint32_t)__shfl_xor((int)key, off, 64));
-            const VectorScale vs = make_scale<NORI_F16>(key, a.scale_div);
-            if (on) {
-                for (int e = e0; e < e1; ++e)
-                    ct_w[row * (a.hg * a.d) + hh * a.d + e] = (int8_t)code_of<NORI_F16>(f16_to_f32(src[e]), vs);
-                const int64_t soff = row_s[wave * 16 + row];
-                if (part == 0 && soff >= 0) a.scales[soff + head0 + hh] = vs.s;
+            // ---- quantize: lane holds columns 16m + 4g + [0, 4) of row (lane & 15)
+#pragma unroll
+            for (int nt = 0; nt < NR; ++nt) {
+                uint16_t hv[MT][4];
+                uint32_t key = 0;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        hv[m][q] = f32_to_f16(acc[m][nt][q]);
+                        if (16 * m + 4 * g + q < a.d) key = max(key, abs_key<NORI_F16>(hv[m][q]));
+                    }
+                }
+                key = max(key, (uint32_t)__shfl_xor((int)key, 16));
+                key = max(key, (uint32_t)__shfl_xor((int)key, 32));
+                const VectorScale vs = make_scale<NORI_F16>(key, a.scale_div);
+                uint32_t words[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    words[m] = pack4(code_fast<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_fast<NORI_F16>(f16_to_f32(hv[m][1]), vs),
+                                     code_fast<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_fast<NORI_F16>(f16_to_f32(hv[m][3]), vs));
+                // scales outside the fast quotient's range (zero, subnormal or huge vectors, NaN):
+                // recode exactly, on a wave-uniform branch that is almost never taken
+                if (__builtin_expect(__builtin_amdgcn_ballot_w64(!vs.fast) != 0, 0)) {
+                    if (!vs.fast) {
+#pragma unroll
+                        for (int m = 0; m < MT; ++m)
+                            words[m] = pack4(code_of<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][1]), vs),
+                                             code_of<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][3]), vs));
+                    }
+                }
+                if (c_off[nt] >= 0) {
+                    int8_t* crow = a.codes + c_off[nt] + (int64_t)(head0 + hh) * a.d;
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+                        if (16 * m + 4 * g < a.d) *reinterpret_cast<uint32_t*>(crow + 16 * m + 4 * g) = words[m];
+                    if (g == 0) a.scales[s_off[nt] + head0 + hh] = vs.s;
+                }
             }
-        }
-        __syncthreads();  // staged codes visible across the lanes that store them
-        // ---- codes out: each row's ghe*d bytes at its group offset, in 4-byte words
-        const int rwords = ghe * a.d / 4;
-        for (int i = lane; i < 16 * rwords; i += 64) {
-            const int row = i / rwords, wd = i % rwords;
-            const int64_t coff = row_c[wave * 16 + row];
-            if (coff >= 0)
-                *reinterpret_cast<uint32_t*>(a.codes + coff + (int64_t)head0 * a.d + 4 * wd) =
-                    *reinterpret_cast<const uint32_t*>(ct_w + row * (a.hg * a.d) + 4 * wd);
         }
     }
 }
@@ -239,37 +349,78 @@ int device_cus() {
     return cus;
 }
 
-size_t lds_bytes(int hg, int dp, int d, int xp) {
-    return (size_t)(kBM * xp + hg * dp * xp + kBM * hg * dp) * 2 + (size_t)kBM * hg * d;
+template <int NR, int KS, int MT>
+int launch_with(const ProjArgs& a, size_t lds, hipStream_t stream) {
+    const dim3 grid((unsigned)(a.streams * a.ngroups));
+    if (hipFuncSetAttribute((const void*)kv_project_quantize_kernel<NR, KS, MT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return fail(NORI_ERR_RUNTIME, "kv_project_quantize_int8: cannot reserve %zu bytes of LDS", lds);
+    hipLaunchKernelGGL((kv_project_quantize_kernel<NR, KS, MT>), grid, dim3(kThreads), lds, stream, a);
+    return launch_status("kv_project_quantize_int8");
 }
 
-constexpr size_t kLdsLimit = 160 * 1024 - 3 * kBM * sizeof(int64_t);  // dynamic LDS beside the row offsets
-
-template <int XDT, int WDT>
-int launch(const ProjArgs& a, size_t lds, hipStream_t stream) {
-    const int nt = a.hg * a.dp / 16;
-    const dim3 grid((unsigned)(a.streams * a.ngroups));
-#define NORI_PROJ_NT(N)                                                                                          \
-    if (nt <= N) {                                                                                              \
-        if (hipFuncSetAttribute((const void*)kv_project_quantize_kernel<XDT, WDT, N>,                           \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)             \
-            return fail(NORI_ERR_RUNTIME, "kv_project_quantize_int8: cannot reserve %zu bytes of LDS", lds);     \
-        hipLaunchKernelGGL((kv_project_quantize_kernel<XDT, WDT, N>), grid, dim3(kThreads), lds, stream, a);   \
-        return launch_status("kv_project_quantize_int8");                                                       \
+template <int NR, int KS>
+int launch_mt(const ProjArgs& a, size_t lds, hipStream_t stream) {
+    switch (a.dp / 16) {
+        case 1: return launch_with<NR, KS, 1>(a, lds, stream);
+        case 2: return launch_with<NR, KS, 2>(a, lds, stream);
+        case 3: return launch_with<NR, KS, 3>(a, lds, stream);
+        case 4: return launch_with<NR, KS, 4>(a, lds, stream);
+        case 6: return launch_with<NR, KS, 6>(a, lds, stream);
+        default: return launch_with<NR, KS, 8>(a, lds, stream);
     }
-    NORI_PROJ_NT(4) NORI_PROJ_NT(8) NORI_PROJ_NT(16)
-#undef NORI_PROJ_NT
-    return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: %d column tiles per group", nt);
+}
+
+// column tiles per head the kernel is built for (a head padded with zero rows up to them)
+int padded_tiles(int d) {
+    const int mt = (d + 15) / 16;
+    return mt <= 4 ? mt : (mt <= 6 ? 6 : 8);
+}
+
+// operand steps the kernel holds in registers (KS >= ksteps; the steps past ksteps are zero)
+int padded_steps(int ksteps) {
+    for (int k : {4, 8, 12, 16, 24}) if (ksteps <= k) return k;
+    return 32;
+}
+
+// 16 * NR rows per wavefront
+int launch(ProjArgs& a, int kpad, size_t lds, hipStream_t stream) {
+    const int nr = kpad <= 16 ? 2 : 1;
+    a.bm = kWaves * 16 * nr;
+    a.nblocks = (a.grid.rows + a.bm - 1) / a.bm;
+    const int64_t slots = (int64_t)device_cus() * (lds <= kLds / kWgPerCu ? kWgPerCu : 1);
+    a.streams = (int)std::max<int64_t>(1, std::min<int64_t>(a.nblocks, slots / a.ngroups));
+    switch (kpad) {
+        case 4: return launch_mt<2, 4>(a, lds, stream);
+        case 8: return launch_mt<2, 8>(a, lds, stream);
+        case 12: return launch_mt<2, 12>(a, lds, stream);
+        case 16: return launch_mt<2, 16>(a, lds, stream);
+        case 24: return launch_mt<1, 24>(a, lds, stream);
+        default: return launch_mt<1, 32>(a, lds, stream);
+    }
+}
+
+// x feeds the MFMAs as it is: f16, no norm, whole 32-element steps
+bool direct_operands(int x_dtype, int32_t embed, int32_t norm) {
+    return x_dtype == NORI_F16 && !norm && embed % 32 == 0;
 }
 
 }  // namespace
+
+extern "C" int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_outer, int64_t n_inner,
+                                                               int32_t embed, int32_t norm) {
+    if (n_outer <= 0 || n_inner <= 0 || embed <= 0 || direct_operands(x_dtype, embed, norm)) return 0;
+    if (n_inner > INT64_MAX / n_outer) return 0;
+    return n_outer * n_inner * (int64_t)((embed + 31) / 32 * 32) * 2;
+}
 
 extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t n_outer, int64_t n_inner,
                                             int32_t embed, int64_t x_outer_stride, int64_t x_row_stride, int32_t norm,
                                             float eps, const void* weight, int weight_dtype, int64_t w_row_stride,
                                             int32_t kv_heads, int32_t d, int8_t* codes, int64_t codes_outer_stride,
                                             int64_t codes_row_stride, float* scales, int64_t scales_outer_stride,
-                                            int64_t scales_row_stride, int32_t scale_div, void* stream_v) {
+                                            int64_t scales_row_stride, int32_t scale_div, void* workspace,
+                                            int64_t workspace_bytes, void* stream_v) {
     clear_error();
     if (n_outer < 0 || n_inner < 0 || embed <= 0 || kv_heads <= 0 || d <= 0)
         return fail(NORI_ERR_INVALID, "kv_project_quantize_int8: bad shape n_outer=%lld n_inner=%lld embed=%d kv_heads=%d d=%d",
@@ -281,8 +432,11 @@ extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t
                     dtype_name(weight_dtype));
     if (scale_div != NORI_SCALE_DIV_TRUE && scale_div != NORI_SCALE_DIV_RECIP)
         return fail(NORI_ERR_INVALID, "kv_project_quantize_int8: unknown scale_div %d", scale_div);
-    if (d % 4 || d > 256)
-        return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: head width %d is not a multiple of 4 up to 256", d);
+    if (d % 4 || d > 128)
+        return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: head width %d is not a multiple of 4 up to 128", d);
+    // an operand row is held in registers: at most 32 steps of 32 elements
+    if (embed > 1024)
+        return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: embed %d exceeds 1024", embed);
     if (n_outer == 0 || n_inner == 0) return NORI_OK;
     if (n_inner > INT64_MAX / n_outer)
         return fail(NORI_ERR_INVALID, "kv_project_quantize_int8: %lld x %lld rows overflow", (long long)n_outer,
@@ -296,31 +450,49 @@ extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t
                     "kv_project_quantize_int8: x and weight rows must be 16-byte aligned whole 16-byte chunks");
     if ((uintptr_t)codes % 4 || codes_row_stride % 4 || codes_outer_stride % 4)
         return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: code rows must be 4-byte aligned");
+    const int64_t ws_need = nori_kv_project_quantize_int8_workspace_size(x_dtype, n_outer, n_inner, embed, norm);
+    if (ws_need > 0 && (!workspace || workspace_bytes < ws_need || (uintptr_t)workspace % 16))
+        return fail(NORI_ERR_INVALID, "kv_project_quantize_int8: needs a 16-byte aligned workspace of %lld bytes",
+                    (long long)ws_need);
+
+    const Grid grid{n_outer * n_inner, n_inner};
+    const int ksteps = (embed + 31) / 32;
+    hipStream_t stream = (hipStream_t)stream_v;
 
     ProjArgs a;
-    a.x = x; a.rows = n_outer * n_inner; a.n_inner = n_inner; a.embed = embed;
-    a.x_outer = x_outer_stride; a.x_row = x_row_stride;
-    a.norm = norm; a.eps = eps;
-    a.w = weight; a.w_stride = w_row_stride;
-    a.nheads = 2 * kv_heads; a.d = d; a.dp = (d + 15) / 16 * 16;
-    a.ep = (embed + 31) / 32 * 32;
-    a.xp = a.ep + 8;  // +16 bytes per row: the 16-byte operand reads of 16 rows spread over the banks
+    a.grid = grid;
+    if (ws_need > 0) {
+        PrepArgs p;
+        p.x = x; p.grid = grid; p.embed = embed; p.x_outer = x_outer_stride; p.x_row = x_row_stride;
+        p.norm = norm; p.eps = eps;
+        p.ws = reinterpret_cast<_Float16*>(workspace); p.pitch = 32 * ksteps;
+        const int64_t waves = std::min<int64_t>((grid.rows + kPrepRows - 1) / kPrepRows, (int64_t)device_cus() * 16);
+        const dim3 pgrid((unsigned)((waves + kPrepWaves - 1) / kPrepWaves));
+        NORI_DISPATCH_FLOAT(x_dtype, XDT,
+                            hipLaunchKernelGGL((prep_rows_kernel<XDT>), pgrid, dim3(kPrepWaves * 64), 0, stream, p));
+        const int st = launch_status("kv_project_quantize_int8 (operand rows)");
+        if (st != NORI_OK) return st;
+        a.xs = p.ws; a.xs_outer = n_inner * (int64_t)p.pitch; a.xs_row = p.pitch;
+    } else {
+        a.xs = reinterpret_cast<const _Float16*>(x); a.xs_outer = x_outer_stride; a.xs_row = x_row_stride;
+    }
+    a.w = weight; a.wdt = weight_dtype; a.w_stride = w_row_stride;
+    a.embed = embed;
+    a.nheads = 2 * kv_heads; a.d = d; a.dp = 16 * padded_tiles(d);
+    a.ksteps = ksteps;
+    const int kpad = padded_steps(ksteps);
+    a.xp = 32 * kpad + 8;  // +16 bytes per row: the 16-byte operand reads of 16 rows spread over the banks
     a.codes = codes; a.codes_outer = codes_outer_stride; a.codes_row = codes_row_stride;
     a.scales = scales; a.scales_outer = scales_outer_stride; a.scales_row = scales_row_stride;
     a.scale_div = scale_div;
-    // heads per group: as many as fit the LDS with the x tile (at most 16 column tiles)
-    int hg = 1;
-    while (hg < a.nheads && (hg + 1) * a.dp <= 256 && lds_bytes(hg + 1, a.dp, d, a.xp) <= kLdsLimit) ++hg;
-    if (lds_bytes(hg, a.dp, d, a.xp) > kLdsLimit)
+    // heads per group: as many as fit half the LDS (two workgroups per CU), else the whole LDS,
+    // then spread evenly over the groups
+    const size_t head_bytes = (size_t)a.dp * a.xp * 2;
+    if (head_bytes > kLds)
         return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: embed %d x head width %d exceeds the LDS", embed, d);
-    a.hg = hg;
-    a.ngroups = (a.nheads + hg - 1) / hg;
-    a.nblocks = (a.rows + kBM - 1) / kBM;
-    const int64_t slots = device_cus();
-    a.streams = (int)std::max<int64_t>(1, std::min<int64_t>(a.nblocks, slots / a.ngroups));
-    const size_t lds = lds_bytes(hg, a.dp, d, a.xp);
-    hipStream_t stream = (hipStream_t)stream_v;
-    int st = NORI_OK;
-    NORI_DISPATCH_FLOAT(x_dtype, XDT, NORI_DISPATCH_FLOAT(weight_dtype, WDT, st = launch<XDT, WDT>(a, lds, stream)));
-    return st;
+    const size_t budget = head_bytes <= kLds / kWgPerCu ? kLds / kWgPerCu : kLds;
+    const int hg_max = std::min<int>(a.nheads, (int)(budget / head_bytes));
+    a.ngroups = (a.nheads + hg_max - 1) / hg_max;
+    a.hg = (a.nheads + a.ngroups - 1) / a.ngroups;
+    return launch(a, kpad, (size_t)a.hg * head_bytes, stream);
 }

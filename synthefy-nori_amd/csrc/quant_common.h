@@ -61,16 +61,20 @@ __device__ __forceinline__ VectorScale make_scale(uint32_t max_key, int scale_di
     return vs;
 }
 
-// Code of one element; `t` is finite whenever vs.fast holds (|t| <= amax < inf).
+// Code of one element of a vector whose scale has vs.fast (then `t` is finite: |t| <= amax < inf).
+template <int DT>
+__device__ __forceinline__ int code_fast(float t, const VectorScale& vs) {
+    const float q0 = t * vs.y;
+    const float r = fmaf(-q0, vs.s, t);
+    const float q = fmaf(r, vs.y, q0);
+    const float k = rintf(round_to<DT>(q));
+    return (int)__builtin_amdgcn_fmed3f(k, -127.0f, 127.0f);
+}
+
+// Code of one element.
 template <int DT>
 __device__ __forceinline__ int code_of(float t, const VectorScale& vs) {
-    if (vs.fast) {
-        const float q0 = t * vs.y;
-        const float r = fmaf(-q0, vs.s, t);
-        const float q = fmaf(r, vs.y, q0);
-        const float k = rintf(round_to<DT>(q));
-        return (int)__builtin_amdgcn_fmed3f(k, -127.0f, 127.0f);
-    }
+    if (vs.fast) return code_fast<DT>(t, vs);
     const float k = rintf(round_to<DT>(t / vs.s));
     if (k != k) return 0;  // NaN -> 0, the GPU's float->int conversion of NaN
     return (int)fminf(fmaxf(k, -127.0f), 127.0f);

@@ -54,8 +54,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "nori_kv_project_quantize_int8": (
         ctypes.c_int,
         [_vp, _i32, _i64, _i64, _i32, _i64, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
-         _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp],
+         _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _vp],
     ),
+    "nori_kv_project_quantize_int8_workspace_size": (_i64, [_i32, _i64, _i64, _i32, _i32]),
 }
 
 _lib: ctypes.CDLL | None = None

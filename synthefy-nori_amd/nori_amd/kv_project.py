@@ -35,7 +35,7 @@ def fusable(x: torch.Tensor, weight: torch.Tensor, head_dim: int) -> bool:
     """Whether ``project_quantize_kv`` takes these operands as they are (dtype, widths, alignment)."""
     if x.dtype not in _FLOATS or weight.dtype not in _FLOATS or x.device.type != "cuda" or weight.device != x.device:
         return False
-    if head_dim % 4 or head_dim > 256 or x.shape[-1] != weight.shape[-1] or weight.dim() != 2:
+    if head_dim % 4 or head_dim > 128 or x.shape[-1] != weight.shape[-1] or weight.dim() != 2 or x.shape[-1] > 1024:
         return False
     if x.stride(-1) != 1 or weight.stride(-1) != 1:
         return False
@@ -93,7 +93,7 @@ def project_quantize_kv(
         raise NotImplementedError(
             f"project_quantize_kv does not take x {x.dtype} {tuple(x.shape)} strides {x.stride()} with weight "
             f"{weight.dtype} {tuple(weight.shape)} and head_dim {head_dim} (needs 16-byte aligned rows of whole "
-            "16-byte chunks and head_dim a multiple of 4 up to 256)"
+            "16-byte chunks, embed up to 1024 and head_dim a multiple of 4 up to 128)"
         )
     if x.numel() == 0:
         return codes, scales
@@ -119,13 +119,19 @@ def _launch(x, weight, kv_heads, head_dim, norm_eps, codes, scales, device) -> N
             _launch(x[i], weight, kv_heads, head_dim, norm_eps, codes[i], scales[i], device)
         return
     n_outer, n_inner, x_outer, x_row = x_layout
+    norm = int(norm_eps is not None)
+    lib = nat.lib()
+    ws_bytes = int(lib.nori_kv_project_quantize_int8_workspace_size(
+        nat.dtype_code(x.dtype), n_outer, n_inner, x.shape[-1], norm))
+    # the f16 operand rows (torch's caching allocator keeps the buffer for the next slice)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
     nat.check(
-        nat.lib().nori_kv_project_quantize_int8(
+        lib.nori_kv_project_quantize_int8(
             x.data_ptr(), nat.dtype_code(x.dtype), n_outer, n_inner, x.shape[-1], x_outer, x_row,
-            int(norm_eps is not None), float(norm_eps if norm_eps is not None else 0.0),
+            norm, float(norm_eps if norm_eps is not None else 0.0),
             weight.data_ptr(), nat.dtype_code(weight.dtype), weight.stride(0), kv_heads, head_dim,
             codes.data_ptr(), c_str[0], c_str[1], scales.data_ptr(), s_str[0], s_str[1],
-            nat.SCALE_DIV_RECIP, nat.stream_of(device),
+            nat.SCALE_DIV_RECIP, nat.ptr(ws), ws_bytes, nat.stream_of(device),
         ),
         "project_quantize_kv",
     )

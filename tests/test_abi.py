@@ -34,6 +34,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_icl_attention",
             "nori_icl_attention_workspace_size",
             "nori_kv_project_quantize_int8",
+            "nori_kv_project_quantize_int8_workspace_size",
         ]
     )
 
@@ -75,7 +76,7 @@ def test_argument_errors_map_to_reference_exceptions():
     assert b"empty" in lib.nori_last_error()
     # fused projection + quantize: bad shape, head width not a multiple of 4, unknown dtype
     proj = [None, nat.NORI_F32, 1, 8, 64, 0, 64, 0, 0.0, None, nat.NORI_F32, 64, 2, 16,
-            None, 0, 64, None, 0, 4, nat.SCALE_DIV_RECIP, None]
+            None, 0, 64, None, 0, 4, nat.SCALE_DIV_RECIP, None, 0, None]
     bad = list(proj); bad[13] = 0
     assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_ERR_INVALID
     bad = list(proj); bad[13] = 18
@@ -88,6 +89,10 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(proj); bad[2] = 0
     assert lib.nori_kv_project_quantize_int8(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_kv_project_quantize_int8(*proj) == nat.NORI_ERR_INVALID  # null pointers
+    # operand-row workspace: f16 rows padded to 32, none when x is already f16 operands
+    assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F32, 3, 5, 44, 1) == 15 * 64 * 2
+    assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 0) == 0
+    assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 1) == 15 * 64 * 2
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
