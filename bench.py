@@ -20,7 +20,8 @@ around each attention call (its kernel and, when the context is split, the merge
 the partials), the same for the quantize kernel against 8 TB/s of HBM, the HBM traffic
 per launch measured by rocprofv3 counters (profiles/traffic_nori30m_64k.md, when
 present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes) of one
-layer against the unfused sequence it replaces, and the CPU baseline: the oracle (quantizer in C, attention as the
+layer against the unfused sequence it replaces, one layer's prefill self-attention over the
+fp16 context K/V, and the CPU baseline: the oracle (quantizer in C, attention as the
 reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
 bounded sample of the same work.
 """
@@ -68,6 +69,10 @@ def parse_args():
         "--probe-traffic", action="store_true",
         help="run a 1 GiB device copy (counter calibration), one quantize, one attention and one dequantize "
         "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
+    )
+    p.add_argument(
+        "--prefill", action="store_true",
+        help="measure only one layer's prefill self-attention (65536 x 65536, fp16 K/V)",
     )
     p.add_argument(
         "--cache-write", action="store_true",
@@ -219,6 +224,43 @@ def cache_write(torch, dev, codes, scales, reps=5):
     }
 
 
+def prefill_attention(torch, dev, kv16, reps=2):
+    """The context self-attention of one layer's prefill (layer.py:1884-1888): all 65,536 context
+    rows attend to the layer's full-precision (fp16) context K/V [33, 65536, 2, 8, 44] with the
+    fp16-cache variant of the attention kernel. HIP events around each call."""
+    import nori_amd
+    from nori_amd import attention as attn
+
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(GROUPS, CONTEXT_ROWS, HEADS, HEAD_DIM, generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(attn.workspace_bytes(GROUPS, CONTEXT_ROWS, HEADS, HEAD_DIM, CONTEXT_ROWS), 1),
+                     dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    nori_amd.icl_attention(q, kv16, out=out, workspace=ws)
+    ev = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        nori_amd.icl_attention(q, kv16, out=out, workspace=ws)
+        e1.record(stream)
+        ev.append((e0, e1))
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in ev) / reps
+    flop = 4.0 * GROUPS * HEADS * CONTEXT_ROWS * CONTEXT_ROWS * HEAD_DIM
+    del q, out, ws
+    return {
+        "what": "one layer's prefill self-attention: 33 x 65536 context rows x 8 heads attending to "
+        "the layer's fp16 context K/V (65536 rows), icl_attention_kernel<48, f16 cache, fold, 16 waves>",
+        "avg_launch_ms": round(ms, 3),
+        "achieved": round(flop / (ms * 1e-3) / 1e12, 1),
+        "unit": "TFLOP/s",
+        "frac": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
+        "work_per_launch": f"{flop:.4e} FLOP = 4*33*8*65536*65536*44",
+    }
+
+
 def measured_traffic():
     """HBM bytes per launch of the attention and quantize kernels from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -253,6 +295,11 @@ def main():
     torch.cuda.set_device(dev)
     if args.probe_traffic:
         probe_traffic(torch, dev)
+        return
+    if args.prefill:
+        shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
+        kv16 = torch.randn(shape, generator=torch.Generator(device=dev).manual_seed(2), device=dev, dtype=torch.float16)
+        print(json.dumps(prefill_attention(torch, dev, kv16)), flush=True)
         return
     if args.cache_write:
         shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
@@ -320,6 +367,7 @@ def main():
     dequant_ms = [a.elapsed_time(b) for a, b in dq_events]
     del dq_out
     write = cache_write(torch, dev, codes[0], scales[0])
+    prefill = prefill_attention(torch, dev, kv[0])
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -394,6 +442,7 @@ def main():
         },
     }
     line["cache_write"] = write
+    line["prefill_attention"] = prefill
     if args.cpu_baseline == "on":
         line["cpu_baseline"] = cpu_baseline(torch, kv[0], codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)
