@@ -21,7 +21,8 @@ the partials), the same for the quantize kernel against 8 TB/s of HBM, the HBM t
 per launch measured by rocprofv3 counters (profiles/traffic_nori30m_64k.md, when
 present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes) of one
 layer against the unfused sequence it replaces, one layer's prefill self-attention over the
-fp16 context K/V, and the CPU baseline: the oracle (quantizer in C, attention as the
+fp16 context K/V, the same configuration through the model-level context-cache API
+(build once, 4 query batches), and the CPU baseline: the oracle (quantizer in C, attention as the
 reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
 bounded sample of the same work.
 """
@@ -69,6 +70,10 @@ def parse_args():
         "--probe-traffic", action="store_true",
         help="run a 1 GiB device copy (counter calibration), one quantize, one attention and one dequantize "
         "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
+    )
+    p.add_argument(
+        "--model", action="store_true",
+        help="measure only the model-level context-cache API end to end (build once, 4 query batches)",
     )
     p.add_argument(
         "--prefill", action="store_true",
@@ -261,6 +266,76 @@ def prefill_attention(torch, dev, kv16, reps=2):
     }
 
 
+def model_config():
+    """A random-init model at this workload's block dims (12 layers, embed 352, 8 heads, 2
+    features per group, SwiGLU, RMSNorm pre-norm, QASS, target-aware embedding), with the
+    encoders of the reference's configuration files."""
+    return dict(
+        preprocess_config_x=dict(
+            num_features=2, nan_handling_enabled=True, normalize_on_train_only=True, normalize_x=True,
+            remove_outliers=True, normalize_by_used_features=True,
+        ),
+        encoder_config_x=dict(
+            num_features=2, embedding_size=EMBED, mask_embedding_size=EMBED, encoder_use_bias=True,
+            numeric_embed_type="RBF",
+            RBF_config=dict(token_embed_dim=8, n_kernels=16, sigma=0.5, use_learn_sigma=False,
+                            use_learn_embeddings=False, use_original_features=False),
+        ),
+        encoder_config_y=dict(num_inputs=1, embedding_size=EMBED, nan_handling_y_encoder=True, max_num_classes=10),
+        decoder_config=dict(num_classes=10, num_reg_quantiles=3, regression_loss="pinball",
+                            regression_quantiles=[0.1, 0.5, 0.9]),
+        nlayers=LAYERS, nhead=HEADS, embed_dim=EMBED, hid_dim=4 * EMBED, features_per_group=2, dropout=0.0,
+        pre_norm=True, activation="swiglu", norm_type="rmsnorm", deepnorm_alpha=DEEPNORM_ALPHA, layer_arch="smf",
+        feature_positional_embedding_type="none", seq_attn_isolated=True, cross_share_all_kv_heads=False,
+        use_qassmax=True, qass_mode="full", use_target_aware_embedding=True, use_column_specific_y_aware=True,
+    )
+
+
+def end_to_end(torch, dev, batches=QUERY_BATCHES):
+    """The long-context configuration through the model-level context-cache API: a 65,536-row
+    context of 64 float32 features (5 % NaN) with a nonlinear target, cached once as int8
+    (FeaturesTransformer.build_context_cache), then 4 query batches of 1,024 rows
+    (apply_context_cache), under the fp16 autocast of GPU inference. Wall clock around each
+    phase with the device synchronized."""
+    import nori_amd
+
+    g = torch.Generator().manual_seed(7)
+    n_feat = 64
+    x = torch.randn(1, CONTEXT_ROWS + batches * QUERY_ROWS, n_feat, generator=g)
+    x[torch.rand(x.shape, generator=g) < 0.05] = float("nan")
+    xf = torch.nan_to_num(x)
+    pair = xf[..., 0::2] * xf[..., 1::2]
+    y = pair.sum(-1) / n_feat ** 0.5 + 0.1 * torch.randn(x.shape[:2], generator=g)
+    x, y = x.to(dev), y.to(dev)
+    model = nori_amd.FeaturesTransformer(**model_config()).eval().to(dev)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ctx = model.build_context_cache(x[:, :CONTEXT_ROWS], y[:, :CONTEXT_ROWS], cache_dtype="int8")
+        torch.cuda.synchronize()
+        t_build = time.perf_counter() - t0
+        # one warm batch, then the timed batches
+        model.apply_context_cache(x[:, CONTEXT_ROWS:CONTEXT_ROWS + QUERY_ROWS], ctx, row_chunk_size=QUERY_ROWS)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(batches):
+            lo = CONTEXT_ROWS + i * QUERY_ROWS
+            pred = model.apply_context_cache(x[:, lo:lo + QUERY_ROWS], ctx, row_chunk_size=QUERY_ROWS)
+        torch.cuda.synchronize()
+        t_apply = time.perf_counter() - t0
+    finite = bool(torch.isfinite(pred).all())
+    del ctx, model, x, y
+    return {
+        "what": "model-level context-cache API at this workload: random-init 12-layer embed-352 model, "
+        "65536-row context of 64 features (5 % NaN) cached once as int8, 4 query batches of 1024 rows, "
+        "fp16 autocast",
+        "build_context_cache_s": round(t_build, 3),
+        "apply_query_rows_per_s": round(batches * QUERY_ROWS / t_apply, 1),
+        "apply_ms_per_batch": round(t_apply * 1e3 / batches, 2),
+        "predictions_finite": finite,
+    }
+
+
 def measured_traffic():
     """HBM bytes per launch of the attention and quantize kernels from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -295,6 +370,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.probe_traffic:
         probe_traffic(torch, dev)
+        return
+    if args.model:
+        print(json.dumps(end_to_end(torch, dev)), flush=True)
         return
     if args.prefill:
         shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
@@ -368,6 +446,7 @@ def main():
     del dq_out
     write = cache_write(torch, dev, codes[0], scales[0])
     prefill = prefill_attention(torch, dev, kv[0])
+    model_e2e = end_to_end(torch, dev)
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -443,6 +522,7 @@ def main():
     }
     line["cache_write"] = write
     line["prefill_attention"] = prefill
+    line["end_to_end"] = model_e2e
     if args.cpu_baseline == "on":
         line["cpu_baseline"] = cpu_baseline(torch, kv[0], codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)
