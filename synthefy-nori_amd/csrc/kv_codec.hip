@@ -168,28 +168,6 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 template <int DT>
-__device__ __forceinline__ uint32_t pack_codes_fast(const float (&q)[4]) {
-    if constexpr (DT == NORI_F16) {
-        const f16x2 magic = {(_Float16)1536.0f, (_Float16)1536.0f};
-        const f16x2 h01 = f16x2{(_Float16)pin_f32(q[0]), (_Float16)pin_f32(q[1])} + magic;
-        const f16x2 h23 = f16x2{(_Float16)pin_f32(q[2]), (_Float16)pin_f32(q[3])} + magic;
-        return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
-    } else {
-        // bf16 rounding of q can reach 127.5 (its spacing there is 0.5), which rounds to 128:
-        // clamp in the shifted domain, where every value is an exact integer
-        constexpr float kMagic = 12582912.0f;
-        uint32_t k[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float v = round_to<DT>(q[i]) + kMagic;
-            if constexpr (DT == NORI_BF16) v = __builtin_amdgcn_fmed3f(v, kMagic - 127.0f, kMagic + 127.0f);
-            k[i] = __float_as_uint(v);
-        }
-        return (k[0] & 0xffu) | ((k[1] & 0xffu) << 8) | ((k[2] & 0xffu) << 16) | (k[3] << 24);
-    }
-}
-
-template <int DT>
 __device__ __forceinline__ float elem_of(const uint32_t* x, int e) {
     if constexpr (DT == NORI_F32) return __uint_as_float(x[e]);
     else {

@@ -317,9 +317,17 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
                 const VectorScale vs = make_scale<NORI_F16>(key, a.scale_div);
                 uint32_t words[MT];
 #pragma unroll
-                for (int m = 0; m < MT; ++m)
-                    words[m] = pack4(code_fast<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_fast<NORI_F16>(f16_to_f32(hv[m][1]), vs),
-                                     code_fast<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_fast<NORI_F16>(f16_to_f32(hv[m][3]), vs));
+                for (int m = 0; m < MT; ++m) {
+                    float q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // the correctly rounded quotient t/s (Markstein)
+                        const float t = f16_to_f32(hv[m][i]);
+                        const float q0 = t * vs.y;
+                        q[i] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
+                    }
+                    words[m] = pack_codes_fast<NORI_F16>(q);
+                }
                 // scales outside the fast quotient's range (zero, subnormal or huge vectors, NaN):
                 // recode exactly, on a wave-uniform branch that is almost never taken
                 if (__builtin_expect(__builtin_amdgcn_ballot_w64(!vs.fast) != 0, 0)) {

@@ -80,6 +80,33 @@ __device__ __forceinline__ int code_of(float t, const VectorScale& vs) {
     return (int)fminf(fmaxf(k, -127.0f), 127.0f);
 }
 
+// Codes of four correctly rounded quotients q = t/s of a fast-domain vector, packed into one
+// word (element 0 in the low byte): rint(RN_T(q)) without a float -> int conversion. For fp16,
+// adding 1536 in fp16 rounds to an integer (the spacing in [1024, 2048) is 1, ties to even)
+// and leaves the code in the low byte of the result; |t| <= amax bounds |q| by 127 * (1 + 2^-11)
+// for fp16 and fp32 sources, so only bf16 (scale rounded to 8 bits) needs a clamp.
+template <int DT>
+__device__ __forceinline__ uint32_t pack_codes_fast(const float (&q)[4]) {
+    if constexpr (DT == NORI_F16) {
+        const f16x2 magic = {(_Float16)1536.0f, (_Float16)1536.0f};
+        const f16x2 h01 = f16x2{(_Float16)pin_f32(q[0]), (_Float16)pin_f32(q[1])} + magic;
+        const f16x2 h23 = f16x2{(_Float16)pin_f32(q[2]), (_Float16)pin_f32(q[3])} + magic;
+        return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
+    } else {
+        // bf16 rounding of q can reach 127.5 (its spacing there is 0.5), which rounds to 128:
+        // clamp in the shifted domain, where every value is an exact integer
+        constexpr float kMagic = 12582912.0f;
+        uint32_t k[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = round_to<DT>(q[i]) + kMagic;
+            if constexpr (DT == NORI_BF16) v = __builtin_amdgcn_fmed3f(v, kMagic - 127.0f, kMagic + 127.0f);
+            k[i] = __float_as_uint(v);
+        }
+        return (k[0] & 0xffu) | ((k[1] & 0xffu) << 8) | ((k[2] & 0xffu) << 16) | (k[3] << 24);
+    }
+}
+
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
            ((uint32_t)(d & 0xff) << 24);
