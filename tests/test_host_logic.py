@@ -100,3 +100,31 @@ def test_split_strides_addresses_contiguous_outputs_of_a_sliced_source():
     assert _split_strides(_vector_layout(codes), 4, 600) == (600 * 44, 44)
     assert _split_strides(_vector_layout(codes), 4, 601) is None
     assert _split_strides(None, 1, 1) is None
+
+
+def test_fused_cache_write_is_taken_only_where_it_computes_the_same():
+    # the fused (RMSNorm ->) projection -> int8 write replaces the separate steps only under the
+    # GPU's fp16 autocast and for a row norm it can fold (none, or RMSNorm without a weight)
+    from nori_amd import kv_project
+    from nori_amd import layer as NL
+
+    attn = NL.MultiheadAttention(64, 4, qkv_combined=False)
+    cpu = torch.device("cpu")
+    assert not kv_project.fp16_autocast(cpu)
+    assert NL._fused_cache_write(attn, None, False, cpu) is None  # no fp16 autocast on the CPU
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        assert not kv_project.fp16_autocast(cpu)
+
+
+def test_fused_rows_report_the_projected_slice_they_stand_for():
+    from nori_amd.kv_project import FusedKVRows, fusable
+
+    x = torch.randn(2, 3, 5, 64)  # [B, G, n, E]
+    w = torch.randn(2 * 4 * 16, 64)
+    rows = FusedKVRows(x, w, 4, 16, 1e-5)
+    assert rows.shape == (6, 5, 2, 4, 16) and rows.dtype == torch.float16
+    with pytest.raises(ValueError, match="B, G, n, E"):
+        FusedKVRows(x[0], w, 4, 16, None)
+    # host tensors are never taken by the kernel
+    assert not fusable(x, w, 16)
+
