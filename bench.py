@@ -72,6 +72,10 @@ def parse_args():
         "launch of the workload twice, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes",
     )
     p.add_argument(
+        "--other-configs", action="store_true",
+        help="measure only the kernel-level legs of configs 2 (nori-6m block) and 4 (nori-100m layer)",
+    )
+    p.add_argument(
         "--model", action="store_true",
         help="measure only the model-level context-cache API end to end (build once, 4 query batches)",
     )
@@ -336,6 +340,63 @@ def end_to_end(torch, dev, batches=QUERY_BATCHES):
     }
 
 
+def other_configs(torch, dev):
+    """Kernel-level legs of the other cached configurations, each timed with HIP events:
+    config 2, the isolated ICL block at nori-6m dims (1 table, G = 9 tokens, 4096 context rows,
+    1024 queries, H = 2, D = 64, bf16 with 3 channels x8), and config 4, one layer of the batched
+    pipeline at nori-100m dims (32 tables x G = 51 tokens, 8192 context rows, 2048 queries,
+    H = 10, D = 56, fp16). Quantize and attention separately."""
+    import nori_amd
+    from nori_amd import attention as attn
+    from nori_amd.kv_cache_scaling import _quantize_into
+
+    stream = torch.cuda.current_stream(dev)
+
+    def avg_ms(fn, reps):
+        fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def leg(name, bg, nk, nq, heads, d, dtype, reps_q, reps_a, outliers):
+        g = torch.Generator(device=dev).manual_seed(1)
+        kv = torch.randn(bg, nk, 2, heads, d, generator=g, device=dev, dtype=dtype)
+        q = torch.randn(bg, nq, heads, d, generator=g, device=dev, dtype=dtype)
+        if outliers:
+            ch = torch.randperm(heads * d, generator=torch.Generator().manual_seed(1))[:outliers]
+            kv.view(bg, nk, 2, heads * d)[..., ch] *= 8
+            q.view(bg, nq, heads * d)[..., ch] *= 8
+        codes = torch.empty(kv.shape, dtype=torch.int8, device=dev)
+        scales = torch.empty(kv.shape[:-1] + (1,), dtype=torch.float32, device=dev)
+        ws = torch.empty(max(attn.workspace_bytes(bg, nq, heads, d, nk), 1), dtype=torch.uint8, device=dev)
+        out = torch.empty_like(q)
+        q_ms = avg_ms(lambda: _quantize_into(kv, codes, scales), reps_q)
+        a_ms = avg_ms(lambda: nori_amd.icl_attention(q, codes, scales, out=out, workspace=ws), reps_a)
+        n = kv.numel()
+        qbytes = n * (kv.element_size() + 1) + 4 * n // d
+        flop = 4.0 * bg * heads * nq * nk * d
+        return {
+            "what": name,
+            "quantize_ms": round(q_ms, 4),
+            "quantize_GBps": round(qbytes / (q_ms * 1e-3) / 1e9, 1),
+            "quantize_frac": round(qbytes / (q_ms * 1e-3) / HBM_PEAK, 4),
+            "attention_ms": round(a_ms, 4),
+            "attention_TFLOPs": round(flop / (a_ms * 1e-3) / 1e12, 1),
+            "attention_frac": round(flop / (a_ms * 1e-3) / MFMA_BF16_PEAK, 4),
+        }
+
+    c2 = leg("config 2: isolated ICL block, nori-6m dims: BG 9, 4096 context rows, 1024 queries, H 2, D 64, "
+             "bf16 with 3 channels x8", 9, 4096, 1024, 2, 64, torch.bfloat16, 200, 50, 3)
+    c4 = leg("config 4: one layer of the batched pipeline, nori-100m dims: BG 32 x 51, 8192 context rows, "
+             "2048 queries, H 10, D 56, fp16", 32 * 51, 8192, 2048, 10, 56, torch.float16, 3, 2, 0)
+    return {"config2": c2, "config4": c4}
+
+
 def measured_traffic():
     """HBM bytes per launch of the attention and quantize kernels from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -370,6 +431,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.probe_traffic:
         probe_traffic(torch, dev)
+        return
+    if args.other_configs:
+        print(json.dumps(other_configs(torch, dev)), flush=True)
         return
     if args.model:
         print(json.dumps(end_to_end(torch, dev)), flush=True)
@@ -447,6 +511,9 @@ def main():
     write = cache_write(torch, dev, codes[0], scales[0])
     prefill = prefill_attention(torch, dev, kv[0])
     model_e2e = end_to_end(torch, dev)
+    kv0 = kv[0]
+    del kv
+    others = other_configs(torch, dev)
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -523,8 +590,9 @@ def main():
     line["cache_write"] = write
     line["prefill_attention"] = prefill
     line["end_to_end"] = model_e2e
+    line["other_configs"] = others
     if args.cpu_baseline == "on":
-        line["cpu_baseline"] = cpu_baseline(torch, kv[0], codes[0], scales[0], args.cpu_sample_queries, layers)
+        line["cpu_baseline"] = cpu_baseline(torch, kv0, codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)
 
 

@@ -251,12 +251,14 @@ struct Geometry {
 };
 
 // Shapes with a 16-wave workgroup: narrow heads, where 32 query rows per wavefront fit in
-// 128 VGPRs (4 wavefronts per SIMD) with the pipelined logits in flight.
-constexpr bool has_16_waves(int dp, int mode) { return dp <= 32 || (dp == 48 && mode == kFold); }
+// 128 VGPRs (4 wavefronts per SIMD) with the pipelined logits in flight. (A 64-wide head in
+// the VALU mode needs more and spills.)
+constexpr bool has_16_waves(int dp, int mode) { return dp <= 32 || ((dp == 48 || dp == 64) && mode == kFold); }
 
-// Register budget: narrow heads keep 4 wavefronts per SIMD (two 8-wave workgroups per CU).
+// Register budget: heads up to 64 wide keep 4 wavefronts per SIMD (two 8-wave workgroups per
+// CU); without the bound the 64-wide fold kernel takes 135 VGPRs and only one workgroup fits.
 template <int DP, int NW>
-struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 48)) ? 4 : 1; };
+struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 64)) ? 4 : 1; };
 
 template <int DP, int KVT, int MODE, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))

@@ -190,14 +190,14 @@ def test_large_logits_exercise_rescaling(cuda, gain, d):
     check(got, exp)
 
 
-@pytest.mark.parametrize("d,nq", [(44, 600), (52, 200), (44, 64)])
+@pytest.mark.parametrize("d,nq", [(44, 600), (56, 600), (52, 200), (44, 64)])
 def test_key_norm_ramp_moves_the_max_late(cuda, d, nq):
     # Key magnitudes grow 20x along the context, so blocks early in the scan satisfy the
     # per-block logit bound (|q| max|k| - m <= slack: the per-step max test is skipped) while
     # later blocks must move the running max by more than the slack, several times. A bound
     # that were too small would let probabilities past the slack through unrescaled. Logits
     # stay within what f16 Q and K resolve at the 2e-2 bar (|q| ~ 3 per element). Shapes: the
-    # 16-wave kernel (d = 44, 600 queries), the 8-wave one (d = 52), the 2-wave one.
+    # 16-wave kernels (d = 44 and 56, 600 queries), the 8-wave one (d = 52), the 2-wave one.
     bg, h, nk = 2, 2, 3000
     kv = make_cache(bg, nk, h, d, cuda, seed=41)
     ramp = torch.linspace(0.05, 1.0, nk, device=cuda).view(1, nk, 1, 1, 1)
