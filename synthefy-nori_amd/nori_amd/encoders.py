@@ -16,10 +16,13 @@ loads into ``nori_amd.transformer.FeaturesTransformer`` with ``strict=True``:
 * the classification y encoder's modules (``EmbYEncoderStep`` :727-782,
   ``MulticlassTargetEncoder`` :785-822), kept for the state-dict schema.
 
+* the prompt-quantile piecewise-linear cell coordinates of Nori 1.5
+  (``PromptQuantilePLEEncoder`` :309-429): per-column context quantile edges built in the
+  preprocessing chain, expanded into the last channels of each cell token by ``MaskEmbEncoder``.
+
 These are small per-row torch expressions around the hot path (a few elementwise passes
-and GEMMs of width E); they run as torch ops on the device the tensors live on. The
-prompt-quantile PLE (Nori 1.5) and PBLD numeric embeddings are not part of the cached
-dense-stack models and raise ``NotImplementedError``.
+and GEMMs of width E); they run as torch ops on the device the tensors live on. The PBLD
+numeric embedding is not part of the nori models and raises ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -37,6 +40,7 @@ __all__ = [
     "MulticlassTargetEncoder",
     "NanEncoder",
     "NormalizationEncoder",
+    "PromptQuantilePLEEncoder",
     "RBFembedding",
     "ValidFeatureEncoder",
     "calc_mean",
@@ -245,9 +249,89 @@ class RBFembedding(nn.Module):
         return out if self.as_tokenizer else out.reshape(rows, -1)
 
 
+class PromptQuantilePLEEncoder(nn.Module):
+    """Context-only quantile edges for piecewise-linear cell coordinates (:309-429).
+
+    Preprocessing step: for every (table, group, feature) column it stores ``n_bins + 1``
+    edges, the quantiles at levels 0, 1/n_bins, ..., 1 of the column's valid context cells
+    (finite and not masked), linearly interpolated between order statistics; a column without
+    valid cells gets zero edges. Query rows never influence the edges, and a caller may pass
+    edges built earlier under ``frozen_reference_key``. ``encode`` turns cell values into the
+    coordinates ``MaskEmbEncoder`` appends to each cell token.
+    """
+
+    reference_key = "_prompt_quantile_ple_reference"
+    frozen_reference_key = "_frozen_prompt_quantile_ple_reference"
+
+    def __init__(self, n_bins: int):
+        super().__init__()
+        if n_bins < 2:
+            raise ValueError("prompt-quantile PLE requires at least 2 bins")
+        self.n_bins = int(n_bins)
+        self.register_buffer(
+            "quantile_levels", torch.linspace(0.0, 1.0, self.n_bins + 1, dtype=torch.float32), persistent=False
+        )
+
+    def _context_edges(self, x: torch.Tensor, valid: torch.Tensor, eval_pos: int) -> dict[str, torch.Tensor]:
+        ctx, ok = x[:, :eval_pos], valid[:, :eval_pos]
+        # invalid cells rank last, so the k-th valid value of a column sits at index k
+        ranked = torch.where(ok, ctx, torch.full_like(ctx, float("inf"))).permute(0, 2, 3, 1).sort(dim=-1).values
+        n_valid = ok.sum(dim=1)  # [B, G, F]
+        rank = (n_valid - 1).clamp(min=0).to(x.dtype).unsqueeze(-1) * self.quantile_levels.to(x.device, x.dtype)
+        below, above = rank.floor().to(torch.long), rank.ceil().to(torch.long)
+        lo, hi = ranked.gather(-1, below), ranked.gather(-1, above)
+        edges = lo + (rank - below.to(rank.dtype)) * (hi - lo)
+        edges = torch.where(n_valid.unsqueeze(-1) > 0, edges, torch.zeros_like(edges))
+        return {"edges": edges.detach()}
+
+    def _checked(self, reference: dict, x: torch.Tensor) -> dict[str, torch.Tensor]:
+        edges = reference.get("edges")
+        if not isinstance(edges, torch.Tensor):
+            raise TypeError("prompt-quantile PLE reference is missing tensor 'edges'")
+        want = (x.shape[0], x.shape[2], x.shape[3], self.n_bins + 1)
+        if tuple(edges.shape) != want:
+            raise ValueError(f"prompt-quantile PLE reference has shape {tuple(edges.shape)}, expected {want}")
+        return {"edges": edges.to(device=x.device, dtype=x.dtype)}
+
+    def forward(self, input: dict[str, Any]) -> dict[str, Any]:
+        x, mask = input.get("data"), input.get("mask")
+        if not isinstance(x, torch.Tensor) or not isinstance(mask, torch.Tensor):
+            raise TypeError("PromptQuantilePLEEncoder requires tensor data and mask inputs")
+        if x.dim() != 4 or mask.shape != x.shape:
+            raise ValueError("PromptQuantilePLEEncoder expects data and mask shaped [batch, rows, groups, features]")
+        frozen = input.get(self.frozen_reference_key)
+        if frozen is None:
+            eval_pos = int(input["eval_pos"])
+            if eval_pos <= 0 or eval_pos > x.shape[1]:
+                raise ValueError(f"eval_pos must select a non-empty context prefix, got {eval_pos} for {x.shape[1]} rows")
+            reference = self._context_edges(x, torch.isfinite(x) & ~mask.to(torch.bool), eval_pos)
+        elif isinstance(frozen, dict):
+            reference = frozen
+        else:
+            raise TypeError("_frozen_prompt_quantile_ple_reference must be a dictionary")
+        input[self.reference_key] = self._checked(reference, x)
+        return input
+
+    @staticmethod
+    def encode(x: torch.Tensor, reference: dict[str, torch.Tensor]) -> torch.Tensor:
+        """Coordinates [B, S, G, F, n_bins] of cells x [B, S, G, F]: channel i is
+        clamp((x - e_i) / (e_{i+1} - e_i), 0, 1), so bins below the value read 1, its own bin
+        the fraction, bins above 0. A bin of zero width and a non-finite cell read 0."""
+        edges = reference["edges"].to(device=x.device, dtype=x.dtype)
+        left = edges[..., :-1].unsqueeze(-2)
+        width = (edges[..., 1:] - edges[..., :-1]).unsqueeze(-2)
+        open_bin = width > 0
+        values = x.permute(0, 2, 3, 1).unsqueeze(-1)  # [B, G, F, S, 1]
+        coords = ((values - left) / torch.where(open_bin, width, torch.ones_like(width))).clamp(0.0, 1.0)
+        coords = torch.where(torch.isfinite(values) & open_bin, coords, torch.zeros_like(coords))
+        return coords.permute(0, 3, 1, 2, 4).contiguous()
+
+
 class MaskEmbEncoder(nn.Module):
     """Per-cell numeric embedding, a learned vector for missing cells, and a fusion MLP over a
-    group's cells (:432-585)."""
+    group's cells (:432-585). With ``prompt_quantile_ple_bins`` > 0 (Nori 1.5) the numeric
+    embedding fills the first E - bins channels of a cell token and the cell's PLE
+    coordinates the rest."""
 
     def __init__(
         self,
@@ -264,13 +348,22 @@ class MaskEmbEncoder(nn.Module):
         out_key: str = "data",
     ):
         super().__init__()
-        if int(prompt_quantile_ple_bins):
-            raise NotImplementedError("prompt-quantile PLE tokens (Nori 1.5) are not part of the cached dense path")
+        bins = int(prompt_quantile_ple_bins)
+        if bins < 0:
+            raise ValueError("prompt_quantile_ple_bins cannot be negative")
+        if bins == 1:
+            raise ValueError("prompt_quantile_ple_bins must be 0 (disabled) or at least 2")
+        if bins >= emsize:
+            raise ValueError("prompt_quantile_ple_bins must be smaller than the embedding dimension")
+        if bins and in_keys != ["data"]:
+            raise ValueError("prompt-quantile PLE requires in_keys=['data']")
+        if bins and numeric_embed_type != "RBF":
+            raise ValueError("prompt-quantile PLE is supported only with the RBF numeric encoder")
         self.embedding_dim = emsize
         self.mask_embedding_size = mask_embedding_size
         self.in_keys = in_keys
         self.out_key = out_key
-        self.prompt_quantile_ple_bins = 0
+        self.prompt_quantile_ple_bins = bins
         self.mask_embedding = nn.Parameter(torch.randn(mask_embedding_size))
         self.numeric_embed_type = numeric_embed_type
         half = emsize // 2
@@ -284,7 +377,7 @@ class MaskEmbEncoder(nn.Module):
                 if key in cfg and cfg[key] != only:
                     raise ValueError(f"Unsupported RBF_config options in this release: {{{key!r}: {cfg[key]!r}}}")
             self.numeric_mlp = RBFembedding(
-                embedding_size=emsize,
+                embedding_size=emsize - bins,
                 exponent_digits=1,
                 token_embed_dim=cfg["token_embed_dim"],
                 n_kernels=cfg["n_kernels"],
@@ -315,7 +408,13 @@ class MaskEmbEncoder(nn.Module):
         b, s, g, _ = x.shape
         x = x.unsqueeze(-1)
         missing = torch.isnan(x)
-        emb = self.numeric_mlp(x.masked_fill(missing, 0.0))
+        x = x.masked_fill(missing, 0.0)
+        emb = self.numeric_mlp(x)
+        if self.prompt_quantile_ple_bins:
+            reference = input.get(PromptQuantilePLEEncoder.reference_key)
+            if not isinstance(reference, dict):
+                raise TypeError("prompt-quantile PLE reference is required when the tokenizer is enabled")
+            emb = torch.cat((emb, PromptQuantilePLEEncoder.encode(x.squeeze(-1), reference).to(emb.dtype)), dim=-1)
         if not self.nan_to_zero:
             emb = torch.where(missing, self.mask_embedding.expand_as(emb), emb)
         input[self.out_key] = self.fusion_network(emb.flatten(3)).view(b, s, g, -1)
@@ -561,12 +660,13 @@ def preprocesss_4_x(
     normalize_by_used_features: bool,
     prompt_quantile_ple_bins: int = 0,
 ):
-    """[NanEncoder] -> NormalizationEncoder -> ValidFeatureEncoder (:972-1009)."""
-    if prompt_quantile_ple_bins:
-        raise NotImplementedError("prompt-quantile PLE preprocessing (Nori 1.5) is not part of the cached dense path")
+    """[NanEncoder] -> NormalizationEncoder -> ValidFeatureEncoder [-> PromptQuantilePLEEncoder]
+    (:972-1009)."""
     steps: list[nn.Module] = []
     if nan_handling_enabled:
         steps.append(NanEncoder(in_keys=["data"], out_key="nan_encoding"))
     steps.append(NormalizationEncoder(train_only=normalize_on_train_only, normalize_x=normalize_x, remove_outliers=remove_outliers))
     steps.append(ValidFeatureEncoder(num_features=num_features, nan_normalize=normalize_by_used_features))
+    if prompt_quantile_ple_bins:
+        steps.append(PromptQuantilePLEEncoder(prompt_quantile_ple_bins))
     return nn.Sequential(*steps)
