@@ -160,8 +160,11 @@ def test_unsupported_and_invalid_levers_raise(gold):
         model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], stream_context=True, fit_row_chunk=32)
     with pytest.raises(ValueError, match="concrete cache_dtype"):
         model.build_context_cache(x[:, :n_ctx], y[:, :n_ctx], cache_dtype="fp8")
+    two_phase = NT.FeaturesTransformer(
+        **config(VARIANTS["a"]), two_phase_config={"target_tokens": 1, "row_layers": 1, "row_heads": 2, "row_hidden_dim": 32}
+    )
     with pytest.raises(NotImplementedError, match="two-phase"):
-        NT.FeaturesTransformer(**config(VARIANTS["a"]), two_phase_config={"target_tokens": 1})
+        two_phase.build_context_cache(x[:, :n_ctx], y[:, :n_ctx])
     cfg = config(VARIANTS["a"])
     cfg["preprocess_config_x"] = dict(cfg["preprocess_config_x"], normalize_on_train_only=False)
     with pytest.raises(NotImplementedError, match="normalize_on_train_only"):
