@@ -76,6 +76,11 @@ def parse_args():
         help="measure only the kernel-level legs of configs 2 (nori-6m block) and 4 (nori-100m layer)",
     )
     p.add_argument(
+        "--small-tables", action="store_true",
+        help="measure only the many-small-tables path: a nori-1-5-shaped two-phase model over 512 tables of "
+        "256 context + 64 query rows",
+    )
+    p.add_argument(
         "--model", action="store_true",
         help="measure only the model-level context-cache API end to end (build once, 4 query batches)",
     )
@@ -340,6 +345,76 @@ def end_to_end(torch, dev, batches=QUERY_BATCHES):
     }
 
 
+# A random-init two-phase model of about Nori 1.5's size (20.8 M parameters; its dims are not in
+# the reference's sources): 128-wide cells with 2 heads of 64, 12 cell layers, 2 target tokens,
+# 6 row layers of width 256 with 4 heads of 64, PLE cells of 32 bins, 999 quantiles.
+SMALL_TABLES = dict(tables=512, context=256, queries=64, features=8, reps=5)
+
+
+def two_phase_config():
+    return dict(
+        preprocess_config_x=dict(
+            num_features=2, nan_handling_enabled=True, normalize_on_train_only=True, normalize_x=True,
+            remove_outliers=False, normalize_by_used_features=True, prompt_quantile_ple_bins=32,
+        ),
+        encoder_config_x=dict(
+            num_features=2, embedding_size=128, mask_embedding_size=128, encoder_use_bias=True, numeric_embed_type="RBF",
+            RBF_config=dict(token_embed_dim=8, n_kernels=16, sigma=0.5, use_learn_sigma=False,
+                            use_learn_embeddings=False, use_original_features=False),
+            prompt_quantile_ple_bins=32,
+        ),
+        encoder_config_y=dict(num_inputs=1, embedding_size=128, nan_handling_y_encoder=True, max_num_classes=10),
+        decoder_config=dict(num_reg_quantiles=999, regression_loss="pinball"),
+        nlayers=12, nhead=2, embed_dim=128, hid_dim=384, features_per_group=2, dropout=0.0, pre_norm=True,
+        activation="swiglu", norm_type="rmsnorm", deepnorm_alpha=18 ** -0.5, feature_positional_embedding_type="subortho",
+        use_target_aware_embedding=True, use_column_specific_y_aware=True, use_qassmax=True, qass_mode="log_only",
+        omit_feature_decoder=True, two_phase_config=dict(target_tokens=2, row_layers=6, row_heads=4, row_hidden_dim=1024),
+    )
+
+
+def small_tables(torch, dev):
+    """The many-small-tables path: 512 independent tables of 256 context + 64 query rows x 8
+    float32 features X ~ U(-3, 3), y a random degree-2 polynomial of X + 0.05 N(0, 1), through
+    the two-phase model's forward (context and query rows together, as Nori 1.5 runs it) under
+    the fp16 autocast of GPU inference; quantiles 0.05 / 0.5 / 0.95 taken from the 999-level
+    head. Wall clock over `reps` forwards with the device synchronized, after one warm-up."""
+    import nori_amd
+
+    c = SMALL_TABLES
+    g = torch.Generator().manual_seed(4)
+    rows = c["context"] + c["queries"]
+    x = torch.rand(c["tables"], rows, c["features"], generator=g) * 6.0 - 3.0
+    quad = torch.randn(c["tables"], c["features"], c["features"], generator=g) / c["features"]
+    lin = torch.randn(c["tables"], c["features"], generator=g) / c["features"] ** 0.5
+    y = torch.einsum("bnf,bfg,bng->bn", x, quad, x) + (x * lin[:, None]).sum(-1)
+    y = y + 0.05 * torch.randn(y.shape, generator=g)
+    x, y = x.to(dev), y[:, : c["context"]].to(dev)
+    model = nori_amd.FeaturesTransformer(**two_phase_config()).eval().to(dev)
+    n_params = sum(p.numel() for p in model.parameters())
+    pick = torch.tensor([49, 499, 949], device=dev)  # levels 0.05, 0.5, 0.95 of (i + 1) / 1000
+
+    def forward():
+        return model(x=x, y=y, eval_pos=c["context"], task_type="reg").index_select(-1, pick)
+
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        out = forward()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(c["reps"]):
+            out = forward()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / c["reps"]
+    assert out.shape == (c["tables"], c["queries"], 3) and bool(torch.isfinite(out).all())
+    return {
+        "what": "config 5: many small tables, a nori-1-5-shaped two-phase model "
+        f"({n_params / 1e6:.1f} M parameters, random init): {c['tables']} tables x ({c['context']} context + "
+        f"{c['queries']} query rows) x {c['features']} features, fp16 autocast, quantiles 0.05/0.5/0.95",
+        "ms_per_forward": round(dt * 1e3, 3),
+        "query_rows_per_s": round(c["tables"] * c["queries"] / dt, 1),
+        "tables_per_s": round(c["tables"] / dt, 1),
+    }
+
+
 def other_configs(torch, dev):
     """Kernel-level legs of the other cached configurations, each timed with HIP events:
     config 2, the isolated ICL block at nori-6m dims (1 table, G = 9 tokens, 4096 context rows,
@@ -437,6 +512,9 @@ def main():
         return
     if args.model:
         print(json.dumps(end_to_end(torch, dev)), flush=True)
+        return
+    if args.small_tables:
+        print(json.dumps(small_tables(torch, dev)), flush=True)
         return
     if args.prefill:
         shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)

@@ -98,7 +98,9 @@ int nori_kv_dequantize_int8(const int8_t* codes, const float* scales, int64_t n_
  * Replaces RMSNorm.forward (src/synthefy_nori/model/layer.py:251-258), native
  * (F.rms_norm) variant: statistic and product in fp32, one rounding to `dtype`.
  * weight may be NULL (elementwise_affine=False, the layer norms of layer.py:1346-1349);
- * otherwise it has `cols` elements of `weight_dtype`.
+ * otherwise it has `cols` elements of `weight_dtype`. y may be x (in place, same row stride):
+ * the per-head key norm of the two-phase attentions (layer.py:497-500) normalizes the K half
+ * of a projected [.., 2, H, D] K/V tensor in place, one head (rows at stride 2*H*D) a call.
  */
 int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
                   const void* weight, int weight_dtype, float eps, void* y, int64_t y_row_stride,

@@ -63,6 +63,7 @@ int device_cu_count() {
 }
 
 struct Plan {
+    bool short_ctx;  // the VALU kernel for few queries over few keys (no tiles, no split)
     int dp;          // head width padded to the logit MFMA granule (16)
     int mode;        // how logits and the denominator are formed (attn::Mode)
     int nw;          // wavefronts per workgroup (32 query rows each)
@@ -80,6 +81,7 @@ struct Plan {
 // the partials' HBM traffic.
 Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     Plan p;
+    p.short_ctx = short_context(nq, nk);
     p.dp = (d + 15) / 16 * 16;
     p.mode = mode_for(d);
     p.nw = (nq > 256 && has_16_waves(p.dp, p.mode)) ? 16 : (nq > 96 ? 8 : 2);
@@ -96,7 +98,7 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     p.n_whole = p.nunits;
     p.nsplit = 1;
     p.kps = nkb * KB;
-    if (tail == 0) return p;
+    if (tail == 0 || p.short_ctx) return p;
     double best = (double)(full + 1) * nkb * t_blk;
     const int64_t max_split = std::max<int64_t>(1, std::min<int64_t>(64, nkb / 4));
     for (int64_t ns = 2; ns <= max_split; ++ns) {
@@ -198,6 +200,10 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
     if (args.grid * plan.nw * 64 > 0xffffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: grid too large");
 
     hipStream_t stream = (hipStream_t)stream_v;
+    if (plan.short_ctx) {
+        const int st = launch_short(kv_dtype, args, stream);
+        return st != NORI_OK ? st : launch_status("icl_attention short");
+    }
     int st = launch_kvt(kv_dtype, plan.dp, plan.mode, plan.nw, args, stream);
     if (st != NORI_OK) return st;
     if ((st = launch_status("icl_attention")) != NORI_OK) return st;

@@ -683,6 +683,13 @@ icl_attention_kernel(const Args a) {
     }
 }
 
+// The short-context kernel (icl_attention_short.hip): one launch over every (b, h, query) row.
+int launch_short(int kv_dtype, const Args& a, hipStream_t stream);
+
+// Few queries attending to few keys: the VALU kernel, whose cost grows with nq * nk, beats the
+// MFMA kernel's fixed cost per (b, h) unit (a 64-query tile over a staged 64-key block).
+constexpr bool short_context(int64_t nq, int64_t nk) { return nq <= 64 && nk <= 128 && nq * nk <= 2048; }
+
 // Launches the kernel instantiation for (cache dtype KVT, dp, mode, nw) over a.grid
 // workgroups. Each icl_attention_<dtype>.hip instantiates one KVT (parallel builds).
 template <int KVT, int DP, int MODE>

@@ -1,0 +1,160 @@
+// Query-row -> context attention for short contexts and few queries (the in-row attentions of
+// the two-phase encoder: a cell over its row's few cells and target tokens, a row over its own
+// cells). Chosen by the planner in icl_attention.hip when the MFMA kernel's fixed cost per
+// (b, h) unit -- a 64-query tile, a 64-key staged block, the pipeline fill -- would dwarf the
+// work. Same arguments and results as that kernel (dense output, LSE, running-output merge).
+//
+// One group of G lanes per (b, h, query) row, G = d/4 rounded up to a power of two: a lane holds
+// 4 head elements of the query, its partial logit per key is summed over the group with DPP
+// (all within a 16-lane row; a 32-lane group adds one swizzle), and the online softmax runs in
+// fp32 on the VALU, key by key, from K/V rows loaded 4 elements per lane (16-, 8- or 4-byte
+// loads). The rows of one (b, h) are consecutive, so the groups of a wavefront read the same
+// K/V rows. Values are computed in fp32 from the exact cache values (codes x scales for int8).
+#include <math.h>
+
+#include "icl_attention_kernel.h"
+
+namespace {
+
+using namespace nori;
+using namespace nori::attn;
+
+constexpr int kThreads = 256;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the G lanes of a group (G a power of two up to 32); every lane gets the sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (G >= 2) v += dpp<0xb1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    if constexpr (G >= 4) v += dpp<0x4e>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    if constexpr (G >= 8) v += dpp<0x141>(v);  // row_half_mirror: the other quad of 8
+    if constexpr (G >= 16) v += dpp<0x140>(v); // row_mirror: the other 8 of 16
+    if constexpr (G >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+// 4 consecutive cache elements at element index i (4-element aligned) as fp32 (int8: codes).
+template <int KVT>
+__device__ __forceinline__ f32x4 load4(const void* p, int64_t i) {
+    f32x4 r;
+    if constexpr (KVT == NORI_F32) {
+        r = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p) + i);
+    } else if constexpr (KVT == NORI_I8) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(p) + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (float)(int8_t)(w >> (8 * e));
+    } else {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(p) + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            r[e] = KVT == NORI_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+        }
+    }
+    return r;
+}
+
+template <int KVT, int G>
+__global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Args a, int64_t rows) {
+    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int64_t row = t / G;  // (b, h, query) with the query fastest
+    const bool valid = row < rows;
+    if (!valid) row = rows - 1;  // keep every lane of the group active through the reductions
+    const int sub = (int)(threadIdx.x % G);
+    const int64_t qi = row % a.nq;
+    const int64_t bh = row / a.nq;
+    const int h = (int)(bh % a.heads);
+    const int64_t b = bh / a.heads;
+    const int hk = h / a.hgroup;
+    const int c0 = 4 * sub;
+    const bool live = c0 < a.d;  // d % 4 == 0: a lane's 4 elements are all in or all out
+
+    f32x4 q = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        const int64_t qb = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head + c0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = load_as_f32(a.q, a.q_dtype, qb + e) * a.scale_log2;
+    }
+    const int64_t kbase = b * a.kv_bg + (int64_t)hk * a.d + c0;
+    const int64_t sbase = b * a.sc_bg + hk;
+    float m = -INFINITY, l = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (int64_t j = 0; j < a.nk; ++j) {
+        f32x4 k = {0.f, 0.f, 0.f, 0.f}, v = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            k = load4<KVT>(a.kv, kbase + j * a.kv_row);
+            v = load4<KVT>(a.kv, kbase + j * a.kv_row + a.kv_half);
+        }
+        float s = group_sum<G>(q[0] * k[0] + q[1] * k[1] + q[2] * k[2] + q[3] * k[3]);
+        float vs = 1.f;
+        if constexpr (KVT == NORI_I8) {
+            s *= a.kvs[sbase + j * a.sc_row];
+            vs = a.kvs[sbase + j * a.sc_row + a.sc_half];
+        }
+        const float m_new = fmaxf(m, s);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        const float p = __builtin_amdgcn_exp2f(s - m_new);
+        l = l * alpha + p;
+        o = o * alpha + (p * vs) * v;
+        m = m_new;
+    }
+    if (!valid) return;
+    const float inv = 1.0f / l;
+    const float lse_part = (m + __log2f(l)) * kLn2;
+    const bool merge = a.flags & NORI_ATTN_MERGE;
+    float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
+    if (merge) merge_weights(a.lse[row], lse_part, w_old, w_new, lse_out);
+    if (live) {
+        const int64_t ob = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head + c0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float r = o[e] * inv;
+            if (merge) r = reinterpret_cast<const float*>(a.out)[ob + e] * w_old + r * w_new;
+            store_from_f32(a.out, a.out_dtype, ob + e, r);
+        }
+    }
+    if (a.lse && sub == 0) a.lse[row] = lse_out;
+}
+
+template <int KVT>
+int launch_group(const Args& a, hipStream_t stream) {
+    const int quads = (a.d + 3) / 4;
+    const int64_t rows = a.bg * a.heads * a.nq;
+    int g = 1;
+    while (g < quads) g *= 2;
+    const int64_t threads = rows * g;
+    if ((threads + kThreads - 1) / kThreads > 0x7fffffffLL)
+        return fail(NORI_ERR_UNSUPPORTED, "icl_attention: %lld query rows exceed one launch", (long long)rows);
+    const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads)), block(kThreads);
+    switch (g) {
+        case 1: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 1>), grid, block, 0, stream, a, rows); break;
+        case 2: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 2>), grid, block, 0, stream, a, rows); break;
+        case 4: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 4>), grid, block, 0, stream, a, rows); break;
+        case 8: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 8>), grid, block, 0, stream, a, rows); break;
+        case 16: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 16>), grid, block, 0, stream, a, rows); break;
+        default: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 32>), grid, block, 0, stream, a, rows); break;
+    }
+    return NORI_OK;
+}
+
+}  // namespace
+
+namespace nori {
+namespace attn {
+
+int launch_short(int kv_dtype, const Args& a, hipStream_t stream) {
+    switch (kv_dtype) {
+        case NORI_I8: return launch_group<NORI_I8>(a, stream);
+        case NORI_F16: return launch_group<NORI_F16>(a, stream);
+        case NORI_BF16: return launch_group<NORI_BF16>(a, stream);
+        default: return launch_group<NORI_F32>(a, stream);
+    }
+}
+
+}  // namespace attn
+}  // namespace nori

@@ -64,11 +64,12 @@ __device__ __forceinline__ uint4 pack_chunk(const float* f) {
     return c;
 }
 
-// G lanes per row; rows_per_block = kThreads / G.
+// G lanes per row; rows_per_block = kThreads / G. A row's lanes load all of it before the
+// reduction and store after it, so y may be x (in place; no restrict qualifiers).
 template <int DT, int WDT, int G>
 __global__ void __launch_bounds__(kThreads)
-rms_norm_chunked_kernel(const uint8_t* __restrict__ x, int64_t rows, int cols, int64_t x_row_bytes,
-                        const void* __restrict__ w, float eps, uint8_t* __restrict__ y, int64_t y_row_bytes) {
+rms_norm_chunked_kernel(const uint8_t* x, int64_t rows, int cols, int64_t x_row_bytes,
+                        const void* w, float eps, uint8_t* y, int64_t y_row_bytes) {
     constexpr int EPC = 16 / (DT == NORI_F32 ? 4 : 2);  // elements per 16-byte chunk
     const int lane_in_row = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
@@ -104,11 +105,12 @@ rms_norm_chunked_kernel(const uint8_t* __restrict__ x, int64_t rows, int cols, i
     }
 }
 
-// One wavefront per row, element-wise loads: any width and alignment.
+// One wavefront per row, element-wise loads: any width and alignment. Each element is read
+// and then written by the same lane, so y may be x.
 template <int DT, int WDT>
 __global__ void __launch_bounds__(kThreads)
-rms_norm_elementwise_kernel(const void* __restrict__ x, int64_t rows, int cols, int64_t x_row_stride,
-                            const void* __restrict__ w, float eps, void* __restrict__ y, int64_t y_row_stride) {
+rms_norm_elementwise_kernel(const void* x, int64_t rows, int cols, int64_t x_row_stride,
+                            const void* w, float eps, void* y, int64_t y_row_stride) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
     if (row >= rows) return;

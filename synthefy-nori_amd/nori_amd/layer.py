@@ -37,7 +37,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
-from .norm import RMSNorm
+from .norm import RMSNorm, rms_norm_
 
 ACTIVATION_FN = {"gelu": nn.GELU(), "relu": nn.ReLU(), "silu": nn.SiLU()}
 _SDPA_BACKENDS_WITHOUT_CUDNN = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]
@@ -245,8 +245,14 @@ class MultiheadAttention(nn.Module):
         return q if self.q_norm is None else self.q_norm(q)
 
     def _norm_kv(self, kv):
-        """kv: [..., 2, heads, head_dim]; normalizes the K half only."""
+        """kv: [..., 2, heads, head_dim], a fresh projection; normalizes the K half only. On the
+        GPU the K rows are normalized in place, head by head (rows at one stride), instead of
+        stacking a normalized copy of K with V (a full copy of the K/V tensor)."""
         if self.k_norm is None:
+            return kv
+        if kv.is_cuda and kv.is_contiguous():
+            for h in range(kv.shape[-2]):
+                rms_norm_(kv[..., 0, h, :], self.k_norm.weight, self.k_norm.eps)
             return kv
         return torch.stack((self.k_norm(kv[..., 0, :, :]), kv[..., 1, :, :]), dim=-3)
 

@@ -8,6 +8,48 @@ import torch.nn as nn
 from . import _native as nat
 
 
+def _strided_rows(t: torch.Tensor, cols: int) -> tuple[int, int] | None:
+    """(rows, row stride) when ``t``'s rows of ``cols`` contiguous elements sit at one stride."""
+    if t.stride(-1) != 1 or (t.dim() > 1 and t.shape[-1] != cols):
+        return None
+    lead = [(n, st) for n, st in zip(t.shape[:-1], t.stride()[:-1]) if n != 1]
+    if not lead:
+        return 1, cols
+    for (n_outer, s_outer), (n_inner, s_inner) in zip(lead, lead[1:]):
+        if s_outer != n_inner * s_inner:
+            return None
+    rows = 1
+    for n, _ in lead:
+        rows *= n
+    return rows, lead[-1][1]
+
+
+def rms_norm_(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """In-place ``rms_norm`` over the last axis of a row view, e.g. the K half of a projected
+    [..., 2, H, D] K/V tensor taken one head at a time: rows of D contiguous elements at one
+    stride. Each row is read whole before it is written."""
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise NotImplementedError(f"rms_norm takes float32/float16/bfloat16, got {x.dtype}")
+    device = nat.require_device(x, weight)
+    cols = int(x.shape[-1])
+    layout = _strided_rows(x, cols)
+    if layout is None:
+        raise ValueError(f"rms_norm_ needs rows at one stride, got shape {tuple(x.shape)} strides {x.stride()}")
+    rows, stride = layout
+    w = None if weight is None else weight.reshape(cols).contiguous()
+    if x.numel() == 0:
+        return x
+    nat.check(
+        nat.lib().nori_rms_norm(
+            x.data_ptr(), nat.dtype_code(x.dtype), rows, cols, stride,
+            nat.ptr(w), nat.dtype_code(w.dtype) if w is not None else nat.NORI_F32, float(eps),
+            x.data_ptr(), stride, nat.stream_of(device),
+        ),
+        "rms_norm",
+    )
+    return x
+
+
 def rms_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
     """x * rsqrt(mean(x^2) + eps) (* weight) over the trailing ``normalized_shape`` axes.
 

@@ -117,6 +117,39 @@ def test_ragged_lengths(cuda, nk, nq):
     check(got, exp)
 
 
+SHORT_CACHES = {"i8": torch.float16, "f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("d", [4, 8, 16, 44, 64, 128])
+@pytest.mark.parametrize("kv_kind", ["i8", "f16", "bf16", "f32"])
+@pytest.mark.parametrize("nq,nk", [(5, 7), (1, 1), (64, 32), (16, 128)])
+def test_short_context_path(cuda, d, kv_kind, nq, nk):
+    """Few queries over few keys (nq <= 64, nk <= 128, nq * nk <= 2048) take the VALU kernel:
+    the in-row attentions of the two-phase encoder. GQA (4 query heads on 2 K/V heads), the
+    LSE output, and the running-output merge of two context halves."""
+    bg, heads, kv_heads = 37, 4, 2
+    kv = make_cache(bg, nk, kv_heads, d, cuda, seed=d + nk, dtype=SHORT_CACHES[kv_kind])
+    q = make_queries(bg, nq, heads, d, cuda, seed=d + nq, dtype=torch.float16)
+    if kv_kind == "i8":
+        codes, scales = nori_amd.quantize_int8(kv)
+        values = codes.double() * scales.double()
+        call = lambda sl, **kw: nori_amd.icl_attention(q, codes[:, sl], scales[:, sl], **kw)  # noqa: E731
+    else:
+        values = kv.double()
+        call = lambda sl, **kw: nori_amd.icl_attention(q, kv[:, sl], **kw)  # noqa: E731
+    lse = torch.empty(bg, heads, nq, device=cuda)
+    got = call(slice(0, nk), lse=lse)
+    exp, exp_lse = reference(q, values)
+    check(got, exp)
+    assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, heads // kv_heads)).all()
+    if nk > 1:
+        run = torch.zeros(bg, nq, heads, d, device=cuda)
+        lse2 = torch.full((bg, heads, nq), float("-inf"), device=cuda)
+        for sl in (slice(0, nk // 2), slice(nk // 2, nk)):
+            call(sl, out=run, lse=lse2, merge=True)
+        check(run, exp)
+
+
 def test_split_context_schedule(cuda):
     # one small (bg, head, query tile) grid over a long context: the kernel splits the
     # context across workgroups and merges the partial (O, LSE) pairs
