@@ -107,6 +107,17 @@ int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t 
                   void* stream);
 
 /*
+ * nori_rms_norm with the result written as `y_dtype`: fp32 rows may be written as fp16 or
+ * bf16 (any other pair is NORI_ERR_UNSUPPORTED). The value is the fp32 norm rounded once to
+ * y_dtype -- bit for bit what an autocast projection's input cast makes of the norm's fp32
+ * output (RMSNorm under torch.autocast, layer.py:251-258, followed by F.linear), so a norm
+ * that feeds a projection hands it its operand directly instead of an fp32 copy to cast.
+ */
+int nori_rms_norm_to(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
+                     const void* weight, int weight_dtype, float eps, void* y, int y_dtype,
+                     int64_t y_row_stride, void* stream);
+
+/*
  * Query-row -> context attention over a K/V cache:
  *     out[b, i, h, :] = softmax_j(scale * q[b, i, h, :] . k[b, j, hk, :]) @ v[b, j, hk, :]
  * with hk = h / (heads / kv_heads) (MQA/GQA broadcast, layer.py:640-649, 956).

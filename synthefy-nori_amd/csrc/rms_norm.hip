@@ -64,13 +64,33 @@ __device__ __forceinline__ uint4 pack_chunk(const float* f) {
     return c;
 }
 
+// The EPC outputs of one chunk, rounded to DT (the norm's result dtype) and stored as OT: a
+// 16-byte store when OT is DT, 8 bytes for an fp32 row written as fp16/bf16 (the cast an
+// autocast projection applies to the fp32 result, bit for bit).
+template <int DT, int OT, int EPC>
+__device__ __forceinline__ void store_chunk(uint8_t* p, const float* o) {
+    if constexpr (OT == DT) {
+        *reinterpret_cast<uint4*>(p) = pack_chunk<DT>(o);
+    } else {
+        static_assert(DT == NORI_F32 && EPC == 4, "narrowing stores are from fp32 rows");
+        uint2 c;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = OT == NORI_F16 ? f32_to_f16(o[e]) : f32_to_bf16(o[e]);
+        c.x = h[0] | ((uint32_t)h[1] << 16);
+        c.y = h[2] | ((uint32_t)h[3] << 16);
+        *reinterpret_cast<uint2*>(p) = c;
+    }
+}
+
 // G lanes per row; rows_per_block = kThreads / G. A row's lanes load all of it before the
 // reduction and store after it, so y may be x (in place; no restrict qualifiers).
-template <int DT, int WDT, int G>
+template <int DT, int WDT, int OT, int G>
 __global__ void __launch_bounds__(kThreads)
 rms_norm_chunked_kernel(const uint8_t* x, int64_t rows, int cols, int64_t x_row_bytes,
                         const void* w, float eps, uint8_t* y, int64_t y_row_bytes) {
     constexpr int EPC = 16 / (DT == NORI_F32 ? 4 : 2);  // elements per 16-byte chunk
+    constexpr int OUT_CHUNK = EPC * (OT == NORI_F32 ? 4 : 2);  // bytes of one chunk's outputs
     const int lane_in_row = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
     const int nchunks = cols / EPC;
@@ -100,14 +120,14 @@ rms_norm_chunked_kernel(const uint8_t* x, int64_t rows, int cols, int64_t x_row_
                 o[e] = round_to<DT>(v[k][e] * inv);
                 if (w) o[e] = o[e] * load_elem<WDT>(w, (int64_t)ch * EPC + e);
             }
-            *reinterpret_cast<uint4*>(y + row * y_row_bytes + (int64_t)ch * 16) = pack_chunk<DT>(o);
+            store_chunk<DT, OT, EPC>(y + row * y_row_bytes + (int64_t)ch * OUT_CHUNK, o);
         }
     }
 }
 
 // One wavefront per row, element-wise loads: any width and alignment. Each element is read
 // and then written by the same lane, so y may be x.
-template <int DT, int WDT>
+template <int DT, int WDT, int OT>
 __global__ void __launch_bounds__(kThreads)
 rms_norm_elementwise_kernel(const void* x, int64_t rows, int cols, int64_t x_row_stride,
                             const void* w, float eps, void* y, int64_t y_row_stride) {
@@ -125,17 +145,19 @@ rms_norm_elementwise_kernel(const void* x, int64_t rows, int cols, int64_t x_row
     for (int c = lane; c < cols; c += 64) {
         float o = round_to<DT>(load_elem<DT>(x, row * x_row_stride + c) * inv);
         if (w) o = o * load_elem<WDT>(w, c);
-        store_elem<DT>(y, row * y_row_stride + c, o);
+        store_elem<OT>(y, row * y_row_stride + c, round_to<DT>(o));
     }
 }
 
-template <int DT, int WDT>
+template <int DT, int WDT, int OT>
 int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, float eps, void* y, int64_t ys,
            hipStream_t stream) {
     constexpr int es = (DT == NORI_F32) ? 4 : 2;
+    constexpr int os = (OT == NORI_F32) ? 4 : 2;
     constexpr int EPC = 16 / es;
-    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ((xs * es) % 16 == 0) &&
-                         ((ys * es) % 16 == 0) && (cols % EPC == 0);
+    constexpr int OUT_CHUNK = EPC * os;
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % OUT_CHUNK == 0) && ((xs * es) % 16 == 0) &&
+                         ((ys * os) % OUT_CHUNK == 0) && (cols % EPC == 0);
     const int nchunks = cols / EPC;
     if (aligned && nchunks <= 64 * kMaxChunksPerLane) {
         int g = 1;
@@ -144,8 +166,8 @@ int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, flo
         const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
 #define NORI_RMS_CASE(GV)                                                                                     \
     case GV:                                                                                                   \
-        hipLaunchKernelGGL((rms_norm_chunked_kernel<DT, WDT, GV>), dim3(grid), dim3(kThreads), 0, stream,       \
-                           (const uint8_t*)x, rows, cols, xs * es, w, eps, (uint8_t*)y, ys * es);              \
+        hipLaunchKernelGGL((rms_norm_chunked_kernel<DT, WDT, OT, GV>), dim3(grid), dim3(kThreads), 0, stream,   \
+                           (const uint8_t*)x, rows, cols, xs * es, w, eps, (uint8_t*)y, ys * os);              \
         break;
         switch (g) {
             NORI_RMS_CASE(1) NORI_RMS_CASE(2) NORI_RMS_CASE(4) NORI_RMS_CASE(8)
@@ -154,7 +176,7 @@ int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, flo
 #undef NORI_RMS_CASE
     } else {
         const unsigned grid = (unsigned)((rows + (kThreads / 64) - 1) / (kThreads / 64));
-        hipLaunchKernelGGL((rms_norm_elementwise_kernel<DT, WDT>), dim3(grid), dim3(kThreads), 0, stream, x, rows,
+        hipLaunchKernelGGL((rms_norm_elementwise_kernel<DT, WDT, OT>), dim3(grid), dim3(kThreads), 0, stream, x, rows,
                            cols, xs, w, eps, y, ys);
     }
     return launch_status("rms_norm");
@@ -162,10 +184,13 @@ int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, flo
 
 }  // namespace
 
-extern "C" int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
-                             const void* weight, int weight_dtype, float eps, void* y, int64_t y_row_stride,
-                             void* stream_v) {
+extern "C" int nori_rms_norm_to(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
+                                const void* weight, int weight_dtype, float eps, void* y, int y_dtype,
+                                int64_t y_row_stride, void* stream_v) {
     clear_error();
+    if (y_dtype != dtype && !(dtype == NORI_F32 && (y_dtype == NORI_F16 || y_dtype == NORI_BF16)))
+        return fail(NORI_ERR_UNSUPPORTED, "rms_norm: %s rows cannot be written as %s (fp32 rows may be written as "
+                    "fp16 or bf16)", dtype_name(dtype), dtype_name(y_dtype));
     if (rows < 0 || cols <= 0) return fail(NORI_ERR_INVALID, "rms_norm: bad shape rows=%lld cols=%d", (long long)rows, cols);
     if (dtype != NORI_F32 && dtype != NORI_F16 && dtype != NORI_BF16)
         return fail(NORI_ERR_UNSUPPORTED, "rms_norm: unsupported dtype %s", dtype_name(dtype));
@@ -176,8 +201,23 @@ extern "C" int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t col
     if (!weight) weight_dtype = dtype;
     hipStream_t stream = (hipStream_t)stream_v;
     int st = NORI_OK;
-    NORI_DISPATCH_FLOAT(dtype, DT,
+    if (y_dtype == dtype) {
+        NORI_DISPATCH_FLOAT(dtype, DT,
+            NORI_DISPATCH_FLOAT(weight_dtype, WDT,
+                st = launch<DT, WDT, DT>(x, rows, cols, x_row_stride, weight, eps, y, y_row_stride, stream)));
+    } else if (y_dtype == NORI_F16) {
         NORI_DISPATCH_FLOAT(weight_dtype, WDT,
-            st = launch<DT, WDT>(x, rows, cols, x_row_stride, weight, eps, y, y_row_stride, stream)));
+            st = launch<NORI_F32, WDT, NORI_F16>(x, rows, cols, x_row_stride, weight, eps, y, y_row_stride, stream));
+    } else {
+        NORI_DISPATCH_FLOAT(weight_dtype, WDT,
+            st = launch<NORI_F32, WDT, NORI_BF16>(x, rows, cols, x_row_stride, weight, eps, y, y_row_stride, stream));
+    }
     return st;
+}
+
+extern "C" int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t cols, int64_t x_row_stride,
+                             const void* weight, int weight_dtype, float eps, void* y, int64_t y_row_stride,
+                             void* stream_v) {
+    return nori_rms_norm_to(x, dtype, rows, cols, x_row_stride, weight, weight_dtype, eps, y, dtype, y_row_stride,
+                            stream_v);
 }

@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         [_vp, _vp, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _vp, _i32, _i64, _i64, _vp],
     ),
     "nori_rms_norm": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _i32, _f32, _vp, _i64, _vp]),
+    "nori_rms_norm_to": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _vp]),
     "nori_icl_attention": (
         ctypes.c_int,
         [

@@ -50,11 +50,16 @@ def rms_norm_(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 
     return x
 
 
-def rms_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+def rms_norm(
+    x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None, eps: float = 1e-5, *,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
     """x * rsqrt(mean(x^2) + eps) (* weight) over the trailing ``normalized_shape`` axes.
 
     The native ``F.rms_norm`` semantics (layer.py:253): statistic and product in fp32,
-    one rounding to x's dtype, then the weight multiply.
+    one rounding to x's dtype, then the weight multiply. ``out_dtype`` (fp16 or bf16, for an
+    fp32 ``x``) writes that result rounded once more to ``out_dtype``: the value
+    ``rms_norm(x).to(out_dtype)`` has, in one pass.
     """
     if isinstance(normalized_shape, int):
         normalized_shape = (normalized_shape,)
@@ -71,21 +76,37 @@ def rms_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = No
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     rows = x2.shape[0]
-    y = torch.empty((rows, cols), dtype=x.dtype, device=device)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    y = torch.empty((rows, cols), dtype=out_dtype, device=device)
     w = None
     if weight is not None:
         w = weight.reshape(cols)
         if not w.is_contiguous():
             w = w.contiguous()
     nat.check(
-        nat.lib().nori_rms_norm(
+        nat.lib().nori_rms_norm_to(
             x2.data_ptr(), nat.dtype_code(x.dtype), rows, cols, x2.stride(0),
             nat.ptr(w), nat.dtype_code(w.dtype) if w is not None else nat.NORI_F32, float(eps),
-            y.data_ptr(), y.stride(0), nat.stream_of(device),
+            y.data_ptr(), nat.dtype_code(out_dtype), y.stride(0), nat.stream_of(device),
         ),
         "rms_norm",
     )
     return y.reshape(x.shape)
+
+
+def projection_operand(norm: "RMSNorm", x: torch.Tensor) -> torch.Tensor:
+    """``norm(x)`` for a caller that only feeds it to projections (F.linear / nn.Linear).
+
+    Under fp16 or bf16 autocast on the GPU, such a projection casts the norm's fp32 output to
+    the autocast dtype before its GEMM; here the norm kernel writes that rounded value
+    directly (bit for bit the same operand), saving the fp32 write and the cast's read and
+    write. Elsewhere it is ``norm(x)``.
+    """
+    if x.dtype == torch.float32 and x.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        if dt in (torch.float16, torch.bfloat16):
+            return rms_norm(x, norm.normalized_shape, norm.weight, norm.eps, out_dtype=dt)
+    return norm(x)
 
 
 class RMSNorm(nn.Module):

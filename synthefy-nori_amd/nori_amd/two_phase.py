@@ -20,7 +20,7 @@ import torch
 from torch import nn
 
 from .layer import MultiheadAttention, SwiGLUMLP
-from .norm import RMSNorm
+from .norm import RMSNorm, projection_operand as _operand
 
 __all__ = [
     "CellLayer2P",
@@ -168,13 +168,13 @@ class CellLayer2P(nn.Module):
     def forward(self, cells: torch.Tensor, targets: torch.Tensor, eval_pos: int) -> tuple[torch.Tensor, torch.Tensor]:
         cells = self.apply_column_attention(cells, eval_pos)
         rows = targets.flatten(-2)
-        normed = self.target_norms[0](rows).unsqueeze(1)
+        normed = _operand(self.target_norms[0], rows).unsqueeze(1)
         rows = self.attend_target_rows_to_context(rows, normed, normed[:, :, :eval_pos])
         return self.apply_row_mlps_and_feature_attention(cells, rows)
 
     def apply_column_attention(self, cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
         """S for the cells; reads a whole column, so it slices by column only."""
-        return cells + self.deepnorm_alpha * self.column_attention(self.cell_norms[0](cells), eval_pos)
+        return cells + self.deepnorm_alpha * self.column_attention(_operand(self.cell_norms[0], cells), eval_pos)
 
     def attend_target_rows_to_context(self, rows: torch.Tensor, normalized: torch.Tensor, context_keys: torch.Tensor) -> torch.Tensor:
         """S for the target stream: ``normalized`` rows (``target_norms[0](rows).unsqueeze(1)``)
@@ -184,10 +184,10 @@ class CellLayer2P(nn.Module):
     def apply_row_mlps_and_feature_attention(self, cells: torch.Tensor, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """M then F; each row reads only itself. Returns (cells, targets [batch, n, K, cell_dim])."""
         a = self.deepnorm_alpha
-        cells = cells + a * self.mlp[0](self.cell_norms[1](cells))
-        rows = rows + a * self.mlp[1](self.target_norms[1](rows))
+        cells = cells + a * self.mlp[0](_operand(self.cell_norms[1], cells))
+        rows = rows + a * self.mlp[1](_operand(self.target_norms[1], rows))
         targets = rows.view(*rows.shape[:-1], self.target_tokens, self.cell_dim)
-        cell_update, target_update = self.feature_attention(self.cell_norms[2](cells), self.target_norms[2](targets))
+        cell_update, target_update = self.feature_attention(_operand(self.cell_norms[2], cells), _operand(self.target_norms[2], targets))
         return cells + a * cell_update, targets + a * target_update
 
 
@@ -207,7 +207,7 @@ class RowLayer2P(nn.Module):
         self.mlp = nn.ModuleList([SwiGLUMLP(width, hidden_dim, width, has_bias=False, device=device, dtype=dtype)])
 
     def forward(self, rows: torch.Tensor, eval_pos: int, cell_memory: torch.Tensor) -> torch.Tensor:
-        normed = self.attn_norm(rows).unsqueeze(1)
+        normed = _operand(self.attn_norm, rows).unsqueeze(1)
         rows = self.attend_rows_to_context(rows, normed, normed[:, :, :eval_pos])
         return self.apply_readback_and_mlp(rows, cell_memory)
 
@@ -220,9 +220,9 @@ class RowLayer2P(nn.Module):
         """The row (one query) reads its own cells ``cell_memory`` [batch, rows, groups, width],
         then the MLP; each row reads only itself."""
         a = self.deepnorm_alpha
-        query = self.readback_norm(rows).unsqueeze(2)
+        query = _operand(self.readback_norm, rows).unsqueeze(2)
         rows = rows + a * _attend(self.feature_attentions[0], query, cell_memory).squeeze(2)
-        return rows + a * self.mlp[0](self.mlp_norm(rows))
+        return rows + a * self.mlp[0](_operand(self.mlp_norm, rows))
 
 
 class TwoPhaseEncoder(nn.Module):
@@ -354,10 +354,10 @@ class TwoPhaseEncoder(nn.Module):
                 cols = slice(c0, min(c0 + column_chunk, n_groups))
                 cells[:, :, cols] = layer.apply_column_attention(dev(cells[:, :, cols]), eval_pos).to(home)
             # keys from the layer's input, before any row chunk below is overwritten
-            keys = layer.target_norms[0](dev(rows[:, :eval_pos])).unsqueeze(1)
+            keys = _operand(layer.target_norms[0], dev(rows[:, :eval_pos])).unsqueeze(1)
             for p in parts:
                 r = dev(rows[:, p])
-                r = layer.attend_target_rows_to_context(r, layer.target_norms[0](r).unsqueeze(1), keys)
+                r = layer.attend_target_rows_to_context(r, _operand(layer.target_norms[0], r).unsqueeze(1), keys)
                 c, t = layer.apply_row_mlps_and_feature_attention(dev(cells[:, p]), r)
                 cells[:, p] = c.to(home)
                 rows[:, p] = t.flatten(-2).to(home)
@@ -374,10 +374,10 @@ class TwoPhaseEncoder(nn.Module):
             cells[:, p] = self.cell_out_norm(dev(cells[:, p])).to(home)
 
         for layer in self._row_stack():
-            keys = layer.attn_norm(dev(rows[:, :eval_pos])).unsqueeze(1)
+            keys = _operand(layer.attn_norm, dev(rows[:, :eval_pos])).unsqueeze(1)
             for p in parts:
                 r = dev(rows[:, p])
-                r = layer.attend_rows_to_context(r, layer.attn_norm(r).unsqueeze(1), keys)
+                r = layer.attend_rows_to_context(r, _operand(layer.attn_norm, r).unsqueeze(1), keys)
                 rows[:, p] = layer.apply_readback_and_mlp(r, self.cell_to_row(dev(cells[:, p]))).to(home)
             del keys
 

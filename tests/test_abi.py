@@ -31,6 +31,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_kv_quantize_int8",
             "nori_kv_dequantize_int8",
             "nori_rms_norm",
+            "nori_rms_norm_to",
             "nori_icl_attention",
             "nori_icl_attention_workspace_size",
             "nori_kv_project_quantize_int8",
@@ -96,6 +97,10 @@ def test_argument_errors_map_to_reference_exceptions():
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
+    f = lib.nori_rms_norm_to
+    assert f(None, nat.NORI_F32, 0, 128, 128, None, nat.NORI_F32, 1e-5, None, nat.NORI_F16, 128, None) == nat.NORI_OK
+    # only fp32 rows narrow; an fp16 row is not widened or re-rounded to bf16
+    assert f(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, nat.NORI_BF16, 128, None) == nat.NORI_ERR_UNSUPPORTED
 
 
 def test_operators_refuse_cpu_tensors():

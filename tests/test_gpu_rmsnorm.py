@@ -67,3 +67,29 @@ def test_rms_norm_module_and_strided_rows(cuda):
     ys = nori_amd.rms_norm(xs, 128, None, 1e-5)
     assert torch.equal(ys, m(xs.contiguous()))
     assert nori_amd.rms_norm(torch.empty(0, 64, device=cuda), 64).shape == (0, 64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cols", [64, 128, 44, 352])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("affine", [False, True])
+def test_norm_written_in_the_autocast_dtype_equals_norm_then_cast(cuda, cols, out_dtype, affine):
+    """nori_rms_norm_to: an fp32 row written as fp16/bf16 is bit for bit the fp32 norm cast to
+    that dtype -- the operand an autocast projection would make of it (chunked path for
+    whole 16-byte chunks, element-wise path for 44-wide rows)."""
+    from nori_amd.norm import RMSNorm, projection_operand, rms_norm
+
+    g = torch.Generator().manual_seed(cols)
+    x = (torch.randn(1000, cols, generator=g) * 3.0).to(cuda)
+    w = (1.0 + 0.3 * torch.randn(cols, generator=g)).to(cuda) if affine else None
+    got = rms_norm(x, cols, w, 1e-5, out_dtype=out_dtype)
+    exp = rms_norm(x, cols, w, 1e-5).to(out_dtype)
+    assert got.dtype == out_dtype and torch.equal(got, exp)
+    norm = RMSNorm(cols, eps=1e-5, elementwise_affine=affine).to(cuda)
+    if affine:
+        with torch.no_grad():
+            norm.weight.copy_(w)
+    with torch.autocast("cuda", dtype=out_dtype):
+        op = projection_operand(norm, x)
+    assert op.dtype == out_dtype and torch.equal(op, norm(x).to(out_dtype))
+    assert projection_operand(norm, x).dtype == torch.float32  # no autocast: the norm itself
