@@ -37,7 +37,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
-from .norm import RMSNorm, rms_norm_
+from .norm import RMSNorm, projection_operand, rms_norm_
 
 ACTIVATION_FN = {"gelu": nn.GELU(), "relu": nn.ReLU(), "silu": nn.SiLU()}
 _SDPA_BACKENDS_WITHOUT_CUDNN = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]
@@ -515,7 +515,7 @@ class EncoderBaseLayer(nn.Module):
     def _run_non_sequence_step(self, x, *, step_idx, feature_atten_mask, eval_pos):
         sublayer, norm = self.layer_steps[step_idx], self.layer_norms[step_idx]
         if self.pre_norm:
-            x_norm = norm(x)
+            x_norm = projection_operand(norm, x)  # the MLP or feature attention projects it
             out = sublayer(x_norm, feature_atten_mask, eval_pos) if isinstance(sublayer, functools.partial) else sublayer(x_norm)
             out = out[0] if isinstance(out, tuple) else out
             return self._residual_add(x, out)
@@ -766,7 +766,7 @@ class EncoderBaseLayer(nn.Module):
         seq_attn_test = self.sequence_attentions[index2]
         seq_norm = self.layer_norms[seq_step]
         residual = x_test
-        src = seq_norm(x_test) if self.pre_norm else x_test
+        src = projection_operand(seq_norm, x_test) if self.pre_norm else x_test
         test_attn, _ = seq_attn_test.forward_with_kv_cache(src.transpose(1, 2), cache["seq_kv"])
         test_attn = test_attn.transpose(1, 2)
         x_test = self._residual_add(residual, test_attn) if self.pre_norm else seq_norm(test_attn + residual)

@@ -102,7 +102,7 @@ def projection_operand(norm: "RMSNorm", x: torch.Tensor) -> torch.Tensor:
     directly (bit for bit the same operand), saving the fp32 write and the cast's read and
     write. Elsewhere it is ``norm(x)``.
     """
-    if x.dtype == torch.float32 and x.is_cuda and torch.is_autocast_enabled("cuda"):
+    if isinstance(norm, RMSNorm) and x.dtype == torch.float32 and x.is_cuda and torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
         if dt in (torch.float16, torch.bfloat16):
             return rms_norm(x, norm.normalized_shape, norm.weight, norm.eps, out_dtype=dt)
