@@ -22,7 +22,9 @@ per launch measured by rocprofv3 counters (profiles/traffic_nori30m_64k.md, when
 present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes) of one
 layer against the unfused sequence it replaces, one layer's prefill self-attention over the
 fp16 context K/V, the same configuration through the model-level context-cache API
-(build once, 4 query batches), and the CPU baseline: the oracle (quantizer in C, attention as the
+(build once, 4 query batches), the kernel-level legs of the nori-6m block and the nori-100m
+layer, the many-small-tables path (512 tables through a nori-1-5-sized two-phase model), and
+the CPU baseline: the oracle (quantizer in C, attention as the
 reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
 bounded sample of the same work.
 """
@@ -592,6 +594,7 @@ def main():
     kv0 = kv[0]
     del kv
     others = other_configs(torch, dev)
+    tables = small_tables(torch, dev)
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -669,6 +672,7 @@ def main():
     line["prefill_attention"] = prefill
     line["end_to_end"] = model_e2e
     line["other_configs"] = others
+    line["small_tables"] = tables
     if args.cpu_baseline == "on":
         line["cpu_baseline"] = cpu_baseline(torch, kv0, codes[0], scales[0], args.cpu_sample_queries, layers)
     print(json.dumps(line), flush=True)
