@@ -155,6 +155,42 @@ int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32
                        int64_t workspace_bytes, void* stream);
 
 /*
+ * What the two-phase encoder's attentions do to q and k between the projection and the
+ * attention (layer.py:1122-1134 with qk_norm and QASS "log_only", layer.py:433-456), applied
+ * by nori_icl_attention_qk to each query row and key row as it is loaded:
+ *     q := T(T(q * rsqrt(mean(q^2) + eps)) * q_weight)   when q_weight is not NULL
+ *     q := T(q * q_mult)                                  when q_mult != 1
+ *     k := T(T(k * rsqrt(mean(k^2) + eps)) * k_weight)   when k_weight is not NULL
+ * (means over the head's d elements in fp32, T = rounding to the q or cache dtype), the
+ * values the per-head RMSNorm (eps 1e-6, elementwise gain) and the fp16 multiply by
+ * fp16(log n) produce when run as separate passes.
+ */
+typedef struct {
+    const void* q_weight; /* [d] query norm gain, or NULL: no query norm */
+    const void* k_weight; /* [d] key norm gain, or NULL: no key norm */
+    int weight_dtype;     /* nori_dtype of both gains */
+    float eps;
+    float q_mult;         /* 1.0f: no multiply */
+} nori_qk_prologue;
+
+/*
+ * nori_icl_attention with the q/k prologue above fused into the loads. Has no counterpart in
+ * the reference as one call (it replaces the RMSNorm passes over q and K, the q multiply and
+ * the attention of MultiheadAttention.forward, layer.py:1062-1162). Taken only where the
+ * short-context kernel runs (few queries over few keys: the in-row attentions of the
+ * two-phase encoder) and for full-precision caches; elsewhere it returns
+ * NORI_ERR_UNSUPPORTED having done nothing, and the caller runs the separate passes.
+ */
+int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                          int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
+                          int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
+                          int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                          int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
+                          void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                          int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
+                          int64_t workspace_bytes, const nori_qk_prologue* prologue, void* stream);
+
+/*
  * Fused context-cache write: K/V projection of context rows straight into the int8 cache.
  * Replaces MultiheadAttention.project_kv_cache (src/synthefy_nori/model/layer.py:651-683)
  * followed by quantize_int8 (kv_cache_scaling.py:29-37) on the GPU's autocast path, with the

@@ -128,15 +128,38 @@ extern "C" int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int
     return workspace_bytes(make_plan(bg, nq, heads, d, nk), d);
 }
 
-extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
-                                  int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
-                                  int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
-                                  int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
-                                  int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
-                                  void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
-                                  int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
-                                  int64_t workspace_bytes_given, void* stream_v) {
+namespace {
+
+// Both entry points: checks, plan, launch. `pro` (may be null) is the q/k prologue, which
+// only the short-context kernel applies.
+int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                  int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv, int kv_dtype,
+                  const float* kv_scales, int64_t nk, int32_t kv_heads, int64_t kv_bg_stride, int64_t kv_row_stride,
+                  int64_t kv_half_stride, int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride,
+                  float scale, void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                  int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
+                  int64_t workspace_bytes_given, const nori_qk_prologue* pro, void* stream_v) {
     clear_error();
+    Prologue prologue;
+    if (pro) {
+        if ((pro->q_weight || pro->k_weight) && pro->weight_dtype != NORI_F32 && pro->weight_dtype != NORI_F16 &&
+            pro->weight_dtype != NORI_BF16)
+            return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported norm gain dtype %s",
+                        dtype_name(pro->weight_dtype));
+        if (pro->k_weight && kv_dtype == NORI_I8)
+            return fail(NORI_ERR_UNSUPPORTED, "icl_attention: a key norm applies to full-precision caches only");
+        if (!(pro->eps >= 0.f) || !(pro->q_mult == pro->q_mult))
+            return fail(NORI_ERR_INVALID, "icl_attention: prologue eps must be >= 0 and q_mult a number");
+        prologue.qw = pro->q_weight;
+        prologue.kw = pro->k_weight;
+        prologue.wdt = pro->weight_dtype;
+        prologue.eps = pro->eps;
+        prologue.qmult = pro->q_mult;
+        if (!short_context(nq, nk))
+            return fail(NORI_ERR_UNSUPPORTED,
+                        "icl_attention: the q/k prologue runs only with few queries over few keys (%lld x %lld)",
+                        (long long)nq, (long long)nk);
+    }
     if (bg < 0 || nq < 0)
         return fail(NORI_ERR_INVALID, "icl_attention: negative batch (%lld) or query count (%lld)", (long long)bg, (long long)nq);
     if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
@@ -201,7 +224,7 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
 
     hipStream_t stream = (hipStream_t)stream_v;
     if (plan.short_ctx) {
-        const int st = launch_short(kv_dtype, args, stream);
+        const int st = launch_short(kv_dtype, args, prologue, stream);
         return st != NORI_OK ? st : launch_status("icl_attention short");
     }
     int st = launch_kvt(kv_dtype, plan.dp, plan.mode, plan.nw, args, stream);
@@ -213,4 +236,38 @@ extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_
         return launch_status("icl_attention combine");
     }
     return NORI_OK;
+}
+
+}  // namespace
+
+extern "C" int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                                  int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
+                                  int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
+                                  int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                                  int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
+                                  void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                                  int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
+                                  int64_t workspace_bytes_given, void* stream_v) {
+    return run_attention(q, q_dtype, bg, nq, heads, d, q_bg_stride, q_row_stride, q_head_stride, kv, kv_dtype,
+                         kv_scales, nk, kv_heads, kv_bg_stride, kv_row_stride, kv_half_stride, sc_bg_stride,
+                         sc_row_stride, sc_half_stride, scale, out, out_dtype, out_bg_stride, out_row_stride,
+                         out_head_stride, lse, flags, workspace, workspace_bytes_given, nullptr, stream_v);
+}
+
+extern "C" int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                                     int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
+                                     int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
+                                     int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                                     int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
+                                     void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                                     int64_t out_head_stride, float* lse, uint32_t flags, void* workspace,
+                                     int64_t workspace_bytes_given, const nori_qk_prologue* prologue, void* stream_v) {
+    if (!prologue) {
+        clear_error();
+        return fail(NORI_ERR_INVALID, "icl_attention_qk: null prologue");
+    }
+    return run_attention(q, q_dtype, bg, nq, heads, d, q_bg_stride, q_row_stride, q_head_stride, kv, kv_dtype,
+                         kv_scales, nk, kv_heads, kv_bg_stride, kv_row_stride, kv_half_stride, sc_bg_stride,
+                         sc_row_stride, sc_half_stride, scale, out, out_dtype, out_bg_stride, out_row_stride,
+                         out_head_stride, lse, flags, workspace, workspace_bytes_given, prologue, stream_v);
 }

@@ -683,8 +683,18 @@ icl_attention_kernel(const Args a) {
     }
 }
 
+// Per-row q/k transforms applied as the short-context kernel loads them (the C ABI's
+// nori_qk_prologue): per-head RMS norms with gains, and a multiply of the normed q.
+struct Prologue {
+    const void* qw = nullptr;  // [d] query norm gain or null
+    const void* kw = nullptr;  // [d] key norm gain or null
+    int wdt = NORI_F32;
+    float eps = 0.f;
+    float qmult = 1.f;
+};
+
 // The short-context kernel (icl_attention_short.hip): one launch over every (b, h, query) row.
-int launch_short(int kv_dtype, const Args& a, hipStream_t stream);
+int launch_short(int kv_dtype, const Args& a, const Prologue& pro, hipStream_t stream);
 
 // Few queries attending to few keys: the VALU kernel, whose cost grows with nq * nk, beats the
 // MFMA kernel's fixed cost per (b, h) unit (a 64-query tile over a staged 64-key block).

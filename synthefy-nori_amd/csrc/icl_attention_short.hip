@@ -10,6 +10,9 @@
 // fp32 on the VALU, key by key, from K/V rows loaded 4 elements per lane (16-, 8- or 4-byte
 // loads). The rows of one (b, h) are consecutive, so the groups of a wavefront read the same
 // K/V rows. Values are computed in fp32 from the exact cache values (codes x scales for int8).
+// With a prologue the per-head q/k RMS norms (and the q multiply) run on the rows as loaded,
+// rounded as the separate passes round them: the group holds a whole row, so the mean of
+// squares is one more group sum.
 #include <math.h>
 
 #include "icl_attention_kernel.h"
@@ -58,8 +61,25 @@ __device__ __forceinline__ f32x4 load4(const void* p, int64_t i) {
     return r;
 }
 
+// Rounding to a runtime dtype (the query's), as torch rounds each op's result.
+__device__ __forceinline__ float round_dt(float v, int dt) {
+    if (dt == NORI_F16) return round_to<NORI_F16>(v);
+    if (dt == NORI_BF16) return round_to<NORI_BF16>(v);
+    return v;
+}
+
+// T(T(v * rsqrt(mean(v^2) + eps)) * w) over the group's row (4 elements per lane; lanes past
+// the row hold zeros), with T rounding to dtype dt: the RMSNorm pass of the reference.
+template <int G>
+__device__ __forceinline__ void norm_row(f32x4& v, const f32x4& w, int d, float eps, int dt) {
+    const float ss = group_sum<G>(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
+    const float inv = rsqrtf(ss / (float)d + eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = round_dt(round_dt(v[e] * inv, dt) * w[e], dt);
+}
+
 template <int KVT, int G>
-__global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Args a, int64_t rows) {
+__global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Args a, int64_t rows, const Prologue pro) {
     const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     int64_t row = t / G;  // (b, h, query) with the query fastest
     const bool valid = row < rows;
@@ -73,12 +93,28 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
     const int c0 = 4 * sub;
     const bool live = c0 < a.d;  // d % 4 == 0: a lane's 4 elements are all in or all out
 
-    f32x4 q = {0.f, 0.f, 0.f, 0.f};
+    f32x4 q = {0.f, 0.f, 0.f, 0.f}, kw = {1.f, 1.f, 1.f, 1.f};
     if (live) {
         const int64_t qb = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head + c0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = load_as_f32(a.q, a.q_dtype, qb + e) * a.scale_log2;
+        for (int e = 0; e < 4; ++e) q[e] = load_as_f32(a.q, a.q_dtype, qb + e);
     }
+    if (pro.qw) {
+        f32x4 qw = {0.f, 0.f, 0.f, 0.f};
+        if (live)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qw[e] = load_as_f32(pro.qw, pro.wdt, c0 + e);
+        norm_row<G>(q, qw, a.d, pro.eps, a.q_dtype);
+    }
+    if (pro.qmult != 1.f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = round_dt(q[e] * pro.qmult, a.q_dtype);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] *= a.scale_log2;
+    const bool knorm = pro.kw != nullptr;
+    if (knorm && live)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw[e] = load_as_f32(pro.kw, pro.wdt, c0 + e);
     const int64_t kbase = b * a.kv_bg + (int64_t)hk * a.d + c0;
     const int64_t sbase = b * a.sc_bg + hk;
     float m = -INFINITY, l = 0.f;
@@ -89,6 +125,9 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
         if (live) {
             k = load4<KVT>(a.kv, kbase + j * a.kv_row);
             v = load4<KVT>(a.kv, kbase + j * a.kv_row + a.kv_half);
+        }
+        if constexpr (KVT != NORI_I8) {
+            if (knorm) norm_row<G>(k, kw, a.d, pro.eps, KVT);
         }
         float s = group_sum<G>(q[0] * k[0] + q[1] * k[1] + q[2] * k[2] + q[3] * k[3]);
         float vs = 1.f;
@@ -122,7 +161,7 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
 }
 
 template <int KVT>
-int launch_group(const Args& a, hipStream_t stream) {
+int launch_group(const Args& a, const Prologue& pro, hipStream_t stream) {
     const int quads = (a.d + 3) / 4;
     const int64_t rows = a.bg * a.heads * a.nq;
     int g = 1;
@@ -132,12 +171,12 @@ int launch_group(const Args& a, hipStream_t stream) {
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: %lld query rows exceed one launch", (long long)rows);
     const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads)), block(kThreads);
     switch (g) {
-        case 1: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 1>), grid, block, 0, stream, a, rows); break;
-        case 2: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 2>), grid, block, 0, stream, a, rows); break;
-        case 4: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 4>), grid, block, 0, stream, a, rows); break;
-        case 8: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 8>), grid, block, 0, stream, a, rows); break;
-        case 16: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 16>), grid, block, 0, stream, a, rows); break;
-        default: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 32>), grid, block, 0, stream, a, rows); break;
+        case 1: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 1>), grid, block, 0, stream, a, rows, pro); break;
+        case 2: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 2>), grid, block, 0, stream, a, rows, pro); break;
+        case 4: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 4>), grid, block, 0, stream, a, rows, pro); break;
+        case 8: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 8>), grid, block, 0, stream, a, rows, pro); break;
+        case 16: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 16>), grid, block, 0, stream, a, rows, pro); break;
+        default: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 32>), grid, block, 0, stream, a, rows, pro); break;
     }
     return NORI_OK;
 }
@@ -147,12 +186,12 @@ int launch_group(const Args& a, hipStream_t stream) {
 namespace nori {
 namespace attn {
 
-int launch_short(int kv_dtype, const Args& a, hipStream_t stream) {
+int launch_short(int kv_dtype, const Args& a, const Prologue& pro, hipStream_t stream) {
     switch (kv_dtype) {
-        case NORI_I8: return launch_group<NORI_I8>(a, stream);
-        case NORI_F16: return launch_group<NORI_F16>(a, stream);
-        case NORI_BF16: return launch_group<NORI_BF16>(a, stream);
-        default: return launch_group<NORI_F32>(a, stream);
+        case NORI_I8: return launch_group<NORI_I8>(a, pro, stream);
+        case NORI_F16: return launch_group<NORI_F16>(a, pro, stream);
+        case NORI_BF16: return launch_group<NORI_BF16>(a, pro, stream);
+        default: return launch_group<NORI_F32>(a, pro, stream);
     }
 }
 

@@ -51,6 +51,16 @@ SIGNATURES: dict[str, tuple[object, list]] = {
             _vp, _u32, _vp, _i64, _vp,  # lse, flags, workspace, bytes, stream
         ],
     ),
+    "nori_icl_attention_qk": (
+        ctypes.c_int,
+        [
+            _vp, _i32, _i64, _i64, _i32, _i32, _i64, _i64, _i64,  # q
+            _vp, _i32, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64,  # kv
+            _f32,  # scale
+            _vp, _i32, _i64, _i64, _i64,  # out
+            _vp, _u32, _vp, _i64, _vp, _vp,  # lse, flags, workspace, bytes, prologue, stream
+        ],
+    ),
     "nori_icl_attention_workspace_size": (_i64, [_i64, _i64, _i32, _i32, _i64]),
     "nori_kv_project_quantize_int8": (
         ctypes.c_int,
@@ -132,3 +142,15 @@ def stream_of(device: torch.device) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+class QKPrologue(ctypes.Structure):
+    """``nori_qk_prologue``: per-head q/k RMS norm gains, eps and a q multiplier."""
+
+    _fields_ = [
+        ("q_weight", ctypes.c_void_p),
+        ("k_weight", ctypes.c_void_p),
+        ("weight_dtype", ctypes.c_int),
+        ("eps", ctypes.c_float),
+        ("q_mult", ctypes.c_float),
+    ]

@@ -16,6 +16,7 @@ layer.py:703-706) and caches ``[BG, N, 2, Hkv, D]``. The default logit scale is
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -38,6 +39,12 @@ def workspace_bytes(bg: int, nq: int, heads: int, d: int, nk: int) -> int:
     return int(nat.lib().nori_icl_attention_workspace_size(bg, nq, heads, d, nk))
 
 
+def short_context(nq: int, nk: int) -> bool:
+    """Whether the attention runs on the short-context kernel: few queries over few keys (the
+    planner's rule, short_context() in csrc/icl_attention_kernel.h)."""
+    return nq <= 64 and nk <= 128 and nq * nk <= 2048
+
+
 def icl_attention(
     q: torch.Tensor,
     kv: torch.Tensor,
@@ -48,6 +55,7 @@ def icl_attention(
     lse: torch.Tensor | None = None,
     merge: bool = False,
     workspace: torch.Tensor | None = None,
+    qk_prologue: dict | None = None,
 ) -> torch.Tensor:
     """softmax(scale * q k^T) v for every (bg, query, head); returns ``out`` ([BG, Q, H, D]).
 
@@ -58,6 +66,11 @@ def icl_attention(
     blocks and fold this block in (layer.py:915-920).
     workspace: optional uint8 device buffer of at least ``workspace_bytes(...)`` bytes for
     the split-context partials; allocated per call when omitted.
+    qk_prologue: ``{"q_weight", "k_weight", "eps", "q_mult"}`` -- per-head RMS norms of the
+    raw q and K rows (gains of d elements, or None) and a multiply of the normed q, applied
+    as the kernel loads them, rounded as the separate passes round them
+    (``nori_icl_attention_qk``). Only for ``short_context(Q, N)`` shapes and full-precision
+    caches; raises NotImplementedError elsewhere.
     """
     if q.dim() != 4:
         raise ValueError(f"query must be [BG, Q, H, D], got {tuple(q.shape)}")
@@ -107,15 +120,29 @@ def icl_attention(
     scb = scr = sch = 0
     if kv_scales is not None:
         scb, scr, sch = kv_scales.stride(0), kv_scales.stride(1), kv_scales.stride(2)
+    common = (
+        q.data_ptr(), nat.dtype_code(q.dtype), bg, nq, heads, d, q.stride(0), q.stride(1), q.stride(2),
+        kv.data_ptr(), nat.dtype_code(kv.dtype), nat.ptr(kv_scales), nk, kv_heads, kvb, kvr, kvh, scb, scr, sch,
+        float(scale),
+        out.data_ptr(), nat.dtype_code(out.dtype), out.stride(0), out.stride(1), out.stride(2),
+        nat.ptr(lse), nat.ATTN_MERGE if merge else 0, nat.ptr(workspace), ws_bytes,
+    )
+    if qk_prologue is None:
+        nat.check(nat.lib().nori_icl_attention(*common, nat.stream_of(device)), "icl_attention")
+        return out
+    gains = [qk_prologue.get("q_weight"), qk_prologue.get("k_weight")]
+    gains = [None if g is None else g.reshape(d).contiguous() for g in gains]
+    present = [g for g in gains if g is not None]
+    nat.require_device(q, *present)
+    if len({g.dtype for g in present}) > 1:
+        gains = [None if g is None else g.float() for g in gains]
+        present = [g for g in gains if g is not None]
+    pro = nat.QKPrologue(
+        nat.ptr(gains[0]), nat.ptr(gains[1]), nat.dtype_code(present[0].dtype) if present else nat.NORI_F32,
+        float(qk_prologue.get("eps", 0.0)), float(qk_prologue.get("q_mult", 1.0)),
+    )
     nat.check(
-        nat.lib().nori_icl_attention(
-            q.data_ptr(), nat.dtype_code(q.dtype), bg, nq, heads, d, q.stride(0), q.stride(1), q.stride(2),
-            kv.data_ptr(), nat.dtype_code(kv.dtype), nat.ptr(kv_scales), nk, kv_heads, kvb, kvr, kvh, scb, scr, sch,
-            float(scale),
-            out.data_ptr(), nat.dtype_code(out.dtype), out.stride(0), out.stride(1), out.stride(2),
-            nat.ptr(lse), nat.ATTN_MERGE if merge else 0, nat.ptr(workspace), ws_bytes, nat.stream_of(device),
-        ),
-        "icl_attention",
+        nat.lib().nori_icl_attention_qk(*common, ctypes.addressof(pro), nat.stream_of(device)), "icl_attention_qk"
     )
     return out
 

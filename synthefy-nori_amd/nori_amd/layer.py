@@ -34,7 +34,7 @@ import torch
 import torch.nn as nn
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from .attention import attend_dense, compute_attention_blockwise, icl_attention
+from .attention import attend_dense, compute_attention_blockwise, icl_attention, short_context
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
 from .norm import RMSNorm, projection_operand, rms_norm_
@@ -244,6 +244,27 @@ class MultiheadAttention(nn.Module):
     def _norm_q(self, q):
         return q if self.q_norm is None else self.q_norm(q)
 
+    def _short_prologue(self, q: torch.Tensor, kv: torch.Tensor) -> dict | None:
+        """The q/k steps between projection and attention as a prologue of the short-context
+        kernel, or None where they run as separate passes. Needs the per-head q/k norms (with
+        gains and one eps), QASS off or "log_only" (a multiply by fp16(log n)), no log-n or
+        temperature scale, a full-precision cache on the GPU and a short-context shape."""
+        if not (self.qk_norm and q.is_cuda and kv.dtype != torch.int8):
+            return None
+        if self.use_logn_attention or self.use_learnable_attn_temperature:
+            return None
+        if self.q_norm.weight is None or self.k_norm.weight is None or self.q_norm.eps != self.k_norm.eps:
+            return None
+        if self.qassmax is not None and self.qassmax.qass_mode != "log_only":
+            return None
+        n_keys = int(kv.shape[1])
+        if not short_context(int(q.shape[1]), n_keys):
+            return None
+        q_mult = 1.0
+        if self.qassmax is not None and n_keys > 1:  # QASSMaxScaling.forward's factor, in q's dtype
+            q_mult = float(torch.tensor(math.log(float(max(n_keys, 2))), dtype=q.dtype))
+        return {"q_weight": self.q_norm.weight, "k_weight": self.k_norm.weight, "eps": self.q_norm.eps, "q_mult": q_mult}
+
     def _norm_kv(self, kv):
         """kv: [..., 2, heads, head_dim], a fresh projection; normalizes the K half only. On the
         GPU the K rows are normalized in place, head by head (rows at one stride), instead of
@@ -366,19 +387,26 @@ class MultiheadAttention(nn.Module):
                 ).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
             else:
                 kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w)
-            if self.qk_norm:
-                q = self._norm_q(q)
-                kv = self._norm_kv(kv)
-            if self.use_qassmax:
-                q = self.apply_qassmax(q, kv.shape[1])
-            q = self._apply_extra_attn_scale(q, kv.shape[1])
-            if attn_mask is not None:
-                k, v = kv.unbind(dim=2)
-                atten_out = self._sdpa(q, k, v, attn_mask, scaled=True)
-            else:
+            prologue = self._short_prologue(q, kv) if attn_mask is None else None
+            if prologue is not None:
+                # q/k norms and the log-n multiply fused into the short-context kernel's loads
                 if self._attention_dropout_p() != 0.0:
                     raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
-                atten_out = icl_attention(q, kv.contiguous() if kv.stride(-1) != 1 else kv)
+                atten_out = icl_attention(q, kv, qk_prologue=prologue)
+            else:
+                if self.qk_norm:
+                    q = self._norm_q(q)
+                    kv = self._norm_kv(kv)
+                if self.use_qassmax:
+                    q = self.apply_qassmax(q, kv.shape[1])
+                q = self._apply_extra_attn_scale(q, kv.shape[1])
+                if attn_mask is not None:
+                    k, v = kv.unbind(dim=2)
+                    atten_out = self._sdpa(q, k, v, attn_mask, scaled=True)
+                else:
+                    if self._attention_dropout_p() != 0.0:
+                        raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
+                    atten_out = icl_attention(q, kv.contiguous() if kv.stride(-1) != 1 else kv)
         atten_out = atten_out.reshape(BS, F, self.num_heads, self.head_dim)
         if self._is_linear_projection_used(atten_out.device):
             out = torch.nn.functional.linear(

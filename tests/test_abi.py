@@ -33,6 +33,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_rms_norm",
             "nori_rms_norm_to",
             "nori_icl_attention",
+            "nori_icl_attention_qk",
             "nori_icl_attention_workspace_size",
             "nori_kv_project_quantize_int8",
             "nori_kv_project_quantize_int8_workspace_size",
@@ -128,3 +129,29 @@ def test_fused_projection_shape_errors():
         nori_amd.project_quantize_kv(torch.randn(5, 32), torch.randn(60, 32), 2, 16)
     with pytest.raises(ValueError, match="embed width"):
         nori_amd.project_quantize_kv(torch.randn(5, 48), torch.randn(64, 32), 2, 16)
+
+
+def test_qk_prologue_only_on_the_short_context_path():
+    """nori_icl_attention_qk refuses (NORI_ERR_UNSUPPORTED, nothing launched) exactly the shapes
+    the planner sends to the MFMA kernel -- attention.short_context() mirrors that rule -- and
+    int8 caches with a key norm; otherwise it goes on to the ordinary argument checks (here the
+    null pointers), all before any device call."""
+    import ctypes
+
+    from nori_amd import _native as nat
+    from nori_amd.attention import short_context
+
+    lib = nat.lib()
+    pro = nat.QKPrologue(None, None, nat.NORI_F32, 1e-6, 1.0)
+    for nq, nk in ((4, 6), (64, 32), (65, 1), (16, 128), (16, 129), (32, 64), (33, 64), (1, 1)):
+        rc = lib.nori_icl_attention_qk(
+            None, nat.NORI_F16, 1, nq, 2, 64, 0, 0, 0, None, nat.NORI_F16, None, nk, 2, 0, 0, 128, 0, 0, 0, 0.125,
+            None, nat.NORI_F16, 0, 0, 0, None, 0, None, 0, ctypes.addressof(pro), None,
+        )
+        assert rc == (nat.NORI_ERR_INVALID if short_context(nq, nk) else nat.NORI_ERR_UNSUPPORTED), (nq, nk, rc)
+    keyed = nat.QKPrologue(None, 1, nat.NORI_F32, 1e-6, 1.0)  # any non-null gain pointer
+    rc = lib.nori_icl_attention_qk(
+        None, nat.NORI_F16, 1, 4, 2, 64, 0, 0, 0, None, nat.NORI_I8, None, 6, 2, 0, 0, 128, 0, 0, 0, 0.125,
+        None, nat.NORI_F16, 0, 0, 0, None, 0, None, 0, ctypes.addressof(keyed), None,
+    )
+    assert rc == nat.NORI_ERR_UNSUPPORTED

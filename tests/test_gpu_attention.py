@@ -345,3 +345,54 @@ def test_shape_errors(cuda):
         nori_amd.icl_attention(q[..., :8], torch.randn(2, 7, 2, 3, 16, device=cuda))
     with pytest.raises(NotImplementedError):
         nori_amd.icl_attention(torch.randn(2, 5, 2, 6, device=cuda), torch.randn(2, 7, 2, 2, 6, device=cuda))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [16, 44, 64])
+def test_qk_prologue_equals_separate_passes(cuda, dtype, d):
+    """icl_attention(qk_prologue=...) -- the per-head q/k RMS norms with gains and the q
+    multiply applied as the short-context kernel loads the rows -- against the same steps as
+    separate passes (nori_amd.rms_norm over q and K, the q multiply in q's dtype, then the
+    attention). Only the order of the mean-of-squares sums differs, so the results agree to
+    within a unit or two of the last place of the normed values."""
+    from nori_amd.norm import rms_norm
+
+    bg, nq, nk, heads = 300, 4, 6, 2
+    g = torch.Generator().manual_seed(d)
+    q = (torch.randn(bg, nq, heads, d, generator=g) * 3).to(dtype).to(cuda)
+    kv = (torch.randn(bg, nk, 2, heads, d, generator=g) * 3).to(dtype).to(cuda)
+    qw = (1 + 0.3 * torch.randn(d, generator=g)).to(cuda)
+    kw = (1 + 0.3 * torch.randn(d, generator=g)).to(cuda)
+    mult = float(torch.tensor(math.log(nk), dtype=dtype))
+    fused = nori_amd.icl_attention(q, kv, qk_prologue={"q_weight": qw, "k_weight": kw, "eps": 1e-6, "q_mult": mult})
+    qn = rms_norm(q, d, qw, 1e-6) * torch.tensor(mult, dtype=dtype, device=cuda)
+    kvn = kv.clone()
+    kvn[:, :, 0] = rms_norm(kv[:, :, 0], d, kw, 1e-6)
+    separate = nori_amd.icl_attention(qn, kvn)
+    tol = 4e-3 if dtype == torch.float16 else 1e-5
+    torch.testing.assert_close(fused.float(), separate.float(), rtol=tol, atol=tol)
+    with pytest.raises(NotImplementedError):  # long contexts keep the separate passes
+        long_kv = torch.randn(bg, 300, 2, heads, d, device=cuda).to(dtype)
+        nori_amd.icl_attention(q, long_kv, qk_prologue={"q_weight": qw, "k_weight": kw, "eps": 1e-6, "q_mult": 1.0})
+
+
+def test_two_phase_attention_module_takes_the_prologue(cuda):
+    """MultiheadAttention with qk_norm and QASS "log_only" (the two-phase attention) computes
+    the same output through the fused prologue as through its separate passes, under the fp16
+    autocast of GPU inference."""
+    from nori_amd.layer import MultiheadAttention
+
+    torch.manual_seed(0)
+    attn = MultiheadAttention(64, 2, qkv_combined=False, use_qassmax=True, qass_mode="log_only", qk_norm=True).to(cuda).eval()
+    with torch.no_grad():
+        attn.q_norm.weight.mul_(1 + 0.2 * torch.randn(32, device=cuda))
+        attn.k_norm.weight.mul_(1 + 0.2 * torch.randn(32, device=cuda))
+    x = torch.randn(50, 30, 4, 64, device=cuda)
+    kv_src = torch.randn(50, 30, 6, 64, device=cuda)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        assert attn._short_prologue(torch.empty(1, 4, 2, 32, device=cuda, dtype=torch.float16),
+                                    torch.empty(1, 6, 2, 2, 32, device=cuda, dtype=torch.float16)) is not None
+        fused = attn(x=x, x_kv=kv_src)[0]
+        attn._short_prologue = lambda q, kv: None
+        separate = attn(x=x, x_kv=kv_src)[0]
+    torch.testing.assert_close(fused.float(), separate.float(), rtol=5e-3, atol=5e-3)
