@@ -367,7 +367,12 @@ class MultiheadAttention(nn.Module):
             if self.use_qassmax:
                 qkv = torch.stack((self.apply_qassmax(qkv[:, :, 0], qkv.shape[1]), qkv[:, :, 1], qkv[:, :, 2]), dim=2)
             q, k, v = qkv.unbind(dim=2)
-            atten_out = self._sdpa(q, k, v, attn_mask)
+            if attn_mask is None and qkv.is_cuda and short_context(F, F) and self._attention_dropout_p() == 0.0:
+                # a row's tokens attending to each other: the short-context kernel, reading K/V
+                # straight out of the [.., 3, H, D] projection (its K then V heads)
+                atten_out = icl_attention(self._apply_extra_attn_scale(q, F), qkv[:, :, 1:])
+            else:
+                atten_out = self._sdpa(q, k, v, attn_mask)
         else:
             assert x_kv is not None, "kv combined attention requires kv input"
             x_kv = x_kv.reshape(-1, *x_kv.shape[-2:])
