@@ -396,3 +396,30 @@ def test_two_phase_attention_module_takes_the_prologue(cuda):
         attn._short_prologue = lambda q, kv: None
         separate = attn(x=x, x_kv=kv_src)[0]
     torch.testing.assert_close(fused.float(), separate.float(), rtol=5e-3, atol=5e-3)
+
+
+def test_short_context_at_two_phase_scale(cuda):
+    """The short-context kernel over the full grid of the nori-1-5-sized model's cell feature
+    attention: 163,840 table rows x 2 heads x 4 queries over 6 keys, d 64, fp16 (1.3 M query
+    rows in one launch), against a float32 torch evaluation of softmax(q k^T / sqrt(d)) v on
+    the GPU, with the q/k prologue and without."""
+    bg, nq, nk, heads, d = 163840, 4, 6, 2, 64
+    g = torch.Generator(device=cuda).manual_seed(5)
+    q = torch.randn(bg, nq, heads, d, generator=g, device=cuda).half()
+    kv = torch.randn(bg, nk, 2, heads, d, generator=g, device=cuda).half()
+    got = nori_amd.icl_attention(q, kv)
+    qf = q.float().permute(0, 2, 1, 3).contiguous()                  # [bg, h, nq, d]
+    kf = kv[:, :, 0].float().permute(0, 2, 3, 1).contiguous()       # [bg, h, d, nk]
+    vf = kv[:, :, 1].float().permute(0, 2, 1, 3).contiguous()       # [bg, h, nk, d]
+    p = torch.softmax(torch.matmul(qf, kf) / math.sqrt(d), dim=-1)
+    exp = torch.matmul(p, vf).permute(0, 2, 1, 3)
+    err = (got.float() - exp).abs()
+    assert err.max().item() < 2e-3, f"max abs err {err.max().item():.3e}"
+    ones = torch.ones(d, device=cuda)
+    fused = nori_amd.icl_attention(q, kv, qk_prologue={"q_weight": ones, "k_weight": ones, "eps": 1e-6, "q_mult": 1.0})
+    qn = q.float() * torch.rsqrt(q.float().pow(2).mean(-1, keepdim=True) + 1e-6)
+    kn = kv[:, :, 0].float() * torch.rsqrt(kv[:, :, 0].float().pow(2).mean(-1, keepdim=True) + 1e-6)
+    p = torch.softmax(torch.matmul(qn.permute(0, 2, 1, 3).contiguous(), kn.permute(0, 2, 3, 1).contiguous()) / math.sqrt(d), -1)
+    exp = torch.matmul(p, vf).permute(0, 2, 1, 3)
+    err = (fused.float() - exp).abs()
+    assert err.max().item() < 4e-3, f"max abs err {err.max().item():.3e}"
