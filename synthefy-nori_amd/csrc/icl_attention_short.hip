@@ -40,26 +40,43 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// 4 consecutive cache elements at element index i (4-element aligned) as fp32 (int8: codes).
+// 4 consecutive cache elements as loaded (one 16-, 8- or 4-byte load), and as fp32 values
+// (int8: the codes).
+template <int KVT> struct Raw4 { u32x2 w; };
+template <> struct Raw4<NORI_F32> { f32x4 w; };
+template <> struct Raw4<NORI_I8> { uint32_t w; };
+
 template <int KVT>
-__device__ __forceinline__ f32x4 load4(const void* p, int64_t i) {
+__device__ __forceinline__ Raw4<KVT> load_raw4(const void* p, int64_t i) {
+    Raw4<KVT> r;
+    if constexpr (KVT == NORI_F32) r.w = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p) + i);
+    else if constexpr (KVT == NORI_I8) r.w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(p) + i);
+    else r.w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(p) + i);
+    return r;
+}
+
+template <int KVT>
+__device__ __forceinline__ f32x4 to_f32x4(const Raw4<KVT>& raw) {
     f32x4 r;
     if constexpr (KVT == NORI_F32) {
-        r = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p) + i);
+        r = raw.w;
     } else if constexpr (KVT == NORI_I8) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const int8_t*>(p) + i);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (float)(int8_t)(w >> (8 * e));
+        for (int e = 0; e < 4; ++e) r[e] = (float)(int8_t)(raw.w >> (8 * e));
     } else {
-        const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(p) + i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            const uint16_t h = (uint16_t)(raw.w[e >> 1] >> (16 * (e & 1)));
             r[e] = KVT == NORI_F16 ? f16_to_f32(h) : bf16_to_f32(h);
         }
     }
     return r;
 }
+
+// Keys whose K/V rows are loaded together and share one rescale: 4 for contexts of more than
+// 8 keys (33 x 33: 14 % faster than key by key), 1 for the in-row attentions of a few keys,
+// where the extra registers cost more occupancy than the overlapped loads gain.
+constexpr int chunk_for(int64_t nk) { return nk > 8 ? 4 : 1; }
 
 // Rounding to a runtime dtype (the query's), as torch rounds each op's result.
 __device__ __forceinline__ float round_dt(float v, int dt) {
@@ -78,7 +95,7 @@ __device__ __forceinline__ void norm_row(f32x4& v, const f32x4& w, int d, float 
     for (int e = 0; e < 4; ++e) v[e] = round_dt(round_dt(v[e] * inv, dt) * w[e], dt);
 }
 
-template <int KVT, int G>
+template <int KVT, int G, int kChunk>
 __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Args a, int64_t rows, const Prologue pro) {
     const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     int64_t row = t / G;  // (b, h, query) with the query fastest
@@ -119,27 +136,59 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
     const int64_t sbase = b * a.sc_bg + hk;
     float m = -INFINITY, l = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    // Keys in chunks of kChunk: all of a chunk's K/V rows are loaded before the first is used
+    // (the loads overlap instead of one latency per key), then its logits, one rescale of the
+    // running sums to the chunk's max, and one exponential per key. The chunk length is
+    // uniform over the wavefront.
 #pragma unroll 2
-    for (int64_t j = 0; j < a.nk; ++j) {
-        f32x4 k = {0.f, 0.f, 0.f, 0.f}, v = {0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            k = load4<KVT>(a.kv, kbase + j * a.kv_row);
-            v = load4<KVT>(a.kv, kbase + j * a.kv_row + a.kv_half);
+    for (int64_t j0 = 0; j0 < a.nk; j0 += kChunk) {
+        const int nj = (int)min((int64_t)kChunk, a.nk - j0);
+        Raw4<KVT> rk[kChunk], rv[kChunk];
+        float ks[kChunk], vsc[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            ks[u] = 1.f;
+            vsc[u] = 1.f;
+            if (u < nj) {
+                const int64_t j = j0 + u;
+                if (live) {
+                    rk[u] = load_raw4<KVT>(a.kv, kbase + j * a.kv_row);
+                    rv[u] = load_raw4<KVT>(a.kv, kbase + j * a.kv_row + a.kv_half);
+                } else {
+                    rk[u] = Raw4<KVT>{};
+                    rv[u] = Raw4<KVT>{};
+                }
+                if constexpr (KVT == NORI_I8) {
+                    ks[u] = a.kvs[sbase + j * a.sc_row];
+                    vsc[u] = a.kvs[sbase + j * a.sc_row + a.sc_half];
+                }
+            }
         }
-        if constexpr (KVT != NORI_I8) {
-            if (knorm) norm_row<G>(k, kw, a.d, pro.eps, KVT);
+        float s[kChunk];
+        float m_new = m;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            s[u] = -INFINITY;
+            if (u < nj) {
+                f32x4 k = to_f32x4<KVT>(rk[u]);
+                if constexpr (KVT != NORI_I8) {
+                    if (knorm) norm_row<G>(k, kw, a.d, pro.eps, KVT);
+                }
+                s[u] = group_sum<G>(q[0] * k[0] + q[1] * k[1] + q[2] * k[2] + q[3] * k[3]) * ks[u];
+                m_new = fmaxf(m_new, s[u]);
+            }
         }
-        float s = group_sum<G>(q[0] * k[0] + q[1] * k[1] + q[2] * k[2] + q[3] * k[3]);
-        float vs = 1.f;
-        if constexpr (KVT == NORI_I8) {
-            s *= a.kvs[sbase + j * a.sc_row];
-            vs = a.kvs[sbase + j * a.sc_row + a.sc_half];
-        }
-        const float m_new = fmaxf(m, s);
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-        const float p = __builtin_amdgcn_exp2f(s - m_new);
-        l = l * alpha + p;
-        o = o * alpha + (p * vs) * v;
+        l *= alpha;
+        o *= alpha;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            if (u < nj) {
+                const float p = __builtin_amdgcn_exp2f(s[u] - m_new);
+                l += p;
+                o += (p * vsc[u]) * to_f32x4<KVT>(rv[u]);
+            }
+        }
         m = m_new;
     }
     if (!valid) return;
@@ -160,8 +209,8 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
     if (a.lse && sub == 0) a.lse[row] = lse_out;
 }
 
-template <int KVT>
-int launch_group(const Args& a, const Prologue& pro, hipStream_t stream) {
+template <int KVT, int KC>
+int launch_chunked(const Args& a, const Prologue& pro, hipStream_t stream) {
     const int quads = (a.d + 3) / 4;
     const int64_t rows = a.bg * a.heads * a.nq;
     int g = 1;
@@ -171,14 +220,19 @@ int launch_group(const Args& a, const Prologue& pro, hipStream_t stream) {
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: %lld query rows exceed one launch", (long long)rows);
     const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads)), block(kThreads);
     switch (g) {
-        case 1: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 1>), grid, block, 0, stream, a, rows, pro); break;
-        case 2: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 2>), grid, block, 0, stream, a, rows, pro); break;
-        case 4: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 4>), grid, block, 0, stream, a, rows, pro); break;
-        case 8: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 8>), grid, block, 0, stream, a, rows, pro); break;
-        case 16: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 16>), grid, block, 0, stream, a, rows, pro); break;
-        default: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 32>), grid, block, 0, stream, a, rows, pro); break;
+        case 1: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 1, KC>), grid, block, 0, stream, a, rows, pro); break;
+        case 2: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 2, KC>), grid, block, 0, stream, a, rows, pro); break;
+        case 4: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 4, KC>), grid, block, 0, stream, a, rows, pro); break;
+        case 8: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 8, KC>), grid, block, 0, stream, a, rows, pro); break;
+        case 16: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 16, KC>), grid, block, 0, stream, a, rows, pro); break;
+        default: hipLaunchKernelGGL((icl_attention_short_kernel<KVT, 32, KC>), grid, block, 0, stream, a, rows, pro); break;
     }
     return NORI_OK;
+}
+
+template <int KVT>
+int launch_group(const Args& a, const Prologue& pro, hipStream_t stream) {
+    return chunk_for(a.nk) == 4 ? launch_chunked<KVT, 4>(a, pro, stream) : launch_chunked<KVT, 1>(a, pro, stream);
 }
 
 }  // namespace
