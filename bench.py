@@ -538,23 +538,29 @@ def main():
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    def timed(fn, sink):
+    def timed(fn, sink, on=None):
+        on = stream if on is None else on
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
+        e0.record(on)
         r = fn()
-        e1.record(stream)
+        e1.record(on)
         sink.append((e0, e1))
         return r
 
-    # The cache build runs on a second stream (default priority) and each layer's first query
-    # attention waits only for that layer's codes: the HBM-bound quantizations of layers 1..11
-    # overlap the MFMA-bound attention of the layers before them instead of running ahead of it.
+    # Streams (all at the default priority). The cache build runs on `side`, and each layer's
+    # attentions wait only for that layer's codes: the HBM-bound quantizations of layers 1..11
+    # overlap the MFMA-bound attention of the layers before them. The query batches, which are
+    # independent, run on a stream each; their attentions stay one at a time (each waits for
+    # the previous one, so every timed launch has the GPU to itself and they share the
+    # workspace), while the other batches' norms, projections and residual adds fill the gaps.
     side = torch.cuda.Stream(dev)
+    bstreams = [stream] + [torch.cuda.Stream(dev) for _ in range(len(queries) - 1)]
 
     def step(record):
         qsink, asink = ([], []) if record else (None, None)
-        side.wait_stream(stream)  # the previous step's attention has read the codes
+        for s_ in [side] + bstreams[1:]:
+            s_.wait_stream(stream)  # inputs written; the previous step's attention has read the codes
         ready = []
         with torch.cuda.stream(side):
             for layer in range(layers):
@@ -562,19 +568,24 @@ def main():
                 ev = torch.cuda.Event()
                 ev.record(side)
                 ready.append(ev)
-        outs = []
-        for bi, x in enumerate(queries):
-            for layer in range(layers):
-                if bi == 0:
-                    stream.wait_event(ready[layer])
-                xn = nori_amd.rms_norm(x, EMBED, None, 1e-5)
-                q = torch.nn.functional.linear(xn, wq[layer]).view(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM)
-                f = lambda q=q, layer=layer: nori_amd.icl_attention(q, codes[layer], scales[layer], workspace=workspace)  # noqa: E731
-                o = timed(f, asink) if record else f()
-                x = x + DEEPNORM_ALPHA * torch.einsum("...hd,hds->...s", o, wo[layer])
-            outs.append(x)
-        stream.wait_stream(side)
-        return outs, qsink, asink
+        xs = list(queries)
+        last = None
+        for layer in range(layers):
+            for bi, st in enumerate(bstreams):
+                with torch.cuda.stream(st):
+                    st.wait_event(ready[layer])
+                    xn = nori_amd.rms_norm(xs[bi], EMBED, None, 1e-5)
+                    q = torch.nn.functional.linear(xn, wq[layer]).view(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM)
+                    if last is not None:
+                        st.wait_event(last)
+                    f = lambda q=q, layer=layer: nori_amd.icl_attention(q, codes[layer], scales[layer], workspace=workspace)  # noqa: E731
+                    o = timed(f, asink, st) if record else f()
+                    last = torch.cuda.Event()
+                    last.record(st)
+                    xs[bi] = xs[bi] + DEEPNORM_ALPHA * torch.einsum("...hd,hds->...s", o, wo[layer])
+        for s_ in [side] + bstreams[1:]:
+            stream.wait_stream(s_)
+        return xs, qsink, asink
 
     for _ in range(args.warmup):
         step(False)
