@@ -135,6 +135,77 @@ class MLP(nn.Module):
         return self.mlp(x)
 
 
+class _HostRowStager:
+    """Row chunks of a host tensor [B, N, ...] staged onto the device ahead of their use, and
+    device results written back to host rows behind the compute.
+
+    Two pinned buffers each way. The uploads, the compute and the downloads are all issued on
+    the current stream, so the device orders them itself; what overlaps is the host's side:
+    chunk i+1 is copied into pinned memory and queued while the device still works on chunk i,
+    and chunk i's result is copied out of pinned memory when its buffer comes round again (or
+    at ``finish``), with the transfers at pinned speed and no synchronization per chunk. Only
+    ``row_chunk`` rows of each tensor are ever on the device. (A separate copy stream gave no
+    further gain at a 64k-row context and is not used.)
+    """
+
+    def __init__(self, src: torch.Tensor, row_chunk: int, device: torch.device):
+        self.src, self.row_chunk, self.device = src, int(row_chunk), device
+        n = src.shape[1]
+        self.slices = [slice(r0, min(r0 + self.row_chunk, n)) for r0 in range(0, n, self.row_chunk)]
+        shape = (src.shape[0], self.row_chunk) + tuple(src.shape[2:])
+        self.pin_in = [torch.empty(shape, dtype=src.dtype, pin_memory=True) for _ in range(2)]
+        self.in_done = [None, None]
+        self.pin_out = None
+        self.pending = [None, None]
+        self.n_out = 0
+
+    def _upload(self, i: int):
+        k, sl = i % 2, self.slices[i]
+        m = sl.stop - sl.start
+        if self.in_done[k] is not None:
+            self.in_done[k].synchronize()  # the pinned buffer's previous upload has left it
+        self.pin_in[k][:, :m].copy_(self.src[:, sl])
+        dev = self.pin_in[k][:, :m].to(self.device, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self.in_done[k] = ev
+        return dev
+
+    def chunks(self):
+        """Yields (row slice, device rows) in order; the next chunk is queued before each yield."""
+        nxt = self._upload(0) if self.slices else None
+        for i, sl in enumerate(self.slices):
+            dev = nxt
+            if i + 1 < len(self.slices):
+                nxt = self._upload(i + 1)
+            yield sl, dev
+
+    def write_back(self, sl: slice, out: torch.Tensor, dst: torch.Tensor) -> None:
+        """dst[:, sl] = out (a device tensor made on the current stream), asynchronously."""
+        if self.pin_out is None:
+            shape = (out.shape[0], self.row_chunk) + tuple(out.shape[2:])
+            self.pin_out = [torch.empty(shape, dtype=out.dtype, pin_memory=True) for _ in range(2)]
+        k = self.n_out % 2
+        self.n_out += 1
+        self._land(k, dst)
+        m = sl.stop - sl.start
+        self.pin_out[k][:, :m].copy_(out, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self.pending[k] = (ev, sl, m)
+
+    def _land(self, k: int, dst: torch.Tensor) -> None:
+        if self.pending[k] is not None:
+            ev, sl, m = self.pending[k]
+            ev.synchronize()
+            dst[:, sl].copy_(self.pin_out[k][:, :m])
+            self.pending[k] = None
+
+    def finish(self, dst: torch.Tensor) -> None:
+        for k in (self.n_out % 2, (self.n_out + 1) % 2):  # oldest first
+            self._land(k, dst)
+
+
 def _fused_cache_write(attn_mod, norm, copy_kv: bool, device: torch.device):
     """(weight, kv_heads, head_dim, norm_eps) for writing ``attn_mod``'s int8 cache rows with
     ``kv_project.project_quantize_kv``, or None where that kernel does not compute what the
@@ -582,11 +653,17 @@ class EncoderBaseLayer(nn.Module):
         compute_device = torch.device(device) if device is not None else attn_mod.qkv_proj_weight.device
         fused = _fused_cache_write(attn_mod, norm, copy_kv, compute_device) if quantize else None
 
-        def row_slices():
+        def host_rows():
+            if x_kv_src.device != compute_device and compute_device.type == "cuda" and x_kv_src.device.type == "cpu":
+                for _, rows in _HostRowStager(x_kv_src, row_chunk, compute_device).chunks():
+                    yield rows
+                return
             for r0 in range(0, n_rows, row_chunk):
                 rows = x_kv_src[:, r0 : min(r0 + row_chunk, n_rows)]
-                if rows.device != compute_device:
-                    rows = rows.to(compute_device)
+                yield rows.to(compute_device) if rows.device != compute_device else rows
+
+        def row_slices():
+            for rows in host_rows():
                 if fused is not None and kv_project.fusable(rows, fused[0], attn_mod.head_dim):
                     # norm, projection and quantizer in one kernel; the fp16 K/V never reach HBM
                     yield kv_project.FusedKVRows(rows.transpose(1, 2), *fused)
@@ -688,11 +765,17 @@ class EncoderBaseLayer(nn.Module):
         def write_host(source, transform):
             if n_rows <= 0:
                 raise ValueError("stream_context received an empty context")
-            for r0 in range(0, n_rows, row_chunk):
-                sl = slice(r0, min(r0 + row_chunk, n_rows))
-                staged = transform(source[:, sl].to(compute_device))
-                source[:, sl].copy_(staged.detach().to("cpu"))
-                del staged
+            if compute_device.type != "cuda":
+                for r0 in range(0, n_rows, row_chunk):
+                    sl = slice(r0, min(r0 + row_chunk, n_rows))
+                    source[:, sl].copy_(transform(source[:, sl].to(compute_device)).detach().to("cpu"))
+                return source
+            # uploads of the next rows and downloads of the last results overlap the transform
+            stager = _HostRowStager(source, row_chunk, compute_device)
+            for sl, rows in stager.chunks():
+                stager.write_back(sl, transform(rows).detach(), source)
+                del rows
+            stager.finish(source)
             return source
 
         def run_rows(rows, steps):
