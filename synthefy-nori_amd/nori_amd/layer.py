@@ -473,16 +473,25 @@ class MultiheadAttention(nn.Module):
                 if self.qk_norm:
                     q = self._norm_q(q)
                     kv = self._norm_kv(kv)
+                n_keys = int(kv.shape[1])
+                logit_scale = None
                 if self.use_qassmax:
-                    q = self.apply_qassmax(q, kv.shape[1])
-                q = self._apply_extra_attn_scale(q, kv.shape[1])
+                    if attn_mask is None and q.is_cuda and self.qassmax.qass_mode == "log_only":
+                        # QASS "log_only" multiplies q by fp16(log n); the kernel multiplies q by its
+                        # logit scale once as it loads it (rounding to f16 there), so the factor
+                        # rides on that scale instead of a separate pass over q
+                        mult = float(torch.tensor(math.log(float(max(n_keys, 2))), dtype=q.dtype)) if n_keys > 1 else 1.0
+                        logit_scale = mult / math.sqrt(float(self.head_dim))
+                    else:
+                        q = self.apply_qassmax(q, n_keys)
+                q = self._apply_extra_attn_scale(q, n_keys)
                 if attn_mask is not None:
                     k, v = kv.unbind(dim=2)
                     atten_out = self._sdpa(q, k, v, attn_mask, scaled=True)
                 else:
                     if self._attention_dropout_p() != 0.0:
                         raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
-                    atten_out = icl_attention(q, kv.contiguous() if kv.stride(-1) != 1 else kv)
+                    atten_out = icl_attention(q, kv.contiguous() if kv.stride(-1) != 1 else kv, scale=logit_scale)
         atten_out = atten_out.reshape(BS, F, self.num_heads, self.head_dim)
         if self._is_linear_projection_used(atten_out.device):
             out = torch.nn.functional.linear(
