@@ -155,6 +155,16 @@ int nori_icl_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32
                        int64_t workspace_bytes, void* stream);
 
 /*
+ * Deep-norm residual update out[i] = x[i] + alpha * u[i] over n elements, x and out fp32, u
+ * of u_dtype (NORI_F32 / NORI_F16 / NORI_BF16), rounded as torch evaluates `x + alpha * u`
+ * for those dtypes: the product in fp32 rounded to u_dtype, then the fp32 sum. Replaces the
+ * two passes of the two-phase encoder's residual updates (two_phase.py:198, 209, 220-225,
+ * 264, 271-272). out may be x.
+ */
+int nori_residual_add(const float* x, const void* u, int u_dtype, float alpha, int64_t n, float* out,
+                      void* stream);
+
+/*
  * What the two-phase encoder's attentions do to q and k between the projection and the
  * attention (layer.py:1122-1134 with qk_norm and QASS "log_only", layer.py:433-456), applied
  * by nori_icl_attention_qk to each query row and key row as it is loaded:

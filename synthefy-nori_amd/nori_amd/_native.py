@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         ],
     ),
     "nori_icl_attention_workspace_size": (_i64, [_i64, _i64, _i32, _i32, _i64]),
+    "nori_residual_add": (ctypes.c_int, [_vp, _vp, _i32, _f32, _i64, _vp, _vp]),
     "nori_kv_project_quantize_int8": (
         ctypes.c_int,
         [_vp, _i32, _i64, _i64, _i32, _i64, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32,

@@ -127,3 +127,23 @@ class RMSNorm(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return rms_norm(x, self.normalized_shape, self.weight, self.eps)
+
+
+def residual_add(x: torch.Tensor, u: torch.Tensor, alpha: float) -> torch.Tensor:
+    """``x + alpha * u`` for an fp32 residual stream and a sublayer output of the same shape, in
+    one pass on the GPU (``nori_residual_add``) with torch's rounding: ``alpha * u`` formed in
+    fp32 and rounded to u's dtype, then the fp32 sum. Other operands take the torch expression."""
+    if not (
+        x.is_cuda and x.dtype == torch.float32 and u.dtype in (torch.float32, torch.float16, torch.bfloat16)
+        and u.device == x.device and tuple(u.shape) == tuple(x.shape) and x.is_contiguous() and u.is_contiguous()
+    ):
+        return x + alpha * u
+    out = torch.empty_like(x)
+    nat.check(
+        nat.lib().nori_residual_add(
+            x.data_ptr(), u.data_ptr(), nat.dtype_code(u.dtype), float(alpha), x.numel(), out.data_ptr(),
+            nat.stream_of(x.device),
+        ),
+        "residual_add",
+    )
+    return out

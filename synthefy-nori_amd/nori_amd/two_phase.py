@@ -20,7 +20,7 @@ import torch
 from torch import nn
 
 from .layer import MultiheadAttention, SwiGLUMLP
-from .norm import RMSNorm, projection_operand as _operand
+from .norm import RMSNorm, projection_operand as _operand, residual_add as _residual
 
 __all__ = [
     "CellLayer2P",
@@ -174,21 +174,21 @@ class CellLayer2P(nn.Module):
 
     def apply_column_attention(self, cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
         """S for the cells; reads a whole column, so it slices by column only."""
-        return cells + self.deepnorm_alpha * self.column_attention(_operand(self.cell_norms[0], cells), eval_pos)
+        return _residual(cells, self.column_attention(_operand(self.cell_norms[0], cells), eval_pos), self.deepnorm_alpha)
 
     def attend_target_rows_to_context(self, rows: torch.Tensor, normalized: torch.Tensor, context_keys: torch.Tensor) -> torch.Tensor:
         """S for the target stream: ``normalized`` rows (``target_norms[0](rows).unsqueeze(1)``)
         attend to the context rows' ``context_keys``; any slice of rows may be passed."""
-        return rows + self.deepnorm_alpha * _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1)
+        return _residual(rows, _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1), self.deepnorm_alpha)
 
     def apply_row_mlps_and_feature_attention(self, cells: torch.Tensor, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """M then F; each row reads only itself. Returns (cells, targets [batch, n, K, cell_dim])."""
         a = self.deepnorm_alpha
-        cells = cells + a * self.mlp[0](_operand(self.cell_norms[1], cells))
-        rows = rows + a * self.mlp[1](_operand(self.target_norms[1], rows))
+        cells = _residual(cells, self.mlp[0](_operand(self.cell_norms[1], cells)), a)
+        rows = _residual(rows, self.mlp[1](_operand(self.target_norms[1], rows)), a)
         targets = rows.view(*rows.shape[:-1], self.target_tokens, self.cell_dim)
         cell_update, target_update = self.feature_attention(_operand(self.cell_norms[2], cells), _operand(self.target_norms[2], targets))
-        return cells + a * cell_update, targets + a * target_update
+        return _residual(cells, cell_update, a), _residual(targets, target_update, a)
 
 
 class RowLayer2P(nn.Module):
@@ -214,15 +214,15 @@ class RowLayer2P(nn.Module):
     def attend_rows_to_context(self, rows: torch.Tensor, normalized: torch.Tensor, context_keys: torch.Tensor) -> torch.Tensor:
         """``normalized`` rows (``attn_norm(rows).unsqueeze(1)``) attend to the context rows'
         ``context_keys``; any slice of rows may be passed."""
-        return rows + self.deepnorm_alpha * _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1)
+        return _residual(rows, _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1), self.deepnorm_alpha)
 
     def apply_readback_and_mlp(self, rows: torch.Tensor, cell_memory: torch.Tensor) -> torch.Tensor:
         """The row (one query) reads its own cells ``cell_memory`` [batch, rows, groups, width],
         then the MLP; each row reads only itself."""
         a = self.deepnorm_alpha
         query = _operand(self.readback_norm, rows).unsqueeze(2)
-        rows = rows + a * _attend(self.feature_attentions[0], query, cell_memory).squeeze(2)
-        return rows + a * self.mlp[0](_operand(self.mlp_norm, rows))
+        rows = _residual(rows, _attend(self.feature_attentions[0], query, cell_memory).squeeze(2), a)
+        return _residual(rows, self.mlp[0](_operand(self.mlp_norm, rows)), a)
 
 
 class TwoPhaseEncoder(nn.Module):

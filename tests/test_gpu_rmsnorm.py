@@ -93,3 +93,24 @@ def test_norm_written_in_the_autocast_dtype_equals_norm_then_cast(cuda, cols, ou
         op = projection_operand(norm, x)
     assert op.dtype == out_dtype and torch.equal(op, norm(x).to(out_dtype))
     assert projection_operand(norm, x).dtype == torch.float32  # no autocast: the norm itself
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("udtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n", [4096 * 33, 1001])
+def test_residual_add_equals_the_torch_expression(cuda, udtype, n):
+    """nori_residual_add: x + alpha * u bit for bit as torch evaluates it (the product rounded
+    to u's dtype, then the fp32 sum), on the vector path (n a multiple of 4, aligned) and the
+    element path (n = 1001); the in-row two-phase residual updates use it."""
+    from nori_amd.norm import residual_add
+
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(n, generator=g) * 5).to(cuda)
+    u = (torch.randn(n, generator=g) * 3).to(udtype).to(cuda)
+    alpha = 18 ** -0.5
+    got = residual_add(x, u, alpha)
+    assert torch.equal(got, x + alpha * u)
+    # a strided update takes the torch expression itself
+    x2 = torch.randn(64, 8, device=cuda)
+    u2 = torch.randn(8, 64, device=cuda).to(udtype).t()
+    assert torch.equal(residual_add(x2, u2, alpha), x2 + alpha * u2)
