@@ -13,38 +13,46 @@ using namespace nori;
 using namespace nori::attn;
 
 // Merges the nsplit partial (O, LSE) pairs of every tail unit's rows -- and the running
-// output when merging -- into the final output. One thread per (tail unit, row of its query
-// tile, 4-element quad of the head vector).
+// output when merging -- into the final output. A row's head vector is spread over LPR lanes
+// (one 4-element quad each, LPR >= d/4), 256 / LPR rows per workgroup. When merging, every lane
+// of a row reads the row's running LSE before the row's first lane overwrites it: the barrier
+// between the two keeps a lane from reading the new value (the lanes of a row all sit in one
+// workgroup, not always in one wavefront).
+template <int LPR>
 __global__ void __launch_bounds__(256)
 combine_splits_kernel(const Args a) {
     const int dqv = a.d >> 2;
     const int64_t ntail = a.nunits - a.n_whole;
     const int64_t prows = ntail * a.qrows;  // partial rows per context range
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= prows * dqv) return;
-    const int64_t prow = idx / dqv;
-    const int dq = (int)(idx - prow * dqv);
+    const int dq = (int)(threadIdx.x % LPR);
+    const int64_t prow = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
     const int64_t unit = a.n_whole + prow / a.qrows;
     const int qt = (int)(unit % a.nqt);
     const int h = (int)((unit / a.nqt) % a.heads);
     const int64_t b = unit / a.nqt / a.heads;
     const int64_t qi = (int64_t)qt * a.qrows + prow % a.qrows;
-    if (qi >= a.nq) return;
-    float mx = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) mx = fmaxf(mx, a.part_lse[s * prows + prow]);
-    float sum = 0.f;
-    for (int s = 0; s < a.nsplit; ++s) sum += expf(a.part_lse[s * prows + prow] - mx);
-    const float lse_part = mx + logf(sum);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.nsplit; ++s) {
-        const float w = expf(a.part_lse[s * prows + prow] - lse_part);
-        const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + (s * prows + prow) * a.d + 4 * dq);
-        acc += w * v;
-    }
-    const int64_t row = (b * a.heads + h) * a.nq + qi;
+    const bool active = prow < prows && dq < dqv && qi < a.nq;
     const bool merge = a.flags & NORI_ATTN_MERGE;
-    float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
-    if (merge) merge_weights(a.lse[row], lse_part, w_old, w_new, lse_out);
+    const int64_t row = (b * a.heads + h) * a.nq + qi;
+    float lse_part = -INFINITY;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float w_old = 0.f, w_new = 1.f, lse_out = 0.f;
+    if (active) {
+        float mx = -INFINITY;
+        for (int s = 0; s < a.nsplit; ++s) mx = fmaxf(mx, a.part_lse[s * prows + prow]);
+        float sum = 0.f;
+        for (int s = 0; s < a.nsplit; ++s) sum += expf(a.part_lse[s * prows + prow] - mx);
+        lse_part = mx + logf(sum);
+        for (int s = 0; s < a.nsplit; ++s) {
+            const float w = expf(a.part_lse[s * prows + prow] - lse_part);
+            const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + (s * prows + prow) * a.d + 4 * dq);
+            acc += w * v;
+        }
+        lse_out = lse_part;
+        if (merge) merge_weights(a.lse[row], lse_part, w_old, w_new, lse_out);
+    }
+    if (merge) __syncthreads();  // every lane has read its row's running LSE
+    if (!active) return;
     const int64_t obase = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head + 4 * dq;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -231,8 +239,10 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     if (st != NORI_OK) return st;
     if ((st = launch_status("icl_attention")) != NORI_OK) return st;
     if (args.nsplit > 1) {
-        const int64_t threads = (args.nunits - args.n_whole) * args.qrows * (d / 4);
-        hipLaunchKernelGGL(combine_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, args);
+        if (d <= 64)
+            hipLaunchKernelGGL(combine_splits_kernel<16>, dim3((unsigned)((prows + 15) / 16)), dim3(256), 0, stream, args);
+        else
+            hipLaunchKernelGGL(combine_splits_kernel<32>, dim3((unsigned)((prows + 7) / 8)), dim3(256), 0, stream, args);
         return launch_status("icl_attention combine");
     }
     return NORI_OK;
@@ -271,3 +281,4 @@ extern "C" int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int
                          sc_row_stride, sc_half_stride, scale, out, out_dtype, out_bg_stride, out_row_stride,
                          out_head_stride, lse, flags, workspace, workspace_bytes_given, prologue, stream_v);
 }
+

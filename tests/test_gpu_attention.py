@@ -261,6 +261,32 @@ def test_merge_of_two_halves_equals_one_call(cuda):
     assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, h)).all()
 
 
+@pytest.mark.parametrize("d", [44, 56, 100])
+def test_merge_with_split_context(cuda, d):
+    # Long host blocks merged into a running output, each block's context split over idle
+    # workgroup slots: the second kernel merges the split partials into the running output and
+    # overwrites the running LSE. A row's lanes (d / 4 of them: 11 at d = 44, not a divisor of
+    # the 64-lane wavefront) must all read the old LSE before it is overwritten. Two scans of
+    # the same blocks give the same bits, and both match the oracle.
+    bg, h, nq, half = 1, 2, 300, 5000
+    assert attn.workspace_bytes(bg, nq, h, d, half) > 0
+    kv = make_cache(bg, 2 * half, 1, d, cuda, seed=d + 7)
+    codes, scales = nori_amd.quantize_int8(kv)
+    q = make_queries(bg, nq, h, d, cuda, seed=d + 7)
+    runs = []
+    for _ in range(2):
+        run = torch.zeros(bg, nq, h, d, device=cuda)
+        lse = torch.full((bg, h, nq), float("-inf"), device=cuda)
+        for a, b in ((0, half), (half, 2 * half)):
+            nori_amd.icl_attention(q, codes[:, a:b], scales[:, a:b], out=run, lse=lse, merge=True)
+        runs.append((run, lse))
+    assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+    values = codes.double() * scales.double()
+    exp, exp_lse = reference(q, values)
+    check(runs[0][0], exp)
+    assert ((runs[0][1].double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, h)).all()
+
+
 @pytest.mark.parametrize("offload", [True, False])
 def test_blockwise_cache_paths(cuda, offload):
     bg, h, nq, d = 3, 2, 40, 44
