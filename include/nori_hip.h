@@ -240,6 +240,29 @@ int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_oute
 /* Bytes of workspace nori_icl_attention uses for these sizes (0 when it never splits). */
 int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk);
 
+/* Bytes of split-context scratch the library holds per device for nori_icl_attention_noalloc. */
+#define NORI_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/*
+ * nori_icl_attention without a workspace argument, allocating nothing: no hipMalloc, no
+ * hipFree, no allocating library call. Has no counterpart in the reference; it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). Arguments mean what they mean for nori_icl_attention.
+ * The split-context partials go to a scratch array of NORI_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every device it runs on until the process ends; its address is looked up
+ * on the first call on a device. Sizes whose partials need more scratch than that
+ * (nori_icl_attention_workspace_size) return NORI_ERR_UNSUPPORTED before any device work.
+ * Every call on a device shares that device's scratch: calls that overlap on one device (on
+ * different streams, or from different threads) race and must be ordered by the caller.
+ */
+int nori_icl_attention_noalloc(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
+                               int64_t q_bg_stride, int64_t q_row_stride, int64_t q_head_stride, const void* kv,
+                               int kv_dtype, const float* kv_scales, int64_t nk, int32_t kv_heads,
+                               int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                               int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride, float scale,
+                               void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
+                               int64_t out_head_stride, float* lse, uint32_t flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "icl_attention_kernel.h"
 
@@ -282,3 +283,63 @@ extern "C" int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int
                          out_head_stride, lse, flags, workspace, workspace_bytes_given, prologue, stream_v);
 }
 
+namespace {
+
+// Scratch of nori_icl_attention_noalloc: the split-context partials (O and LSE of the tail
+// units' context ranges) live in this array instead of a caller's workspace. Every device the
+// library runs on holds its own copy, from module load until the process ends. Nothing in it
+// has to start at zero: every partial the merge kernel reads is written by the attention
+// kernel of the same call first.
+static __device__ __align__(256) unsigned char scratch[NORI_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_addr[kMaxDevices] = {};  // device address of `scratch` per device
+
+// The address of the current device's copy of `scratch`, looked up once per device with that
+// device current. The host-side name `scratch` is only a handle for the lookup: kernels and
+// copies take the returned address.
+int device_scratch(void** addr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(NORI_ERR_RUNTIME, "icl_attention_noalloc: no current HIP device");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(NORI_ERR_RUNTIME, "icl_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                        dev, hipGetErrorString(e));
+        scratch_addr[dev] = p;
+    }
+    *addr = scratch_addr[dev];
+    return NORI_OK;
+}
+
+}  // namespace
+
+extern "C" int nori_icl_attention_noalloc(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads,
+                                          int32_t d, int64_t q_bg_stride, int64_t q_row_stride,
+                                          int64_t q_head_stride, const void* kv, int kv_dtype,
+                                          const float* kv_scales, int64_t nk, int32_t kv_heads,
+                                          int64_t kv_bg_stride, int64_t kv_row_stride, int64_t kv_half_stride,
+                                          int64_t sc_bg_stride, int64_t sc_row_stride, int64_t sc_half_stride,
+                                          float scale, void* out, int out_dtype, int64_t out_bg_stride,
+                                          int64_t out_row_stride, int64_t out_head_stride, float* lse,
+                                          uint32_t flags, void* stream_v) {
+    clear_error();
+    // the size check comes first and touches no device state
+    const int64_t need = nori_icl_attention_workspace_size(bg, nq, heads, d, nk);
+    if (need > NORI_NOALLOC_SCRATCH_BYTES)
+        return fail(NORI_ERR_UNSUPPORTED,
+                    "icl_attention_noalloc: these sizes need %lld bytes of split-context scratch, more than the "
+                    "%lld bytes the library holds per device; call nori_icl_attention with a workspace",
+                    (long long)need, (long long)NORI_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    const int st = device_scratch(&ws);
+    if (st != NORI_OK) return st;
+    return run_attention(q, q_dtype, bg, nq, heads, d, q_bg_stride, q_row_stride, q_head_stride, kv, kv_dtype,
+                         kv_scales, nk, kv_heads, kv_bg_stride, kv_row_stride, kv_half_stride, sc_bg_stride,
+                         sc_row_stride, sc_half_stride, scale, out, out_dtype, out_bg_stride, out_row_stride,
+                         out_head_stride, lse, flags, ws, NORI_NOALLOC_SCRATCH_BYTES, nullptr, stream_v);
+}

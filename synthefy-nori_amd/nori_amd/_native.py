@@ -18,6 +18,7 @@ NORI_OK, NORI_ERR_INVALID, NORI_ERR_RUNTIME, NORI_ERR_UNSUPPORTED, NORI_ERR_OUT_
 NORI_F32, NORI_F16, NORI_BF16, NORI_I8 = range(4)
 SCALE_DIV_TRUE, SCALE_DIV_RECIP = 0, 1
 ATTN_MERGE = 1
+NOALLOC_SCRATCH_BYTES = 32 << 20  # NORI_NOALLOC_SCRATCH_BYTES
 
 _DTYPE_CODES = {
     torch.float32: NORI_F32,
@@ -62,6 +63,16 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         ],
     ),
     "nori_icl_attention_workspace_size": (_i64, [_i64, _i64, _i32, _i32, _i64]),
+    "nori_icl_attention_noalloc": (
+        ctypes.c_int,
+        [
+            _vp, _i32, _i64, _i64, _i32, _i32, _i64, _i64, _i64,  # q
+            _vp, _i32, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64,  # kv
+            _f32,  # scale
+            _vp, _i32, _i64, _i64, _i64,  # out
+            _vp, _u32, _vp,  # lse, flags, stream
+        ],
+    ),
     "nori_residual_add": (ctypes.c_int, [_vp, _vp, _i32, _f32, _i64, _vp, _vp]),
     "nori_kv_project_quantize_int8": (
         ctypes.c_int,

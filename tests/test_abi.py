@@ -36,6 +36,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_icl_attention",
             "nori_icl_attention_qk",
             "nori_icl_attention_workspace_size",
+            "nori_icl_attention_noalloc",
             "nori_kv_project_quantize_int8",
             "nori_kv_project_quantize_int8_workspace_size",
         ]
