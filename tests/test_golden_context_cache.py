@@ -13,9 +13,9 @@ reference's context tokens and statistics (fp32 on both sides, up to summation o
 unsupported levers raise; the query-chunk OOM ladder halves and reports as the reference's.
 GPU tests: the whole build/apply through the HIP kernels. The layer K/V cache from the
 context encode is fp32 end to end: device and host differ only in summation order, which
-the normalizations amplify to ~1e-4 at worst (bar 1e-3). Outputs downstream of the f16
-attention use the reference's bf16 attention tolerance assert_close(rtol=2e-2, atol=2e-2)
-(tests/test_blockwise_context_attention.py:172).
+the normalizations amplify to ~3e-4 relative at worst. The layer stack's output and the
+quantile predictions are held to a relative error max|got - exp| / max|exp| <= 1e-3, the
+bar for predictions (measured near 2e-6; each check prints its figure).
 """
 
 from __future__ import annotations
@@ -25,11 +25,11 @@ import os
 import numpy as np
 import pytest
 import torch
+from parity import PREDICTION_BAR, check_relative
 
 from nori_amd import transformer as NT
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layer_cache_goldens.npz")
-TOL = 2e-2
 # Mirrors the configurations tests/golden/make_golden.py builds the reference models with.
 VARIANTS = {
     "a": dict(pos="none", remove_outliers=False, cross_share=False, column_y=True),
@@ -81,12 +81,13 @@ def table(gold, tag, device="cpu"):
     return x, y, int(gold[f"ctx_{tag}/n_ctx"])
 
 
-def check(got, exp, tol=TOL):
-    got = got.detach().double().cpu()
-    exp = torch.as_tensor(exp).double()
-    err = (got - exp).abs()
-    assert bool((err <= tol + tol * exp.abs()).all()), f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e})"
-    return err.max().item()
+def check(got, exp, bar=PREDICTION_BAR):
+    """max|got - exp| / max|exp| <= bar (relative 1e-3 by default, the bar for predictions)."""
+    got = torch.as_tensor(got).detach()
+    exp = torch.as_tensor(exp)
+    assert tuple(got.shape) == tuple(exp.shape), (tuple(got.shape), tuple(exp.shape))
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    return check_relative(got, exp, bar, test)
 
 
 def encode_context(model, x, y, n_ctx):
@@ -223,7 +224,7 @@ def test_build_and_apply_match_reference(gold, cuda, tag, cache_dtype):
     if cache_dtype == "bf16":
         check(ctx.caches[0]["seq_kv"]["kv"], gold[f"ctx_{tag}/kv0"], 1e-3)
     else:
-        d = ctx.caches[0]["seq_kv"]._q.cpu().numpy().astype(np.int32) - gold[f"ctx_{tag}/codes0"].astype(np.int32)
+        d = ctx.caches[0]["seq_kv"].device_payload()[0].cpu().numpy().astype(np.int32) - gold[f"ctx_{tag}/codes0"].astype(np.int32)
         assert np.abs(d).max() <= 1 and np.mean(d != 0) < 0.01
     check(seen["out"], gold[f"ctx_{tag}/stack_out_{cache_dtype}"])
     check(pred, gold[f"ctx_{tag}/pred_{cache_dtype}"])

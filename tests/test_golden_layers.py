@@ -10,9 +10,10 @@ tests/golden/make_golden.py. Cases: a multi-head cache (Hkv = H) and a shared-he
 CPU tests: the fixture loads without pickle, and this package's modules accept the
 reference's state dicts strictly (same parameter names and shapes).
 GPU tests: the same computation through the HIP kernels. Attention runs on f16 MFMA with
-fp32 accumulation against the reference's fp32 CPU path, so the bar is the reference's
-own bf16 attention tolerance, assert_close(rtol=2e-2, atol=2e-2)
-(tests/test_blockwise_context_attention.py:172); the errors reported are near 1e-3.
+fp32 accumulation against the reference's fp32 CPU path. Every output is held to a relative
+error max|got - exp| / max|exp| <= 1e-3, the bar for predictions; the measured figures
+(printed by each check) are at most 4e-4 on attention outputs and below 1e-5 downstream of
+the layer norms.
 The int8 codes are compared with the reference's CPU codes up to the scale-rounding
 difference between torch's CPU division and its GPU reciprocal multiply.
 """
@@ -24,12 +25,12 @@ import os
 import numpy as np
 import pytest
 import torch
+from parity import PREDICTION_BAR, check_relative
 
 from nori_amd import layer as NL
 from nori_amd.kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layer_cache_goldens.npz")
-TOL = 2e-2
 
 
 @pytest.fixture(scope="module")
@@ -60,12 +61,13 @@ def make_stack(gold, tag):
     return NL.LayerStack(layers).eval()
 
 
-def check(got, exp, tol=TOL):
-    got = got.detach().double().cpu()
-    exp = torch.as_tensor(exp).double()
-    err = (got - exp).abs()
-    assert bool((err <= tol + tol * exp.abs()).all()), f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e})"
-    return err.max().item()
+def check(got, exp, bar=PREDICTION_BAR):
+    """max|got - exp| / max|exp| <= bar (relative 1e-3 by default, the bar for predictions)."""
+    got = torch.as_tensor(got).detach()
+    exp = torch.as_tensor(exp)
+    assert tuple(got.shape) == tuple(exp.shape), (tuple(got.shape), tuple(exp.shape))
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    return check_relative(got, exp, bar, test)
 
 
 # ------------------------------------------------------------------------------- CPU
@@ -133,15 +135,14 @@ def test_attention_cache_paths_match_reference(gold, cuda, tag):
         dense, _ = attn.forward_with_kv_cache(x_q, cache)
         check(dense, gold[f"{tag}/out_dense"])
         # the int8 cache the reference built, consumed by the kernel as codes + scales
-        ref_scal = ScalableSeqKV.__new__(ScalableSeqKV)
-        ref_scal.batch, ref_scal.groups, ref_scal.device, ref_scal.dtype = 2, 3, cuda, torch.float32
-        ref_scal.quantized, ref_scal.offloaded, ref_scal._kv = True, False, None
-        ref_scal._q = torch.from_numpy(gold[f"{tag}/codes"]).to(cuda)
-        ref_scal._scale = torch.from_numpy(gold[f"{tag}/scales"]).to(cuda)
+        ref_scal = ScalableSeqKV.from_payload(
+            torch.from_numpy(gold[f"{tag}/codes"]).to(cuda), torch.from_numpy(gold[f"{tag}/scales"]).to(cuda), 2, 3,
+            dtype=torch.float32,
+        )
         check(attn.forward_with_kv_cache(x_q, ref_scal)[0], gold[f"{tag}/out_int8"])
         # this package's own int8 cache of the same K/V
         scal = ScalableSeqKV(cache["kv"], cache["batch"], cache["groups"], quantize=True, device=cuda)
-        codes = scal._q.cpu().numpy().astype(np.int32)
+        codes = scal.device_payload()[0].cpu().numpy().astype(np.int32)
         ref_codes = gold[f"{tag}/codes"].astype(np.int32)
         assert np.abs(codes - ref_codes).max() <= 1 and np.mean(codes != ref_codes) < 0.01
         check(attn.forward_with_kv_cache(x_q, scal)[0], gold[f"{tag}/out_int8"])
@@ -169,11 +170,11 @@ def test_layer_stack_cache_build_and_apply_match_reference(gold, cuda, tag, quan
         check(train_out, gold[f"{tag}/train_out_{sfx}"])
         if quant:
             for c in caches:
-                assert isinstance(c["seq_kv"], ScalableSeqKV) and c["seq_kv"]._q.dtype == torch.int8
+                assert isinstance(c["seq_kv"], ScalableSeqKV) and c["seq_kv"].device_payload()[0].dtype == torch.int8
             # layer 0's cache comes from the inputs through one norm and one projection, so its
             # codes match the reference's up to the division difference; deeper layers inherit
             # the attention's f16 rounding (~1e-3), which moves codes near a rounding boundary
-            d = caches[0]["seq_kv"]._q.cpu().numpy().astype(np.int32) - gold[f"{tag}/codes0"].astype(np.int32)
+            d = caches[0]["seq_kv"].device_payload()[0].cpu().numpy().astype(np.int32) - gold[f"{tag}/codes0"].astype(np.int32)
             assert np.abs(d).max() <= 1 and np.mean(d != 0) < 0.01
         test_out = stack.forward_test_with_cache(x_test, caches)
         check(test_out, gold[f"{tag}/test_out_{sfx}"])

@@ -13,9 +13,10 @@ CPU tests: the state dicts load strictly; the preprocessing chain and the PLE ed
 coordinates match the reference (fp32 on both sides; the edges are order statistics and
 interpolations of the same values); the PLE token split and the refusals of the reference's
 tests/test_model_v3.py hold. GPU tests: the whole forward and the chunked encoder through
-the HIP attention and norm kernels, to the reference's bf16 attention tolerance
-assert_close(rtol=2e-2, atol=2e-2) (tests/test_blockwise_context_attention.py:172); and
-the reference's own property that a query row never sees another (test_model_v3.py:69-84).
+the HIP attention and norm kernels, held to a relative error max|got - exp| / max|exp| <=
+1e-3 on the row states and the quantile predictions (measured near 1e-6, printed by each
+check); and the reference's own property that a query row never sees another
+(test_model_v3.py:69-84).
 """
 
 from __future__ import annotations
@@ -25,12 +26,12 @@ import os
 import numpy as np
 import pytest
 import torch
+from parity import PREDICTION_BAR, check_relative
 
 from nori_amd import transformer as NT
 from nori_amd.encoders import MaskEmbEncoder, PromptQuantilePLEEncoder
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "two_phase_goldens.npz")
-TOL = 2e-2
 PLE_BINS = 8
 EVAL_POS = 28
 # Mirrors the configurations tests/golden/make_two_phase_golden.py builds the reference models with.
@@ -81,14 +82,13 @@ def table(gold, tag, device="cpu"):
     return torch.from_numpy(gold[f"tp_{tag}/x"]).to(device), torch.from_numpy(gold[f"tp_{tag}/y"]).to(device)
 
 
-def check(got, exp, tol=TOL):
-    got = got.detach().double().cpu()
-    exp = torch.as_tensor(exp).double().cpu()
-    assert got.shape == exp.shape, (tuple(got.shape), tuple(exp.shape))
-    err = (got - exp).abs()
-    assert bool((err <= tol + tol * exp.abs()).all()), f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e})"
-    print(f"max abs err {err.max().item():.3e} (mean {err.mean().item():.2e}, bar {tol})")
-    return err.max().item()
+def check(got, exp, bar=PREDICTION_BAR):
+    """max|got - exp| / max|exp| <= bar (relative 1e-3 by default, the bar for predictions)."""
+    got = torch.as_tensor(got).detach()
+    exp = torch.as_tensor(exp)
+    assert tuple(got.shape) == tuple(exp.shape), (tuple(got.shape), tuple(exp.shape))
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    return check_relative(got, exp, bar, test)
 
 
 # ------------------------------------------------------------------------------- CPU

@@ -232,6 +232,6 @@ def test_bounded_int8_builds_fuse_the_cache_write(cuda, monkeypatch, tag, mode):
             uq = torch.cat([p for p, _ in uk.iter_payload_blocks()], dim=1)
             us = torch.cat([s for _, s in uk.iter_payload_blocks()], dim=1)
         assert_codes_close(fq.to(cuda), fs.to(cuda), uq.to(cuda), us.to(cuda), max_frac=1e-2)
-    check(f_test, u_test.float().cpu().numpy(), tol=1e-2)
+    check(f_test, u_test.float().cpu().numpy(), 1e-2)
     check(f_test, gold[f"{tag}/test_out_{mode}_int8"])
     check(f_out, gold[f"{tag}/train_out_{mode}_int8"])
