@@ -175,7 +175,13 @@ def compute_attention_blockwise(q: torch.Tensor, kv_cache: BlockwiseSeqKV, *, sd
         return icl_attention(q, payload, scales, scale=scale)
     running_output = torch.zeros((batch_groups, n_query, n_heads, head_dim), dtype=torch.float32, device=q.device)
     running_lse = torch.full((batch_groups, n_heads, n_query), float("-inf"), dtype=torch.float32, device=q.device)
-    _streamed_scan(q, kv_cache, scale, running_output, running_lse)
+    if kv_cache.offloaded:
+        _streamed_scan(q, kv_cache, scale, running_output, running_lse)
+    else:
+        # device-resident blocks in separate allocations: merged launch by launch, nothing staged
+        kv_cache.max_staged_rows = 0
+        for payload, scales in kv_cache.device_blocks():
+            icl_attention(q, payload, scales, scale=scale, out=running_output, lse=running_lse, merge=True)
     return running_output.to(q.dtype)
 
 

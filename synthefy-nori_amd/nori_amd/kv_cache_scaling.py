@@ -1,21 +1,21 @@
-"""MI355X drop-in for ``synthefy_nori.model.kv_cache_scaling``.
+"""MI355X drop-in for ``synthefy_nori.model.kv_cache_scaling``: the int8 K/V cache codec and
+the cache containers, with the reference's names, signatures, storage layout and exception
+types (src/synthefy_nori/model/kv_cache_scaling.py) and every byte of arithmetic done by
+libnori_hip.so.
 
-Same names, signatures, storage layouts and error behaviour as the reference module
-(src/synthefy_nori/model/kv_cache_scaling.py), with every byte of arithmetic done by
-libnori_hip.so:
-
-* ``quantize_int8`` / ``dequantize_int8`` (reference :29-41) run the HIP codec, whose
-  codes and scales are bit-identical to the reference torch expression evaluated on the
-  GPU.
-* ``ScalableSeqKV`` (reference :44-178) and ``BlockwiseSeqKV`` (reference :181-380) keep
-  the reference's payload layout ``[BG, N, 2, Hkv, D]`` int8 + ``[BG, N, 2, Hkv, 1]`` fp32.
-  They additionally expose the int8 payload itself (``device_payload``,
-  ``iter_payload_blocks``, ``resident_payload``) so the attention kernel reads codes
-  straight from HBM instead of re-dequantizing the whole layer for every query chunk
-  (the reference's ``cache["kv"]`` read, :78-90).
-* Resident int8 blockwise storage is filled in place: each slice is quantized straight
-  into its rows of the preallocated payload (two-level addressing in the kernel), so not
-  even one quantized slice is materialized outside the final storage.
+* ``quantize_int8`` / ``dequantize_int8`` (reference :29-41) run the HIP codec; codes and
+  scales are bit-identical to the reference torch expression evaluated on the GPU.
+* The containers are built around the stored payload, ``KVRows``: a layer's rows as int8 codes
+  + fp32 scales (or projected values) in the reference's ``[BG, N, 2, Hkv, D]`` layout, cut
+  into row parts that are either views of one device allocation or pinned host blocks. The
+  attention kernel reads that payload directly -- codes straight from HBM, dequantized in
+  registers -- instead of the reference's full-layer dequantization on every ``cache["kv"]``
+  read (:78-90). ``ScalableSeqKV`` (reference :44-178) keeps one joined payload and the
+  reference's full-layer ``["kv"]`` read; ``BlockwiseSeqKV`` (reference :181-380) has no
+  full-layer read and hands its rows out block by block, or as its one resident allocation.
+* Device-resident int8 rows are coded slice by slice straight into their place in one
+  allocation sized up front (two-level addressing in the kernel): no quantized slice exists
+  outside the final storage and nothing is concatenated on the device.
 
 There is no CPU path: quantizing or dequantizing a CPU tensor raises. Pure transport
 (unquantized host blocks, offload copies) needs no kernel and works on any device.
@@ -166,9 +166,183 @@ def quantize_int8(t: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return codes, scale
 
 
+# ----------------------------------------------------------------------------- stored rows
+# Largest int8 scale the attention kernel takes: it holds dequantized K/V as f16 values, and
+# code * scale reaches 127 * scale, which must stay within f16's 65504. Scales of caches
+# quantized from fp16 K/V (the GPU autocast path) are f16 values below it by construction;
+# caches quantized from bf16 or fp32 K/V are checked the first time the kernel reads them.
+# Scales below f16's normal range (2^-14) keep an absolute error under 127 * 2^-25 per element.
+F16_SCALE_LIMIT = 65504.0 / 127.0
+
+
+def _rows(payload: torch.Tensor) -> int:
+    return int(payload.shape[1])
+
+
+def _pinned_copy(t: torch.Tensor) -> torch.Tensor:
+    """``t`` in host memory: a pinned copy of a device tensor (so staging it back is an
+    asynchronous copy), or the host tensor itself when already there and contiguous."""
+    t = t.detach()
+    if t.device.type == "cpu":
+        return t if t.is_contiguous() else t.contiguous()
+    host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    host.copy_(t)
+    return host
+
+
+class KVRows:
+    """One layer's cached context K/V, ``[BG, N, 2, Hkv, D]``, stored as the payload the kernels read.
+
+    * ``quantized``: int8 codes plus fp32 scales ``[BG, N, 2, Hkv, 1]`` (what the reference's
+      ``quantize_int8`` returns, kv_cache_scaling.py:29-37); otherwise the projected values.
+    * ``parts``: the payload cut along the row axis, in row order, as (payload, scales or None)
+      pairs. Device-resident rows are views of one allocation, ``whole``, so the attention
+      reads the layer in one launch and nothing is ever concatenated on the device; host rows
+      are separate pinned blocks, staged onto the device one at a time (the host-offloaded
+      and streamed caches of kv_cache_scaling.py:44-90, 181-358).
+    * ``dtype``: the projected rows' dtype, which a dequantized read returns.
+    """
+
+    def __init__(self, parts, *, dtype: torch.dtype, device: torch.device, quantized: bool, on_host: bool, whole=None):
+        parts = list(parts)
+        if not parts:
+            raise ValueError("a K/V cache needs at least one block of rows")
+        self.parts = parts
+        self.whole = whole
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.quantized = bool(quantized)
+        self.on_host = bool(on_host)
+        self.n_rows = sum(_rows(p) for p, _ in parts)
+        self.max_part_rows = max(_rows(p) for p, _ in parts)
+        self._range_checked = not self.quantized or dtype == torch.float16
+
+    # ------------------------------------------------------------------ building
+    @classmethod
+    def gather(cls, slices, *, quantize: bool, on_host: bool, device=None, dtype=None, n_rows: int | None = None,
+               joined: bool = False) -> "KVRows":
+        """Store projected row slices (``[BG, n, 2, Hkv, D]`` tensors, or ``FusedKVRows`` still to
+        be projected), consumed one at a time in row order, so the full-precision layer never
+        exists beyond one slice.
+
+        * quantized on the device with ``n_rows`` known: one allocation for every row, each slice
+          coded straight into its rows (int8 codes are per row, so slice-wise coding gives the
+          whole-layer codes bit for bit);
+        * otherwise each slice is stored as it comes -- in pinned host memory when ``on_host`` --
+          and ``joined`` puts the parts back into one tensor at the end.
+        """
+        it = iter(slices)
+        first = next(it, None)
+        if first is None:
+            raise ValueError("from_row_slices: no row slices, so there is nothing to cache")
+        if dtype is None:
+            dtype = first.dtype
+        if device is None:
+            device = first.device
+        if quantize and not on_host and n_rows is not None:
+            return cls._gather_in_place(first, it, device=torch.device(device), dtype=dtype, n_rows=n_rows)
+        parts = []
+        for kv_slice in _chain(first, it):
+            if quantize:
+                payload, scales = _quantize_slice(kv_slice)
+            else:
+                payload, scales = _projected(kv_slice), None
+            if on_host:
+                payload = _pinned_copy(payload)
+                scales = None if scales is None else _pinned_copy(scales)
+            elif payload.device != torch.device(device):
+                payload = payload.to(device)
+                scales = None if scales is None else scales.to(device)
+            parts.append((payload, scales))
+            del kv_slice, payload, scales
+        whole = parts[0] if len(parts) == 1 else None
+        if joined and whole is None:
+            whole = (torch.cat([p for p, _ in parts], dim=1),
+                     torch.cat([s for _, s in parts], dim=1) if quantize else None)
+            parts = [whole]
+        return cls(parts, dtype=dtype, device=device, quantized=quantize, on_host=on_host, whole=whole)
+
+    @classmethod
+    def _gather_in_place(cls, first, rest, *, device, dtype, n_rows: int) -> "KVRows":
+        grid = tuple(first.shape)
+        codes = torch.empty((grid[0], n_rows, *grid[2:]), dtype=torch.int8, device=device)
+        scales = torch.empty((grid[0], n_rows, *grid[2:-1], 1), dtype=torch.float32, device=device)
+        parts, row = [], 0
+        for kv_slice in _chain(first, rest):
+            width = int(kv_slice.shape[1])
+            if row + width > n_rows:
+                raise ValueError(f"row slices run past the n_rows={n_rows} the cache was sized for")
+            view = (codes[:, row : row + width], scales[:, row : row + width])
+            if isinstance(kv_slice, torch.Tensor):
+                _quantize_into(kv_slice.to(device), *view)
+            else:
+                kv_slice.quantize_into(*view)
+            parts.append(view)
+            row += width
+            del kv_slice
+        if row != n_rows:
+            raise ValueError(f"row slices hold {row} rows, but the cache was sized for n_rows={n_rows}")
+        return cls(parts, dtype=dtype, device=device, quantized=True, on_host=False, whole=(codes, scales))
+
+    # ------------------------------------------------------------------ reading
+    def check_kernel_range(self) -> None:
+        """Refuse int8 scales whose values the f16 attention kernel cannot hold (above
+        F16_SCALE_LIMIT); runs once per cache, only for caches not quantized from fp16."""
+        if self._range_checked:
+            return
+        top = max(float(s.amax()) for _, s in self.parts)
+        if not top <= F16_SCALE_LIMIT:
+            raise NotImplementedError(
+                f"int8 cache scales reach {top:.4g}: its K/V values exceed the fp16 range (65504) the HIP "
+                f"attention computes in (scales up to {F16_SCALE_LIMIT:.4g} are taken)"
+            )
+        self._range_checked = True
+
+    def full(self) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """The whole layer's payload on the compute device (moved there when stored on the host)."""
+        if self.whole is None:
+            raise RuntimeError("these K/V rows are stored as separate blocks; read them block by block")
+        payload, scales = self.whole
+        if self.on_host:
+            payload = payload.to(self.device, non_blocking=True)
+            scales = None if scales is None else scales.to(self.device, non_blocking=True)
+        return payload, scales
+
+    def staged(self, block_rows: int | None):
+        """(payload, scales) blocks of at most ``block_rows`` rows (the stored parts when None)
+        on the compute device, in row order; only the block being yielded is staged."""
+        if block_rows is not None and block_rows <= 0:
+            raise ValueError("block_rows must be positive")
+        for payload, scales in self.parts:
+            n = _rows(payload)
+            step = n if block_rows is None else min(block_rows, n)
+            for r0 in range(0, n, step):
+                r1 = min(r0 + step, n)
+                # cut on the storage side, then move only the cut rows
+                p = payload[:, r0:r1].to(self.device, non_blocking=True)
+                s = None if scales is None else scales[:, r0:r1].to(self.device, non_blocking=True)
+                yield p, s
+                del p, s
+
+    def bytes_where(self, on_host: bool) -> int:
+        if self.on_host != on_host:
+            return 0
+        total = 0
+        for payload, scales in self.parts:
+            total += payload.numel() * payload.element_size()
+            if scales is not None:
+                total += scales.numel() * scales.element_size()
+        return total
+
+
+def _chain(first, rest):
+    yield first
+    yield from rest
+
+
 def _quantize_slice(kv_slice) -> tuple[torch.Tensor, torch.Tensor]:
-    """Codes and scales of a projected row slice, or of a ``FusedKVRows`` slice that is projected
-    and quantized by one kernel (nori_amd.kv_project)."""
+    """Codes and scales of a projected row slice, or of a ``FusedKVRows`` slice that one kernel
+    projects and quantizes (nori_amd.kv_project)."""
     if isinstance(kv_slice, torch.Tensor):
         return quantize_int8(kv_slice)
     return kv_slice.quantize()
@@ -176,8 +350,8 @@ def _quantize_slice(kv_slice) -> tuple[torch.Tensor, torch.Tensor]:
 
 def _projected(kv_slice) -> torch.Tensor:
     if isinstance(kv_slice, torch.Tensor):
-        return kv_slice
-    raise TypeError("a fused projection slice only builds an int8 cache (quantize=True)")
+        return kv_slice.detach()
+    raise TypeError("a fused projection slice is only ever stored as an int8 cache (quantize=True)")
 
 
 def dequantize_int8(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -194,39 +368,77 @@ def dequantize_int8(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) ->
 
 # ----------------------------------------------------------------------------- caches
 class ScalableSeqKV:
-    """Dict-like drop-in for the ``{"kv","batch","groups"}`` seq-attn cache.
+    """Whole-layer seq-attn cache, dict-like ``{"kv", "batch", "groups"}`` (reference
+    kv_cache_scaling.py:44-178), int8 and/or host-resident.
 
-    Stores ``kv`` int8-quantized and/or on host RAM; ``self["kv"]`` returns the
-    full-precision tensor on ``device`` (dequantized + moved). Reference
-    kv_cache_scaling.py:44-178. The attention operators of this package do not read
-    ``["kv"]``: they take ``device_payload()`` and dequantize inside the kernel.
+    The stored rows are a ``KVRows`` held as one payload. The attention operators of this
+    package read it through ``device_payload()`` and dequantize inside the kernel;
+    ``cache["kv"]`` is the full-precision layer the reference's readers expect, dequantized by
+    the HIP codec (and moved, when offloaded) on each read.
     """
 
-    def __init__(
-        self,
-        kv: torch.Tensor,
-        batch: int,
-        groups: int,
-        *,
-        quantize: bool = False,
-        offload: bool = False,
-        device: torch.device | None = None,
-    ):
+    def __init__(self, kv: torch.Tensor, batch: int, groups: int, *, quantize: bool = False, offload: bool = False,
+                 device: torch.device | None = None):
+        target = torch.device(device) if device is not None else kv.device
+        rows = KVRows.gather([kv], quantize=quantize, on_host=offload, device=target, dtype=kv.dtype,
+                             n_rows=int(kv.shape[1]), joined=True)
+        self._bind(rows, batch, groups)
+
+    def _bind(self, rows: KVRows, batch: int, groups: int) -> None:
+        self.rows = rows
         self.batch = int(batch)
         self.groups = int(groups)
-        self.device = torch.device(device) if device is not None else kv.device
-        self.dtype = kv.dtype
-        self.quantized = quantize
-        self.offloaded = offload
-        store_dev = torch.device("cpu") if offload else self.device
-        if quantize:
-            q, scale = quantize_int8(kv)
-            self._q = q.to(store_dev, non_blocking=False)
-            self._scale = scale.to(store_dev, non_blocking=False)
-            self._kv = None
-        else:
-            self._q = self._scale = None
-            self._kv = kv.to(store_dev, non_blocking=False)
+
+    @classmethod
+    def from_payload(cls, payload: torch.Tensor, scales: torch.Tensor | None, batch: int, groups: int, *,
+                     dtype: torch.dtype | None = None, offload: bool = False) -> "ScalableSeqKV":
+        """Wrap stored rows as they are: int8 codes with their fp32 scales (``dtype`` names what
+        they dequantize to), or full-precision values (``scales`` None)."""
+        quantized = scales is not None
+        if quantized and (payload.dtype != torch.int8 or scales.dtype != torch.float32):
+            raise ValueError("an int8 payload needs int8 codes and float32 scales")
+        obj = cls.__new__(cls)
+        rows = KVRows([(payload, scales)], dtype=dtype or (torch.float32 if quantized else payload.dtype),
+                      device=payload.device, quantized=quantized, on_host=offload, whole=(payload, scales))
+        obj._bind(rows, batch, groups)
+        return obj
+
+    @classmethod
+    def from_row_slices(cls, slices, batch: int, groups: int, *, quantize: bool = False, offload: bool = False,
+                        device: torch.device | None = None, dtype: torch.dtype | None = None) -> "ScalableSeqKV":
+        """The cache of row-axis slices taken in order (reference :92-170): each slice is coded
+        or moved as it arrives, so only one full-precision slice exists at a time; the stored
+        parts are joined into one payload at the end (int8 codes are per row, so they join to
+        the whole-layer codes bit for bit).
+
+        Raises:
+            ValueError: if ``slices`` is empty.
+        """
+        rows = KVRows.gather(slices, quantize=quantize, on_host=offload, device=device, dtype=dtype, joined=True)
+        obj = cls.__new__(cls)
+        obj._bind(rows, batch, groups)
+        return obj
+
+    # -- the reference's attributes
+    @property
+    def device(self) -> torch.device:
+        return self.rows.device
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.rows.dtype
+
+    @property
+    def quantized(self) -> bool:
+        return self.rows.quantized
+
+    @property
+    def offloaded(self) -> bool:
+        return self.rows.on_host
+
+    @property
+    def n_rows(self) -> int:
+        return self.rows.n_rows
 
     def __getitem__(self, key: str):
         if key == "batch":
@@ -234,125 +446,84 @@ class ScalableSeqKV:
         if key == "groups":
             return self.groups
         if key == "kv":
-            if self.quantized:
-                q, scale = self.device_payload()
-                return dequantize_int8(q, scale, self.dtype)
-            kv = self._kv
-            return kv.to(self.device, non_blocking=True) if self.offloaded else kv
+            payload, scales = self.rows.full()
+            return dequantize_int8(payload, scales, self.dtype) if self.quantized else payload
         raise KeyError(key)
 
     def device_payload(self) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """(payload, scale) on the compute device: int8 codes + fp32 scales, or (kv, None)."""
-        if self.quantized:
-            q = self._q.to(self.device, non_blocking=True) if self.offloaded else self._q
-            s = self._scale.to(self.device, non_blocking=True) if self.offloaded else self._scale
-            return q, s
-        kv = self._kv.to(self.device, non_blocking=True) if self.offloaded else self._kv
-        return kv, None
-
-    @property
-    def n_rows(self) -> int:
-        return int((self._q if self.quantized else self._kv).shape[1])
-
-    @classmethod
-    def from_row_slices(
-        cls,
-        slices,
-        batch: int,
-        groups: int,
-        *,
-        quantize: bool = False,
-        offload: bool = False,
-        device: torch.device | None = None,
-        dtype: torch.dtype | None = None,
-    ) -> "ScalableSeqKV":
-        """Build from row-axis slices, quantizing/moving each one as it arrives (reference :92-170).
-
-        Quantization is per (row, head) vector, so per-slice codes concatenate to the
-        whole-tensor codes bit for bit.
-
-        Raises:
-            ValueError: if ``slices`` is empty.
-        """
-        store = torch.device("cpu") if offload else None
-        q_parts: list[torch.Tensor] = []
-        scale_parts: list[torch.Tensor] = []
-        kv_parts: list[torch.Tensor] = []
-        for kv_slice in slices:
-            if dtype is None:
-                dtype = kv_slice.dtype
-            if device is None:
-                device = kv_slice.device
-            if quantize:
-                q, scale = _quantize_slice(kv_slice)
-                q_parts.append(q if store is None else q.to(store))
-                scale_parts.append(scale if store is None else scale.to(store))
-            else:
-                kv_parts.append(_projected(kv_slice) if store is None else _projected(kv_slice).to(store))
-        if not (q_parts or kv_parts):
-            raise ValueError("from_row_slices got no slices; nothing to cache")
-
-        obj = cls.__new__(cls)
-        obj.batch = int(batch)
-        obj.groups = int(groups)
-        obj.device = device if device is not None else torch.device("cpu")
-        obj.dtype = dtype
-        obj.quantized = bool(quantize)
-        obj.offloaded = bool(offload)
-        if quantize:
-            obj._q = torch.cat(q_parts, dim=1)
-            obj._scale = torch.cat(scale_parts, dim=1)
-            obj._kv = None
-        else:
-            obj._q = obj._scale = None
-            obj._kv = torch.cat(kv_parts, dim=1)
-        return obj
+        """(payload, scales) on the compute device: int8 codes + fp32 scales, or (values, None)."""
+        self.rows.check_kernel_range()
+        return self.rows.full()
 
     def resident_gpu_bytes(self) -> int:
-        """Bytes this cache holds resident on the GPU (0 if offloaded)."""
-        if self.offloaded:
-            return 0
-        if self.quantized:
-            return self._q.numel() + self._scale.numel() * 4
-        return self._kv.numel() * self._kv.element_size()
+        """Bytes held on the compute device between reads (0 when offloaded)."""
+        return self.rows.bytes_where(on_host=False)
 
 
 class BlockwiseSeqKV:
-    """Blockwise K/V storage for bounded-device attention (reference :181-380).
+    """Bounded-device seq-attn cache (reference kv_cache_scaling.py:181-380): the layer is never
+    materialized on the device, ``cache["kv"]`` raises, and readers take blocks of rows.
 
-    Host-streamed blocks live in pinned host memory; the resident int8 form is one
-    preallocated device payload exposed as disjoint row views. ``cache["kv"]`` raises;
-    consumers iterate blocks (``iter_kv_blocks`` for dequantized blocks, or
-    ``iter_payload_blocks`` / ``resident_payload`` for the raw int8 payload that the
-    attention kernel dequantizes in registers).
+    The stored rows are a ``KVRows``: pinned host blocks staged one at a time (host-streamed), or
+    one device allocation of int8 codes filled slice by slice (resident). The attention reads a
+    resident cache in one launch (``resident_payload``) and streams a host one block by block
+    with exact LSE merging (``host_blocks``); ``iter_kv_blocks`` gives the reference's
+    dequantized blocks.
     """
 
-    def __init__(
-        self,
-        blocks: list[tuple[torch.Tensor, torch.Tensor | None]],
-        batch: int,
-        groups: int,
-        *,
-        device: torch.device,
-        dtype: torch.dtype,
-        quantized: bool,
-        offloaded: bool = True,
-        _storage: tuple[torch.Tensor, torch.Tensor] | None = None,
-    ):
-        if not blocks:
-            raise ValueError("BlockwiseSeqKV requires at least one K/V block")
+    def __init__(self, blocks, batch: int, groups: int, *, device: torch.device, dtype: torch.dtype, quantized: bool,
+                 offloaded: bool = True):
+        self._bind(KVRows(blocks, dtype=dtype, device=device, quantized=quantized, on_host=offloaded), batch, groups)
+
+    def _bind(self, rows: KVRows, batch: int, groups: int) -> None:
+        self.rows = rows
         self.batch = int(batch)
         self.groups = int(groups)
-        self.device = torch.device(device)
-        self.dtype = dtype
-        self.quantized = bool(quantized)
-        self.offloaded = bool(offloaded)
-        self._blocks = blocks
-        self._storage = _storage
-        self.n_rows = sum(int(payload.shape[1]) for payload, _ in blocks)
-        self.max_block_rows = max(int(payload.shape[1]) for payload, _ in blocks)
-        # Diagnostic used by reports/tests. It is reset at the start of each scan.
+        # rows of the largest block staged by the last scan (a report of the bound held)
         self.max_staged_rows = 0
+
+    @classmethod
+    def from_row_slices(cls, slices, batch: int, groups: int, *, quantize: bool, device: torch.device,
+                        dtype: torch.dtype | None = None, offload: bool = True,
+                        n_rows: int | None = None) -> "BlockwiseSeqKV":
+        """The cache of row-axis slices taken in order (reference :232-330), with no
+        concatenation: host-streamed caches keep one pinned block per slice; resident caches are
+        int8, sized by ``n_rows`` up front and coded slice by slice into their rows."""
+        if not offload:
+            if not quantize:
+                raise ValueError("a device-resident blockwise cache is stored as int8 (quantize=True)")
+            if n_rows is None or n_rows <= 0:
+                raise ValueError("a device-resident blockwise cache must be sized by a positive n_rows")
+        rows = KVRows.gather(slices, quantize=quantize, on_host=offload, device=device, dtype=dtype,
+                             n_rows=None if offload else int(n_rows))
+        obj = cls.__new__(cls)
+        obj._bind(rows, batch, groups)
+        return obj
+
+    # -- the reference's attributes
+    @property
+    def device(self) -> torch.device:
+        return self.rows.device
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.rows.dtype
+
+    @property
+    def quantized(self) -> bool:
+        return self.rows.quantized
+
+    @property
+    def offloaded(self) -> bool:
+        return self.rows.on_host
+
+    @property
+    def n_rows(self) -> int:
+        return self.rows.n_rows
+
+    @property
+    def max_block_rows(self) -> int:
+        return self.rows.max_part_rows
 
     def __getitem__(self, key: str):
         if key == "batch":
@@ -361,189 +532,67 @@ class BlockwiseSeqKV:
             return self.groups
         if key == "kv":
             raise RuntimeError(
-                "BlockwiseSeqKV cannot materialize a full layer on the compute "
-                "device; consume iter_kv_blocks() with online-softmax attention"
+                "BlockwiseSeqKV cannot materialize a full layer on the compute device: its rows are read "
+                "block by block (iter_kv_blocks, or the HIP attention's blockwise scan)"
             )
         raise KeyError(key)
 
-    @classmethod
-    def from_row_slices(
-        cls,
-        slices,
-        batch: int,
-        groups: int,
-        *,
-        quantize: bool,
-        device: torch.device,
-        dtype: torch.dtype | None = None,
-        offload: bool = True,
-        n_rows: int | None = None,
-    ) -> "BlockwiseSeqKV":
-        """Consume projected row slices without a concatenation peak (reference :232-330).
-
-        Resident int8 caches preallocate the final payload and scales once and quantize
-        each slice directly into its rows. Host-offloaded caches keep one pinned host
-        block per slice.
-        """
-        if not offload:
-            if not quantize:
-                raise ValueError("resident blockwise K/V requires quantize=True")
-            if n_rows is None or n_rows <= 0:
-                raise ValueError("resident blockwise K/V requires a positive n_rows")
-            iterator = iter(slices)
-            try:
-                first_slice = next(iterator)
-            except StopIteration as exc:
-                raise ValueError("from_row_slices got no slices; nothing to cache") from exc
-            if dtype is None:
-                dtype = first_slice.dtype
-            target_device = torch.device(device)
-            payload_shape = (first_slice.shape[0], n_rows, *first_slice.shape[2:])
-            scale_shape = (first_slice.shape[0], n_rows, *first_slice.shape[2:-1], 1)
-            payload_storage = torch.empty(payload_shape, dtype=torch.int8, device=target_device)
-            scale_storage = torch.empty(scale_shape, dtype=torch.float32, device=target_device)
-            blocks: list[tuple[torch.Tensor, torch.Tensor | None]] = []
-            offset = 0
-
-            def store(kv_slice: torch.Tensor) -> None:
-                nonlocal offset
-                width = int(kv_slice.shape[1])
-                end = offset + width
-                if end > n_rows:
-                    raise ValueError(f"row slices exceed declared n_rows={n_rows}")
-                payload_view = payload_storage[:, offset:end]
-                scale_view = scale_storage[:, offset:end]
-                if isinstance(kv_slice, torch.Tensor):
-                    _quantize_into(kv_slice.to(target_device), payload_view, scale_view)
-                else:
-                    kv_slice.quantize_into(payload_view, scale_view)
-                blocks.append((payload_view, scale_view))
-                offset = end
-
-            store(first_slice)
-            del first_slice
-            for kv_slice in iterator:
-                store(kv_slice)
-                del kv_slice
-            if offset != n_rows:
-                raise ValueError(f"row slices covered {offset} rows, expected n_rows={n_rows}")
-            return cls(
-                blocks,
-                batch,
-                groups,
-                device=target_device,
-                dtype=dtype,
-                quantized=True,
-                offloaded=False,
-                _storage=(payload_storage, scale_storage),
-            )
-
-        blocks = []
-        for kv_slice in slices:
-            if dtype is None:
-                dtype = kv_slice.dtype
-            if quantize:
-                payload, scale = _quantize_slice(kv_slice)
-                blocks.append((_to_host(payload), _to_host(scale)))
-                del payload, scale
-            else:
-                blocks.append((_to_host(_projected(kv_slice).detach()), None))
-            del kv_slice
-        if dtype is None:
-            raise ValueError("from_row_slices got no slices; nothing to cache")
-        return cls(blocks, batch, groups, device=device, dtype=dtype, quantized=quantize, offloaded=True)
-
-    def _staged_blocks(self, block_rows: int | None):
-        if block_rows is not None and block_rows <= 0:
-            raise ValueError("block_rows must be positive")
+    def _scan(self, block_rows: int | None):
         self.max_staged_rows = 0
-        for payload, stored_scale in self._blocks:
-            stored_rows = int(payload.shape[1])
-            step = stored_rows if block_rows is None else min(block_rows, stored_rows)
-            for start in range(0, stored_rows, step):
-                end = min(start + step, stored_rows)
-                # Slice while still on the host; only this block is staged.
-                staged_payload = payload[:, start:end].to(self.device, non_blocking=True)
-                staged_scale = None
-                if self.quantized:
-                    assert stored_scale is not None
-                    staged_scale = stored_scale[:, start:end].to(self.device, non_blocking=True)
-                self.max_staged_rows = max(self.max_staged_rows, end - start)
-                yield staged_payload, staged_scale
-                del staged_payload, staged_scale
+        for payload, scales in self.rows.staged(block_rows):
+            self.max_staged_rows = max(self.max_staged_rows, _rows(payload))
+            yield payload, scales
 
     def iter_kv_blocks(self, block_rows: int | None = None):
-        """Yield full-precision K/V blocks on the compute device, in row order."""
-        for payload, scale in self._staged_blocks(block_rows):
-            yield dequantize_int8(payload, scale, self.dtype) if self.quantized else payload
+        """Full-precision K/V blocks on the compute device, in row order."""
+        for payload, scales in self._scan(block_rows):
+            yield dequantize_int8(payload, scales, self.dtype) if self.quantized else payload
 
     def iter_payload_blocks(self, block_rows: int | None = None):
-        """Yield (payload, scale-or-None) blocks on the compute device without dequantizing."""
-        yield from self._staged_blocks(block_rows)
+        """(payload, scales or None) blocks on the compute device, not dequantized."""
+        self.rows.check_kernel_range()
+        yield from self._scan(block_rows)
 
     def host_blocks(self) -> list[tuple[torch.Tensor, torch.Tensor | None]]:
-        """The stored (payload, scale-or-None) blocks of a host-offloaded cache, in row order: the
-        source of the overlapped streamed scan, which stages them itself."""
+        """The stored (payload, scales or None) host blocks in row order: what the overlapped
+        streamed scan stages itself."""
         if not self.offloaded:
             raise RuntimeError("host_blocks() is for host-offloaded caches; use resident_payload()")
-        return list(self._blocks)
+        self.rows.check_kernel_range()
+        return list(self.rows.parts)
+
+    def device_blocks(self) -> list[tuple[torch.Tensor, torch.Tensor | None]]:
+        """The stored (payload, scales or None) blocks of a device-resident cache, in row order."""
+        if self.offloaded:
+            raise RuntimeError("device_blocks() is for device-resident caches; use host_blocks()")
+        self.rows.check_kernel_range()
+        return list(self.rows.parts)
 
     def resident_payload(self) -> tuple[torch.Tensor, torch.Tensor] | None:
-        """The whole resident int8 payload and scales, when the cache is device resident."""
-        if self.offloaded or self._storage is None:
+        """The whole device-resident payload and scales (one allocation), else None."""
+        if self.offloaded or self.rows.whole is None:
             return None
-        return self._storage
+        self.rows.check_kernel_range()
+        return self.rows.whole
 
     def resident_gpu_bytes(self) -> int:
-        """Bytes retained on the compute device between iterator steps."""
-        if self.offloaded:
-            return 0
-        total = 0
-        for payload, scale in self._blocks:
-            total += payload.numel() * payload.element_size()
-            if scale is not None:
-                total += scale.numel() * scale.element_size()
-        return total
+        """Bytes held on the compute device between scans."""
+        return self.rows.bytes_where(on_host=False)
 
     def host_bytes(self) -> int:
-        """Bytes retained by the host block list."""
-        if not self.offloaded:
-            return 0
-        total = 0
-        for payload, scale in self._blocks:
-            total += payload.numel() * payload.element_size()
-            if scale is not None:
-                total += scale.numel() * scale.element_size()
-        return total
+        """Bytes held in host memory."""
+        return self.rows.bytes_where(on_host=True)
 
 
-def _to_host(t: torch.Tensor) -> torch.Tensor:
-    """Copy to host memory; pinned when the source is on a GPU so later H2D staging is async."""
-    if t.device.type == "cpu":
-        return t.detach().clone() if not t.is_contiguous() else t.detach()
-    host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-    host.copy_(t.detach())
-    return host
-
-
-def scale_caches(
-    caches: list[dict], *, quantize: bool = False, offload: bool = False, device: torch.device | None = None
-) -> list[dict]:
-    """Wrap each layer cache's ``seq_kv`` in a ScalableSeqKV (in place), reference :383-404."""
-    if not (quantize or offload):
-        return caches
-    for layer_cache in caches:
-        skv = layer_cache.get("seq_kv")
-        if skv is None or isinstance(skv, (ScalableSeqKV, BlockwiseSeqKV)):
-            continue
-        if "kv" not in skv:
-            continue
-        layer_cache["seq_kv"] = ScalableSeqKV(
-            skv["kv"],
-            skv["batch"],
-            skv["groups"],
-            quantize=quantize,
-            offload=offload,
-            device=device,
-        )
+def scale_caches(caches: list[dict], *, quantize: bool = False, offload: bool = False,
+                 device: torch.device | None = None) -> list[dict]:
+    """Store every layer's ``seq_kv`` dict as a ScalableSeqKV, int8 and/or host-resident, in
+    place (reference :383-404). Nothing to do when neither is asked; caches already converted,
+    and caches without a ``kv`` entry, are left as they are."""
+    if quantize or offload:
+        for layer_cache in caches:
+            entry = layer_cache.get("seq_kv")
+            if isinstance(entry, dict) and "kv" in entry:
+                layer_cache["seq_kv"] = ScalableSeqKV(entry["kv"], entry["batch"], entry["groups"], quantize=quantize,
+                                                      offload=offload, device=device)
     return caches

@@ -449,3 +449,29 @@ def test_short_context_at_two_phase_scale(cuda):
     exp = torch.matmul(p, vf).permute(0, 2, 1, 3)
     err = (fused.float() - exp).abs()
     assert err.max().item() < 4e-3, f"max abs err {err.max().item():.3e}"
+
+
+def test_int8_scales_outside_the_f16_range(cuda):
+    # Caches quantized from bf16 K/V may carry scales outside f16's range. Tiny ones (vectors
+    # with amax ~1e-9, scales below f16's subnormals) dequantize to ~0 in the kernel: an
+    # absolute error below 127 * 2^-25 per element, far inside the bar. Scales whose K/V values
+    # exceed f16's range (127 * scale > 65504) are refused when a container hands the payload
+    # to the kernel.
+    bg, h, nq, nk, d = 2, 2, 40, 300, 44
+    kv = make_cache(bg, nk, h, d, cuda, seed=51, dtype=torch.bfloat16)
+    kv[:, 7:40] *= 1e-9
+    cache = ScalableSeqKV(kv, 1, bg, quantize=True, device=cuda)
+    payload, scales = cache.device_payload()
+    assert float(scales.min()) < 2.0**-24
+    q = make_queries(bg, nq, h, d, cuda, seed=51)
+    got = nori_amd.attend_dense(q, cache)
+    exp, _ = reference(q, payload.double() * scales.double())
+    check(got, exp)
+    big = ScalableSeqKV(make_cache(bg, nk, h, d, cuda, seed=52, dtype=torch.bfloat16) * 1e6, 1, bg, quantize=True,
+                        device=cuda)
+    with pytest.raises(NotImplementedError, match="fp16 range"):
+        nori_amd.attend_dense(q, big)
+    blocks = BlockwiseSeqKV.from_row_slices(iter([kv[:, :100] * 1e6, kv[:, 100:]]), 1, bg, quantize=True, device=cuda,
+                                            offload=True)
+    with pytest.raises(NotImplementedError, match="fp16 range"):
+        nori_amd.compute_attention_blockwise(q, blocks)

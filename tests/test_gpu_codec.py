@@ -138,11 +138,11 @@ def test_row_slices_into_preallocated_storage_equal_whole_tensor(cuda):
     )
     payload, scales = cache.resident_payload()
     assert_bits_equal(payload, scales, whole_q, whole_s)
-    assert len({p.untyped_storage().data_ptr() for p, _ in cache._blocks}) == 1
+    assert len({p.untyped_storage().data_ptr() for p, _ in cache.device_blocks()}) == 1
     dense = ScalableSeqKV(kv, 3, 4, quantize=True, device=cuda)
     assert torch.equal(torch.cat(list(cache.iter_kv_blocks()), dim=1), dense["kv"])
     built = ScalableSeqKV.from_row_slices(iter([kv[:, :100], kv[:, 100:]]), 3, 4, quantize=True, device=cuda)
-    assert_bits_equal(built._q, built._scale, whole_q, whole_s)
+    assert_bits_equal(*built.device_payload(), whole_q, whole_s)
 
 
 def test_roundtrip_error_and_empty_input(cuda):
