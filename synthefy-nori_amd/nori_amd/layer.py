@@ -27,6 +27,7 @@ from __future__ import annotations
 import functools
 import math
 import os
+import warnings
 from functools import partial
 from typing import Optional
 
@@ -135,6 +136,12 @@ class MLP(nn.Module):
         return self.mlp(x)
 
 
+def _front_rows(flat: torch.Tensor, shape, m: int) -> torch.Tensor:
+    """The first ``m`` rows of a [B, rows, ...] layout over flat storage, as a contiguous view."""
+    rest = tuple(shape[2:])
+    return flat[: shape[0] * m * math.prod(rest)].view(shape[0], m, *rest)
+
+
 class _HostRowStager:
     """Row chunks of a host tensor [B, N, ...] staged onto the device ahead of their use, and
     device results written back to host rows behind the compute.
@@ -152,8 +159,10 @@ class _HostRowStager:
         self.src, self.row_chunk, self.device = src, int(row_chunk), device
         n = src.shape[1]
         self.slices = [slice(r0, min(r0 + self.row_chunk, n)) for r0 in range(0, n, self.row_chunk)]
-        shape = (src.shape[0], self.row_chunk) + tuple(src.shape[2:])
-        self.pin_in = [torch.empty(shape, dtype=src.dtype, pin_memory=True) for _ in range(2)]
+        # flat pinned buffers: the rows of a chunk (also the last, shorter one) are a contiguous
+        # view at their front, so every transfer is one asynchronous pinned copy
+        numel = src.shape[0] * self.row_chunk * math.prod(src.shape[2:])
+        self.pin_in = [torch.empty(numel, dtype=src.dtype, pin_memory=True) for _ in range(2)]
         self.in_done = [None, None]
         self.pin_out = None
         self.pending = [None, None]
@@ -164,8 +173,9 @@ class _HostRowStager:
         m = sl.stop - sl.start
         if self.in_done[k] is not None:
             self.in_done[k].synchronize()  # the pinned buffer's previous upload has left it
-        self.pin_in[k][:, :m].copy_(self.src[:, sl])
-        dev = self.pin_in[k][:, :m].to(self.device, non_blocking=True)
+        rows = _front_rows(self.pin_in[k], self.src.shape, m)
+        rows.copy_(self.src[:, sl])
+        dev = rows.to(self.device, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
         self.in_done[k] = ev
@@ -183,13 +193,14 @@ class _HostRowStager:
     def write_back(self, sl: slice, out: torch.Tensor, dst: torch.Tensor) -> None:
         """dst[:, sl] = out (a device tensor made on the current stream), asynchronously."""
         if self.pin_out is None:
-            shape = (out.shape[0], self.row_chunk) + tuple(out.shape[2:])
-            self.pin_out = [torch.empty(shape, dtype=out.dtype, pin_memory=True) for _ in range(2)]
+            numel = out.shape[0] * self.row_chunk * math.prod(out.shape[2:])
+            self.pin_out = [torch.empty(numel, dtype=out.dtype, pin_memory=True) for _ in range(2)]
+            self.out_shape = tuple(out.shape)
         k = self.n_out % 2
         self.n_out += 1
         self._land(k, dst)
         m = sl.stop - sl.start
-        self.pin_out[k][:, :m].copy_(out, non_blocking=True)
+        _front_rows(self.pin_out[k], self.out_shape, m).copy_(out, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
         self.pending[k] = (ev, sl, m)
@@ -198,7 +209,7 @@ class _HostRowStager:
         if self.pending[k] is not None:
             ev, sl, m = self.pending[k]
             ev.synchronize()
-            dst[:, sl].copy_(self.pin_out[k][:, :m])
+            dst[:, sl].copy_(_front_rows(self.pin_out[k], self.out_shape, m))
             self.pending[k] = None
 
     def finish(self, dst: torch.Tensor) -> None:
@@ -294,6 +305,19 @@ class MultiheadAttention(nn.Module):
     # -------------------------------------------------------------- query scaling
     def apply_qassmax(self, q: torch.Tensor, key_len: int) -> torch.Tensor:
         return q if self.qassmax is None else self.qassmax(q, key_len)
+
+    # QASS "log_only" on the MFMA attention path: fold the log-n multiply into the kernel's
+    # logit scale (True) or run it as QASSMaxScaling's separate multiply (False).
+    fold_log_only_qass = True
+
+    def log_only_logit_scale(self, n_keys: int, dtype: torch.dtype) -> float:
+        """The logit scale that carries QASS "log_only" (layer.py:433-456): T(log n) / sqrt(D),
+        with T(log n) the factor QASSMaxScaling.forward multiplies q by in q's dtype T, and no
+        factor for a single key (its forward returns q unscaled there). The kernel multiplies
+        q by this scale as it loads it and rounds the product to f16 once, where the separate
+        passes round q * T(log n) to T and then q * scale to f16."""
+        mult = float(torch.tensor(math.log(float(max(n_keys, 2))), dtype=dtype)) if n_keys > 1 else 1.0
+        return mult / math.sqrt(float(self.head_dim))
 
     def _apply_extra_attn_scale(self, q: torch.Tensor, n_keys: int) -> torch.Tensor:
         """q * temperature * log(n)/log(n_ref) (reference layer.py:555-583)."""
@@ -438,9 +462,10 @@ class MultiheadAttention(nn.Module):
             if self.use_qassmax:
                 qkv = torch.stack((self.apply_qassmax(qkv[:, :, 0], qkv.shape[1]), qkv[:, :, 1], qkv[:, :, 2]), dim=2)
             q, k, v = qkv.unbind(dim=2)
-            if attn_mask is None and qkv.is_cuda and short_context(F, F) and self._attention_dropout_p() == 0.0:
-                # a row's tokens attending to each other: the short-context kernel, reading K/V
-                # straight out of the [.., 3, H, D] projection (its K then V heads)
+            if attn_mask is None and qkv.is_cuda and self._attention_dropout_p() == 0.0:
+                # a row's tokens attending to each other: the HIP kernel (the short-context one
+                # for up to 2048 query x key pairs, the MFMA one beyond), reading K/V straight
+                # out of the [.., 3, H, D] projection (its K then V heads)
                 atten_out = icl_attention(self._apply_extra_attn_scale(q, F), qkv[:, :, 1:])
             else:
                 atten_out = self._sdpa(q, k, v, attn_mask)
@@ -476,12 +501,12 @@ class MultiheadAttention(nn.Module):
                 n_keys = int(kv.shape[1])
                 logit_scale = None
                 if self.use_qassmax:
-                    if attn_mask is None and q.is_cuda and self.qassmax.qass_mode == "log_only":
-                        # QASS "log_only" multiplies q by fp16(log n); the kernel multiplies q by its
-                        # logit scale once as it loads it (rounding to f16 there), so the factor
-                        # rides on that scale instead of a separate pass over q
-                        mult = float(torch.tensor(math.log(float(max(n_keys, 2))), dtype=q.dtype)) if n_keys > 1 else 1.0
-                        logit_scale = mult / math.sqrt(float(self.head_dim))
+                    if (attn_mask is None and q.is_cuda and self.qassmax.qass_mode == "log_only"
+                            and self.fold_log_only_qass):
+                        # QASS "log_only" multiplies q by T(log n) in q's dtype T; the kernel
+                        # multiplies q by its logit scale once as it loads it, so the factor rides
+                        # on that scale instead of a separate pass over q
+                        logit_scale = self.log_only_logit_scale(n_keys, q.dtype)
                     else:
                         q = self.apply_qassmax(q, n_keys)
                 q = self._apply_extra_attn_scale(q, n_keys)
@@ -503,7 +528,12 @@ class MultiheadAttention(nn.Module):
         return out.reshape(B, S, *out.shape[1:]), None, None
 
     def _sdpa(self, q, k, v, attn_mask, scaled: bool = False):
-        """torch SDPA over [B, seq, heads, D] (the reference's own op, layer.py:1008-1049)."""
+        """torch SDPA over [B, seq, heads, D] (the reference's own op, layer.py:1008-1049): the
+        masked attentions, which the HIP kernel does not take. The model's cache paths never
+        pass a mask (the reference calls its layers with feature_atten_mask=None,
+        transformer.py:467, 945, 1052, 1283); a direct masked call is reported once."""
+        if q.is_cuda:
+            _report_sdpa_once()
         if not scaled:
             q = self._apply_extra_attn_scale(q, k.size(1))
         enable_gqa = k.size(2) != q.size(2)
@@ -513,6 +543,21 @@ class MultiheadAttention(nn.Module):
                 dropout_p=self._attention_dropout_p(), enable_gqa=enable_gqa,
             )
         return o.transpose(1, 2)
+
+
+_SDPA_REPORTED = False
+
+
+def _report_sdpa_once() -> None:
+    global _SDPA_REPORTED
+    if not _SDPA_REPORTED:
+        _SDPA_REPORTED = True
+        warnings.warn(
+            "nori_amd: a masked attention runs on torch SDPA, not on the HIP attention kernel "
+            "(the kernel takes no attention mask)",
+            RuntimeWarning,
+            stacklevel=3,
+        )
 
 
 class EncoderBaseLayer(nn.Module):

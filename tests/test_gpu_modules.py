@@ -1,0 +1,71 @@
+"""Module-level routes into the HIP attention kernel.
+
+* QASS "log_only" on the MFMA path (the two-phase column/row attentions): the log-n multiply
+  rides on the kernel's logit scale instead of a separate fp16 multiply over q
+  (QASSMaxScaling.forward, layer.py:433-456). Same module, fold on and off, under fp16
+  autocast at the config-5 column-attention shape (320 queries over 256 context keys): the
+  only difference is one f16 rounding of q, so the outputs agree to 5e-3.
+* The combined-QKV feature attention over a row's tokens at a width past the short-context
+  kernel (51 tokens, nori-100m's token groups): the MFMA kernel, against the float64 oracle
+  on the same projected q/k/v.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nori_amd.layer import MultiheadAttention
+from oracle import attention as oa
+from parity import check_relative
+
+pytestmark = pytest.mark.gpu
+
+
+def _module(cuda, embed, heads, **kw):
+    torch.manual_seed(7)
+    mod = MultiheadAttention(embed_dim=embed, num_heads=heads, dropout=0.0, **kw).to(cuda).eval()
+    if mod.q_norm is not None:  # gains away from 1, so the norms' gains are exercised
+        with torch.no_grad():
+            mod.q_norm.weight.uniform_(0.5, 1.5)
+            mod.k_norm.weight.uniform_(0.5, 1.5)
+    return mod
+
+
+@pytest.mark.parametrize("n_ctx", [256, 1])
+def test_log_only_qass_fold_matches_separate_multiply(cuda, n_ctx):
+    mod = _module(cuda, 128, 2, qkv_combined=False, use_qassmax=True, qass_mode="log_only", qk_norm=True)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    cells = torch.randn(2, 3, 320, 128, generator=g).to(cuda)  # [tables, columns, rows, width]
+    outs = {}
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        for fold in (True, False):
+            mod.fold_log_only_qass = fold
+            outs[fold] = mod(cells, x_kv=cells[:, :, :n_ctx])[0].float()
+    mod.fold_log_only_qass = True
+    err = (outs[True] - outs[False]).abs().max().item()
+    print(f"[parity] QASS log_only fold vs separate multiply, {n_ctx} keys: max abs {err:.3e}", flush=True)
+    assert err <= 5e-3
+    if n_ctx == 1:
+        # one key: every query reads that key's value whatever its scale, and no log-n factor applies
+        assert mod.log_only_logit_scale(1, torch.float16) == 1.0 / math.sqrt(64)
+
+
+def test_wide_combined_qkv_feature_attention_runs_on_the_kernel(cuda):
+    tokens, embed, heads = 51, 112, 2
+    mod = _module(cuda, embed, heads, qkv_combined=True)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    x = torch.randn(1, 300, tokens, embed, generator=g).to(cuda)  # [tables, rows, tokens, width]
+    with torch.inference_mode():
+        out = mod(x)[0]
+        qkv = torch.einsum("... s, j h d s -> ... j h d", x.reshape(-1, tokens, embed), mod.qkv_proj_weight)
+        ref, _ = oa.attention_f64(*(qkv[:, :, j].double().cpu().numpy() for j in range(3)))
+        d = embed // heads
+        ref = torch.from_numpy(ref).reshape(300, tokens, heads * d)
+        w_out = mod.out_proj_weight.double().cpu().reshape(heads * d, embed)
+        expected = (ref @ w_out).reshape(1, 300, tokens, embed)
+    check_relative(out, expected, 1e-3, "51-token combined-QKV feature attention vs float64 oracle")
+    assert np.isfinite(out.cpu().numpy()).all()

@@ -128,3 +128,20 @@ def test_fused_rows_report_the_projected_slice_they_stand_for():
     # host tensors are never taken by the kernel
     assert not fusable(x, w, 16)
 
+
+
+def test_log_only_qass_logit_scale_rounds_log_n_in_the_query_dtype():
+    # QASSMaxScaling.forward (layer.py:433-456) multiplies q by log(n) cast to q's dtype, and
+    # returns q untouched for a single key; the folded logit scale carries exactly that factor
+    import math
+
+    from nori_amd.layer import MultiheadAttention
+
+    mod = MultiheadAttention(embed_dim=128, num_heads=2, use_qassmax=True, qass_mode="log_only", qk_norm=True)
+    for n in (2, 256, 65536, 70000):
+        for dtype in (torch.float16, torch.bfloat16, torch.float32):
+            factor = torch.tensor(math.log(n), dtype=dtype).item()
+            assert mod.log_only_logit_scale(n, dtype) == factor / 8.0
+    assert mod.log_only_logit_scale(256, torch.float16) != math.log(256) / 8.0  # the fp16 rounding is kept
+    assert mod.log_only_logit_scale(1, torch.float16) == 1.0 / 8.0
+    assert mod.log_only_logit_scale(0, torch.float32) == 1.0 / 8.0
