@@ -165,6 +165,17 @@ int nori_residual_add(const float* x, const void* u, int u_dtype, float alpha, i
                       void* stream);
 
 /*
+ * SwiGLU gate over the [gate | up] output of one fused projection (gate and up weights stacked,
+ * so the operand is read once): out[r, j] = T(T(silu(gu[r, j])) * gu[r, hidden + j]) with
+ * silu(x) = x / (1 + exp(-x)) in fp32 and T the rounding to `dtype` (NORI_F32 / NORI_F16 /
+ * NORI_BF16) -- torch's F.silu(gate) * up in that dtype, the middle of SwiGLUMLP.forward
+ * (src/synthefy_nori/model/layer.py:261-274). Rows at row_stride (>= 2 * hidden) elements in,
+ * out_row_stride (>= hidden) out.
+ */
+int nori_silu_mul(const void* gu, int dtype, int64_t rows, int32_t hidden, int64_t row_stride, void* out,
+                  int64_t out_row_stride, void* stream);
+
+/*
  * What the two-phase encoder's attentions do to q and k between the projection and the
  * attention (layer.py:1122-1134 with qk_norm and QASS "log_only", layer.py:433-456), applied
  * by nori_icl_attention_qk to each query row and key row as it is loaded:

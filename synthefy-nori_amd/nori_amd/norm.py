@@ -1,4 +1,5 @@
-"""RMSNorm on libnori_hip.so -- drop-in for ``RMSNorm`` (src/synthefy_nori/model/layer.py:233-258)."""
+"""Row-wise kernels of libnori_hip.so around the attention: RMSNorm (drop-in for ``RMSNorm``,
+src/synthefy_nori/model/layer.py:233-258), the deep-norm residual update and the SwiGLU gate."""
 
 from __future__ import annotations
 
@@ -52,15 +53,19 @@ def rms_norm_(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 
 
 def rms_norm(
     x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None, eps: float = 1e-5, *,
-    out_dtype: torch.dtype | None = None,
+    out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """x * rsqrt(mean(x^2) + eps) (* weight) over the trailing ``normalized_shape`` axes.
 
     The native ``F.rms_norm`` semantics (layer.py:253): statistic and product in fp32,
     one rounding to x's dtype, then the weight multiply. ``out_dtype`` (fp16 or bf16, for an
     fp32 ``x``) writes that result rounded once more to ``out_dtype``: the value
-    ``rms_norm(x).to(out_dtype)`` has, in one pass.
+    ``rms_norm(x).to(out_dtype)`` has, in one pass. ``out`` (x's shape, rows at one stride, its
+    dtype the output dtype) receives the rows in place of a new tensor -- e.g. a slice of a
+    buffer that stacks several normalized operands.
     """
+    if out is not None:
+        return _rms_norm_into(x, normalized_shape, weight, eps, out)
     if isinstance(normalized_shape, int):
         normalized_shape = (normalized_shape,)
     normalized_shape = tuple(normalized_shape)
@@ -92,6 +97,43 @@ def rms_norm(
         "rms_norm",
     )
     return y.reshape(x.shape)
+
+
+def _rms_norm_into(x, normalized_shape, weight, eps, out):
+    cols = 1
+    for n in (normalized_shape,) if isinstance(normalized_shape, int) else normalized_shape:
+        cols *= int(n)
+    if tuple(out.shape) != tuple(x.shape):
+        raise ValueError(f"rms_norm out {tuple(out.shape)} does not match x {tuple(x.shape)}")
+    device = nat.require_device(x, weight, out)
+    src = _strided_rows(x, cols)
+    if src is None:
+        x = x.contiguous()
+        src = _strided_rows(x, cols)
+    dst = _strided_rows(out, cols)
+    if dst is None or dst[0] != src[0]:
+        raise ValueError(f"rms_norm out needs rows of {cols} at one stride, got strides {out.stride()}")
+    w = None if weight is None else weight.reshape(cols).contiguous()
+    if x.numel():
+        nat.check(
+            nat.lib().nori_rms_norm_to(
+                x.data_ptr(), nat.dtype_code(x.dtype), src[0], cols, src[1],
+                nat.ptr(w), nat.dtype_code(w.dtype) if w is not None else nat.NORI_F32, float(eps),
+                out.data_ptr(), nat.dtype_code(out.dtype), dst[1], nat.stream_of(device),
+            ),
+            "rms_norm",
+        )
+    return out
+
+
+def operand_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype a projection of ``x`` computes in: the autocast dtype for an fp32 ``x`` under
+    fp16/bf16 autocast on the GPU, else x's own."""
+    if x.dtype == torch.float32 and x.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        if dt in (torch.float16, torch.bfloat16):
+            return dt
+    return x.dtype
 
 
 def projection_operand(norm: "RMSNorm", x: torch.Tensor) -> torch.Tensor:
@@ -129,16 +171,19 @@ class RMSNorm(nn.Module):
         return rms_norm(x, self.normalized_shape, self.weight, self.eps)
 
 
-def residual_add(x: torch.Tensor, u: torch.Tensor, alpha: float) -> torch.Tensor:
+def residual_add(x: torch.Tensor, u: torch.Tensor, alpha: float, *, inplace: bool = False) -> torch.Tensor:
     """``x + alpha * u`` for an fp32 residual stream and a sublayer output of the same shape, in
     one pass on the GPU (``nori_residual_add``) with torch's rounding: ``alpha * u`` formed in
-    fp32 and rounded to u's dtype, then the fp32 sum. Other operands take the torch expression."""
+    fp32 and rounded to u's dtype, then the fp32 sum. ``inplace`` writes the sum over x (same
+    values). Other operands take the torch expression."""
     if not (
         x.is_cuda and x.dtype == torch.float32 and u.dtype in (torch.float32, torch.float16, torch.bfloat16)
         and u.device == x.device and tuple(u.shape) == tuple(x.shape) and x.is_contiguous() and u.is_contiguous()
     ):
+        if inplace:
+            return x.add_(alpha * u)
         return x + alpha * u
-    out = torch.empty_like(x)
+    out = x if inplace else torch.empty_like(x)
     nat.check(
         nat.lib().nori_residual_add(
             x.data_ptr(), u.data_ptr(), nat.dtype_code(u.dtype), float(alpha), x.numel(), out.data_ptr(),
@@ -147,3 +192,24 @@ def residual_add(x: torch.Tensor, u: torch.Tensor, alpha: float) -> torch.Tensor
         "residual_add",
     )
     return out
+
+
+def silu_mul(gu: torch.Tensor, hidden: int) -> torch.Tensor:
+    """``F.silu(gu[..., :hidden]) * gu[..., hidden:]`` for the [gate | up] output of a stacked
+    projection, in gu's dtype with torch's rounding of the two ops, one HIP pass
+    (``nori_silu_mul``). SwiGLUMLP.forward's gate (layer.py:261-274)."""
+    if gu.shape[-1] != 2 * hidden:
+        raise ValueError(f"silu_mul expects the [gate | up] width {2 * hidden}, got {gu.shape[-1]}")
+    device = nat.require_device(gu)
+    g2 = gu.reshape(-1, 2 * hidden)
+    if g2.stride(-1) != 1:
+        g2 = g2.contiguous()
+    out = torch.empty((g2.shape[0], hidden), dtype=gu.dtype, device=device)
+    nat.check(
+        nat.lib().nori_silu_mul(
+            g2.data_ptr(), nat.dtype_code(gu.dtype), g2.shape[0], hidden, g2.stride(0), out.data_ptr(), hidden,
+            nat.stream_of(device),
+        ),
+        "silu_mul",
+    )
+    return out.view(*gu.shape[:-1], hidden)

@@ -69,3 +69,39 @@ def test_wide_combined_qkv_feature_attention_runs_on_the_kernel(cuda):
         expected = (ref @ w_out).reshape(1, 300, tokens, embed)
     check_relative(out, expected, 1e-3, "51-token combined-QKV feature attention vs float64 oracle")
     assert np.isfinite(out.cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hidden", [170, 341, 64])
+def test_silu_mul_is_torch_silu_times_up(cuda, dtype, hidden):
+    # the SwiGLU gate of one stacked [gate | up] projection against torch's own two ops in the
+    # same dtype (F.silu then *), element for element; widths with and without the 4-wide path
+    from nori_amd.norm import silu_mul
+
+    g = torch.Generator(device="cpu").manual_seed(hidden)
+    gu = (torch.randn(777, 2 * hidden, generator=g) * 3).to(dtype).to(cuda)
+    got = silu_mul(gu, hidden)
+    exp = torch.nn.functional.silu(gu[:, :hidden]) * gu[:, hidden:]
+    diff = (got.float() - exp.float()).abs()
+    ulp = exp.float().abs() * (2.0**-10 if dtype == torch.float16 else 2.0**-7 if dtype == torch.bfloat16 else 2.0**-23)
+    mismatches = int((got != exp).sum())
+    print(f"[parity] silu_mul {dtype} hidden {hidden}: {mismatches} of {exp.numel()} differ from torch", flush=True)
+    assert bool((diff <= ulp + 1e-30).all()), "silu_mul differs from torch by more than one unit in the last place"
+    assert mismatches <= exp.numel() // 1000
+
+
+def test_swiglu_module_matches_separate_projections(cuda):
+    from nori_amd.layer import SwiGLUMLP
+
+    torch.manual_seed(11)
+    mlp = SwiGLUMLP(128, 256, 128, has_bias=False, device=cuda, dtype=torch.float32)
+    x = torch.randn(4, 300, 128, device=cuda)
+    results = []
+    for step in range(2):
+        if step:
+            with torch.no_grad():
+                mlp.w_up.weight.mul_(0.5)  # a changed weight rebuilds the stacked one
+        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+            results.append((mlp(x), mlp.w_down(torch.nn.functional.silu(mlp.w_gate(x)) * mlp.w_up(x))))
+    for a, b in results:
+        check_relative(a, b, 2e-3, "stacked SwiGLU vs separate gate/up projections (fp16 autocast)")
