@@ -38,7 +38,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention, short_context
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
-from .norm import RMSNorm, projection_operand, rms_norm_
+from .norm import RMSNorm, projection_operand, rms_norm_, silu_mul
 
 ACTIVATION_FN = {"gelu": nn.GELU(), "relu": nn.ReLU(), "silu": nn.SiLU()}
 _SDPA_BACKENDS_WITHOUT_CUDNN = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]
@@ -111,7 +111,41 @@ class SwiGLUMLP(nn.Module):
         torch.nn.init.normal_(self.w_down.weight, std=0.02)
 
     def forward(self, x):
-        return self.w_down(nn.functional.silu(self.w_gate(x)) * self.w_up(x))
+        if not x.is_cuda:
+            return self.w_down(nn.functional.silu(self.w_gate(x)) * self.w_up(x))
+        # One GEMM over the stacked [gate | up] weight (the operand is read once), the HIP gate
+        # silu(g) * u with torch's rounding in the projection dtype, then the down projection.
+        # The hidden width is padded to a multiple of 8 with zero gate/up rows and zero down
+        # columns, so every row is 16-byte aligned; the padding contributes exact zeros.
+        gate_up, gate_up_bias, down, hidden = self._stacked_weights(x)
+        gu = nn.functional.linear(x, gate_up, gate_up_bias)
+        return nn.functional.linear(silu_mul(gu, hidden), down, self.w_down.bias)
+
+    def _stacked_weights(self, x: torch.Tensor):
+        """(gate|up weight [2 hp, in], its bias, down weight [out, hp], hp) in the dtype the
+        projections compute in, rebuilt when a weight changes."""
+        dtype = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.w_gate.weight.dtype
+        params = [self.w_gate.weight, self.w_up.weight, self.w_down.weight]
+        if self.w_gate.bias is not None:
+            params += [self.w_gate.bias, self.w_up.bias]
+        key = (dtype, x.device) + tuple((p.data_ptr(), p._version) for p in params)
+        cached = getattr(self, "_stacked", None)
+        if cached is None or cached[0] != key:
+            h = self.w_gate.out_features
+            hp = (h + 7) // 8 * 8
+            with torch.no_grad():
+                gate_up = torch.zeros((2 * hp, self.w_gate.in_features), device=x.device, dtype=dtype)
+                gate_up[:h] = self.w_gate.weight
+                gate_up[hp : hp + h] = self.w_up.weight
+                bias = None
+                if self.w_gate.bias is not None:
+                    bias = torch.zeros(2 * hp, device=x.device, dtype=dtype)
+                    bias[:h] = self.w_gate.bias
+                    bias[hp : hp + h] = self.w_up.bias
+                down = torch.zeros((self.w_down.out_features, hp), device=x.device, dtype=dtype)
+                down[:, :h] = self.w_down.weight
+            cached = self._stacked = (key, gate_up, bias, down, hp)
+        return cached[1:]
 
 
 class MLP(nn.Module):
@@ -319,6 +353,25 @@ class MultiheadAttention(nn.Module):
         mult = float(torch.tensor(math.log(float(max(n_keys, 2))), dtype=dtype)) if n_keys > 1 else 1.0
         return mult / math.sqrt(float(self.head_dim))
 
+    def _linear_weights(self, device: torch.device):
+        """(q weight [H*D, E], k|v weight [2*H*D, E], output weight [E, H*D]) as F.linear takes
+        them, in the dtype the projections compute in (the autocast dtype under GPU autocast),
+        cached until a weight changes. Autocast does not keep casts of these reshaped views, so
+        without the cache every call would cast them again; the values are the same casts."""
+        dtype = self.qkv_proj_weight.dtype
+        if device.type == "cuda" and torch.is_autocast_enabled("cuda"):
+            dtype = torch.get_autocast_dtype("cuda")
+        hd = self.num_heads * self.head_dim
+        key = (dtype, device, self.qkv_proj_weight.data_ptr(), self.qkv_proj_weight._version,
+               self.out_proj_weight.data_ptr(), self.out_proj_weight._version)
+        cached = getattr(self, "_cast", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = self.qkv_proj_weight.to(device=device, dtype=dtype)
+                out_w = self.out_proj_weight.reshape(hd, self.embed_dim).t().to(device=device, dtype=dtype).contiguous()
+                cached = self._cast = (key, w[0].reshape(hd, self.embed_dim), w[1:].reshape(2 * hd, self.embed_dim), out_w)
+        return cached[1:]
+
     def _apply_extra_attn_scale(self, q: torch.Tensor, n_keys: int) -> torch.Tensor:
         """q * temperature * log(n)/log(n_ref) (reference layer.py:555-583)."""
         if not self.use_logn_attention and not self.use_learnable_attn_temperature:
@@ -406,9 +459,8 @@ class MultiheadAttention(nn.Module):
                 f"cache=({kv_cache['batch']}, {kv_cache['groups']}), query=({B}, {S})"
             )
         x_flat = x.reshape(-1, *x.shape[-2:])
-        q = torch.nn.functional.linear(
-            x_flat, self.qkv_proj_weight[0].reshape(self.num_heads * self.head_dim, self.embed_dim)
-        ).view(*x_flat.shape[:-1], self.num_heads, self.head_dim)
+        q = torch.nn.functional.linear(x_flat, self._linear_weights(x.device)[0])
+        q = q.view(*x_flat.shape[:-1], self.num_heads, self.head_dim)
         blockwise = isinstance(kv_cache, BlockwiseSeqKV)
         if blockwise:
             n_keys = kv_cache.n_rows
@@ -427,7 +479,8 @@ class MultiheadAttention(nn.Module):
             atten_out = compute_attention_blockwise(q, kv_cache, sdpa_scale=None)
         else:
             atten_out = attend_dense(q, kv_cache)
-        out = torch.einsum("... h d, h d s -> ... s", atten_out, self.out_proj_weight.to(atten_out.dtype))
+        w_out = self._linear_weights(atten_out.device)[2]
+        out = torch.nn.functional.linear(atten_out.reshape(*atten_out.shape[:-2], -1), w_out.to(atten_out.dtype))
         return out.reshape(B, S, *out.shape[1:]), None
 
     def compute_attention_blockwise(self, q: torch.Tensor, kv_cache: BlockwiseSeqKV, *, sdpa_scale: float | None = None):
@@ -446,9 +499,10 @@ class MultiheadAttention(nn.Module):
         calculate_sample_attention: bool = False,
         calculate_feature_attention: bool = False,
     ):
-        """Reference layer.py:1062-1162. Separate Q/KV (sequence attention over rows) runs on
-        the HIP kernel with the projected K/V as a full-precision cache; the combined-QKV
-        feature attention over a row's tokens (and any masked call) uses torch SDPA."""
+        """Reference layer.py:1062-1162. Both forms run on the HIP kernel: separate Q/KV
+        (sequence attention over rows) with the projected K/V as a full-precision cache, and
+        combined QKV (the feature attention over a row's tokens) reading K/V out of the QKV
+        projection. Only a masked call takes torch SDPA."""
         if calculate_sample_attention or calculate_feature_attention:
             raise NotImplementedError("attention-score diagnostics are not computed by the HIP attention path")
         B, S, _, _ = x.shape
@@ -474,58 +528,63 @@ class MultiheadAttention(nn.Module):
             x_kv = x_kv.reshape(-1, *x_kv.shape[-2:])
             use_linear = self._is_linear_projection_used(x.device)
             if use_linear:
-                q = torch.nn.functional.linear(
-                    x, self.qkv_proj_weight[0].reshape(self.num_heads * self.head_dim, self.embed_dim)
-                ).view(*x.shape[:-1], self.num_heads, self.head_dim)
+                w_q, w_kv, _ = self._linear_weights(x.device)
+                q = torch.nn.functional.linear(x, w_q).view(*x.shape[:-1], self.num_heads, self.head_dim)
             else:
                 q = torch.einsum("... s, h d s -> ... h d", x, self.qkv_proj_weight[0])
             kv_w = self.qkv_proj_weight[1:]
             if copy_first_head_kv:
                 kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w[:, :1])
             elif use_linear:
-                kv = torch.nn.functional.linear(
-                    x_kv, kv_w.reshape(2 * self.num_heads * self.head_dim, self.embed_dim)
-                ).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
+                kv = torch.nn.functional.linear(x_kv, w_kv).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
             else:
                 kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w)
-            prologue = self._short_prologue(q, kv) if attn_mask is None else None
-            if prologue is not None:
-                # q/k norms and the log-n multiply fused into the short-context kernel's loads
-                if self._attention_dropout_p() != 0.0:
-                    raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
-                atten_out = icl_attention(q, kv, qk_prologue=prologue)
-            else:
-                if self.qk_norm:
-                    q = self._norm_q(q)
-                    kv = self._norm_kv(kv)
-                n_keys = int(kv.shape[1])
-                logit_scale = None
-                if self.use_qassmax:
-                    if (attn_mask is None and q.is_cuda and self.qassmax.qass_mode == "log_only"
-                            and self.fold_log_only_qass):
-                        # QASS "log_only" multiplies q by T(log n) in q's dtype T; the kernel
-                        # multiplies q by its logit scale once as it loads it, so the factor rides
-                        # on that scale instead of a separate pass over q
-                        logit_scale = self.log_only_logit_scale(n_keys, q.dtype)
-                    else:
-                        q = self.apply_qassmax(q, n_keys)
-                q = self._apply_extra_attn_scale(q, n_keys)
-                if attn_mask is not None:
-                    k, v = kv.unbind(dim=2)
-                    atten_out = self._sdpa(q, k, v, attn_mask, scaled=True)
-                else:
-                    if self._attention_dropout_p() != 0.0:
-                        raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
-                    atten_out = icl_attention(q, kv.contiguous() if kv.stride(-1) != 1 else kv, scale=logit_scale)
-        atten_out = atten_out.reshape(BS, F, self.num_heads, self.head_dim)
-        if self._is_linear_projection_used(atten_out.device):
-            out = torch.nn.functional.linear(
-                atten_out.reshape(*atten_out.shape[:-2], self.num_heads * self.head_dim),
-                self.out_proj_weight.reshape(self.num_heads * self.head_dim, self.embed_dim).transpose(0, 1),
-            )
-        else:
-            out = torch.einsum("... h d, h d s -> ... s", atten_out, self.out_proj_weight)
+            atten_out = self.attend_projected(q, kv, attn_mask)
+        out = self.project_out(atten_out.reshape(BS, F, self.num_heads, self.head_dim))
         return out.reshape(B, S, *out.shape[1:]), None, None
+
+    def attend_projected(self, q: torch.Tensor, kv: torch.Tensor, attn_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """The separate-Q/KV attention after its projections (layer.py:1114-1162 less the
+        projections): ``q`` [BS, F, H, D] and ``kv`` [BS, N, 2, Hkv, D] (any strides with a
+        contiguous head axis, e.g. views into one stacked projection) through the q/k norms,
+        QASS and the HIP kernel; returns the attention output [BS, F, H, D] before the output
+        projection."""
+        prologue = self._short_prologue(q, kv) if attn_mask is None else None
+        if prologue is not None:
+            # q/k norms and the log-n multiply fused into the short-context kernel's loads
+            if self._attention_dropout_p() != 0.0:
+                raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
+            return icl_attention(q, kv, qk_prologue=prologue)
+        if self.qk_norm:
+            q = self._norm_q(q)
+            kv = self._norm_kv(kv if kv.is_contiguous() else kv.contiguous())
+        n_keys = int(kv.shape[1])
+        logit_scale = None
+        if self.use_qassmax:
+            if (attn_mask is None and q.is_cuda and self.qassmax.qass_mode == "log_only"
+                    and self.fold_log_only_qass):
+                # QASS "log_only" multiplies q by T(log n) in q's dtype T; the kernel
+                # multiplies q by its logit scale once as it loads it, so the factor rides
+                # on that scale instead of a separate pass over q
+                logit_scale = self.log_only_logit_scale(n_keys, q.dtype)
+            else:
+                q = self.apply_qassmax(q, n_keys)
+        q = self._apply_extra_attn_scale(q, n_keys)
+        if attn_mask is not None:
+            k, v = kv.unbind(dim=2)
+            return self._sdpa(q, k, v, attn_mask, scaled=True)
+        if self._attention_dropout_p() != 0.0:
+            raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
+        return icl_attention(q, kv if kv.stride(-1) == 1 else kv.contiguous(), scale=logit_scale)
+
+    def project_out(self, atten_out: torch.Tensor) -> torch.Tensor:
+        """Output projection of an attention output [..., H, D] -> [..., E]."""
+        if self._is_linear_projection_used(atten_out.device):
+            return torch.nn.functional.linear(
+                atten_out.reshape(*atten_out.shape[:-2], self.num_heads * self.head_dim),
+                self._linear_weights(atten_out.device)[2],
+            )
+        return torch.einsum("... h d, h d s -> ... s", atten_out, self.out_proj_weight)
 
     def _sdpa(self, q, k, v, attn_mask, scaled: bool = False):
         """torch SDPA over [B, seq, heads, D] (the reference's own op, layer.py:1008-1049): the

@@ -1,17 +1,31 @@
-"""Drop-in for ``synthefy_nori.model.two_phase``: the two-phase encoder of Nori 1.5 ("Model v3").
+"""The two-phase encoder of Nori 1.5 ("Model v3", src/synthefy_nori/model/two_phase.py), planned
+around the HIP kernels.
 
-Phase A (cell layers) keeps one token per feature-group cell beside a stream of K target
-tokens per row; phase B (row layers) runs row-level in-context learning on each row's
-flattened target stream (src/synthefy_nori/model/two_phase.py:1-486). Module and parameter
-names are the reference's, so its state dicts load with ``strict=True``.
+What it computes is the reference's: a cell phase (per cell layer: column attention of each
+cell over its column's context cells; a context-only row attention of each row's target
+stream; SwiGLU MLPs for cells and targets; a decoupled feature attention inside each row),
+the boundary (target tokens flattened into one row vector, context labels embedded into it
+again, final cell states projected into a read-back memory), then a row phase (context-only
+row attention, a read-back from the row's own cells, a SwiGLU MLP). Every update is a
+deep-norm residual ``x + alpha * u`` with alpha = (cell layers + row layers)^-1/2; every
+attention has per-head q/k RMS norms and QASS "log_only". Module and parameter names are the
+reference's state-dict keys, so its checkpoints load with ``strict=True``.
 
-Every attention is a separate-Q/KV ``MultiheadAttention`` with per-head query/key RMS norm
-and log-n query scaling (two_phase.py:34-50). All of them -- the column attention of a
-cell over the context rows of its column, the target-stream and phase-B row attentions
-over the context rows, the feature attention inside a row and the read-back from a row's
-own cells -- run on the HIP attention kernel over the projected full-precision K/V
-(``MultiheadAttention.forward``); the RMS norms run on the HIP norm kernel; projections,
-MLPs and the label encoders are torch GEMMs and elementwise ops.
+How it is laid out here:
+
+* Two fp32 residual streams per batch of tables, the cells ``[B, R, G, C]`` and the target
+  stream ``[B, R, K, C]`` (whose ``[B, R, K * C]`` view is the row vector of the row phase),
+  updated in place by the fused residual kernel (``nori_residual_add``: one pass, torch's
+  rounding of ``x + alpha * u``).
+* Every RMS norm that feeds a projection writes the projection's operand dtype directly.
+* The decoupled feature attention is one GEMM: the per-token norms of cells and targets
+  write one ``[B, R, G + K, C]`` operand buffer, and the q/k/v weights of both of its
+  attentions are stacked, so the operand is read once. Each attention then reads its q and
+  K/V as strided views of that projection -- the cell queries attend to every token, the
+  target queries to the cells -- with its q/k norms and log-n factor applied as the
+  short-context kernel loads the rows.
+* The MLPs are ``SwiGLUMLP``: one stacked gate/up GEMM, the HIP SwiGLU gate, the down GEMM.
+* Column and row attentions over the context rows run on the MFMA attention kernel.
 """
 
 from __future__ import annotations
@@ -20,7 +34,7 @@ import torch
 from torch import nn
 
 from .layer import MultiheadAttention, SwiGLUMLP
-from .norm import RMSNorm, projection_operand as _operand, residual_add as _residual
+from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, rms_norm
 
 __all__ = [
     "CellLayer2P",
@@ -32,359 +46,398 @@ __all__ = [
 ]
 
 
-def _attention(width: int, heads: int, *, device, dtype, prefer_cudnn_inference: bool = False) -> MultiheadAttention:
-    """The one attention shape of the encoder (two_phase.py:34-50)."""
+def _icl_attention_module(width: int, heads: int, device, dtype, cudnn_hint: bool = False) -> MultiheadAttention:
+    """The attention every sublayer of the encoder uses (two_phase.py:34-50): separate Q/KV
+    projections, per-head q/k RMS norms, QASS "log_only"."""
     return MultiheadAttention(
-        embed_dim=width,
-        num_heads=heads,
-        qkv_combined=False,
-        dropout=0.0,
-        use_qassmax=True,
-        qass_mode="log_only",
-        device=device,
-        dtype=dtype,
-        qk_norm=True,
-        reuse_projected_kv_storage=True,
-        prefer_cudnn_inference=prefer_cudnn_inference,
+        embed_dim=width, num_heads=heads, qkv_combined=False, dropout=0.0, use_qassmax=True, qass_mode="log_only",
+        device=device, dtype=dtype, qk_norm=True, reuse_projected_kv_storage=True, prefer_cudnn_inference=cudnn_hint,
     )
 
 
-def _attend(module: MultiheadAttention, queries: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
-    """``queries`` [batch, groups, n, width] attend over the third axis of ``keys`` (:53-55)."""
-    return module(x=queries, x_kv=keys, copy_first_head_kv=False)[0]
-
-
-def _rms(width: int, eps: float) -> RMSNorm:
+def _plain_norm(width: int, eps: float) -> RMSNorm:
     return RMSNorm(width, eps=eps, elementwise_affine=False)
 
 
-class TargetStreamEncoder(nn.Module):
-    """K target tokens per row from its label: a small GELU MLP of the value (regression) or a
-    class embedding; rows without a label (NaN: the query rows) get a learned query vector
-    (:58-107). ``y`` [batch, rows] -> [batch, rows, K, cell_dim]."""
+def _accumulate(stream: torch.Tensor, update: torch.Tensor, alpha: float) -> torch.Tensor:
+    """stream += alpha * update (deep-norm residual), in place."""
+    return residual_add(stream, update.reshape(stream.shape), alpha, inplace=True)
 
-    def __init__(self, cell_dim: int, target_tokens: int, *, task_type: str, max_num_classes: int, device=None, dtype=None):
+
+def _row_vectors(targets: torch.Tensor) -> torch.Tensor:
+    """The [batch, n, K * width] row-vector view of a target stream [batch, n, K, width] (a view:
+    updates through it land in the stream)."""
+    return targets.view(*targets.shape[:2], -1)
+
+
+def _put(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst[...] = src, skipped when src already is dst's memory (a chunk worked on in place)."""
+    if src.data_ptr() != dst.data_ptr() or src.device != dst.device or src.stride() != dst.stride():
+        dst.copy_(src)
+
+
+def _over_keys(attn: MultiheadAttention, queries: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
+    """``queries`` [batch, groups, n, width] attend over the third axis of ``keys``
+    [batch, groups, m, width]; the output projection is applied (two_phase.py:53-55)."""
+    return attn(x=queries, x_kv=keys, copy_first_head_kv=False)[0]
+
+
+class TargetStreamEncoder(nn.Module):
+    """The K target tokens of each row from its label (two_phase.py:58-107): a GELU MLP of the
+    value for regression or a class embedding; rows whose label is not finite (the query rows)
+    take the learned query vector. ``y`` [batch, rows] -> [batch, rows, K, cell_dim]."""
+
+    def __init__(self, cell_dim: int, target_tokens: int, *, task_type: str, max_num_classes: int, device=None,
+                 dtype=None):
         super().__init__()
-        self.cell_dim = int(cell_dim)
-        self.target_tokens = int(target_tokens)
-        self.task_type = task_type
+        self.cell_dim, self.target_tokens, self.task_type = int(cell_dim), int(target_tokens), task_type
         self.width = width = self.cell_dim * self.target_tokens
-        self.mlp = (
-            nn.Sequential(
-                nn.Linear(1, width // 2, device=device, dtype=dtype),
-                nn.GELU(),
-                nn.Linear(width // 2, width, device=device, dtype=dtype),
-            )
-            if task_type == "reg"
-            else None
-        )
-        self.class_embedding = nn.Embedding(max_num_classes, width, device=device, dtype=dtype) if task_type == "cls" else None
+        self.mlp = None
+        self.class_embedding = None
+        if task_type == "reg":
+            self.mlp = nn.Sequential(nn.Linear(1, width // 2, device=device, dtype=dtype), nn.GELU(),
+                                     nn.Linear(width // 2, width, device=device, dtype=dtype))
+        if task_type == "cls":
+            self.class_embedding = nn.Embedding(max_num_classes, width, device=device, dtype=dtype)
         self.query_embedding = nn.Parameter(torch.empty(width, device=device, dtype=dtype))
         nn.init.normal_(self.query_embedding, std=0.02)
 
     def forward(self, y: torch.Tensor) -> torch.Tensor:
-        labelled = torch.isfinite(y)
-        labels = torch.where(labelled, y, torch.zeros_like(y))
-        if self.class_embedding is not None:
-            tokens = self.class_embedding(labels.long().clamp(0, self.class_embedding.num_embeddings - 1))
+        known = torch.isfinite(y)
+        label = y.masked_fill(~known, 0.0)
+        if self.mlp is not None:
+            tokens = self.mlp(label[..., None].to(self.mlp[0].weight.dtype))
         else:
-            tokens = self.mlp(labels.unsqueeze(-1).to(self.mlp[0].weight.dtype))
-        tokens = torch.where(labelled.unsqueeze(-1), tokens, self.query_embedding.to(tokens.dtype))
-        return tokens.view(*y.shape, self.target_tokens, self.cell_dim)
+            n_classes = self.class_embedding.num_embeddings
+            tokens = self.class_embedding(label.long().clamp(0, n_classes - 1))
+        tokens = torch.where(known[..., None], tokens, self.query_embedding.to(tokens.dtype))
+        return tokens.unflatten(-1, (self.target_tokens, self.cell_dim))
 
 
 class FullColumnAttention(nn.Module):
-    """Each row's cell attends to the context rows' cells of its column (:110-119)."""
+    """Holds the column attention (two_phase.py:110-119): a cell attends to the context cells of
+    its column. ``forward`` takes the normalized cells [batch, rows, groups, width]."""
 
     def __init__(self, cell_dim: int, heads: int, *, device, dtype):
         super().__init__()
-        self.sequence_attentions = nn.ModuleList(
-            [_attention(cell_dim, heads, device=device, dtype=dtype, prefer_cudnn_inference=True)]
-        )
+        self.sequence_attentions = nn.ModuleList([_icl_attention_module(cell_dim, heads, device, dtype, cudnn_hint=True)])
 
-    def forward(self, cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
-        columns = cells.transpose(1, 2)  # [batch, groups, rows, width]
-        return _attend(self.sequence_attentions[0], columns, columns[:, :, :eval_pos]).transpose(1, 2)
+    def forward(self, normed_cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
+        columns = normed_cells.transpose(1, 2)  # [batch, groups, rows, width]
+        return _over_keys(self.sequence_attentions[0], columns, columns[:, :, :eval_pos]).transpose(1, 2)
 
 
 class DecoupledFeatureAttention(nn.Module):
-    """Inside a row: cells read [cells, target tokens]; target tokens read the cells only, and
-    their K read-outs are mixed by one linear map (:122-138)."""
+    """Holds the feature attention inside a row (two_phase.py:122-138): attention 0 lets the
+    cells read every token of the row, attention 1 lets the target tokens read the cells, and
+    ``target_mix`` mixes the K target read-outs. The stacked projection of both is built by
+    ``stacked_weight``; ``forward`` takes the normalized [cells | targets] token buffer."""
 
     def __init__(self, cell_dim: int, heads: int, target_tokens: int, *, device, dtype):
         super().__init__()
         self.target_tokens = int(target_tokens)
-        self.feature_attentions = nn.ModuleList([_attention(cell_dim, heads, device=device, dtype=dtype) for _ in range(2)])
+        self.feature_attentions = nn.ModuleList([_icl_attention_module(cell_dim, heads, device, dtype) for _ in range(2)])
         width = cell_dim * self.target_tokens
         self.target_mix = nn.Linear(width, width, bias=False, device=device, dtype=dtype)
         nn.init.normal_(self.target_mix.weight, std=0.02)
 
-    def forward(self, cells: torch.Tensor, targets: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """``cells`` [batch, rows, groups, width], ``targets`` [batch, rows, K, width]."""
-        cell_update = _attend(self.feature_attentions[0], cells, torch.cat((cells, targets), dim=2))
-        readout = _attend(self.feature_attentions[1], targets, cells)
-        return cell_update, self.target_mix(readout.flatten(-2)).view_as(targets)
+    def stacked_weight(self, dtype: torch.dtype, device) -> torch.Tensor:
+        """[q0; k0; v0; q1; k1; v1] projection weight [6 * H * D, width] in ``dtype``, cached
+        until a weight changes."""
+        parts = [m.qkv_proj_weight for m in self.feature_attentions]
+        key = (dtype, device) + tuple((p.data_ptr(), p._version) for p in parts)
+        cached = getattr(self, "_stacked", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = torch.cat([p.reshape(-1, p.shape[-1]) for p in parts]).to(device=device, dtype=dtype)
+            cached = self._stacked = (key, w)
+        return cached[1]
+
+    def forward(self, tokens: torch.Tensor, n_cells: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """``tokens`` [batch, rows, groups + K, width]: the normalized cells, then the normalized
+        target tokens of each row. Returns (cell update [batch, rows, groups, width], target
+        update [batch, rows, K, width])."""
+        b, r, t, width = tokens.shape
+        a0, a1 = self.feature_attentions
+        h, d = a0.num_heads, a0.head_dim
+        proj = torch.nn.functional.linear(tokens.reshape(b * r, t, width), self.stacked_weight(tokens.dtype, tokens.device))
+        proj = proj.view(b * r, t, 2, 3, h, d)  # [row, token, attention, q|k|v, head, d]
+        cell_q = proj[:, :n_cells, 0, 0]
+        all_kv = proj[:, :, 0, 1:]              # every token of the row: K then V
+        target_q = proj[:, n_cells:, 1, 0]
+        cell_kv = proj[:, :n_cells, 1, 1:]      # the cells only
+        cells_out = a0.project_out(a0.attend_projected(cell_q, all_kv))
+        readout = a1.project_out(a1.attend_projected(target_q, cell_kv))
+        target_update = self.target_mix(readout.reshape(b * r, -1)).view(b, r, self.target_tokens, width)
+        return cells_out.view(b, r, n_cells, width), target_update
 
 
 class CellLayer2P(nn.Module):
-    """A phase-A layer, S -> M -> F (:141-232): column attention for the cells and context-only
-    row attention for the flattened target stream; separate SwiGLU MLPs; the decoupled feature
-    attention. Deep-norm residuals with ``deepnorm_alpha``; pre-norm RMS norms without
-    weights. The steps are split by what they read so the chunked forward can run each on a
-    slice of the table."""
+    """A cell-phase layer (two_phase.py:141-232). Norms: ``cell_norms`` (column attention, MLP,
+    feature attention) over a cell, ``target_norms`` (row attention and MLP over the row vector
+    of K target tokens, feature attention over one token); all without gains. Its steps take the
+    two residual streams and update them in place; ``forward`` runs them in order."""
 
-    def __init__(
-        self,
-        cell_dim: int,
-        heads: int,
-        hidden_dim: int,
-        *,
-        target_tokens: int,
-        target_heads: int,
-        target_hidden_dim: int,
-        deepnorm_alpha: float,
-        layer_norm_eps: float = 1e-5,
-        device=None,
-        dtype=None,
-    ):
+    def __init__(self, cell_dim: int, heads: int, hidden_dim: int, *, target_tokens: int, target_heads: int,
+                 target_hidden_dim: int, deepnorm_alpha: float, layer_norm_eps: float = 1e-5, device=None, dtype=None):
         super().__init__()
-        self.cell_dim = int(cell_dim)
-        self.target_tokens = int(target_tokens)
+        self.cell_dim, self.target_tokens = int(cell_dim), int(target_tokens)
         self.target_width = self.cell_dim * self.target_tokens
         self.deepnorm_alpha = float(deepnorm_alpha)
         eps = layer_norm_eps
-        self.cell_norms = nn.ModuleList([_rms(self.cell_dim, eps) for _ in range(3)])
-        self.target_norms = nn.ModuleList([_rms(self.target_width, eps), _rms(self.target_width, eps), _rms(self.cell_dim, eps)])
-        self.column_attention = FullColumnAttention(self.cell_dim, heads, device=device, dtype=dtype)
-        self.sequence_attentions = nn.ModuleList([_attention(self.target_width, target_heads, device=device, dtype=dtype)])
-        self.mlp = nn.ModuleList(
-            [
-                SwiGLUMLP(self.cell_dim, hidden_dim, self.cell_dim, has_bias=False, device=device, dtype=dtype),
-                SwiGLUMLP(self.target_width, target_hidden_dim, self.target_width, has_bias=False, device=device, dtype=dtype),
-            ]
+        self.cell_norms = nn.ModuleList([_plain_norm(self.cell_dim, eps) for _ in range(3)])
+        self.target_norms = nn.ModuleList(
+            [_plain_norm(self.target_width, eps), _plain_norm(self.target_width, eps), _plain_norm(self.cell_dim, eps)]
         )
-        self.feature_attention = DecoupledFeatureAttention(self.cell_dim, heads, self.target_tokens, device=device, dtype=dtype)
+        self.column_attention = FullColumnAttention(self.cell_dim, heads, device=device, dtype=dtype)
+        self.sequence_attentions = nn.ModuleList([_icl_attention_module(self.target_width, target_heads, device, dtype)])
+        self.mlp = nn.ModuleList([
+            SwiGLUMLP(self.cell_dim, hidden_dim, self.cell_dim, has_bias=False, device=device, dtype=dtype),
+            SwiGLUMLP(self.target_width, target_hidden_dim, self.target_width, has_bias=False, device=device, dtype=dtype),
+        ])
+        self.feature_attention = DecoupledFeatureAttention(self.cell_dim, heads, self.target_tokens, device=device,
+                                                           dtype=dtype)
 
     def forward(self, cells: torch.Tensor, targets: torch.Tensor, eval_pos: int) -> tuple[torch.Tensor, torch.Tensor]:
-        cells = self.apply_column_attention(cells, eval_pos)
-        rows = targets.flatten(-2)
-        normed = _operand(self.target_norms[0], rows).unsqueeze(1)
-        rows = self.attend_target_rows_to_context(rows, normed, normed[:, :, :eval_pos])
-        return self.apply_row_mlps_and_feature_attention(cells, rows)
+        """Out-of-place form: returns the updated (cells, targets); the inputs are left as they are."""
+        cells, targets = cells.clone(), targets.contiguous().clone()
+        self.column_step(cells, eval_pos)
+        rows = _row_vectors(targets)
+        self.target_row_step(rows, self.row_operand(rows), eval_pos)
+        self.row_local_steps(cells, targets)
+        return cells, targets
 
-    def apply_column_attention(self, cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
-        """S for the cells; reads a whole column, so it slices by column only."""
-        return _residual(cells, self.column_attention(_operand(self.cell_norms[0], cells), eval_pos), self.deepnorm_alpha)
+    # --- steps on the streams (in place)
+    def column_step(self, cells: torch.Tensor, eval_pos: int) -> None:
+        """Each cell reads its column's context cells. Reads whole columns: a slice of the
+        groups axis may be passed."""
+        normed = projection_operand(self.cell_norms[0], cells)
+        _accumulate(cells, self.column_attention(normed, eval_pos), self.deepnorm_alpha)
 
-    def attend_target_rows_to_context(self, rows: torch.Tensor, normalized: torch.Tensor, context_keys: torch.Tensor) -> torch.Tensor:
-        """S for the target stream: ``normalized`` rows (``target_norms[0](rows).unsqueeze(1)``)
-        attend to the context rows' ``context_keys``; any slice of rows may be passed."""
-        return _residual(rows, _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1), self.deepnorm_alpha)
+    def row_operand(self, rows: torch.Tensor) -> torch.Tensor:
+        """The normalized row vectors the target-stream row attention reads, [batch, 1, n, width]."""
+        return projection_operand(self.target_norms[0], rows).unsqueeze(1)
 
-    def apply_row_mlps_and_feature_attention(self, cells: torch.Tensor, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """M then F; each row reads only itself. Returns (cells, targets [batch, n, K, cell_dim])."""
-        a = self.deepnorm_alpha
-        cells = _residual(cells, self.mlp[0](_operand(self.cell_norms[1], cells)), a)
-        rows = _residual(rows, self.mlp[1](_operand(self.target_norms[1], rows)), a)
-        targets = rows.view(*rows.shape[:-1], self.target_tokens, self.cell_dim)
-        cell_update, target_update = self.feature_attention(_operand(self.cell_norms[2], cells), _operand(self.target_norms[2], targets))
-        return _residual(cells, cell_update, a), _residual(targets, target_update, a)
+    def target_row_step(self, rows: torch.Tensor, normed: torch.Tensor, eval_pos: int | None = None,
+                        context: torch.Tensor | None = None) -> None:
+        """The row vectors ``rows`` [batch, n, width] (normalized: ``normed``) read the context
+        rows' normalized vectors: ``context``, or the first ``eval_pos`` of ``normed``."""
+        keys = normed[:, :, :eval_pos] if context is None else context
+        update = _over_keys(self.sequence_attentions[0], normed, keys)
+        _accumulate(rows, update.squeeze(1), self.deepnorm_alpha)
+
+    def row_local_steps(self, cells: torch.Tensor, targets: torch.Tensor) -> None:
+        """The MLPs, then the feature attention: each row reads only itself, so any slice of rows
+        may be passed. ``targets`` [batch, n, K, width] (its row-vector view is what the target
+        MLP transforms)."""
+        alpha = self.deepnorm_alpha
+        rows = _row_vectors(targets)
+        _accumulate(cells, self.mlp[0](projection_operand(self.cell_norms[1], cells)), alpha)
+        _accumulate(rows, self.mlp[1](projection_operand(self.target_norms[1], rows)), alpha)
+        tokens = self.feature_tokens(cells, targets)
+        cell_update, target_update = self.feature_attention(tokens, cells.shape[2])
+        _accumulate(cells, cell_update, alpha)
+        _accumulate(targets, target_update, alpha)
+
+    def feature_tokens(self, cells: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+        """The feature attention's operand: every cell normalized by ``cell_norms[2]`` then every
+        target token by ``target_norms[2]``, [batch, n, groups + K, width], written token by token
+        into one buffer in the projection's dtype."""
+        b, n, g, w = cells.shape
+        out = torch.empty((b, n, g + self.target_tokens, w), dtype=operand_dtype(cells), device=cells.device)
+        if not cells.is_cuda:
+            out[:, :, :g] = self.cell_norms[2](cells)
+            out[:, :, g:] = self.target_norms[2](targets)
+            return out
+        for j, (norm, src) in enumerate([(self.cell_norms[2], cells[:, :, i]) for i in range(g)]
+                                        + [(self.target_norms[2], targets[:, :, i]) for i in range(self.target_tokens)]):
+            rms_norm(src, norm.normalized_shape, None, norm.eps, out=out[:, :, j])
+        return out
 
 
 class RowLayer2P(nn.Module):
-    """A phase-B layer (:235-284): context-only row attention on the row vector, a read-back
-    from the row's own final cell states, then a SwiGLU MLP."""
+    """A row-phase layer (two_phase.py:235-284): context-only row attention, a read-back of the
+    row's own cells, a SwiGLU MLP. Steps update the row stream in place."""
 
     def __init__(self, width: int, heads: int, hidden_dim: int, *, deepnorm_alpha: float, layer_norm_eps: float = 1e-5,
                  device=None, dtype=None):
         super().__init__()
         self.deepnorm_alpha = float(deepnorm_alpha)
-        self.attn_norm = _rms(width, layer_norm_eps)
-        self.mlp_norm = _rms(width, layer_norm_eps)
-        self.readback_norm = _rms(width, layer_norm_eps)
-        self.sequence_attentions = nn.ModuleList([_attention(width, heads, device=device, dtype=dtype)])
-        self.feature_attentions = nn.ModuleList([_attention(width, heads, device=device, dtype=dtype)])
+        self.attn_norm = _plain_norm(width, layer_norm_eps)
+        self.mlp_norm = _plain_norm(width, layer_norm_eps)
+        self.readback_norm = _plain_norm(width, layer_norm_eps)
+        self.sequence_attentions = nn.ModuleList([_icl_attention_module(width, heads, device, dtype)])
+        self.feature_attentions = nn.ModuleList([_icl_attention_module(width, heads, device, dtype)])
         self.mlp = nn.ModuleList([SwiGLUMLP(width, hidden_dim, width, has_bias=False, device=device, dtype=dtype)])
 
     def forward(self, rows: torch.Tensor, eval_pos: int, cell_memory: torch.Tensor) -> torch.Tensor:
-        normed = _operand(self.attn_norm, rows).unsqueeze(1)
-        rows = self.attend_rows_to_context(rows, normed, normed[:, :, :eval_pos])
-        return self.apply_readback_and_mlp(rows, cell_memory)
+        """Out-of-place form: returns the updated rows; ``rows`` is left as it is."""
+        rows = rows.clone()
+        self.context_step(rows, self.row_operand(rows), eval_pos)
+        self.readback_steps(rows, cell_memory)
+        return rows
 
-    def attend_rows_to_context(self, rows: torch.Tensor, normalized: torch.Tensor, context_keys: torch.Tensor) -> torch.Tensor:
-        """``normalized`` rows (``attn_norm(rows).unsqueeze(1)``) attend to the context rows'
-        ``context_keys``; any slice of rows may be passed."""
-        return _residual(rows, _attend(self.sequence_attentions[0], normalized, context_keys).squeeze(1), self.deepnorm_alpha)
+    def row_operand(self, rows: torch.Tensor) -> torch.Tensor:
+        return projection_operand(self.attn_norm, rows).unsqueeze(1)
 
-    def apply_readback_and_mlp(self, rows: torch.Tensor, cell_memory: torch.Tensor) -> torch.Tensor:
-        """The row (one query) reads its own cells ``cell_memory`` [batch, rows, groups, width],
-        then the MLP; each row reads only itself."""
-        a = self.deepnorm_alpha
-        query = _operand(self.readback_norm, rows).unsqueeze(2)
-        rows = _residual(rows, _attend(self.feature_attentions[0], query, cell_memory).squeeze(2), a)
-        return _residual(rows, self.mlp[0](_operand(self.mlp_norm, rows)), a)
+    def context_step(self, rows: torch.Tensor, normed: torch.Tensor, eval_pos: int | None = None,
+                     context: torch.Tensor | None = None) -> None:
+        """``rows`` [batch, n, width] (normalized: ``normed``) read the context rows' normalized
+        vectors: ``context``, or the first ``eval_pos`` of ``normed``."""
+        keys = normed[:, :, :eval_pos] if context is None else context
+        _accumulate(rows, _over_keys(self.sequence_attentions[0], normed, keys).squeeze(1), self.deepnorm_alpha)
+
+    def readback_steps(self, rows: torch.Tensor, cell_memory: torch.Tensor) -> None:
+        """The row reads its own cells ``cell_memory`` [batch, n, groups, width], then the MLP;
+        each row reads only itself."""
+        alpha = self.deepnorm_alpha
+        query = projection_operand(self.readback_norm, rows).unsqueeze(2)
+        _accumulate(rows, _over_keys(self.feature_attentions[0], query, cell_memory).squeeze(2), alpha)
+        _accumulate(rows, self.mlp[0](projection_operand(self.mlp_norm, rows)), alpha)
 
 
 class TwoPhaseEncoder(nn.Module):
-    """Phase-A cell layers, the boundary, phase-B row layers (:287-486).
+    """Cell layers, the boundary and row layers of Nori 1.5 (two_phase.py:287-486).
 
-    At the boundary the K target tokens of a row become one vector of width K * cell_dim,
-    the context rows get their label embedding added again (``row_y_encoder``), the cells are
-    RMS-normed into the final cell states and projected once (``cell_to_row``) into the memory
-    the row layers read back from. Deep-norm alpha is (cell layers + row layers)^-1/2.
-    """
+    ``forward`` / ``forward_chunked`` take the embedded cells [batch, rows, groups, cell_dim] and
+    the labels [batch, rows] (not finite on query rows) and return the normalized row states
+    [batch, rows, K * cell_dim] (``forward`` also the final cell states)."""
 
-    def __init__(
-        self,
-        cell_dim: int,
-        heads: int,
-        hidden_dim: int,
-        *,
-        target_tokens: int,
-        cell_layers: int,
-        row_layers: int,
-        row_heads: int,
-        row_hidden_dim: int,
-        task_type: str,
-        max_num_classes: int,
-        layer_norm_eps: float = 1e-5,
-        device=None,
-        dtype=None,
-    ):
+    def __init__(self, cell_dim: int, heads: int, hidden_dim: int, *, target_tokens: int, cell_layers: int,
+                 row_layers: int, row_heads: int, row_hidden_dim: int, task_type: str, max_num_classes: int,
+                 layer_norm_eps: float = 1e-5, device=None, dtype=None):
         super().__init__()
-        if min(cell_layers, target_tokens, row_heads) <= 0 or row_layers < 0:
+        if cell_layers <= 0 or target_tokens <= 0 or row_heads <= 0 or row_layers < 0:
             raise ValueError("two-phase encoder needs positive cell-layer, token and head counts and row_layers >= 0")
-        self.cell_dim = int(cell_dim)
-        self.target_tokens = int(target_tokens)
-        self.task_type = task_type
+        self.cell_dim, self.target_tokens, self.task_type = int(cell_dim), int(target_tokens), task_type
         self.width = self.cell_dim * self.target_tokens
         if self.width % int(row_heads):
             raise ValueError("two-phase target width (target_tokens * embed_dim) must be divisible by row_heads")
-        self.num_cell_layers = int(cell_layers)
-        self.num_row_layers = int(row_layers)
+        self.num_cell_layers, self.num_row_layers = int(cell_layers), int(row_layers)
         self.gradient_checkpointing = False
-        self.deepnorm_alpha = alpha = float(self.num_cell_layers + self.num_row_layers) ** -0.5
-        self.target_encoder = TargetStreamEncoder(
-            self.cell_dim, self.target_tokens, task_type=task_type, max_num_classes=max_num_classes, device=device, dtype=dtype
-        )
+        alpha = (self.num_cell_layers + self.num_row_layers) ** -0.5
+        self.deepnorm_alpha = alpha
+        self.target_encoder = TargetStreamEncoder(self.cell_dim, self.target_tokens, task_type=task_type,
+                                                  max_num_classes=max_num_classes, device=device, dtype=dtype)
         if task_type == "cls":
             self.row_y_encoder = nn.Embedding(max_num_classes, self.width, device=device, dtype=dtype)
         else:
-            self.row_y_encoder = nn.Sequential(
-                nn.Linear(1, self.width, device=device, dtype=dtype), nn.LayerNorm(self.width, device=device, dtype=dtype)
-            )
-        cell = [
-            CellLayer2P(
-                self.cell_dim, heads, hidden_dim, target_tokens=self.target_tokens, target_heads=row_heads,
-                target_hidden_dim=row_hidden_dim, deepnorm_alpha=alpha, layer_norm_eps=layer_norm_eps,
-                device=device, dtype=dtype,
-            )
+            self.row_y_encoder = nn.Sequential(nn.Linear(1, self.width, device=device, dtype=dtype),
+                                               nn.LayerNorm(self.width, device=device, dtype=dtype))
+        layers: list[nn.Module] = [
+            CellLayer2P(self.cell_dim, heads, hidden_dim, target_tokens=self.target_tokens, target_heads=row_heads,
+                        target_hidden_dim=row_hidden_dim, deepnorm_alpha=alpha, layer_norm_eps=layer_norm_eps,
+                        device=device, dtype=dtype)
             for _ in range(self.num_cell_layers)
         ]
         self.cell_to_row = nn.Linear(self.cell_dim, self.width, bias=False, device=device, dtype=dtype)
-        row = [
+        layers += [
             RowLayer2P(self.width, row_heads, row_hidden_dim, deepnorm_alpha=alpha, layer_norm_eps=layer_norm_eps,
                        device=device, dtype=dtype)
             for _ in range(self.num_row_layers)
         ]
-        self.layers = nn.ModuleList(cell + row)
-        self.cell_out_norm = _rms(self.cell_dim, layer_norm_eps)
-        self.row_out_norm = _rms(self.width, layer_norm_eps)
+        self.layers = nn.ModuleList(layers)
+        self.cell_out_norm = _plain_norm(self.cell_dim, layer_norm_eps)
+        self.row_out_norm = _plain_norm(self.width, layer_norm_eps)
 
-    def _cell_stack(self):
+    @property
+    def cell_layers(self):
         return self.layers[: self.num_cell_layers]
 
-    def _row_stack(self):
+    @property
+    def row_layers(self):
         return self.layers[self.num_cell_layers :]
 
-    def _embed_context_labels(self, context_y: torch.Tensor) -> torch.Tensor:
-        """The boundary's label embedding of the context rows: [batch, n] -> [batch, n, width]."""
+    def label_embedding(self, context_y: torch.Tensor) -> torch.Tensor:
+        """What the boundary adds to the context rows' vectors: [batch, n] labels -> [batch, n, width]."""
         labels = torch.nan_to_num(context_y)
         if isinstance(self.row_y_encoder, nn.Embedding):
             return self.row_y_encoder(labels.long().clamp(0, self.row_y_encoder.num_embeddings - 1))
-        return self.row_y_encoder(labels.unsqueeze(-1).to(self.row_y_encoder[0].weight.dtype))
+        return self.row_y_encoder(labels[..., None].to(self.row_y_encoder[0].weight.dtype))
 
-    @staticmethod
-    def _check_context(eval_pos: int, rows: int) -> None:
-        if not 0 < eval_pos <= rows:
+    def _require_context(self, eval_pos: int, n_rows: int) -> None:
+        if not 0 < eval_pos <= n_rows:
             raise ValueError("two-phase encoder requires a non-empty context prefix")
 
     def forward(self, cells: torch.Tensor, y: torch.Tensor, eval_pos: int, **_: object) -> tuple[torch.Tensor, torch.Tensor]:
-        """``cells`` [batch, rows, groups, cell_dim], ``y`` [batch, rows] (NaN on query rows) ->
-        (row states [batch, rows, width], cell states [batch, rows, groups, cell_dim])."""
-        self._check_context(eval_pos, cells.shape[1])
-        targets = self.target_encoder(y).to(cells.dtype)
-        for layer in self._cell_stack():
-            cells, targets = layer(cells, targets, eval_pos)
-        rows = targets.flatten(-2)
-        bias = self._embed_context_labels(y[:, :eval_pos]).to(rows.dtype)
-        rows = torch.cat((rows[:, :eval_pos] + bias, rows[:, eval_pos:]), dim=1)
+        self._require_context(eval_pos, cells.shape[1])
+        cells = cells.clone()  # the streams are updated in place
+        targets = self.target_encoder(y).to(cells.dtype).contiguous()
+        rows = _row_vectors(targets)
+        for layer in self.cell_layers:
+            layer.column_step(cells, eval_pos)
+            layer.target_row_step(rows, layer.row_operand(rows), eval_pos)
+            layer.row_local_steps(cells, targets)
+        rows[:, :eval_pos] += self.label_embedding(y[:, :eval_pos]).to(rows.dtype)
         cell_states = self.cell_out_norm(cells)
         memory = self.cell_to_row(cell_states)
-        for layer in self._row_stack():
-            rows = layer(rows, eval_pos, memory)
+        for layer in self.row_layers:
+            layer.context_step(rows, layer.row_operand(rows), eval_pos)
+            layer.readback_steps(rows, memory)
         return self.row_out_norm(rows), cell_states
 
     @torch.no_grad()
     def forward_chunked(self, cells: torch.Tensor, y: torch.Tensor, eval_pos: int, *, row_chunk: int, column_chunk: int,
                         compute_device: torch.device) -> torch.Tensor:
         """``forward``'s normalized row states without the whole table on ``compute_device``
-        (:380-486). ``cells`` [batch, rows, groups, cell_dim] lives on its residual device (the
-        GPU or host memory) and is overwritten; the target stream lives beside it. Column
-        attention runs ``column_chunk`` columns at a time; the row attentions normalize the
-        context keys once per layer and attend ``row_chunk`` rows at a time; everything per
-        row (MLPs, feature attention, the read-back, whose cell memory each chunk projects
-        for itself) runs per row chunk. Matches ``forward`` up to reassociation in the smaller
-        batches. Returns [batch, rows, width] on the residual device."""
-        self._check_context(eval_pos, cells.shape[1])
+        (two_phase.py:380-486). ``cells`` lives on its home device (the GPU or host memory) and
+        is overwritten; the target stream is kept beside it. Per cell layer the column step runs
+        ``column_chunk`` columns at a time; the row attentions take the context rows' normalized
+        vectors once per layer and run ``row_chunk`` rows at a time, as do all the row-local
+        steps (each chunk projects its own read-back memory). Matches ``forward`` up to the
+        reassociation of smaller batches. Returns [batch, rows, width] on the home device."""
+        self._require_context(eval_pos, cells.shape[1])
         home = cells.device
-        batch, n_rows, n_groups, _ = cells.shape
-        parts = [slice(s, min(s + row_chunk, n_rows)) for s in range(0, n_rows, row_chunk)]
+        n_batch, n_rows, n_groups, _ = cells.shape
+        chunks = [slice(r, min(r + row_chunk, n_rows)) for r in range(0, n_rows, row_chunk)]
         y = y.to(compute_device)
+        targets = torch.empty((n_batch, n_rows, self.target_tokens, self.cell_dim), dtype=cells.dtype, device=home)
 
-        def dev(t):
-            return t.to(compute_device)
+        def load(t: torch.Tensor) -> torch.Tensor:
+            return t.to(compute_device).contiguous()
 
-        rows = torch.empty((batch, n_rows, self.width), dtype=cells.dtype, device=home)
-        for p in parts:
-            rows[:, p] = self.target_encoder(y[:, p]).to(cells.dtype).flatten(-2).to(home)
+        for part in chunks:
+            targets[:, part] = self.target_encoder(y[:, part]).to(cells.dtype).to(home)
+        rows = targets.view(n_batch, n_rows, self.width)
 
-        for layer in self._cell_stack():
-            for c0 in range(0, n_groups, column_chunk):
-                cols = slice(c0, min(c0 + column_chunk, n_groups))
-                cells[:, :, cols] = layer.apply_column_attention(dev(cells[:, :, cols]), eval_pos).to(home)
-            # keys from the layer's input, before any row chunk below is overwritten
-            keys = _operand(layer.target_norms[0], dev(rows[:, :eval_pos])).unsqueeze(1)
-            for p in parts:
-                r = dev(rows[:, p])
-                r = layer.attend_target_rows_to_context(r, _operand(layer.target_norms[0], r).unsqueeze(1), keys)
-                c, t = layer.apply_row_mlps_and_feature_attention(dev(cells[:, p]), r)
-                cells[:, p] = c.to(home)
-                rows[:, p] = t.flatten(-2).to(home)
-            del keys
+        for layer in self.cell_layers:
+            for g0 in range(0, n_groups, column_chunk):
+                cols = slice(g0, min(g0 + column_chunk, n_groups))
+                block = load(cells[:, :, cols])
+                layer.column_step(block, eval_pos)
+                _put(cells[:, :, cols], block)
+            context = layer.row_operand(load(rows[:, :eval_pos]))  # from the layer's input rows
+            for part in chunks:
+                c, t = load(cells[:, part]), load(targets[:, part])
+                r = _row_vectors(t)
+                layer.target_row_step(r, layer.row_operand(r), context=context)
+                layer.row_local_steps(c, t)
+                _put(cells[:, part], c)
+                _put(targets[:, part], t)
+            del context
 
-        # the boundary: context labels re-injected; cells become the final cell states in place
-        for p in parts:
-            r = dev(rows[:, p])
-            n_ctx = min(max(eval_pos - p.start, 0), p.stop - p.start)
+        # the boundary: context labels go into the row vectors; cells become the final states
+        for part in chunks:
+            n_ctx = min(max(eval_pos - part.start, 0), part.stop - part.start)
             if n_ctx:
-                bias = self._embed_context_labels(y[:, p.start : p.start + n_ctx]).to(r.dtype)
-                r = torch.cat((r[:, :n_ctx] + bias, r[:, n_ctx:]), dim=1)
-            rows[:, p] = r.to(home)
-            cells[:, p] = self.cell_out_norm(dev(cells[:, p])).to(home)
+                r = load(rows[:, part.start : part.start + n_ctx])
+                r += self.label_embedding(y[:, part.start : part.start + n_ctx]).to(r.dtype)
+                _put(rows[:, part.start : part.start + n_ctx], r)
+            _put(cells[:, part], self.cell_out_norm(load(cells[:, part])))
 
-        for layer in self._row_stack():
-            keys = _operand(layer.attn_norm, dev(rows[:, :eval_pos])).unsqueeze(1)
-            for p in parts:
-                r = dev(rows[:, p])
-                r = layer.attend_rows_to_context(r, _operand(layer.attn_norm, r).unsqueeze(1), keys)
-                rows[:, p] = layer.apply_readback_and_mlp(r, self.cell_to_row(dev(cells[:, p]))).to(home)
-            del keys
+        for layer in self.row_layers:
+            context = layer.row_operand(load(rows[:, :eval_pos]))
+            for part in chunks:
+                r = load(rows[:, part])
+                layer.context_step(r, layer.row_operand(r), context=context)
+                layer.readback_steps(r, self.cell_to_row(load(cells[:, part])))
+                _put(rows[:, part], r)
+            del context
 
         out = None
-        for p in parts:
-            normed = self.row_out_norm(dev(rows[:, p]))
+        for part in chunks:
+            normed = self.row_out_norm(load(rows[:, part]))
             if out is None:
-                out = torch.empty((batch, n_rows, self.width), dtype=normed.dtype, device=home)
-            out[:, p] = normed.to(home)
+                out = torch.empty((n_batch, n_rows, self.width), dtype=normed.dtype, device=home)
+            _put(out[:, part], normed)
         return out
