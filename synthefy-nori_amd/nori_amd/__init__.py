@@ -14,6 +14,7 @@ from . import _native, encoders, layer, transformer
 from .attention import attend_dense, compute_attention_blockwise, icl_attention
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, dequantize_int8, quantize_int8, scale_caches
 from .kv_project import project_quantize_kv
+from .api import NoriRegressor
 from .norm import RMSNorm, rms_norm
 from .transformer import ContextCache, FeaturesTransformer
 
@@ -21,6 +22,7 @@ __all__ = [
     "BlockwiseSeqKV",
     "ContextCache",
     "FeaturesTransformer",
+    "NoriRegressor",
     "encoders",
     "layer",
     "RMSNorm",

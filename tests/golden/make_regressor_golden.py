@@ -1,0 +1,128 @@
+"""Write the golden vectors of the nori-6m end-to-end case and of the memory-policy ladder.
+
+Runs the reference's own code on the CPU in fp32 (in this container only; the product of this
+script is the .npz data beside it, never the reference's code):
+
+* the nori-6m case (tests/regressor_case.py): a random-init nori-6m model whose weights are a
+  pure function of a stored per-parameter scale table and numpy's integer-based stream is
+  built with this package, its state dict loaded strictly into the reference's ``FeaturesTransformer``
+  (src/synthefy_nori/model/transformer.py:70-369), and the reference's context-cache API runs
+  the table with an int8 cache -- ``build_context_cache(cache_dtype="int8")`` then
+  ``apply_context_cache`` (:813-1078) -- on the standardized target, as ``NoriRegressor``'s
+  cached path does (api.py:1122-1151; predictor.py:3228-3265). Stored: the table, the scale
+  table and the SHA-256 of the weights, the 999-level quantile bank, the reference's point prediction
+  (``quantile_dist_mean_simple``, quantile_dist.py:95-135) mapped back to target units, and
+  the reference's layer-0 int8 cache codes and scales of the first 128 context rows.
+* the ladder: the reference's ``MemoryPolicy.resolve`` (inference/memory_policy.py:1173-1300)
+  over presets, fields and cache sizes, with the report keys (``model_dump``).
+
+Usage: python tests/golden/make_regressor_golden.py   (writes tests/golden/regressor_goldens.npz)
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+import types
+
+import numpy as np
+import torch
+
+REFERENCE_SRC = "/root/reference/src"
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT = os.path.join(HERE, "regressor_goldens.npz")
+sys.path[:0] = [os.path.dirname(HERE), os.path.join(os.path.dirname(os.path.dirname(HERE)), "synthefy-nori_amd")]
+
+import regressor_case as case  # noqa: E402
+
+# (label, policy request, est_cache_gb, bytes_per_element, head_dim, vram_gb, ram_gb)
+LADDER_CASES = [
+    ("default fits", None, 2.0, 2, 64, 24.0, 64.0),
+    ("default int8 fallback", None, 12.0, 2, 64, 24.0, 64.0),
+    ("default offload", None, 30.0, 2, 64, 24.0, 256.0),
+    ("default plain loop", None, 300.0, 2, 64, 24.0, 64.0),
+    ("exact offloads", "exact", 12.0, 2, 64, 24.0, 64.0),
+    ("max_context", "max_context", 2.0, 2, 64, 24.0, 64.0),
+    ("off", "off", 2.0, 2, 64, 24.0, 64.0),
+    ("stream bf16", {"stream_context": True}, 2.0, 2, 64, 288.0, 64.0),
+    ("stream int8", {"stream_context": True}, 30.0, 2, 44, 288.0, 64.0),
+    ("stream explicit chunk", {"stream_context": True, "context_row_chunk": 4096}, 2.0, 4, 56, 24.0, 64.0),
+    ("absolute gpu budget", {"gpu_budget_absolute_gb": 1.0}, 1.5, 2, 64, 288.0, 512.0),
+    ("no offload", {"offload_to_host": False}, 200.0, 2, 64, 288.0, 512.0),
+    ("fp32 footprint", {"cache_dtype": "int8"}, 100.0, 4, 44, 288.0, 64.0),
+]
+
+
+def load_reference():
+    for name, sub in (("synthefy_nori", "synthefy_nori"), ("synthefy_nori.model", "synthefy_nori/model"),
+                      ("synthefy_nori.inference", "synthefy_nori/inference")):
+        mod = types.ModuleType(name)
+        mod.__path__ = [os.path.join(REFERENCE_SRC, sub)]
+        sys.modules[name] = mod
+    import synthefy_nori.inference.memory_policy as mp
+    import synthefy_nori.model.layer as layer
+    import synthefy_nori.model.quantile_dist as qd
+    import synthefy_nori.model.transformer as tr
+
+    return tr, layer, qd, mp
+
+
+def main():
+    tr, layer, qd, mp = load_reference()
+    from nori_amd import api, transformer as our_tr
+
+    torch.set_num_threads(8)
+    out: dict[str, np.ndarray] = {}
+
+    # ---- the nori-6m case
+    torch.manual_seed(0)
+    scales = case.weight_scales(api.build_model(api.NORI_6M_CONFIG))
+    ours = case.seeded_model(our_tr.FeaturesTransformer, api.NORI_6M_CONFIG, scales)
+    ref = tr.FeaturesTransformer(**api.NORI_6M_CONFIG).eval()
+    ref.load_state_dict(ours.state_dict(), strict=True)
+    for m in ref.modules():
+        if isinstance(m, layer.RMSNorm):
+            m.use_native = True
+    x_tr, y_tr, x_te, y_te = case.table()
+    y_mean, y_std = float(y_tr.mean()), float(y_tr.std())
+    y_norm = ((y_tr - y_mean) / y_std).astype(np.float32)
+    with torch.inference_mode():
+        ctx = ref.build_context_cache(torch.from_numpy(x_tr)[None], torch.from_numpy(y_norm)[None], cache_dtype="int8")
+        bank = ref.apply_context_cache(torch.from_numpy(x_te)[None], ctx)[0].float()
+        taus = torch.tensor(ref.regression_quantiles, dtype=torch.float64)
+        point = qd.quantile_dist_mean_simple(bank.double(), taus, enforce_monotone_first=True)
+        skv = ctx.caches[0]["seq_kv"]
+        codes0, scales0 = skv._q, skv._scale
+    out["case/x_train"], out["case/y_train"], out["case/x_test"], out["case/y_test"] = x_tr, y_tr, x_te, y_te
+    out["case/weights_sha256"] = np.array(case.weights_sha256(ours))
+    out["case/weight_scales"] = np.array(json.dumps(scales))
+    out["case/bank_norm"] = bank.numpy()
+    out["case/taus"] = taus.numpy()
+    out["case/point_norm"] = point.numpy()
+    out["case/point"] = point.numpy() * y_std + y_mean
+    out["case/codes0"] = codes0[:, :128].numpy()  # layer 0's cache, first 128 context rows
+    out["case/scales0"] = scales0[:, :128].numpy()
+
+    # ---- the ladder
+    rows = []
+    for label, request, est, bpe, hd, vram, ram in LADDER_CASES:
+        row = {"label": label, "request": request, "est": est, "bpe": bpe, "head_dim": hd, "vram": vram, "ram": ram}
+        try:
+            resolved = mp.MemoryPolicy.coerce(request).resolve(
+                est_cache_gb=est, bytes_per_element=bpe, head_dim=hd, total_vram_gb=vram, total_ram_gb=ram
+            )
+        except Exception as exc:  # the refusal is the recorded outcome
+            row["error"] = type(exc).__name__
+        else:
+            dump = resolved.model_dump()
+            row["report"] = {k: dump[k] for k in dump if k != "attempt_history"}
+            row["report_keys"] = sorted(dump)
+        rows.append(row)
+    out["ladder/json"] = np.array(json.dumps(rows))
+    np.savez_compressed(OUT, **out)
+    print(f"wrote {OUT}: point predictions {out['case/point'][:4]}, ladder {[r.get('report', {}).get('rung', r.get('error')) for r in rows]}")
+
+
+if __name__ == "__main__":
+    main()

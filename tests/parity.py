@@ -22,6 +22,6 @@ def relative_error(got, exp) -> float:
 def check_relative(got, exp, bar: float, what: str) -> float:
     """Assert relative_error(got, exp) <= bar; prints the measured figure either way."""
     rel = relative_error(got, exp)
-    print(f"[parity] {what}: relative error {rel:.3e} (bar {bar:.0e})", flush=True)
-    assert rel <= bar, f"{what}: relative error {rel:.3e} exceeds {bar:.0e}"
+    print(f"[parity] {what}: relative error {rel:.3e} (bar {bar:.1e})", flush=True)
+    assert rel <= bar, f"{what}: relative error {rel:.3e} exceeds {bar:.1e}"
     return rel

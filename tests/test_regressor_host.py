@@ -1,0 +1,159 @@
+"""Host-side parity of the NoriRegressor surface (no kernel runs here).
+
+* The nori-6m case's weights: this package's seeded build hashes to the SHA-256 the golden
+  recipe recorded for the weights it ran the reference with (tests/regressor_case.py).
+* The quantile collapse (quantile_dist.py:95-135): equal to the reference's own output on the
+  golden quantile bank, and pinned by closed forms -- a constant bank, the identity quantile
+  function, invariance to the order of the bank.
+* Quantiles read at the head's own levels are the sorted bank's columns; between levels they
+  interpolate linearly (api.py:1330-1345).
+* The memory-policy ladder: rung, precision, placement, budgets and footprints equal to the
+  reference's MemoryPolicy.resolve on the same requests and sizes, refusals included, and
+  the report carries every key of the reference's memory_report_.
+* fit/predict argument errors, as the reference raises them.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import regressor_case as case
+from nori_amd import api
+from nori_amd.memory_policy import ContextTooLargeError, MemoryPolicy
+from nori_amd.transformer import FeaturesTransformer
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "regressor_goldens.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def test_seeded_nori_6m_weights_are_the_ones_the_reference_ran(gold):
+    model = case.seeded_model(FeaturesTransformer, api.NORI_6M_CONFIG, json.loads(str(gold["case/weight_scales"])))
+    assert case.weights_sha256(model) == str(gold["case/weights_sha256"])
+    assert sum(p.numel() for p in model.parameters()) > 5_000_000  # nori-6m's size
+
+
+def test_table_is_the_recorded_one(gold):
+    x_tr, y_tr, x_te, y_te = case.table()
+    for got, key in ((x_tr, "x_train"), (y_tr, "y_train"), (x_te, "x_test"), (y_te, "y_test")):
+        assert np.array_equal(got, gold[f"case/{key}"])
+
+
+def test_quantile_collapse_equals_the_reference_on_its_bank(gold):
+    bank = torch.from_numpy(gold["case/bank_norm"]).double()
+    taus = torch.from_numpy(gold["case/taus"])
+    got = api.quantile_dist_mean(bank, taus).numpy()
+    np.testing.assert_allclose(got, gold["case/point_norm"], rtol=0, atol=1e-12)
+
+
+def test_quantile_collapse_closed_forms():
+    taus = torch.tensor([(i + 1) / 1000.0 for i in range(999)], dtype=torch.float64)
+    # a constant quantile function is that constant
+    assert torch.allclose(api.quantile_dist_mean(torch.full((3, 999), 2.5, dtype=torch.float64), taus),
+                          torch.full((3,), 2.5, dtype=torch.float64), rtol=0, atol=1e-12)
+    # q(tau) = tau between the outer levels, flat outside: t0^2 + (t1^2 - t0^2) / 2 + (1 - t1) t1
+    t0, t1 = 1e-3, 0.999
+    exact = t0 * t0 + (t1 * t1 - t0 * t0) / 2 + (1 - t1) * t1
+    assert abs(api.quantile_dist_mean(taus[None], taus).item() - exact) < 1e-12
+    # the bank is sorted first: any order of the same values gives the same mean
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(5, 999, generator=g, dtype=torch.float64)
+    perm = torch.randperm(999, generator=g)
+    assert torch.allclose(api.quantile_dist_mean(q, taus), api.quantile_dist_mean(q[:, perm], taus), rtol=0, atol=1e-12)
+    # half-precision banks integrate in fp32; a single level returns itself
+    assert api.quantile_dist_mean(q.half(), taus).dtype == torch.float32
+    assert torch.equal(api.quantile_dist_mean(q[:, :1], taus[:1]), q[:, 0])
+    with pytest.raises(ValueError):
+        api.quantile_dist_mean(q, taus.flip(0))
+
+
+def test_quantiles_at_the_head_levels_are_bank_columns(gold):
+    bank = np.sort(gold["case/bank_norm"].astype(np.float64), axis=1)
+    taus = gold["case/taus"]
+    got = api._interpolated_quantiles(bank, taus, np.asarray(case.QUANTILE_LEVELS))
+    for i, level in enumerate(case.QUANTILE_LEVELS):
+        assert np.array_equal(got[i], bank[:, int(round(level * 1000)) - 1])
+    mid = api._interpolated_quantiles(bank, taus, np.asarray([0.1005]))[0]
+    np.testing.assert_allclose(mid, 0.5 * (bank[:, 99] + bank[:, 100]), rtol=0, atol=1e-12)
+
+
+def test_memory_ladder_matches_the_reference(gold):
+    rows = json.loads(str(gold["ladder/json"]))
+    ours_keys = set(MemoryPolicy().as_report())
+    for row in rows:
+        policy = MemoryPolicy.coerce(row["request"])
+        args = dict(est_cache_gb=row["est"], bytes_per_element=row["bpe"], head_dim=row["head_dim"],
+                    total_vram_gb=row["vram"], total_ram_gb=row["ram"])
+        if "error" in row:
+            assert row["error"] == "ContextTooLargeError"
+            with pytest.raises(ContextTooLargeError):
+                policy.resolve(**args)
+            continue
+        got = policy.resolve(**args).as_report()
+        exp = row["report"]
+        for key in ("rung", "cache", "cache_dtype", "offload_to_host", "reuse_context_cache", "context_row_chunk",
+                    "stream_context", "allow_quantization"):
+            assert got[key] == exp[key], (row["label"], key, got[key], exp[key])
+        for key in ("est_cache_gb", "resident_gb", "gpu_budget_absolute_gb", "host_budget_absolute_gb"):
+            if exp[key] is None:
+                assert got[key] is None, (row["label"], key)
+            else:
+                assert math.isclose(got[key], exp[key], rel_tol=1e-12), (row["label"], key, got[key], exp[key])
+        missing = set(row["report_keys"]) - ours_keys
+        assert not missing, f"report lacks the reference's keys {sorted(missing)}"
+
+
+def test_policy_coercion_and_refusals():
+    assert MemoryPolicy.coerce("exact").allow_quantization is False
+    assert MemoryPolicy.coerce("max_context").cache_dtype == "int8"
+    off = MemoryPolicy.coerce("off")
+    assert off.cache is False and off.reuse_context_cache is False
+    with pytest.raises(ValueError):
+        MemoryPolicy.coerce("fastest")
+    with pytest.raises(ValueError):
+        MemoryPolicy.coerce({"cache": False, "cache_dtype": "int8"})
+    with pytest.raises(ValueError):
+        MemoryPolicy.coerce({"rung": "resident_int8"})
+    with pytest.raises(ValueError):
+        MemoryPolicy.coerce({"no_such_field": 1})
+    with pytest.raises(TypeError):
+        MemoryPolicy.coerce(3)
+
+
+def test_fit_and_predict_argument_errors():
+    x_tr, y_tr, x_te, _ = case.table()
+    reg = api.NoriRegressor(model=object(), device="cpu")
+    with pytest.raises(ValueError, match="before predict"):
+        reg.predict(x_te)
+    with pytest.raises(ValueError, match="same number of rows"):
+        reg.fit(x_tr, y_tr[:-1])
+    with pytest.raises(ValueError, match="finite"):
+        reg.fit(x_tr, np.where(np.arange(len(y_tr)) == 3, np.nan, y_tr))
+    with pytest.raises(ValueError, match="one-dimensional"):
+        reg.fit(x_tr, np.stack([y_tr, y_tr], 1))
+    reg.fit(x_tr, y_tr)
+    assert reg.y_mean_ == pytest.approx(float(y_tr.mean())) and reg.n_features_in_ == case.N_FEATURES
+    with pytest.raises(ValueError, match="Unknown output_type"):
+        reg.predict(x_te, output_type="best")
+    with pytest.raises(NotImplementedError):
+        reg.predict(x_te, output_type="main")
+    with pytest.raises(ValueError, match="requires quantiles"):
+        reg.predict(x_te, output_type="quantiles")
+    with pytest.raises(ValueError, match="strictly in"):
+        reg.predict(x_te, output_type="quantiles", quantiles=[0.0, 0.5])
+    with pytest.raises(ValueError, match="only valid"):
+        reg.predict(x_te, quantiles=[0.5])
+    with pytest.raises(ValueError, match="features"):
+        reg.predict(x_te[:, :5])
+    with pytest.raises(ValueError, match="memory preset"):
+        api.NoriRegressor(model=object(), memory_policy="nope").fit(x_tr, y_tr)
