@@ -116,7 +116,9 @@ __device__ __forceinline__ uint32_t scale_f16x2(uint32_t w, _Float16 s) {
 // Max of 16 values as a depth-3 tree of v_max3_f32, without the NaN-quieting copies the
 // compiler puts in front of fmaxf operands (the inputs are MFMA results; NaN inputs give NaN
 // outputs either way), in one asm block (the compiler follows every asm statement with a
-// hazard nop; one block pays it once).
+// hazard nop; one block pays it once). The compiler pads no wait states in front of an asm
+// block for MFMA results it reads, so its inputs must be MFMA results issued well before
+// (here: one pipeline step earlier).
 __device__ __forceinline__ float max16f(const float (&x)[16]) {
     float r, t0, t1, t2, t3;
     asm("v_max3_f32 %1, %5, %6, %7\n\t"
@@ -446,13 +448,19 @@ icl_attention_kernel(const Args a) {
     // S^T[32 keys x 32 queries] of the 32 K rows whose first row is at this lane's Kl - its own
     // row offset (lane: keys 8g + 4hh + i, query qi)
     const int k_lane = l32 * G::KPITCH + 8 * hh;  // this lane's A-operand element in a 32-row step
-    auto logits = [&](const lds_f16* Kl) {
+    // PREFETCH (the shapes whose register budget has room) holds the K operands of the step
+    // after next in registers across a step, so the logit MFMAs never wait on LDS, and reads a
+    // step's V operands before its softmax.
+    constexpr bool PREFETCH = (DP <= 48 && !(KVT == NORI_F32 && NW == 8)) || WavesPerEU<DP, NW>::value == 1;
+    // K operands of one 32-key step (the A operands of its logit MFMAs) at this lane's Kl
+    auto read_k = [&](const lds_f16* Kl, f16x8 (&kfr)[G::KSTEPS]) {
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks) kfr[ks] = *reinterpret_cast<const lds_f16x8*>(Kl + 16 * ks);
+    };
+    auto logits = [&](const f16x8 (&kfr)[G::KSTEPS]) {
         f32x16 acc = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < G::KSTEPS; ++ks) {
-            const f16x8 kfr = *reinterpret_cast<const lds_f16x8*>(Kl + 16 * ks);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qf[ks], acc, 0, 0, 0);
-        }
+        for (int ks = 0; ks < G::KSTEPS; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr[ks], qf[ks], acc, 0, 0, 0);
         return acc;
     };
 
@@ -467,14 +475,60 @@ icl_attention_kernel(const Args a) {
     const int v_lane = (16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) * G::VPITCH + 4 * (vt & 3);
     const lds_f16* const KsL = (const lds_f16*)Ks;
     const lds_f16* const VsL = (const lds_f16*)Vs;
+    auto read_v = [&](const lds_f16* Vl, f16x8 (&vf)[G::VT]) {
+#pragma unroll
+        for (int t = 0; t < G::VT; ++t) {
+            const f16x4 lo = read_tr16(Vl + 16 * t);
+            const f16x4 hi = read_tr16(Vl + 8 * G::VPITCH + 16 * t);
+            vf[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
 
-    // Online softmax of one 32-key step whose first key is kstep (relative to the range start)
-    // (logits s, per-key factors kf[0..32), this lane's V operand address Vl in the step), then
-    // O^T += V^T P^T. s_next holds the following step's logits, already in flight; with the
-    // offset folded into the MFMA they carry the running max they were issued with and follow
-    // it when it moves.
-    auto softmax_pv = [&](const f32x16& s, f32x16& s_next, const float* kf, const lds_f16* Vl, int kstep,
-                          bool first) {
+    // Probabilities of keys 2t, 2t + 1 of a step's 16 (f16, RN) from their base-2 logit
+    // offsets, as one word (keys 8(t/2) + 4hh + 2(t%2) + 0..1); lsum takes their sum
+    // (VALU-summed head widths).
+    auto prob_pair = [&](const float (&x)[16], int t, float& lsum) {
+        const f16x2 pp = f16x2{(_Float16)__builtin_amdgcn_exp2f(x[2 * t]), (_Float16)__builtin_amdgcn_exp2f(x[2 * t + 1])};
+        if constexpr (!FOLD) {
+            const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+            lsum = __builtin_amdgcn_fdot2(pp, ones, lsum, false);
+        }
+        return __builtin_bit_cast(uint32_t, pp);
+    };
+    // The B operands of the two 16-query blocks from a step's 8 probability words: swapping
+    // words t and t + 4 between 16-lane rows gives block 0 (queries 0-15) and block 1
+    // (queries 16-31) their 32 keys each.
+    auto b_operands = [&](const uint32_t (&pw)[8], f16x8& p0, f16x8& p1) {
+        u32x4 pa, pb;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const auto r = __builtin_amdgcn_permlane16_swap(pw[t], pw[t + 4], false, false);
+            pa[t] = r[0];
+            pb[t] = r[1];
+        }
+        p0 = __builtin_bit_cast(f16x8, pa);
+        p1 = __builtin_bit_cast(f16x8, pb);
+    };
+
+    // One 32-key step whose first key is kstep (relative to the range start): s holds its
+    // logits S (issued one step earlier), kfr the K operands of the following step, kf its
+    // per-key factors (int8 VALU mode) and Vl this lane's V operand address in the step. On
+    // return s holds the following step's logits and O^T has taken V^T P^T.
+    //   * With PREFETCH, one straight run issues the following step's logit MFMAs and,
+    //     between them, this step's softmax on the VALU (the lane max, the 16 exponentials,
+    //     the f16 conversions and the swaps into B operands), so a wavefront's VALU work runs
+    //     while its own MFMAs do. The probabilities are formed against the current running max
+    //     before it is known whether the step moves it; a step that does (rare once the max
+    //     settles, always the first) forms them again after the rescale. Otherwise (fewer
+    //     registers) the logit MFMAs are issued first and the softmax follows the rescale test.
+    //   * The PV MFMAs follow; the block staging and the K operand reads of the step after
+    //     next are issued behind them.
+    auto step = [&](f32x16& s, f16x8 (&kfr)[G::KSTEPS], const lds_f16* Kl, const float* kf, const lds_f16* Vl, int kstep,
+                    bool first) {
+        // V operands: read first where the register budget allows (PREFETCH shapes), so their
+        // LDS latency passes under the softmax, else after it
+        f16x8 vf[G::VT];
+        if constexpr (PREFETCH) read_v(Vl, vf);
         float x[16];
         if constexpr (FOLD) {
 #pragma unroll
@@ -496,9 +550,33 @@ icl_attention_kernel(const Args a) {
                 for (int i = 0; i < 4; ++i)
                     if (kstep + 8 * g + 4 * hh + i >= klen) x[4 * g + i] = -INFINITY;
         }
-        // the lane's max over its 16 keys decides whether any query of the wavefront must move
-        // its running max; only then is the per-query max (both half-waves) formed
-        float bm = max16f(x);
+        // ---- the straight run: following step's logits on the MFMAs, this step's softmax on
+        // the VALU
+        // With PREFETCH, logit MFMA ks is followed by its share of the probabilities, each
+        // segment fenced off so the wavefront issues them while that MFMA runs (the next MFMA
+        // waits for its result). The lane's max over its 16 keys decides whether any query of the
+        // wavefront must move its running max (max16f reads logits issued one step earlier, long
+        // complete).
+        f32x16 s_next = f32x16{};
+        float bm = 0.0f, l_step = 0.0f;
+        uint32_t pw[8];
+        f16x8 p0, p1;
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks) {
+            // without PREFETCH each K operand is read just before its MFMA (fewer live registers)
+            const f16x8 kop = PREFETCH ? kfr[ks] : *reinterpret_cast<const lds_f16x8*>(Kl + 16 * ks);
+            s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qf[ks], s_next, 0, 0, 0);
+            if (ks == 0) {
+                if constexpr (PREFETCH) __builtin_amdgcn_sched_barrier(0);
+                bm = max16f(x);
+            }
+            if constexpr (PREFETCH) {
+#pragma unroll
+                for (int t = 8 * ks / G::KSTEPS; t < 8 * (ks + 1) / G::KSTEPS; ++t) pw[t] = prob_pair(x, t, l_step);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if constexpr (PREFETCH) b_operands(pw, p0, p1);
         if (first || __any(bm > kRescaleSlack)) {
             {
                 // both halves of the swap together hold lanes l and l ^ 32 in every lane
@@ -527,6 +605,7 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) x[r] -= shift;
             if constexpr (FOLD) {
+                // the following step's logits were issued with the old max
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s_next[r] -= shift;
 #pragma unroll
@@ -535,54 +614,42 @@ icl_attention_kernel(const Args a) {
                     for (int j = 0; j < 8; ++j)
                         if (16 * ks + 8 * hh + j == d) qf[ks][j] = (_Float16)(-m_run);
             }
-        }
-        // probabilities (f16, RN): word t of pw holds x[2t], x[2t + 1] (keys 8(t/2) + 4hh + 2(t%2) + 0..1)
-        uint32_t pw[8];
+            if constexpr (PREFETCH) {  // formed against the old max: again
+                l_step = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float p0 = __builtin_amdgcn_exp2f(x[2 * t]);
-            const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1]);
-            const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
-            if constexpr (!FOLD) {
-                const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-                l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
+                for (int t = 0; t < 8; ++t) pw[t] = prob_pair(x, t, l_step);
+                b_operands(pw, p0, p1);
             }
-            pw[t] = __builtin_bit_cast(uint32_t, pp);
         }
-        // B operands of the two 16-query blocks: swapping words t and t + 4 between 16-lane
-        // rows gives block 0 (queries 0-15) and block 1 (queries 16-31) their 32 keys each
-        u32x4 pa, pb;
+        if constexpr (!PREFETCH) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const auto r = __builtin_amdgcn_permlane16_swap(pw[t], pw[t + 4], false, false);
-            pa[t] = r[0];
-            pb[t] = r[1];
+            for (int t = 0; t < 8; ++t) pw[t] = prob_pair(x, t, l_step);
+            b_operands(pw, p0, p1);
         }
-        const f16x8 p0 = __builtin_bit_cast(f16x8, pa);
-        const f16x8 p1 = __builtin_bit_cast(f16x8, pb);
+        if constexpr (!FOLD) l_run += l_step;
+        if constexpr (!PREFETCH) read_v(Vl, vf);
 #pragma unroll
         for (int t = 0; t < G::VT; ++t) {
-            const f16x4 lo = read_tr16(Vl + 16 * t);
-            const f16x4 hi = read_tr16(Vl + 8 * G::VPITCH + 16 * t);
-            const f16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            o[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p0, o[t][0], 0, 0, 0);
-            o[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p1, o[t][1], 0, 0, 0);
+            o[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[t], p0, o[t][0], 0, 0, 0);
+            o[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[t], p1, o[t][1], 0, 0, 0);
         }
+        s = s_next;
     };
 
     // Software pipeline over 32-key steps: each step issues the logit MFMAs of the following
-    // step before its own softmax, so every wavefront always holds MFMA work that is
-    // independent of the VALU work in front of it. Blocks are staged into the LDS ring ahead
-    // of use from raw words loaded one block before that.
+    // step, whose K operands were read one step (or, with PREFETCH, two steps) earlier. Blocks
+    // are staged into the LDS ring ahead of use from raw words loaded one block before that.
     //   * three buffers: block i+2 is staged while block i is computed (after its first
     //     step) and one barrier closes each block, so the staging overlaps the compute of
     //     the other wavefronts;
-    //   * two buffers (wide heads): block i+1 is staged before the last step of block i,
-    //     fenced by a barrier on each side.
+    //   * two buffers (wide heads): block i+1 is staged before the second-to-last step of
+    //     block i, fenced by a barrier on each side, so the K operands of its first step can
+    //     be read during the last step of block i.
     Raw<KVT> raw[NU];
     load_block(k_begin, raw);
     store_block(0, raw);
     constexpr int AHEAD = G::NBUF >= 3 ? 2 : 1;
+    static_assert(G::SPB >= 2, "a block spans at least two steps");
     if constexpr (AHEAD == 2) {
         if (nblk > 1) {
             load_block(k_begin + KB, raw);
@@ -591,7 +658,10 @@ icl_attention_kernel(const Args a) {
     }
     if (nblk > AHEAD) load_block(k_begin + AHEAD * KB, raw);
     __syncthreads();
-    f32x16 s_cur = logits(KsL + k_lane);
+    f16x8 kfr[G::KSTEPS];
+    read_k(KsL + k_lane, kfr);
+    f32x16 s_cur = logits(kfr);
+    read_k(KsL + k_lane + 32 * G::KPITCH, kfr);  // the K operands of step 1
 
     for (int blk = 0; blk < nblk; ++blk) {
         const int64_t kb = k_begin + (int64_t)blk * KB;
@@ -605,7 +675,7 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
         for (int st = 0; st < G::SPB; ++st) {
             if constexpr (AHEAD == 1) {
-                if (st == G::SPB - 1) {
+                if (st == G::SPB - 2) {
                     __syncthreads();  // every wavefront is done with block blk-1, the target buffer
                     if (blk + 1 < nblk) {
                         store_block(nxt, raw);
@@ -614,12 +684,12 @@ icl_attention_kernel(const Args a) {
                     __syncthreads();
                 }
             }
-            // logits of the following step in flight: the next 32 rows of this block, or the
-            // first 32 rows of the next block (a stale buffer after the last block, unused)
-            f32x16 s_next = logits(st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn);
-            softmax_pv(s_cur, s_next, kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH,
-                       blk * KB + 32 * st, blk == 0 && st == 0);
-            s_cur = s_next;
+            step(s_cur, kfr, st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn, kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH, blk * KB + 32 * st,
+                 blk == 0 && st == 0);
+            // K operands of the step after next: this block's rows, or the next block's (a
+            // stale buffer after the last block, unused)
+            if constexpr (PREFETCH)
+                read_k(st + 2 < G::SPB ? Kc + 32 * (st + 2) * G::KPITCH : Kn + 32 * (st + 2 - G::SPB) * G::KPITCH, kfr);
             if constexpr (AHEAD == 2) {
                 if (st == 0 && blk + 2 < nblk) {
                     store_block((blk + 2) % G::NBUF, raw);
