@@ -23,10 +23,13 @@ present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes
 layer against the unfused sequence it replaces, one layer's prefill self-attention over the
 fp16 context K/V, the same configuration through the model-level context-cache API
 (build once, 4 query batches), the kernel-level legs of the nori-6m block and the nori-100m
-layer, the many-small-tables path (512 tables through a nori-1-5-sized two-phase model), and
-the CPU baseline: the oracle (quantizer in C, attention as the
-reference's fp32 online-softmax scan, layer.py:777-839) timed on the host cores over a
-bounded sample of the same work.
+layer, the many-small-tables path (512 tables through a nori-1-5-sized two-phase model), the
+context-side RMSNorm against HBM bandwidth, config 1 (NoriRegressor fit/predict on a nori-6m
+table of 1024 + 256 rows with an int8 cache), and the CPU baseline: the same step as the
+reference runs it on the CPU -- fp32 torch on every host core, through oracle.sublayer (the
+reference's quantizer expression, and the cached sequence-attention sublayer with the
+online-softmax scan of layer.py:777-839 over the GPU-built int8 codes) -- timed on a bounded
+sample of token groups and extrapolated.
 """
 
 from __future__ import annotations
@@ -62,7 +65,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
     p.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
-    p.add_argument("--cpu-sample-queries", type=int, default=512, help="query rows of the CPU attention sample")
+    p.add_argument("--cpu-sample-groups", type=int, default=8,
+                   help="token groups (of 33) of one layer in the CPU baseline's timed sample")
     p.add_argument(
         "--streamed", action="store_true",
         help="measure the host-streamed long-context path instead: one layer's int8 cache in pinned host "
@@ -81,6 +85,10 @@ def parse_args():
         "--small-tables", action="store_true",
         help="measure only the many-small-tables path: a nori-1-5-shaped two-phase model over 512 tables of "
         "256 context + 64 query rows",
+    )
+    p.add_argument(
+        "--config1", action="store_true",
+        help="measure only config 1: NoriRegressor fit/predict on a nori-6m table of 1024 context + 256 query rows",
     )
     p.add_argument(
         "--model", action="store_true",
@@ -518,6 +526,9 @@ def main():
     if args.small_tables:
         print(json.dumps(small_tables(torch, dev)), flush=True)
         return
+    if args.config1:
+        print(json.dumps(config1(torch, dev)), flush=True)
+        return
     if args.prefill:
         shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
         kv16 = torch.randn(shape, generator=torch.Generator(device=dev).manual_seed(2), device=dev, dtype=torch.float16)
@@ -622,10 +633,12 @@ def main():
     write = cache_write(torch, dev, codes[0], scales[0])
     prefill = prefill_attention(torch, dev, kv[0])
     model_e2e = end_to_end(torch, dev)
-    kv0 = kv[0]
+    kv0 = [kv[0]]
     del kv
     others = other_configs(torch, dev)
     tables = small_tables(torch, dev)
+    norm_leg = rmsnorm_leg(torch, dev)
+    c1 = config1(torch, dev)
 
     rows_per_step = QUERY_BATCHES * QUERY_ROWS
     ms_per_step = elapsed * 1e3 / args.steps
@@ -704,58 +717,146 @@ def main():
     line["end_to_end"] = model_e2e
     line["other_configs"] = others
     line["small_tables"] = tables
+    line["rmsnorm_roofline"] = norm_leg
+    line["config1"] = c1
     if args.cpu_baseline == "on":
-        line["cpu_baseline"] = cpu_baseline(torch, kv0, codes[0], scales[0], args.cpu_sample_queries, layers)
+        line["cpu_baseline"] = cpu_baseline(torch, kv0, codes, scales, wq, wo, queries, layers, args.cpu_sample_groups)
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(torch, kv, codes, scales, n_query, layers):
-    """Time the oracle on the host: the reference's CPU path for the same step.
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu reports), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
 
-    Sample (about 10 s): the quantizer (oracle C restatement, one thread) over 2 of the 33
-    token groups of one layer's fp16 cache, and the attention (the reference's fp32
-    online-softmax scan over 32k-row blocks dequantized as BlockwiseSeqKV.iter_kv_blocks
-    does, torch on all host cores) for all 33 token groups x ``n_query`` query rows of one
-    layer. Both scale linearly in their sizes; the step is 12 layers x (quantize + 4
-    batches x 1024 query rows of attention).
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(torch, kv, codes, scales, wq, wo, queries, layers, groups):
+    """The same step on the host CPU, as the reference runs it there: fp32 torch on every core
+    (predictor.py:318-321 turns mixed precision off on the CPU), through oracle.sublayer -- the
+    quantizer as the reference's expression (kv_cache_scaling.py:29-37) on the fp32 cache, and
+    per query batch the cached sequence-attention step (RMSNorm, Q projection, the online-softmax
+    scan over the dequantized int8 cache in 32768-row blocks, layer.py:777-839, output
+    projection, residual) over the codes the GPU built (bit-exact, so moved to the host as they
+    are).
+
+    Sample (about 10-20 s on a 16-core host): ``groups`` of the 33 token groups of one layer --
+    their quantize and one 1024-row query batch; the step scales linearly in groups, layers and
+    batches: 12 layers x 33/groups x (quantize + 4 batches), reported as extrapolated.
     """
-    from oracle import attention as oa
-    from oracle import codec
+    from oracle import sublayer as osl
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    # quantize: 2 token groups of one layer, fp16 source, GPU scale mode
-    qgroups = 2
-    src = kv[:qgroups].cpu().numpy()
+    src = kv[0][:groups].float().cpu()
+    osl.quantize_int8(src[:1, :1024])  # first-call set-up outside the timing
     t0 = time.perf_counter()
-    codec.quantize_int8(src, "f16", codec.DIV_RECIP)
-    t_quant = (time.perf_counter() - t0) * GROUPS / qgroups
-    # attention: every token group, n_query rows, one layer
-    g = torch.Generator().manual_seed(5)
-    q = torch.randn(GROUPS, n_query, HEADS, HEAD_DIM, generator=g)
-    c = codes.cpu()
-    s = scales.cpu()
-
-    def blocks():
-        step = 32768
-        for a in range(0, CONTEXT_ROWS, step):
-            yield c[:, a : a + step].float() * s[:, a : a + step]
-
+    osl.quantize_int8(src)
+    t_quant = time.perf_counter() - t0
+    del src
+    x = queries[0][:groups].float().cpu()
+    w_q, w_o = wq[0].float().cpu(), wo[0].float().cpu()
+    c, s = codes[0][:groups].cpu(), scales[0][:groups].cpu()
     t0 = time.perf_counter()
-    oa.blockwise_attention_fp32(q, blocks())
-    t_attn = (time.perf_counter() - t0) * QUERY_ROWS / n_query
-    seconds_per_step = layers * (t_quant + QUERY_BATCHES * t_attn)
+    osl.sequence_attention_step(x, w_q, w_o, c, s, heads=HEADS, head_dim=HEAD_DIM, alpha=DEEPNORM_ALPHA)
+    t_batch = time.perf_counter() - t0
+    seconds_per_step = layers * (GROUPS / groups) * (t_quant + QUERY_BATCHES * t_batch)
     return {
         "value": round(QUERY_BATCHES * QUERY_ROWS / seconds_per_step, 4),
         "unit": "query rows/s",
         "cores": cores,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"quantize: oracle C restatement (1 thread) over {qgroups} of {GROUPS} token groups of one layer, "
-        f"{t_quant * qgroups / GROUPS:.2f} s; attention: fp32 online softmax (oracle.attention."
-        f"blockwise_attention_fp32, layer.py:777-839; torch, {cores} threads) over {GROUPS} token groups x "
-        f"{n_query} query rows x 1 layer against the 65536-row int8 cache, {t_attn * n_query / QUERY_ROWS:.2f} s; "
-        f"extrapolated linearly to {layers} layers x (quantize + {QUERY_BATCHES} x {QUERY_ROWS} query rows) = "
-        f"{seconds_per_step:.0f} s per step",
+        "extrapolated": True,
+        "seconds_per_step": round(seconds_per_step, 2),
+        "sample": f"oracle.sublayer, fp32 torch, {cores} threads: quantize of {groups} of {GROUPS} token groups of one "
+        f"layer's fp32 K/V ({t_quant:.2f} s) and one {QUERY_ROWS}-row query batch through that layer's cached "
+        f"sequence attention over the GPU-built int8 codes of the same {groups} groups ({t_batch:.2f} s); "
+        f"extrapolated linearly to {layers} layers x {GROUPS} groups x (quantize + {QUERY_BATCHES} batches)",
+    }
+
+
+def rmsnorm_leg(torch, dev, reps=6):
+    """The context-side RMSNorm of one layer at this workload (33 x 65536 rows of 352 fp32, no
+    weight, eps 1e-5) writing the fp16 projection operand, as the whole-context build does:
+    HIP events around each launch."""
+    import nori_amd
+
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = torch.randn(GROUPS * CONTEXT_ROWS, EMBED, generator=g, device=dev)
+    out = torch.empty(x.shape, dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    nori_amd.rms_norm(x, EMBED, None, 1e-5, out=out)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        nori_amd.rms_norm(x, EMBED, None, 1e-5, out=out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = x.numel() * (4 + 2)
+    return {
+        "kernel": "rms_norm (fp32 in, fp16 out)", "bound": "hbm",
+        "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+        "frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4), "avg_launch_ms": round(ms, 4),
+        "work_per_launch": f"{nbytes:.4e} B = n*(4+2), n = 33*65536*352",
+    }
+
+
+# config 1: the reference's CPU end-to-end case on its NoriRegressor surface, run here on the
+# GPU: a random-init nori-6m model, one table of 1024 context + 256 query rows x 16 features
+CONFIG1 = dict(context=1024, queries=256, features=16, quantiles=(0.1, 0.5, 0.9), reps=5)
+
+
+def config1(torch, dev):
+    """NoriRegressor fit/predict on config 1's table (seed 0: X ~ N(0, 1), w ~ N(0, 1/16),
+    y = X.w + 0.5 sin(X[:, 0]) + 0.1 N(0, 1)) with an int8 context cache (memory_policy
+    {"cache_dtype": "int8"}; fp16 autocast). The first predict builds the context cache, later
+    ones reuse it; wall clock with the device synchronized."""
+    import numpy as np
+
+    from nori_amd import api
+    from nori_amd.transformer import FeaturesTransformer
+
+    c = CONFIG1
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((c["context"] + c["queries"], c["features"])).astype(np.float32)
+    w = rng.normal(0.0, 0.25, c["features"])
+    y = x.astype(np.float64) @ w + 0.5 * np.sin(x[:, 0].astype(np.float64)) + 0.1 * rng.standard_normal(len(x))
+    torch.manual_seed(0)
+    model = FeaturesTransformer(**api.NORI_6M_CONFIG)
+    reg = api.NoriRegressor(model=model, device=dev, memory_policy={"cache_dtype": "int8"})
+    xc, yc, xq = x[: c["context"]], y[: c["context"]], x[c["context"]:]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reg.fit(xc, yc)
+    point = reg.predict(xq)
+    torch.cuda.synchronize()
+    t_first = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(c["reps"]):
+        point = reg.predict(xq)
+        qs = reg.predict(xq, output_type="quantiles", quantiles=list(c["quantiles"]))
+    torch.cuda.synchronize()
+    t_again = (time.perf_counter() - t0) / c["reps"]
+    report = reg.memory_report_
+    assert np.isfinite(point).all() and np.isfinite(qs).all() and qs.shape == (3, c["queries"])
+    return {
+        "what": "config 1: NoriRegressor fit/predict, random-init nori-6m, 1 table of 1024 context + 256 query rows "
+        "x 16 features, int8 context cache, point + quantiles 0.1/0.5/0.9, fp16 autocast",
+        "path": f"memory_policy {{'cache_dtype': 'int8'}} -> rung {report['rung']} (cache {report['cache_dtype']}, "
+        "build_context_cache + apply_context_cache, dense ScalableSeqKV)",
+        "fit_and_first_predict_s": round(t_first, 4),
+        "predict_point_and_quantiles_s": round(t_again, 4),
+        "query_rows_per_s": round(c["queries"] / t_again, 1),
+        "context_reused": bool(report["context_reused"]),
     }
 
 
