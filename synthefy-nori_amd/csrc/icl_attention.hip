@@ -94,6 +94,12 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     p.dp = (d + 15) / 16 * 16;
     p.mode = mode_for(d);
     p.nw = (nq > 256 && has_16_waves(p.dp, p.mode)) ? 16 : (nq > 96 ? 8 : 2);
+    // a 160-row tile where it covers the queries with fewer padded rows (320 queries: two
+    // exact tiles instead of two 256-row ones)
+    if (p.nw != 2 && has_5_waves(p.dp)) {
+        auto padded = [&](int nw) { return (nq + nw * QPW - 1) / (nw * QPW) * nw * QPW; };
+        if (padded(5) * 5 < padded(p.nw) * 4) p.nw = 5;
+    }
     p.nqt = (int)((nq + p.nw * QPW - 1) / (p.nw * QPW));
     p.nunits = bg * heads * (int64_t)p.nqt;
     const int KB = block_keys(p.nw);

@@ -20,6 +20,12 @@ int occupancy(int nw) {
             return e == hipSuccess ? n : 1;
         }
     }
+    if constexpr (has_5_waves(DP)) {
+        if (nw == 5) {
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 5>, 5 * 64, 0);
+            return e == hipSuccess ? n : 1;
+        }
+    }
     if (nw == 8) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 8>, 8 * 64, 0);
     else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_attention_kernel<DP, NORI_I8, MODE, 2>, 2 * 64, 0);
     return e == hipSuccess ? n : 1;
@@ -34,8 +40,8 @@ int occupancy_of(int mode, int nw) {
 
 int resident_workgroups(int dp, int mode, int nw) {
     // cached per shape: the answer depends only on the compiled kernel and the device
-    static int cache[8][2][3] = {};
-    const int di = dp / 16 - 1, ni = nw == 16 ? 2 : (nw == 8 ? 1 : 0);
+    static int cache[8][2][4] = {};
+    const int di = dp / 16 - 1, ni = nw == 16 ? 2 : (nw == 8 ? 1 : (nw == 5 ? 3 : 0));
     if (di < 0 || di > 7 || mode < 0 || mode > 1) return 1;
     int& slot = cache[di][mode][ni];
     if (slot == 0) {

@@ -246,10 +246,10 @@ struct Geometry {
     static constexpr int VBUF = KB * VPITCH;
     // LDS buffers in the K/V ring: three let a block be staged while the previous block's V
     // and the next block's K are both being read (one barrier per block); wide heads, whose
-    // buffers are large, use two and a second barrier. The budget keeps two 8-wave
-    // workgroups on a CU (a 16-wave workgroup has the CU to itself).
+    // buffers are large, use two and a second barrier. The budget keeps two 8-wave or three
+    // 5-wave workgroups on a CU (a 16-wave workgroup has the CU to itself).
     static constexpr int BUF_BYTES = (KBUF + VBUF) * 2 + KB * 4;
-    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : 64) * 1024 ? 3 : 2;
+    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : (NW == 5 ? 52 : 64)) * 1024 ? 3 : 2;
 };
 
 // Shapes with a 16-wave workgroup: narrow heads, where 32 query rows per wavefront fit in
@@ -257,12 +257,17 @@ struct Geometry {
 // the VALU mode needs more and spills.)
 constexpr bool has_16_waves(int dp, int mode) { return dp <= 32 || ((dp == 48 || dp == 64) && mode == kFold); }
 
+// Shapes with a 5-wave workgroup (160 query rows; three per CU): heads up to 64 wide, for query
+// counts that 160-row tiles cover with less padding than 256- or 512-row ones (320 rows: two
+// exact tiles instead of two 256-row tiles).
+constexpr bool has_5_waves(int dp) { return dp <= 64; }
+
 // Register budget: heads up to 64 wide keep 4 wavefronts per SIMD (two 8-wave workgroups per
 // CU). Without the bound the 64-wide 8-wave fold kernel takes 135 VGPRs and only one workgroup
 // fits; with it, it (and the 48-wide VALU-mode kernel) spills 6 registers to scratch and still
 // runs faster (nori-100m layer shape on 8-wave workgroups: 94.4 ms unbounded, 80.7 ms bounded).
 template <int DP, int NW>
-struct WavesPerEU { static constexpr int value = (NW == 16 || (NW == 8 && DP <= 64)) ? 4 : 1; };
+struct WavesPerEU { static constexpr int value = (NW == 16 || ((NW == 8 || NW == 5) && DP <= 64)) ? 4 : 1; };
 
 template <int DP, int KVT, int MODE, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
@@ -778,6 +783,12 @@ int launch_shape(int nw, const Args& a, hipStream_t stream) {
     if constexpr (has_16_waves(DP, MODE)) {
         if (nw == 16) {
             hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 16>), grid, dim3(16 * 64), 0, stream, a);
+            return NORI_OK;
+        }
+    }
+    if constexpr (has_5_waves(DP)) {
+        if (nw == 5) {
+            hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 5>), grid, dim3(5 * 64), 0, stream, a);
             return NORI_OK;
         }
     }
