@@ -165,6 +165,25 @@ int nori_residual_add(const float* x, const void* u, int u_dtype, float alpha, i
                       void* stream);
 
 /*
+ * A deep-norm residual update and the RMSNorm (no weight) that reads its result, in one pass:
+ * x_out = x + alpha * u exactly as nori_residual_add forms it (x, x_out fp32 [rows, cols],
+ * contiguous; x_out may be x; u's rows contiguous, or -- u_rows = {d1, d2, s0, s1, s2} -- row
+ * r = (i0 * d1 + i1) * d2 + i2 of u at element i0 * s0 + i1 * s1 + i2 * s2, e.g. a transposed
+ * [batch, groups, rows] update of a [batch, rows, groups] stream; u_rows NULL for contiguous
+ * rows), then y = x_out * rsqrt(mean(x_out^2) + eps) exactly as
+ * nori_rms_norm_to forms it from fp32 rows, written as y_dtype (NORI_F32, or NORI_F16 /
+ * NORI_BF16: the projection operand an autocast F.linear makes of it). Row r of y starts at
+ * element (r / y_group) * y_group_stride + (r % y_group) * y_row_stride, so the rows of several
+ * streams can be interleaved into one token buffer. The two-phase encoder's residual updates
+ * followed by the pre-norm of the next sublayer (two_phase.py:198-225, 264-272 with
+ * layer.py:251-253), bit for bit the two separate calls. Rows of more than 1024 elements, cols
+ * not a multiple of 4 and unaligned operands return NORI_ERR_UNSUPPORTED before any device work.
+ */
+int nori_residual_add_rms_norm(const float* x, const void* u, int u_dtype, const int64_t* u_rows, float alpha,
+                               int64_t rows, int32_t cols, float eps, float* x_out, void* y, int y_dtype,
+                               int64_t y_group, int64_t y_group_stride, int64_t y_row_stride, void* stream);
+
+/*
  * SwiGLU gate over the [gate | up] output of one fused projection (gate and up weights stacked,
  * so the operand is read once): out[r, j] = T(T(silu(gu[r, j])) * gu[r, hidden + j]) with
  * silu(x) = x / (1 + exp(-x)) in fp32 and T the rounding to `dtype` (NORI_F32 / NORI_F16 /

@@ -149,6 +149,84 @@ rms_norm_elementwise_kernel(const void* x, int64_t rows, int cols, int64_t x_row
     }
 }
 
+// The deep-norm residual update and the RMSNorm that reads its result, in one pass over an fp32
+// residual stream of rows x cols: xo = x + RN_UT(alpha * u) (nori_residual_add's rounding), then
+// y = rms_norm(xo) written as OT. The statistic is formed by the same G lanes, chunk order and
+// shuffles as rms_norm_chunked_kernel<NORI_F32, *, OT, G>, so y equals that kernel run on xo, bit
+// for bit. Row r of y starts at byte (r / y_group) * y_group_bytes + (r % y_group) * y_row_bytes
+// (rows of a token buffer that interleaves several streams). Row r of u, with r = (i0 * u_d1 + i1) *
+// u_d2 + i2, starts at element i0 * u_s0 + i1 * u_s1 + i2 * u_s2 (a transposed update, e.g. a
+// column attention's [batch, groups, rows] output added to a [batch, rows, groups] stream).
+// xo may be x.
+struct UpdateRows {
+    int64_t d1, d2, s0, s1, s2;  // row r -> (r / (d1 d2), (r / d2) % d1, r % d2) at these strides
+};
+
+template <int UT, int OT, int G>
+__global__ void __launch_bounds__(kThreads)
+residual_rms_norm_kernel(const float* x, const void* u, UpdateRows ur, float alpha, int64_t rows, int cols, float eps,
+                         float* xo, uint8_t* y, int64_t y_group, int64_t y_group_bytes, int64_t y_row_bytes) {
+    constexpr int EPC = 4;
+    constexpr int OUT_CHUNK = EPC * (OT == NORI_F32 ? 4 : 2);
+    const int lane_in_row = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
+    const int nchunks = cols / EPC;
+    const bool active = row < rows;
+    float v[kMaxChunksPerLane][EPC];
+    float acc = 0.0f;
+    int64_t u_row = 0;
+    if (active) {
+        const int64_t t = row / ur.d2;
+        u_row = (t / ur.d1) * ur.s0 + (t % ur.d1) * ur.s1 + (row % ur.d2) * ur.s2;
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxChunksPerLane; ++k) {
+        const int ch = lane_in_row + k * G;
+        if (active && ch < nchunks) {
+            const int64_t at = row * cols + (int64_t)ch * EPC;
+            const int64_t u_at = u_row + (int64_t)ch * EPC;
+            const f32x4 xv = *reinterpret_cast<const f32x4*>(x + at);
+            float uv[EPC];
+            if constexpr (UT == NORI_F32) {
+                const f32x4 w = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(u) + u_at);
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) uv[e] = w[e];
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(u) + u_at);
+                const uint32_t h[2] = {w.x, w.y};
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) {
+                    const uint16_t b = (uint16_t)(h[e >> 1] >> (16 * (e & 1)));
+                    uv[e] = UT == NORI_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+                }
+            }
+            f32x4 r;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+                v[k][e] = xv[e] + round_to<UT>(uv[e] * alpha);
+                r[e] = v[k][e];
+            }
+            *reinterpret_cast<f32x4*>(xo + at) = r;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) acc = fmaf(v[k][e], v[k][e], acc);
+        }
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, G);
+    const float inv = rsqrtf(acc / (float)cols + eps);
+    const int64_t y_at = active ? (row / y_group) * y_group_bytes + (row % y_group) * y_row_bytes : 0;
+#pragma unroll
+    for (int k = 0; k < kMaxChunksPerLane; ++k) {
+        const int ch = lane_in_row + k * G;
+        if (active && ch < nchunks) {
+            float o[EPC];
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) o[e] = v[k][e] * inv;
+            store_chunk<NORI_F32, OT, EPC>(y + y_at + (int64_t)ch * OUT_CHUNK, o);
+        }
+    }
+}
+
 template <int DT, int WDT, int OT>
 int launch(const void* x, int64_t rows, int cols, int64_t xs, const void* w, float eps, void* y, int64_t ys,
            hipStream_t stream) {
@@ -220,4 +298,76 @@ extern "C" int nori_rms_norm(const void* x, int dtype, int64_t rows, int32_t col
                              void* stream_v) {
     return nori_rms_norm_to(x, dtype, rows, cols, x_row_stride, weight, weight_dtype, eps, y, dtype, y_row_stride,
                             stream_v);
+}
+
+namespace {
+
+template <int UT, int OT>
+int launch_residual(const float* x, const void* u, const UpdateRows& ur, float alpha, int64_t rows, int cols, float eps,
+                    float* xo, void* y, int64_t y_group, int64_t y_group_bytes, int64_t y_row_bytes, hipStream_t stream) {
+    const int nchunks = cols / 4;
+    int g = 1;
+    while (g < nchunks && g < 64) g <<= 1;
+    const int rows_per_block = kThreads / g;
+    const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+#define NORI_RES_CASE(GV)                                                                                         \
+    case GV:                                                                                                       \
+        hipLaunchKernelGGL((residual_rms_norm_kernel<UT, OT, GV>), dim3(grid), dim3(kThreads), 0, stream, x, u, ur, \
+                           alpha, rows, cols, eps, xo, (uint8_t*)y, y_group, y_group_bytes, y_row_bytes);          \
+        break;
+    switch (g) {
+        NORI_RES_CASE(1) NORI_RES_CASE(2) NORI_RES_CASE(4) NORI_RES_CASE(8)
+        NORI_RES_CASE(16) NORI_RES_CASE(32) NORI_RES_CASE(64)
+    }
+#undef NORI_RES_CASE
+    return launch_status("residual_add_rms_norm");
+}
+
+}  // namespace
+
+extern "C" int nori_residual_add_rms_norm(const float* x, const void* u, int u_dtype, const int64_t* u_rows,
+                                          float alpha, int64_t rows, int32_t cols, float eps, float* x_out, void* y,
+                                          int y_dtype, int64_t y_group, int64_t y_group_stride, int64_t y_row_stride,
+                                          void* stream_v) {
+    clear_error();
+    if (rows < 0 || cols <= 0 || y_group <= 0)
+        return fail(NORI_ERR_INVALID, "residual_add_rms_norm: bad shape rows=%lld cols=%d y_group=%lld",
+                    (long long)rows, cols, (long long)y_group);
+    // the update's rows: contiguous unless u_rows = {d1, d2, s0, s1, s2} says otherwise
+    UpdateRows ur{1, 1, cols, 0, 0};
+    if (u_rows) {
+        ur = UpdateRows{u_rows[0], u_rows[1], u_rows[2], u_rows[3], u_rows[4]};
+        if (ur.d1 <= 0 || ur.d2 <= 0 || rows % (ur.d1 * ur.d2) != 0)
+            return fail(NORI_ERR_INVALID, "residual_add_rms_norm: update rows (%lld x %lld) do not tile %lld rows",
+                        (long long)ur.d1, (long long)ur.d2, (long long)rows);
+    }
+    if (u_dtype != NORI_F32 && u_dtype != NORI_F16 && u_dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "residual_add_rms_norm: unsupported update dtype %s", dtype_name(u_dtype));
+    if (y_dtype != NORI_F32 && y_dtype != NORI_F16 && y_dtype != NORI_BF16)
+        return fail(NORI_ERR_UNSUPPORTED, "residual_add_rms_norm: unsupported output dtype %s", dtype_name(y_dtype));
+    if (rows == 0) return NORI_OK;
+    if (!x || !u || !x_out || !y) return fail(NORI_ERR_INVALID, "residual_add_rms_norm: null pointer");
+    const int us = u_dtype == NORI_F32 ? 4 : 2, os = y_dtype == NORI_F32 ? 4 : 2, out_chunk = 4 * os;
+    const bool fits = cols % 4 == 0 && cols / 4 <= 64 * kMaxChunksPerLane && (uintptr_t)x % 16 == 0 &&
+                      (uintptr_t)x_out % 16 == 0 && (uintptr_t)u % (4 * us) == 0 && (uintptr_t)y % out_chunk == 0 &&
+                      (y_row_stride * os) % out_chunk == 0 && (y_group_stride * os) % out_chunk == 0 &&
+                      (ur.s0 * us) % (4 * us) == 0 && (ur.s1 * us) % (4 * us) == 0 && (ur.s2 * us) % (4 * us) == 0;
+    if (!fits)
+        return fail(NORI_ERR_UNSUPPORTED, "residual_add_rms_norm: rows of %d elements at these alignments take the "
+                    "separate residual_add and rms_norm", cols);
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int64_t gb = y_group_stride * os, rb = y_row_stride * os;
+    if (u_dtype == NORI_F16) {
+        if (y_dtype == NORI_F16) return launch_residual<NORI_F16, NORI_F16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+        if (y_dtype == NORI_BF16) return launch_residual<NORI_F16, NORI_BF16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+        return launch_residual<NORI_F16, NORI_F32>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+    }
+    if (u_dtype == NORI_BF16) {
+        if (y_dtype == NORI_F16) return launch_residual<NORI_BF16, NORI_F16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+        if (y_dtype == NORI_BF16) return launch_residual<NORI_BF16, NORI_BF16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+        return launch_residual<NORI_BF16, NORI_F32>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+    }
+    if (y_dtype == NORI_F16) return launch_residual<NORI_F32, NORI_F16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+    if (y_dtype == NORI_BF16) return launch_residual<NORI_F32, NORI_BF16>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
+    return launch_residual<NORI_F32, NORI_F32>(x, u, ur, alpha, rows, cols, eps, x_out, y, y_group, gb, rb, stream);
 }

@@ -3,6 +3,8 @@ src/synthefy_nori/model/layer.py:233-258), the deep-norm residual update and the
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn as nn
 
@@ -191,6 +193,105 @@ def residual_add(x: torch.Tensor, u: torch.Tensor, alpha: float, *, inplace: boo
         ),
         "residual_add",
     )
+    return out
+
+
+def _grouped_rows(t: torch.Tensor, cols: int) -> tuple[int, int, int, int] | None:
+    """(rows, group, group stride, row stride) when ``t``'s rows of ``cols`` contiguous elements
+    sit in groups of ``group`` rows at one stride, the groups at another -- e.g. a slice
+    [B, n, g, cols] of a [B, n, g + k, cols] token buffer -- or None."""
+    if t.stride(-1) != 1 or t.shape[-1] != cols:
+        return None
+    lead = [(n, st) for n, st in zip(t.shape[:-1], t.stride()[:-1]) if n != 1]
+    if not lead:
+        return 1, 1, cols, cols
+
+    def consistent(dims):
+        return all(so == ni * si for (_, so), (ni, si) in zip(dims, dims[1:]))
+
+    split = len(lead) - 1
+    while split > 0 and consistent(lead[split - 1:]):
+        split -= 1
+    inner, outer = lead[split:], lead[:split]
+    if not consistent(outer):
+        return None
+    group = 1
+    for n, _ in inner:
+        group *= n
+    rows = group
+    for n, _ in outer:
+        rows *= n
+    return rows, group, (outer[-1][1] if outer else group * inner[-1][1]), inner[-1][1]
+
+
+def _row_levels(t: torch.Tensor) -> tuple[int, int, int, int, int] | None:
+    """(d1, d2, s0, s1, s2) such that row r = (i0 * d1 + i1) * d2 + i2 of ``t`` (rows over its
+    leading axes in order, each of its last axis' contiguous elements) starts at element
+    i0 * s0 + i1 * s1 + i2 * s2 -- at most three row levels after merging axes that follow each
+    other in memory -- or None."""
+    if t.stride(-1) != 1:
+        return None
+    dims = []
+    for n, st in zip(t.shape[:-1], t.stride()[:-1]):
+        if n == 1:
+            continue
+        if dims and dims[-1][1] == n * st:
+            dims[-1] = (dims[-1][0] * n, st)
+        else:
+            dims.append((n, st))
+    if len(dims) > 3:
+        return None
+    dims = [(1, 0)] * (3 - len(dims)) + dims
+    return dims[1][0], dims[2][0], dims[0][1], dims[1][1], dims[2][1]
+
+
+def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMSNorm", *,
+                      out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x += alpha * u`` in place (``residual_add``'s rounding), then ``norm`` of the updated x,
+    in one HIP pass (``nori_residual_add_rms_norm``), bit for bit the two separate calls.
+
+    ``norm`` is an ``RMSNorm`` without weight over x's trailing width. The result is written in
+    ``out_dtype`` (default x's; a projection operand under autocast passes ``operand_dtype(x)``,
+    the value ``projection_operand`` gives) or into ``out`` (x's shape, rows in groups at two
+    strides -- e.g. a slice of a token buffer). Operands the kernel does not take (non-fp32 or
+    non-contiguous streams, a norm with a weight, rows past 1024 elements) run the two calls.
+    """
+    ns = tuple(norm.normalized_shape)
+    cols = 1
+    for n in ns:
+        cols *= int(n)
+    dt = (out.dtype if out is not None else (x.dtype if out_dtype is None else out_dtype))
+    fused = (
+        isinstance(norm, RMSNorm) and norm.weight is None and x.is_cuda and x.dtype == torch.float32
+        and x.is_contiguous() and tuple(u.shape) == tuple(x.shape) and u.device == x.device
+        and u.dtype in (torch.float32, torch.float16, torch.bfloat16) and dt in (torch.float32, torch.float16, torch.bfloat16)
+        and tuple(x.shape[-len(ns):]) == ns and cols % 4 == 0 and cols <= 1024
+    )
+    u_levels = None if not fused or u.is_contiguous() else _row_levels(u)
+    if fused and (u.is_contiguous() or u_levels is not None):
+        y = out if out is not None else torch.empty(x.shape, dtype=dt, device=x.device)
+        layout = _grouped_rows(y, cols) if out is not None else (x.numel() // cols, 1, cols, cols)
+        if layout is not None and layout[0] == x.numel() // cols:
+            rows, group, gstride, rstride = layout
+            levels = None if u_levels is None else (ctypes.c_int64 * 5)(*u_levels)
+            rc = nat.lib().nori_residual_add_rms_norm(
+                x.data_ptr(), u.data_ptr(), nat.dtype_code(u.dtype), levels, float(alpha), rows, cols,
+                float(norm.eps), x.data_ptr(), y.data_ptr(), nat.dtype_code(dt), group, gstride, rstride,
+                nat.stream_of(x.device),
+            )
+            if rc == nat.NORI_OK:
+                return y
+            if rc != nat.NORI_ERR_UNSUPPORTED:
+                nat.check(rc, "residual_add_rms_norm")
+    residual_add(x, u, alpha, inplace=True)
+    if out is None:
+        if dt == x.dtype:
+            return norm(x)
+        return rms_norm(x, ns, None, norm.eps, out_dtype=dt)
+    if _strided_rows(out, cols) is not None:
+        return rms_norm(x, ns, None, norm.eps, out=out)
+    for j in range(out.shape[-2]):  # rows at two strides: one call per index of the group axis
+        rms_norm(x[..., j, :], ns, None, norm.eps, out=out[..., j, :])
     return out
 
 

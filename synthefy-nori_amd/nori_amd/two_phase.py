@@ -34,7 +34,7 @@ import torch
 from torch import nn
 
 from .layer import MultiheadAttention, SwiGLUMLP
-from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, rms_norm
+from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, residual_add_norm
 
 __all__ = [
     "CellLayer2P",
@@ -59,9 +59,17 @@ def _plain_norm(width: int, eps: float) -> RMSNorm:
     return RMSNorm(width, eps=eps, elementwise_affine=False)
 
 
-def _accumulate(stream: torch.Tensor, update: torch.Tensor, alpha: float) -> torch.Tensor:
-    """stream += alpha * update (deep-norm residual), in place."""
-    return residual_add(stream, update.reshape(stream.shape), alpha, inplace=True)
+def _accumulate(stream: torch.Tensor, update: torch.Tensor, alpha: float, then: RMSNorm | None = None, *,
+                operand: bool = True, out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """stream += alpha * update (deep-norm residual), in place. With ``then``, also returns the
+    next sublayer's normalized stream -- ``projection_operand(then, stream)`` when ``operand``,
+    else ``then(stream)`` -- formed in the same pass (``residual_add_norm``), or writes it into
+    ``out``."""
+    if then is None:
+        residual_add(stream, update.reshape(stream.shape), alpha, inplace=True)
+        return None
+    dt = operand_dtype(stream) if operand else stream.dtype
+    return residual_add_norm(stream, update.reshape(stream.shape), alpha, then, out_dtype=dt, out=out)
 
 
 def _row_vectors(targets: torch.Tensor) -> torch.Tensor:
@@ -201,58 +209,77 @@ class CellLayer2P(nn.Module):
     def forward(self, cells: torch.Tensor, targets: torch.Tensor, eval_pos: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Out-of-place form: returns the updated (cells, targets); the inputs are left as they are."""
         cells, targets = cells.clone(), targets.contiguous().clone()
-        self.column_step(cells, eval_pos)
+        cell_op = self.column_step(cells, eval_pos, then=True)
         rows = _row_vectors(targets)
-        self.target_row_step(rows, self.row_operand(rows), eval_pos)
-        self.row_local_steps(cells, targets)
+        row_op = self.target_row_step(rows, self.row_operand(rows), eval_pos, then=True)
+        self.row_local_steps(cells, targets, cell_op, row_op)
         return cells, targets
 
-    # --- steps on the streams (in place)
-    def column_step(self, cells: torch.Tensor, eval_pos: int) -> None:
+    # --- steps on the streams (in place). Each step may take its normalized input, and with
+    # ``then`` returns the normalized input of the step after it from the same pass as its
+    # residual update (so a stream is not read again for the next norm).
+    def column_step(self, cells: torch.Tensor, eval_pos: int, normed: torch.Tensor | None = None,
+                    then: bool = False) -> torch.Tensor | None:
         """Each cell reads its column's context cells. Reads whole columns: a slice of the
-        groups axis may be passed."""
-        normed = projection_operand(self.cell_norms[0], cells)
-        _accumulate(cells, self.column_attention(normed, eval_pos), self.deepnorm_alpha)
+        groups axis may be passed. ``normed``: the cells through ``cell_norms[0]``; ``then``:
+        return the cells through ``cell_norms[1]`` (the cell MLP's operand)."""
+        if normed is None:
+            normed = projection_operand(self.cell_norms[0], cells)
+        update = self.column_attention(normed, eval_pos)
+        del normed
+        return _accumulate(cells, update, self.deepnorm_alpha, self.cell_norms[1] if then else None)
 
     def row_operand(self, rows: torch.Tensor) -> torch.Tensor:
         """The normalized row vectors the target-stream row attention reads, [batch, 1, n, width]."""
         return projection_operand(self.target_norms[0], rows).unsqueeze(1)
 
     def target_row_step(self, rows: torch.Tensor, normed: torch.Tensor, eval_pos: int | None = None,
-                        context: torch.Tensor | None = None) -> None:
+                        context: torch.Tensor | None = None, then: bool = False) -> torch.Tensor | None:
         """The row vectors ``rows`` [batch, n, width] (normalized: ``normed``) read the context
-        rows' normalized vectors: ``context``, or the first ``eval_pos`` of ``normed``."""
+        rows' normalized vectors: ``context``, or the first ``eval_pos`` of ``normed``. ``then``:
+        return the rows through ``target_norms[1]`` (the target MLP's operand)."""
         keys = normed[:, :, :eval_pos] if context is None else context
         update = _over_keys(self.sequence_attentions[0], normed, keys)
-        _accumulate(rows, update.squeeze(1), self.deepnorm_alpha)
+        return _accumulate(rows, update.squeeze(1), self.deepnorm_alpha, self.target_norms[1] if then else None)
 
-    def row_local_steps(self, cells: torch.Tensor, targets: torch.Tensor) -> None:
+    def row_local_steps(self, cells: torch.Tensor, targets: torch.Tensor, cell_operand: torch.Tensor | None = None,
+                        row_operand: torch.Tensor | None = None,
+                        then: tuple[RMSNorm | None, RMSNorm | None, bool] | None = None):
         """The MLPs, then the feature attention: each row reads only itself, so any slice of rows
         may be passed. ``targets`` [batch, n, K, width] (its row-vector view is what the target
-        MLP transforms)."""
+        MLP transforms). ``cell_operand`` / ``row_operand``: the MLPs' normalized inputs.
+        ``then`` = (cell norm, target-row norm, operand): return the streams through those norms
+        (in the projection dtype when ``operand``), from the feature attention's update passes."""
         alpha = self.deepnorm_alpha
         rows = _row_vectors(targets)
-        _accumulate(cells, self.mlp[0](projection_operand(self.cell_norms[1], cells)), alpha)
-        _accumulate(rows, self.mlp[1](projection_operand(self.target_norms[1], rows)), alpha)
-        tokens = self.feature_tokens(cells, targets)
-        cell_update, target_update = self.feature_attention(tokens, cells.shape[2])
-        _accumulate(cells, cell_update, alpha)
-        _accumulate(targets, target_update, alpha)
-
-    def feature_tokens(self, cells: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
-        """The feature attention's operand: every cell normalized by ``cell_norms[2]`` then every
-        target token by ``target_norms[2]``, [batch, n, groups + K, width], written token by token
-        into one buffer in the projection's dtype."""
+        if cell_operand is None:
+            cell_operand = projection_operand(self.cell_norms[1], cells)
+        if row_operand is None:
+            row_operand = projection_operand(self.target_norms[1], rows)
+        cell_update = self.mlp[0](cell_operand)
+        del cell_operand
+        row_update = self.mlp[1](row_operand)
+        del row_operand
+        # the two MLP updates, each with the feature attention's norm of its stream written
+        # token by token into the attention's operand buffer
         b, n, g, w = cells.shape
-        out = torch.empty((b, n, g + self.target_tokens, w), dtype=operand_dtype(cells), device=cells.device)
-        if not cells.is_cuda:
-            out[:, :, :g] = self.cell_norms[2](cells)
-            out[:, :, g:] = self.target_norms[2](targets)
-            return out
-        for j, (norm, src) in enumerate([(self.cell_norms[2], cells[:, :, i]) for i in range(g)]
-                                        + [(self.target_norms[2], targets[:, :, i]) for i in range(self.target_tokens)]):
-            rms_norm(src, norm.normalized_shape, None, norm.eps, out=out[:, :, j])
-        return out
+        tokens = torch.empty((b, n, g + self.target_tokens, w), dtype=operand_dtype(cells), device=cells.device)
+        _accumulate(cells, cell_update, alpha, self.cell_norms[2], out=tokens[:, :, :g])
+        _accumulate(targets, row_update, alpha, self.target_norms[2], out=tokens[:, :, g:])
+        del cell_update, row_update
+        cell_update, target_update = self.feature_attention(tokens, g)
+        del tokens
+        if then is None:
+            _accumulate(cells, cell_update, alpha)
+            _accumulate(targets, target_update, alpha)
+            return None
+        cell_norm, row_norm, operand = then
+        cell_next = _accumulate(cells, cell_update, alpha, cell_norm, operand=operand)
+        if row_norm is None:
+            _accumulate(targets, target_update, alpha)
+            return cell_next, None
+        row_next = _accumulate(rows, target_update.reshape(rows.shape), alpha, row_norm, operand=operand)
+        return cell_next, row_next
 
 
 class RowLayer2P(nn.Module):
@@ -273,27 +300,35 @@ class RowLayer2P(nn.Module):
     def forward(self, rows: torch.Tensor, eval_pos: int, cell_memory: torch.Tensor) -> torch.Tensor:
         """Out-of-place form: returns the updated rows; ``rows`` is left as it is."""
         rows = rows.clone()
-        self.context_step(rows, self.row_operand(rows), eval_pos)
-        self.readback_steps(rows, cell_memory)
+        query = self.context_step(rows, self.row_operand(rows), eval_pos, then=True)
+        self.readback_steps(rows, cell_memory, query)
         return rows
 
     def row_operand(self, rows: torch.Tensor) -> torch.Tensor:
         return projection_operand(self.attn_norm, rows).unsqueeze(1)
 
     def context_step(self, rows: torch.Tensor, normed: torch.Tensor, eval_pos: int | None = None,
-                     context: torch.Tensor | None = None) -> None:
+                     context: torch.Tensor | None = None, then: bool = False) -> torch.Tensor | None:
         """``rows`` [batch, n, width] (normalized: ``normed``) read the context rows' normalized
-        vectors: ``context``, or the first ``eval_pos`` of ``normed``."""
+        vectors: ``context``, or the first ``eval_pos`` of ``normed``. ``then``: return the rows
+        through ``readback_norm`` (the read-back query)."""
         keys = normed[:, :, :eval_pos] if context is None else context
-        _accumulate(rows, _over_keys(self.sequence_attentions[0], normed, keys).squeeze(1), self.deepnorm_alpha)
+        update = _over_keys(self.sequence_attentions[0], normed, keys).squeeze(1)
+        return _accumulate(rows, update, self.deepnorm_alpha, self.readback_norm if then else None)
 
-    def readback_steps(self, rows: torch.Tensor, cell_memory: torch.Tensor) -> None:
+    def readback_steps(self, rows: torch.Tensor, cell_memory: torch.Tensor, query: torch.Tensor | None = None,
+                       then: RMSNorm | None = None, operand: bool = True) -> torch.Tensor | None:
         """The row reads its own cells ``cell_memory`` [batch, n, groups, width], then the MLP;
-        each row reads only itself."""
+        each row reads only itself. ``query``: the rows through ``readback_norm``; ``then``:
+        return the rows through that norm after the MLP's update (in the projection dtype
+        when ``operand``)."""
         alpha = self.deepnorm_alpha
-        query = projection_operand(self.readback_norm, rows).unsqueeze(2)
-        _accumulate(rows, _over_keys(self.feature_attentions[0], query, cell_memory).squeeze(2), alpha)
-        _accumulate(rows, self.mlp[0](projection_operand(self.mlp_norm, rows)), alpha)
+        if query is None:
+            query = projection_operand(self.readback_norm, rows)
+        update = _over_keys(self.feature_attentions[0], query.unsqueeze(2), cell_memory).squeeze(2)
+        del query
+        mlp_in = _accumulate(rows, update, alpha, self.mlp_norm)
+        return _accumulate(rows, self.mlp[0](mlp_in), alpha, then, operand=operand)
 
 
 class TwoPhaseEncoder(nn.Module):
@@ -364,17 +399,38 @@ class TwoPhaseEncoder(nn.Module):
         cells = cells.clone()  # the streams are updated in place
         targets = self.target_encoder(y).to(cells.dtype).contiguous()
         rows = _row_vectors(targets)
-        for layer in self.cell_layers:
-            layer.column_step(cells, eval_pos)
-            layer.target_row_step(rows, layer.row_operand(rows), eval_pos)
-            layer.row_local_steps(cells, targets)
+        # every residual update hands the next sublayer its normalized stream (one pass)
+        cell_layers = list(self.cell_layers)
+        col_op = row_op = cell_states = None
+        for i, layer in enumerate(cell_layers):
+            mlp_op = layer.column_step(cells, eval_pos, normed=col_op, then=True)
+            if row_op is None:
+                row_op = layer.row_operand(rows)
+            tmlp_op = layer.target_row_step(rows, row_op, eval_pos, then=True)
+            if i + 1 < len(cell_layers):
+                nxt = cell_layers[i + 1]
+                col_op, row_op = layer.row_local_steps(cells, targets, mlp_op, tmlp_op,
+                                                       then=(nxt.cell_norms[0], nxt.target_norms[0], True))
+                row_op = row_op.unsqueeze(1)
+            else:
+                # the last update of the cells gives the cell states; the rows take the labels next
+                cell_states, _ = layer.row_local_steps(cells, targets, mlp_op, tmlp_op,
+                                                       then=(self.cell_out_norm, None, False))
         rows[:, :eval_pos] += self.label_embedding(y[:, :eval_pos]).to(rows.dtype)
-        cell_states = self.cell_out_norm(cells)
+        if cell_states is None:
+            cell_states = self.cell_out_norm(cells)
         memory = self.cell_to_row(cell_states)
-        for layer in self.row_layers:
-            layer.context_step(rows, layer.row_operand(rows), eval_pos)
-            layer.readback_steps(rows, memory)
-        return self.row_out_norm(rows), cell_states
+        row_layers = list(self.row_layers)
+        row_op, out = None, None
+        for i, layer in enumerate(row_layers):
+            if row_op is None:
+                row_op = layer.row_operand(rows)
+            query = layer.context_step(rows, row_op, eval_pos, then=True)
+            if i + 1 < len(row_layers):
+                row_op = layer.readback_steps(rows, memory, query, then=row_layers[i + 1].attn_norm).unsqueeze(1)
+            else:
+                out = layer.readback_steps(rows, memory, query, then=self.row_out_norm, operand=False)
+        return (self.row_out_norm(rows) if out is None else out), cell_states
 
     @torch.no_grad()
     def forward_chunked(self, cells: torch.Tensor, y: torch.Tensor, eval_pos: int, *, row_chunk: int, column_chunk: int,

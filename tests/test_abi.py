@@ -34,6 +34,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_rms_norm_to",
             "nori_residual_add",
             "nori_silu_mul",
+            "nori_residual_add_rms_norm",
             "nori_icl_attention",
             "nori_icl_attention_qk",
             "nori_icl_attention_workspace_size",

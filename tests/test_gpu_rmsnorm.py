@@ -114,3 +114,46 @@ def test_residual_add_equals_the_torch_expression(cuda, udtype, n):
     x2 = torch.randn(64, 8, device=cuda)
     u2 = torch.randn(8, 64, device=cuda).to(udtype).t()
     assert torch.equal(residual_add(x2, u2, alpha), x2 + alpha * u2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("udtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("cols", [128, 256, 44, 1024])
+def test_residual_add_norm_equals_the_two_calls(cuda, udtype, out_dtype, cols):
+    """nori_residual_add_rms_norm: the residual update and the norm of its result in one pass
+    equal nori_residual_add followed by nori_rms_norm_to bit for bit -- the stream and the
+    normalized rows -- also written into a slice of a token buffer (rows in groups at two
+    strides); rows past the kernel's width take the two calls."""
+    from nori_amd.norm import RMSNorm, residual_add, residual_add_norm, rms_norm
+
+    g = torch.Generator().manual_seed(cols)
+    x = (torch.randn(3, 37, 4, cols, generator=g) * 5).to(cuda)
+    u = (torch.randn(3, 37, 4, cols, generator=g) * 3).to(udtype).to(cuda)
+    alpha = 18 ** -0.5
+    norm = RMSNorm(cols, eps=1e-5)
+    ref_x = residual_add(x, u, alpha)
+    ref_y = rms_norm(ref_x, cols, None, 1e-5, out_dtype=out_dtype if out_dtype != torch.float32 else None)
+    got_x = x.clone()
+    got_y = residual_add_norm(got_x, u, alpha, norm, out_dtype=out_dtype)
+    assert got_y.dtype == out_dtype
+    assert torch.equal(got_x, ref_x) and torch.equal(got_y, ref_y)
+    # into the first 4 of 6 token slots of a buffer
+    buf = torch.full((3, 37, 6, cols), 7.0, dtype=out_dtype, device=cuda)
+    got_x = x.clone()
+    residual_add_norm(got_x, u, alpha, norm, out=buf[:, :, :4])
+    assert torch.equal(got_x, ref_x) and torch.equal(buf[:, :, :4], ref_y) and bool((buf[:, :, 4:] == 7.0).all())
+    # a transposed update (a column attention's [batch, groups, rows] output over a
+    # [batch, rows, groups] stream): rows at three strides
+    u_t = u.transpose(1, 2).contiguous().transpose(1, 2)
+    assert not u_t.is_contiguous()
+    got_x = x.clone()
+    got_y = residual_add_norm(got_x, u_t, alpha, norm, out_dtype=out_dtype)
+    assert torch.equal(got_x, ref_x) and torch.equal(got_y, ref_y)
+    # rows wider than the kernel's 1024 elements take the two calls
+    wide = RMSNorm(2 * cols + 1024, eps=1e-5)
+    xw = torch.randn(5, 2 * cols + 1024, device=cuda)
+    uw = torch.randn(5, 2 * cols + 1024, device=cuda).to(udtype)
+    ref = rms_norm(residual_add(xw, uw, alpha), 2 * cols + 1024, None, 1e-5)
+    xg = xw.clone()
+    assert torch.equal(residual_add_norm(xg, uw, alpha, wide), ref)
