@@ -23,7 +23,8 @@ present), the fused context-cache write (RMSNorm -> K/V projection -> int8 codes
 layer against the unfused sequence it replaces, one layer's prefill self-attention over the
 fp16 context K/V, the same configuration through the model-level context-cache API
 (build once, 4 query batches), the kernel-level legs of the nori-6m block and the nori-100m
-layer, the many-small-tables path (512 tables through a nori-1-5-sized two-phase model), the
+layer, config 4 end to end (a nori-100m-dims model over 32 tables of 8192 context + 2048 query
+rows, built and applied 8 tables at a time), the many-small-tables path (512 tables through a nori-1-5-sized two-phase model), the
 context-side RMSNorm against HBM bandwidth, config 1 (NoriRegressor fit/predict on a nori-6m
 table of 1024 + 256 rows with an int8 cache), and the CPU baseline: the same step as the
 reference runs it on the CPU -- fp32 torch on every host core, through oracle.sublayer (the
@@ -89,6 +90,11 @@ def parse_args():
     p.add_argument(
         "--config1", action="store_true",
         help="measure only config 1: NoriRegressor fit/predict on a nori-6m table of 1024 context + 256 query rows",
+    )
+    p.add_argument(
+        "--config4", action="store_true",
+        help="measure only config 4 end to end: a nori-100m-dims model over 32 tables of 8192 context + 2048 query "
+        "rows, built and applied 8 tables at a time through the context-cache API",
     )
     p.add_argument(
         "--model", action="store_true",
@@ -285,26 +291,27 @@ def prefill_attention(torch, dev, kv16, reps=2):
     }
 
 
-def model_config():
-    """A random-init model at this workload's block dims (12 layers, embed 352, 8 heads, 2
-    features per group, SwiGLU, RMSNorm pre-norm, QASS, target-aware embedding), with the
-    encoders of the reference's configuration files."""
+def model_config(layers=LAYERS, embed=EMBED, heads=HEADS, hid=4 * EMBED, quantiles=(0.1, 0.5, 0.9), rbf=(8, 16)):
+    """A random-init model at the given block dims (by default this workload's: 12 layers, embed
+    352, 8 heads; 2 features per group, SwiGLU, RMSNorm pre-norm, QASS, target-aware
+    embedding), with the encoders of the reference's configuration files."""
     return dict(
         preprocess_config_x=dict(
             num_features=2, nan_handling_enabled=True, normalize_on_train_only=True, normalize_x=True,
             remove_outliers=True, normalize_by_used_features=True,
         ),
         encoder_config_x=dict(
-            num_features=2, embedding_size=EMBED, mask_embedding_size=EMBED, encoder_use_bias=True,
+            num_features=2, embedding_size=embed, mask_embedding_size=embed, encoder_use_bias=True,
             numeric_embed_type="RBF",
-            RBF_config=dict(token_embed_dim=8, n_kernels=16, sigma=0.5, use_learn_sigma=False,
+            RBF_config=dict(token_embed_dim=rbf[0], n_kernels=rbf[1], sigma=0.5, use_learn_sigma=False,
                             use_learn_embeddings=False, use_original_features=False),
         ),
-        encoder_config_y=dict(num_inputs=1, embedding_size=EMBED, nan_handling_y_encoder=True, max_num_classes=10),
-        decoder_config=dict(num_classes=10, num_reg_quantiles=3, regression_loss="pinball",
-                            regression_quantiles=[0.1, 0.5, 0.9]),
-        nlayers=LAYERS, nhead=HEADS, embed_dim=EMBED, hid_dim=4 * EMBED, features_per_group=2, dropout=0.0,
-        pre_norm=True, activation="swiglu", norm_type="rmsnorm", deepnorm_alpha=DEEPNORM_ALPHA, layer_arch="smf",
+        encoder_config_y=dict(num_inputs=1, embedding_size=embed, nan_handling_y_encoder=True, max_num_classes=10),
+        decoder_config=dict(num_classes=10, num_reg_quantiles=len(quantiles), regression_loss="pinball",
+                            regression_quantiles=list(quantiles)),
+        nlayers=layers, nhead=heads, embed_dim=embed, hid_dim=hid,
+        features_per_group=2, dropout=0.0,
+        pre_norm=True, activation="swiglu", norm_type="rmsnorm", deepnorm_alpha=layers ** -0.5, layer_arch="smf",
         feature_positional_embedding_type="none", seq_attn_isolated=True, cross_share_all_kv_heads=False,
         use_qassmax=True, qass_mode="full", use_target_aware_embedding=True, use_column_specific_y_aware=True,
     )
@@ -351,6 +358,96 @@ def end_to_end(torch, dev, batches=QUERY_BATCHES):
         "build_context_cache_s": round(t_build, 3),
         "apply_query_rows_per_s": round(batches * QUERY_ROWS / t_apply, 1),
         "apply_ms_per_batch": round(t_apply * 1e3 / batches, 2),
+        "predictions_finite": finite,
+    }
+
+
+# The batched configuration at nori-100m block dims (assumed: 16 layers, embed 560, 10 heads of
+# 56, hidden 1680): 32 tables of 8192 context + 2048 query rows and 100 features, 80 Gaussian
+# and 20 categorical codes; the tables go through the context-cache API 8 at a time (the
+# 16-layer int8 cache of all 32 tables is about 257 GB, beside the build's transients).
+CONFIG4 = dict(tables=32, context=8192, queries=2048, numeric=80, categorical=20, sub_batch=8)
+
+
+def config4_table(np):
+    """Config 4's synthetic tables (numpy default_rng(3)): per table, 80 N(0, 1) features and 20
+    categorical columns with k ~ U{2..50} levels each and uniform codes (as floats, after the
+    numeric ones); y = X_num a + t_3 with a ~ N(0, 1/80) and Student-t noise of 3 degrees of
+    freedom."""
+    c = CONFIG4
+    rng = np.random.default_rng(3)
+    rows = c["context"] + c["queries"]
+    xn = rng.standard_normal((c["tables"], rows, c["numeric"])).astype(np.float32)
+    levels = rng.integers(2, 51, size=(c["tables"], 1, c["categorical"]))
+    xc = np.floor(rng.random((c["tables"], rows, c["categorical"])) * levels).astype(np.float32)
+    a = rng.normal(0.0, c["numeric"] ** -0.5, size=(c["tables"], c["numeric"], 1))
+    y = (xn.astype(np.float64) @ a)[..., 0] + rng.standard_t(3, size=(c["tables"], rows))
+    return np.concatenate([xn, xc], axis=-1), y.astype(np.float32)
+
+
+def config4_model(torch, dev):
+    """Config 4 end to end through the model-level context-cache API: a random-init model at
+    nori-100m block dims with the 999-level quantile head, 32 tables built and applied 8 at a
+    time (build_context_cache(cache_dtype="int8"), then apply_context_cache over the tables'
+    2048 query rows in chunks of 1024), under fp16 autocast; the point prediction is the
+    quantile bank's trapezoid mean. Wall clock with the device synchronized, after one warm
+    sub-batch of a single 1024-row table."""
+    import numpy as np
+
+    import nori_amd
+    from nori_amd.api import quantile_dist_mean
+
+    c = CONFIG4
+    levels = [(i + 1) / 1000.0 for i in range(999)]
+    x_np, y_np = config4_table(np)
+    x, y = torch.from_numpy(x_np).to(dev), torch.from_numpy(y_np).to(dev)
+    torch.manual_seed(3)
+    model = nori_amd.FeaturesTransformer(**model_config(layers=16, embed=560, heads=10, hid=1680, quantiles=levels,
+                                                        rbf=(16, 64))).eval().to(dev)
+    params = sum(p.numel() for p in model.parameters())
+    tau = torch.tensor(levels, device=dev)
+    n_ctx, tb = c["context"], c["sub_batch"]
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        warm = model.build_context_cache(x[:1, :1024], y[:1, :1024], cache_dtype="int8")
+        model.apply_context_cache(x[:1, n_ctx:n_ctx + 256], warm, row_chunk_size=256)
+        del warm
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        t_build = t_apply = 0.0
+        points = []
+        for t0 in range(0, c["tables"], tb):
+            torch.cuda.synchronize()
+            s0 = time.perf_counter()
+            ctx = model.build_context_cache(x[t0:t0 + tb, :n_ctx], y[t0:t0 + tb, :n_ctx], cache_dtype="int8")
+            torch.cuda.synchronize()
+            s1 = time.perf_counter()
+            bank = model.apply_context_cache(x[t0:t0 + tb, n_ctx:], ctx, row_chunk_size=1024)
+            points.append(quantile_dist_mean(bank, tau))
+            torch.cuda.synchronize()
+            s2 = time.perf_counter()
+            t_build += s1 - s0
+            t_apply += s2 - s1
+            del ctx, bank
+            print(f"config 4: tables {t0}-{t0 + tb - 1} built in {s1 - s0:.2f} s, applied in {s2 - s1:.2f} s",
+                  file=sys.stderr, flush=True)
+    pred = torch.cat(points)
+    finite = bool(torch.isfinite(pred).all())
+    peak = torch.cuda.max_memory_allocated(dev)
+    del model, x, y, pred, points
+    q_rows = c["tables"] * c["queries"]
+    return {
+        "what": "config 4 end to end: random-init nori-100m-dims model (16 layers, embed 560, 10 heads of 56, "
+        f"hidden 1680, 999 quantiles; {params / 1e6:.1f} M parameters), 32 tables x (8192 context + 2048 query rows) "
+        "x 100 features (80 Gaussian, 20 categorical codes with 2-50 levels), Student-t (df 3) target; "
+        "int8 context cache built and applied 8 tables at a time, fp16 autocast, point prediction by the "
+        "quantile bank's trapezoid mean",
+        "total_s": round(t_build + t_apply, 3),
+        "build_context_cache_s": round(t_build, 3),
+        "apply_s": round(t_apply, 3),
+        "query_rows_per_s": round(q_rows / (t_build + t_apply), 1),
+        "apply_query_rows_per_s": round(q_rows / t_apply, 1),
+        "tables_per_s": round(c["tables"] / (t_build + t_apply), 3),
+        "peak_allocated_gb": round(peak / 2 ** 30, 1),
         "predictions_finite": finite,
     }
 
@@ -523,6 +620,9 @@ def main():
     if args.model:
         print(json.dumps(end_to_end(torch, dev)), flush=True)
         return
+    if args.config4:
+        print(json.dumps(config4_model(torch, dev)), flush=True)
+        return
     if args.small_tables:
         print(json.dumps(small_tables(torch, dev)), flush=True)
         return
@@ -636,6 +736,7 @@ def main():
     kv0 = [kv[0]]
     del kv
     others = other_configs(torch, dev)
+    c4 = config4_model(torch, dev)
     tables = small_tables(torch, dev)
     norm_leg = rmsnorm_leg(torch, dev)
     c1 = config1(torch, dev)
@@ -716,6 +817,7 @@ def main():
     line["prefill_attention"] = prefill
     line["end_to_end"] = model_e2e
     line["other_configs"] = others
+    line["config4_end_to_end"] = c4
     line["small_tables"] = tables
     line["rmsnorm_roofline"] = norm_leg
     line["config1"] = c1
