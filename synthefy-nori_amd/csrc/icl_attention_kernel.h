@@ -528,8 +528,10 @@ icl_attention_kernel(const Args a) {
     //     registers) the logit MFMAs are issued first and the softmax follows the rescale test.
     //   * The PV MFMAs follow; the block staging and the K operand reads of the step after
     //     next are issued behind them.
-    auto step = [&](f32x16& s, f16x8 (&kfr)[G::KSTEPS], const lds_f16* Kl, const float* kf, const lds_f16* Vl, int kstep,
-                    bool first) {
+    //   * check = false (uniform over the workgroup) leaves out the lane max and the rescale
+    //     test: the optimistic scan of the folded kernels (see the block loop).
+    auto step = [&](bool check, f32x16& s, f16x8 (&kfr)[G::KSTEPS], const lds_f16* Kl, const float* kf, const lds_f16* Vl,
+                    int kstep, bool first) {
         // V operands: read first where the register budget allows (PREFETCH shapes), so their
         // LDS latency passes under the softmax, else after it
         f16x8 vf[G::VT];
@@ -561,7 +563,7 @@ icl_attention_kernel(const Args a) {
         // segment fenced off so the wavefront issues them while that MFMA runs (the next MFMA
         // waits for its result). The lane's max over its 16 keys decides whether any query of the
         // wavefront must move its running max (max16f reads logits issued one step earlier, long
-        // complete).
+        // complete); the folded kernels take it after the straight run, in checked steps only.
         f32x16 s_next = f32x16{};
         float bm = 0.0f, l_step = 0.0f;
         uint32_t pw[8];
@@ -573,7 +575,7 @@ icl_attention_kernel(const Args a) {
             s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qf[ks], s_next, 0, 0, 0);
             if (ks == 0) {
                 if constexpr (PREFETCH) __builtin_amdgcn_sched_barrier(0);
-                bm = max16f(x);
+                if constexpr (!FOLD) bm = max16f(x);
             }
             if constexpr (PREFETCH) {
 #pragma unroll
@@ -582,7 +584,12 @@ icl_attention_kernel(const Args a) {
             }
         }
         if constexpr (PREFETCH) b_operands(pw, p0, p1);
-        if (first || __any(bm > kRescaleSlack)) {
+        bool moves = false;
+        if (check) {
+            if constexpr (FOLD) bm = max16f(x);
+            moves = first || __any(bm > kRescaleSlack);
+        }
+        if (moves) {
             {
                 // both halves of the swap together hold lanes l and l ^ 32 in every lane
                 const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), true, false);
@@ -650,6 +657,31 @@ icl_attention_kernel(const Args a) {
     //   * two buffers (wide heads): block i+1 is staged before the second-to-last step of
     //     block i, fenced by a barrier on each side, so the K operands of its first step can
     //     be read during the last step of block i.
+    // The folded kernels scan optimistically: every block after the first skips the per-step
+    // rescale test and keeps the running max the first block anchored. Probabilities then stay
+    // finite in f16 while no logit exceeds that max by 16 (log2 units); one that does turns into
+    // inf, and the denominator the PV MFMA sums in its last row becomes inf or NaN (no rescale
+    // runs in such a scan, so nothing multiplies it back). Each wavefront tests its denominators
+    // after the scan; if any is not finite, the workgroup scans its context range again with the
+    // test on every step (pass 1, the lazy-rescale scan). The two scans do the same arithmetic
+    // otherwise. (The VALU-mode kernels scan once with the test on: at DP 64 the second pass's
+    // live state spills inside their loop and costs more than the test.)
+    __shared__ int rescan;
+    if (tid == 0) rescan = 0;  // ordered before its readers by the barriers of the scan
+    constexpr int PASSES = FOLD ? 2 : 1;
+    for (int pass = 0; pass < PASSES; ++pass) {
+    const bool checked_scan = !FOLD || pass == 1;
+    if (pass == 1) {
+#pragma unroll
+        for (int t = 0; t < G::VT; ++t) o[t][0] = o[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m_run = 0.0f;
+        l_run = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (16 * ks + 8 * hh + j == d) qf[ks][j] = (_Float16)0.0f;
+    }
     Raw<KVT> raw[NU];
     load_block(k_begin, raw);
     store_block(0, raw);
@@ -689,7 +721,8 @@ icl_attention_kernel(const Args a) {
                     __syncthreads();
                 }
             }
-            step(s_cur, kfr, st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn, kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH, blk * KB + 32 * st,
+            step(checked_scan || blk == 0, s_cur, kfr, st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn,
+                 kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH, blk * KB + 32 * st,
                  blk == 0 && st == 0);
             // K operands of the step after next: this block's rows, or the next block's (a
             // stale buffer after the last block, unused)
@@ -703,6 +736,15 @@ icl_attention_kernel(const Args a) {
             }
         }
         if constexpr (AHEAD == 2) __syncthreads();
+    }
+    if (checked_scan) break;
+    {
+        // the denominators sit in O^T row DP-1: tile VT-1, element 3 of lanes 48-63
+        const bool bad = lane >= 48 && !(__builtin_isfinite(o[G::VT - 1][0][3]) && __builtin_isfinite(o[G::VT - 1][1][3]));
+        if (__any(bad) && lane == 0) rescan = 1;
+    }
+    __syncthreads();  // every flag written; every read of the ring done before pass 1 restages it
+    if (!rescan) break;
     }
 
     // ---------------- epilogue: per query, its denominator and running max in the O^T layout

@@ -246,6 +246,37 @@ def test_key_norm_ramp_moves_the_max_late(cuda, d, nq):
     assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, 1)).all()
 
 
+@pytest.mark.parametrize("d", [44, 56])
+@pytest.mark.parametrize("lift", [11.0, 24.0])
+def test_late_key_above_the_anchored_max(cuda, d, lift):
+    # The folded kernels scan every block after the first without the per-step rescale test,
+    # keeping the running max the first block anchored, and rescan a work unit with the test
+    # on when a probability overflowed f16 on the way (its denominator turns inf/NaN). One key
+    # late in a 2048-row context (block 14 of 16) is lifted `lift` log2 units above the logits of
+    # every other key: 11 stays within f16 (probabilities up to 2^11 in the unchecked scan), 24
+    # overflows and must be rescanned. Either way the output is that key's value row, within the
+    # reference's bar, and the LSE within its rounding bound. d = 44 runs the prefetching
+    # 16-wave kernel, d = 56 the one that reads K operands just before their MFMAs.
+    bg, h, nq, nk = 2, 2, 300, 2048
+    scale = 1.0 / math.sqrt(d)
+    g = torch.Generator().manual_seed(61)
+    q0 = torch.randn(bg, 1, h, d, generator=g)
+    q = q0 + 0.05 * torch.randn(bg, nq, h, d, generator=g)
+    kv = 0.3 * torch.randn(bg, nk, 2, h, d, generator=g)
+    late = 1800
+    # q0 . k* = lift * ln 2 / scale for the late key: logit lift log2 units above ~0
+    kv[:, late, 0] = q0[:, 0] * (lift * math.log(2.0) / scale) / (q0[:, 0] ** 2).sum(-1, keepdim=True)
+    codes, scales = nori_amd.quantize_int8(kv.to(torch.float16).to(cuda))
+    q = q.to(torch.float16).to(cuda)
+    lse = torch.empty(bg, h, nq, device=cuda)
+    got = nori_amd.icl_attention(q, codes, scales, lse=lse)
+    values = codes.double() * scales.double()
+    exp, exp_lse = reference(q, values)
+    check(got, exp)
+    assert torch.isfinite(got).all() and torch.isfinite(lse).all()
+    assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, values, 1)).all()
+
+
 def test_merge_of_two_halves_equals_one_call(cuda):
     bg, h, nq, nk, d = 2, 4, 50, 300, 56
     kv = make_cache(bg, nk, 1, d, cuda, seed=31)
