@@ -18,11 +18,18 @@ cached path (src/synthefy_nori/api.py:158, 464-620, 862-968, 1122-1151, 1256-134
    linear quantile function (``quantile_dist_mean``, quantile_dist.py:95-135), its median, or
    quantiles at requested levels (api.py:1256-1345), and is mapped back to the target's units.
 
-What the reference does around this and this surface does not: the preprocessing ensemble
-of the inference config (one member here, on the raw numeric features), DataFrame /
-categorical / text feature handling, multi-target prediction, large-context policies and
-checkpoint download. A model comes from a local checkpoint (``model_path``, loaded without
-unpickling) or as a built ``FeaturesTransformer`` (``model=``).
+The rows go through the preprocessing ensemble of the inference configuration first
+(``nori_amd.ensemble``; by default the reference's eight members of
+configs/default_inference.json): every member builds its own feature matrices from the context
+and query rows, gets its own context cache, and the members' quantile banks are averaged
+(predictor.py:2972-3000, 3533) before the collapse. With ``augmentations=("yj",)`` (the
+default) a target whose skew exceeds ``yj_skew_threshold`` is also scored in Yeo-Johnson space
+and the two point predictions averaged (predictor.py:1880-1990).
+
+What the reference does around this and this surface does not: DataFrame / categorical-string /
+text feature handling, multi-target prediction, large-context policies and checkpoint download.
+A model comes from a local checkpoint (``model_path``, loaded without unpickling) or as a built
+``FeaturesTransformer`` (``model=``).
 """
 
 from __future__ import annotations
@@ -32,6 +39,7 @@ import math
 import numpy as np
 import torch
 
+from . import ensemble
 from .memory_policy import MemoryPolicy, estimate_cache_gb, warn_quantized
 from .transformer import FeaturesTransformer
 
@@ -155,27 +163,38 @@ class NoriRegressor:
 
     ``model_path``: a local checkpoint; ``model``: a built ``FeaturesTransformer`` (a name such
     as "nori-6m" needs the checkpoint download, which this build does not do). ``device``: a
-    ROCm GPU (the kernels have no CPU path). ``quantile_collapse``: "mean" (default) or
-    "median". ``memory_policy``: None, a preset ("exact", "max_context", "off"), a dict of
-    ``MemoryPolicy`` fields, or a ``MemoryPolicy``. ``mix_precision``: run the cached path
-    under fp16 autocast (the reference predictor's GPU default).
+    ROCm GPU (the kernels have no CPU path). ``inference_config``: the preprocessing ensemble,
+    a list of member dictionaries or a JSON path (None: the reference's default eight members;
+    ``[{}]`` scores the raw columns, constant ones dropped). ``augmentations``: ``("yj",)`` adds
+    the Yeo-Johnson target pass for targets skewed beyond ``yj_skew_threshold``; ``seed`` seeds
+    the members' steps. ``quantile_collapse``: "mean" (default) or "median". ``memory_policy``:
+    None, a preset ("exact", "max_context", "off"), a dict of ``MemoryPolicy`` fields, or a
+    ``MemoryPolicy``. ``mix_precision``: run the cached path under fp16 autocast (the reference
+    predictor's GPU default).
     """
 
-    def __init__(self, model_path: str | None = None, *, model=None, device=None, quantile_collapse: str = "mean",
+    def __init__(self, model_path: str | None = None, *, model=None, device=None, inference_config=None,
+                 augmentations=("yj",), yj_skew_threshold: float = 10.0, seed: int = 0, quantile_collapse: str = "mean",
                  memory_policy=None, mix_precision: bool = True):
         self.model_path = model_path
         self.model = model
         self.device = device
+        self.inference_config = inference_config
+        self.augmentations = tuple(augmentations) if augmentations else ()
+        self.yj_skew_threshold = float(yj_skew_threshold)
+        self.seed = int(seed)
         self.quantile_collapse = quantile_collapse
         self.memory_policy = memory_policy
         self.mix_precision = mix_precision
         self._net = None
-        self._context = None  # (cache key, x bytes, y bytes, ContextCache)
+        self._contexts = {}  # member slot -> (cache key, x bytes, y bytes, ContextCache)
         self._report = None
 
     # ------------------------------------------------------------------ sklearn surface
     def get_params(self, deep: bool = True) -> dict:
         return {"model_path": self.model_path, "model": self.model, "device": self.device,
+                "inference_config": self.inference_config, "augmentations": self.augmentations,
+                "yj_skew_threshold": self.yj_skew_threshold, "seed": self.seed,
                 "quantile_collapse": self.quantile_collapse, "memory_policy": self.memory_policy,
                 "mix_precision": self.mix_precision}
 
@@ -216,7 +235,7 @@ class NoriRegressor:
         self.y_mean_ = float(y_arr.mean())
         std = float(y_arr.std())
         self.y_std_ = std if std >= 1e-12 else 1.0
-        self._context = None
+        self._contexts = {}
         return self
 
     # ------------------------------------------------------------------ predict
@@ -242,17 +261,14 @@ class NoriRegressor:
         if x_test.shape[1] != self.n_features_in_:
             raise ValueError(f"X has {x_test.shape[1]} features, the context has {self.n_features_in_}")
         net = self._network()
-        bank = self._quantile_bank(net, x_test)  # [rows, K] in standardized target units, fp32
+        y_norm = ((self.y_train_ - self.y_mean_) / self.y_std_).astype(np.float32)
+        bank = self._ensemble_bank(net, x_test, y_norm)  # [rows, K] in standardized target units, fp32
         taus = torch.tensor(net.regression_quantiles, dtype=torch.float64, device=bank.device)
         if output_type in ("mean", "median", "mode"):
             collapse = self.quantile_collapse if output_type == "mean" else "median"
-            if collapse == "mean":
-                point = quantile_dist_mean(bank.double(), taus)
-            else:
-                ordered = torch.sort(bank.double(), dim=-1).values
-                mid = ordered.shape[-1] // 2
-                point = ordered[..., mid] if ordered.shape[-1] % 2 else ordered[..., mid - 1 : mid + 1].mean(-1)
-            return point.cpu().numpy() * self.y_std_ + self.y_mean_
+            point = self._collapse(bank, taus, collapse)
+            point = self._yeo_johnson_pass(net, x_test, y_norm, point, taus, collapse)
+            return point * self.y_std_ + self.y_mean_
         values = np.sort(bank.double().cpu().numpy() * self.y_std_ + self.y_mean_, axis=1)
         grid = taus.cpu().numpy()
         if output_type == "full":
@@ -261,6 +277,68 @@ class NoriRegressor:
         return _interpolated_quantiles(values, grid, levels)
 
     # ------------------------------------------------------------------ internals
+    @staticmethod
+    def _collapse(bank: torch.Tensor, taus: torch.Tensor, collapse: str) -> np.ndarray:
+        if collapse == "mean":
+            point = quantile_dist_mean(bank.double(), taus)
+        else:
+            ordered = torch.sort(bank.double(), dim=-1).values
+            mid = ordered.shape[-1] // 2
+            point = ordered[..., mid] if ordered.shape[-1] % 2 else ordered[..., mid - 1 : mid + 1].mean(-1)
+        return point.cpu().numpy()
+
+    def _ensemble_bank(self, net: FeaturesTransformer, x_test: np.ndarray, y_norm: np.ndarray, slot0: int = 0):
+        """The mean of the members' quantile banks (predictor.py:2972-3000, 3533): each member's
+        features from the context and query rows, scored through that member's context cache."""
+        config = ensemble.DEFAULT_MEMBERS if self.inference_config is None else self.inference_config
+        members = ensemble.build_members(config, self.seed, self.device_)
+        categorical = ensemble.categorical_columns(self.X_train_)
+        total = None
+        reused = True
+        quantized = None
+        for i, member in enumerate(members):
+            x_ctx, x_q, _ = member.features(self.X_train_, x_test, categorical, y_norm)
+            bank, was_reused, policy = self._quantile_bank(net, np.ascontiguousarray(x_ctx, dtype=np.float32),
+                                                           np.ascontiguousarray(x_q, dtype=np.float32), y_norm, slot0 + i)
+            reused &= was_reused
+            if policy.cache_dtype == "int8":
+                quantized = policy
+            total = bank if total is None else total + bank
+        self._report["context_reused"] = reused
+        self._report["ensemble_members"] = len(members)
+        if quantized is not None:
+            warn_quantized(quantized)  # once per predict, as the reference warns once per call
+        return total / len(members)
+
+    def _yeo_johnson_pass(self, net, x_test, y_norm, point, taus, collapse) -> np.ndarray:
+        """With "yj" among the augmentations and a target skew (unbiased) of at least
+        ``yj_skew_threshold`` in magnitude: the ensemble again on the Yeo-Johnson-transformed
+        target, its point prediction clipped to the transformed context range +/- 3 widths and
+        mapped back, averaged with the plain one (rows whose inverse is not finite keep the plain
+        one) -- predictor.py:1880-1990."""
+        if "yj" not in self.augmentations:
+            return point
+        from scipy import stats
+        from sklearn.preprocessing import PowerTransformer
+
+        y = np.asarray(y_norm, dtype=np.float64)
+        y = y[np.isfinite(y)]
+        if len(y) < 10:
+            return point
+        skew = float(stats.skew(y, bias=False))
+        if not np.isfinite(skew) or abs(skew) < self.yj_skew_threshold:
+            return point
+        pt = PowerTransformer(method="yeo-johnson", standardize=True)
+        y_yj = pt.fit_transform(np.asarray(y_norm, dtype=np.float64).reshape(-1, 1)).ravel()
+        bank = self._ensemble_bank(net, x_test, y_yj.astype(np.float32), slot0=1000)
+        p_yj = self._collapse(bank, taus, collapse)
+        lo, hi = y_yj.min(), y_yj.max()
+        width = (hi - lo) * 3.0 + 1e-6
+        back = pt.inverse_transform(np.clip(p_yj, lo - width, hi + width).reshape(-1, 1)).ravel()
+        bad = ~np.isfinite(back)
+        back[bad] = point[bad]
+        return 0.5 * (point + back)
+
     def _network(self) -> FeaturesTransformer:
         if self._net is None:
             if isinstance(self.model, FeaturesTransformer):
@@ -289,19 +367,21 @@ class NoriRegressor:
         return policy.resolve(est_cache_gb=est, bytes_per_element=compute_bytes,
                               head_dim=net.embed_dim // net.nhead, total_vram_gb=vram)
 
-    def _quantile_bank(self, net: FeaturesTransformer, x_test: np.ndarray) -> torch.Tensor:
+    def _quantile_bank(self, net: FeaturesTransformer, x_ctx: np.ndarray, x_test: np.ndarray, y_norm: np.ndarray,
+                       slot: int) -> tuple[torch.Tensor, bool]:
+        """One member's bank: its context cache (built, or the one an earlier call built from the
+        same bytes) applied to its query rows."""
         dev = self.device_
         if dev.type != "cuda":
             raise RuntimeError("NoriRegressor runs on a ROCm GPU: the nori_amd kernels have no CPU path")
         amp = bool(self.mix_precision)
-        n_groups = math.ceil(self.n_features_in_ / net.features_per_group) + 1
+        n_groups = math.ceil(x_ctx.shape[1] / net.features_per_group) + 1
         policy = self._policy(net, n_groups, 2 if amp else 4)
         if not policy.cache:
             raise NotImplementedError(
                 f"memory policy resolved to rung {policy.rung!r}: the uncached forward is not part of this build; "
                 "allow the cache (the int8 rungs hold about 1.9x more context than bf16)"
             )
-        y_norm = ((self.y_train_ - self.y_mean_) / self.y_std_).astype(np.float32)
         build = dict(cache_dtype=policy.cache_dtype, offload_kv_cache=policy.offload_to_host,
                      fit_row_chunk=policy.context_row_chunk)
         streaming = policy.rung.startswith("stream_")
@@ -309,33 +389,32 @@ class NoriRegressor:
             build["stream_context"] = True
         key = (tuple(sorted(build.items())), amp, str(dev))
         with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16, enabled=amp):
-            context = self._reused_context(key, y_norm) if policy.reuse_context_cache and not streaming else None
+            context = self._reused_context(slot, key, x_ctx, y_norm) if policy.reuse_context_cache and not streaming \
+                else None
             reused = context is not None
             if context is None:
                 home = torch.device("cpu") if streaming else dev
-                xc = torch.from_numpy(self.X_train_).to(home)[None]
+                xc = torch.from_numpy(x_ctx).to(home)[None]
                 yc = torch.from_numpy(y_norm).to(home)[None]
                 context = net.build_context_cache(xc, yc, **build)
-                self._context = (key, self.X_train_.tobytes(), y_norm.tobytes(), context) if policy.reuse_context_cache \
-                    and not streaming else None
+                if policy.reuse_context_cache and not streaming:
+                    self._contexts[slot] = (key, x_ctx.tobytes(), y_norm.tobytes(), context)
             xq = torch.from_numpy(x_test).to(torch.device("cpu") if streaming else dev)[None]
             bank = net.apply_context_cache(xq, context)[0].float()
         if not bool(torch.isfinite(bank).all()):
             raise RuntimeError("the model produced non-finite predictions")  # predictor.py:731-765
         self._report = policy.with_outcome(query_chunk=int(x_test.shape[0])).as_report()
-        self._report["context_reused"] = reused
-        if policy.cache_dtype == "int8":
-            warn_quantized(policy)
-        return bank
+        return bank, reused, policy
 
-    def _reused_context(self, key, y_norm: np.ndarray):
-        """The context encoded by an earlier call, when its cache parameters and its context rows
-        and targets are byte for byte the ones of this call."""
-        if self._context is None:
+    def _reused_context(self, slot: int, key, x_ctx: np.ndarray, y_norm: np.ndarray):
+        """The context a member encoded in an earlier call, when its cache parameters, its context
+        features and its targets are byte for byte the ones of this call."""
+        held = self._contexts.get(slot)
+        if held is None:
             return None
-        k, xb, yb, context = self._context
-        if k == key and xb == self.X_train_.tobytes() and yb == y_norm.tobytes():
+        k, xb, yb, context = held
+        if k == key and xb == x_ctx.tobytes() and yb == y_norm.tobytes():
             return context
-        self._context = None
+        del self._contexts[slot]
         return None
 

@@ -1,0 +1,241 @@
+"""The preprocessing ensemble in front of NoriRegressor (nori_amd.ensemble), on the CPU.
+
+The reference's module (src/synthefy_nori/inference/preprocess.py) cannot be imported here: it
+imports ``kditransform``, which this image does not have, so no member's features could be
+written as golden vectors from the reference itself. Each step is pinned instead by what fixes
+it independently of this code: the default configuration against the reference's own
+configuration file (tests/golden/default_inference_members.json), the seed draws against
+Python's and numpy's generators as the reference calls them, the column operations by closed
+forms (which columns a step keeps, which products it forms, what a permutation does), the
+distribution steps by the sklearn / scipy routines the reference builds them from, and the
+SVD block by the decomposition's own identities. End to end, a member's features are parity
+unpinned against the reference.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import random
+
+import numpy as np
+import pytest
+from scipy import stats
+from sklearn.preprocessing import QuantileTransformer
+
+import regressor_case as case
+from nori_amd import ensemble as en
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "default_inference_members.json")
+
+
+def test_default_members_are_the_reference_configuration():
+    with open(GOLDEN) as f:
+        assert json.loads(json.dumps(list(en.DEFAULT_MEMBERS), sort_keys=True)) == json.load(f)
+
+
+def test_seed_slots_follow_the_reference_draws():
+    members = en.build_members(en.DEFAULT_MEMBERS, 7, "cpu")
+    draw = random.Random(7)
+    seeds = [draw.randint(0, 10000) for _ in range(8 * en.SEED_SLOTS)]
+    for i, m in enumerate(members):
+        slots = seeds[i * en.SEED_SLOTS:(i + 1) * en.SEED_SLOTS]
+        kinds = [type(s).__name__ for s in m.steps]
+        assert kinds == ["WideTableProjection", "FeatureCap", "PairProducts", "DropConstantColumns", "Redistribute",
+                         "CategoryCodes", "RowFingerprint", "ColumnOrder"]
+        # the projection takes the last slot; the others their position among the rest
+        assert m.seeds == [slots[9]] + slots[:7]
+    g = np.random.default_rng(7)
+    start = g.integers(0, 1000)
+    shifts = g.choice(list(range(start, start + 8)), size=8, replace=False)
+    assert [m.steps[-1].offset for m in members] == [int(v) for v in shifts]
+    with pytest.raises(ValueError):
+        en.build_members([], 0, "cpu")
+
+
+def test_drop_constant_columns():
+    x = np.array([[1.0, 2.0, np.nan, 5.0, np.nan], [1.0, 3.0, np.nan, 5.0, 1.0], [1.0, 4.0, np.nan, 6.0, 2.0]])
+    step = en.DropConstantColumns()
+    cat = step.fit(x, [0, 3, 4], 0)
+    out, cat_out = step.apply(x)
+    # column 0 constant, column 2 all NaN; column 4 keeps its NaN in row 0 (NaN != NaN)
+    np.testing.assert_array_equal(out, x[:, [1, 3, 4]])
+    assert cat == cat_out == [1, 2]
+    with pytest.raises(ValueError, match="All features are constant"):
+        en.DropConstantColumns().fit(np.ones((4, 3)), [], 0)
+
+
+def test_feature_cap():
+    x = np.arange(60.0).reshape(3, 20)
+    step = en.FeatureCap(max_features=8)
+    cat = step.fit(x, [1, 5, 19], 11)
+    keep = np.sort(np.random.default_rng(11).choice(20, size=8, replace=False))
+    np.testing.assert_array_equal(step.apply(x)[0], x[:, keep])
+    assert cat == sorted(list(keep).index(c) for c in (1, 5, 19) if c in keep)
+    small = en.FeatureCap(max_features=50)
+    small.fit(x, [], 0)
+    np.testing.assert_array_equal(small.apply(x)[0], x)
+
+
+@pytest.mark.parametrize("p", [1, 3, 4, 9])
+def test_pair_products(p):
+    g = np.random.default_rng(p)
+    x = g.standard_normal((40, p)).astype(np.float32) * np.arange(1, p + 1, dtype=np.float32)
+    step = en.PairProducts(max_interaction_features=10)
+    step.fit(x, [], 123)
+    out, _ = step.apply(x)
+    scaled = x / x.std(axis=0)  # StandardScaler without centering: population std
+    np.testing.assert_allclose(out[:, :p], scaled, rtol=1e-5)
+    count = min(10, p * (p + 1) // 2)
+    assert out.shape[1] == p + count
+    pairs = list(zip(step.first.tolist(), step.second.tolist()))
+    assert all(a <= b for a, b in pairs) and len(set(pairs)) == count
+    if count == p * (p + 1) // 2:  # every pair a <= b is taken when there are at most 10
+        assert set(pairs) == {(a, b) for a in range(p) for b in range(a, p)}
+    for k, (a, b) in enumerate(pairs):
+        np.testing.assert_allclose(out[:, p + k], scaled[:, a] * scaled[:, b], rtol=1e-4, atol=1e-6)
+
+
+def test_column_order():
+    x = np.arange(24.0).reshape(2, 12)
+    step = en.ColumnOrder(mode="shuffle", offset=5)
+    cat = step.fit(x, [0, 7], 99)
+    perm = np.random.default_rng(99).permutation(12)
+    np.testing.assert_array_equal(step.apply(x)[0], x[:, perm])
+    assert cat == sorted(int(np.where(perm == c)[0][0]) for c in (0, 7))
+    rot = en.ColumnOrder(mode="rotate", offset=5)
+    rot.fit(x, [], 0)
+    np.testing.assert_array_equal(rot.apply(x)[0], x[:, np.roll(np.arange(12), 5)])
+
+
+def test_quantile_member_blocks():
+    # original columns, their capped uniform quantile transform, then the SVD of the mean-imputed
+    # columns scaled to unit variance
+    g = np.random.default_rng(3)
+    n, p = 300, 6
+    x = g.standard_normal((n, p)) * np.array([1, 2, 3, 4, 5, 6]) + 10
+    step = en.Redistribute(worker_tags=["quantile_uniform_all_data"], original_flag=True, svd_tag="svd", device="cpu")
+    step.fit(x, [], 42)
+    out, cat = step.apply(x)
+    k = max(1, min(n // 10 + 1, p // 2))
+    assert out.shape == (n, 2 * p + k) and cat == []
+    np.testing.assert_array_equal(out[:, :p], x)
+    qt = QuantileTransformer(output_distribution="uniform", n_quantiles=min(n // 5, n, 256), subsample=n,
+                             random_state=42).fit(x)
+    np.testing.assert_allclose(out[:, p:2 * p], qt.transform(x), rtol=0, atol=1e-12)
+    assert (out[:, p:2 * p] >= 0).all() and (out[:, p:2 * p] <= 1).all()
+    # the SVD block: U * S of the scaled matrix, components orthonormal, each component's
+    # largest |U| entry positive
+    scaled = np.hstack([x, qt.transform(x)])
+    scaled = scaled / scaled.std(axis=0)
+    svd = out[:, 2 * p:]
+    comps = step.worker.named_steps["svd_worker"].transformer_list[1][1].named_steps["svd"].components_
+    np.testing.assert_allclose(comps @ comps.T, np.eye(k), atol=1e-10)
+    np.testing.assert_allclose(svd, scaled @ comps.T, rtol=1e-9, atol=1e-9)
+    u = svd / np.linalg.norm(svd, axis=0)
+    assert all(u[np.argmax(np.abs(u[:, j])), j] > 0 for j in range(k))
+    sv = np.linalg.svd(scaled, compute_uv=False)[:k]
+    np.testing.assert_allclose(np.linalg.norm(svd, axis=0), sv, rtol=1e-9)
+
+
+def test_per_column_kinds():
+    g = np.random.default_rng(8)
+    n = 2500
+    cols = {
+        "ordinal": g.integers(0, 5, n).astype(float),
+        "normal": g.standard_normal(n),
+        "positive_heavy_skew": g.pareto(1.5, n),
+        "skewed_pos_01": g.beta(0.3, 6.0, n),
+        "skewed": g.standard_normal(n) - 10.0 * (g.random(n) < 0.3),
+        "other": g.standard_normal(n) + 6.0 * (g.random(n) < 0.5),
+    }
+    for want, col in cols.items():
+        assert en.PerColumnTransform.kind(col) == want, want
+    # the fitted transforms: standardized Yeo-Johnson for the negative skewed column, identity
+    # for the normal one; fit rows capped at 2000 by a seeded draw
+    x = np.stack([cols["normal"], cols["skewed"]], axis=1)
+    t = en.PerColumnTransform(random_state=4, n_quantiles=max(n // 10, 2)).fit(x)
+    out = t.transform(x)
+    np.testing.assert_array_equal(out[:, 0], x[:, 0])
+    rows = np.random.default_rng(4).choice(n, size=2000, replace=False)
+    lam = stats.yeojohnson(x[rows, 1])[1]
+    yj = stats.yeojohnson(x[:, 1], lmbda=lam)
+    ref = (yj - stats.yeojohnson(x[rows, 1], lmbda=lam).mean()) / stats.yeojohnson(x[rows, 1], lmbda=lam).std()
+    np.testing.assert_allclose(out[:, 1], ref, rtol=1e-3, atol=1e-3)
+
+
+def test_category_codes():
+    g = np.random.default_rng(2)
+    n = 400
+    levels = np.array([7.0, 3.0, 11.0])
+    x = np.stack([g.standard_normal(n), levels[g.integers(0, 3, n)], g.standard_normal(n)], axis=1)
+    step = en.CategoryCodes(encoding_strategy="ordinal_strict_feature_shuffled")
+    cat = step.fit(x, [1], 17)
+    out, cat_out = step.apply(x)
+    assert cat == cat_out == [0]
+    perm = np.random.default_rng(17).permutation(3)
+    code = np.searchsorted(np.sort(levels), x[:, 1])  # OrdinalEncoder: sorted levels
+    np.testing.assert_array_equal(out[:, 0], perm[code])
+    np.testing.assert_array_equal(out[:, 1:], x[:, [0, 2]])
+    # a column whose rarest level has fewer than 10 rows is not encoded
+    x2 = x.copy()
+    x2[:5, 1] = 99.0
+    step2 = en.CategoryCodes(encoding_strategy="ordinal_strict_feature_shuffled")
+    assert step2.fit(x2, [1], 17) == []
+    np.testing.assert_array_equal(step2.apply(x2)[0], x2)
+
+
+def test_row_fingerprint():
+    g = np.random.default_rng(6)
+    x = g.standard_normal((50, 4))
+    x[10] = x[3]  # a duplicate context row
+    step = en.RowFingerprint()
+    step.fit(x, [2], 31)
+    salt = int(np.random.default_rng(31).integers(0, 65536))
+    out, cat = step.apply(x, is_test=False)
+    fp = out[:, -1]
+    assert cat == [2] and np.array_equal(out[:, :4], x)
+    assert len(np.unique(fp)) == 50 and ((fp >= 0) & (fp < 1)).all()
+
+    def h(row):
+        return (int(hashlib.sha256(row.tobytes()).hexdigest(), 16) % 10**12) / 10**12
+
+    assert fp[0] == h(x[0] + salt)
+    q, _ = step.apply(x[:5], is_test=True)
+    assert q[0, -1] == h(x[0] + salt + salt)  # query rows are salted twice and keep their hash
+
+
+def test_members_on_config1_table():
+    x_tr, y_tr, x_te, _ = case.table()
+    y = ((y_tr - y_tr.mean()) / y_tr.std()).astype(np.float32)
+    members = en.build_members(en.DEFAULT_MEMBERS, 0, "cpu")
+    assert en.categorical_columns(x_tr) == []
+    for i, m in enumerate(members):
+        a, b, cat = m.features(x_tr, x_te, [], y)
+        # 16 columns + 10 products; quantile members keep the originals, add their transform
+        # and a 13-column SVD block; adaptive members transform in place; + 1 fingerprint
+        assert a.shape == (1024, 66 if i < 4 else 27) and b.shape == (256, a.shape[1]) and cat == []
+        assert np.isfinite(a).all() and np.isfinite(b).all()
+    raw = en.build_members([{}], 0, "cpu")[0]
+    a, b, _ = raw.features(x_tr, x_te, [], y)
+    np.testing.assert_array_equal(a, x_tr)
+    np.testing.assert_array_equal(b, x_te)
+
+
+def test_wide_table_projection_gate():
+    g = np.random.default_rng(1)
+    narrow = g.standard_normal((60, 20))
+    step = en.WideTableProjection(strategy="svd_all", n_features_threshold=256, binary_threshold=1.01,
+                                  svd_components=512, svd_rows_per_component=3, device="cpu")
+    assert step.fit(narrow, [3], 5) == [3]
+    assert step.apply(narrow)[0] is narrow
+    wide = g.standard_normal((90, 300))
+    step.fit(wide, [], 5)
+    out, cat = step.apply(wide)
+    k = min(512, 299, 89, 90 // 3)
+    assert out.shape == (90, k) and cat == []
+    sv = np.linalg.svd(wide, compute_uv=False)[:k]
+    np.testing.assert_allclose(np.linalg.norm(out, axis=0), sv, rtol=1e-4)
+    with pytest.raises(NotImplementedError):
+        en.WideTableProjection(strategy="corr")

@@ -31,6 +31,9 @@ from parity import PREDICTION_BAR, check_relative
 pytestmark = pytest.mark.gpu
 
 AUTOCAST_BAR = 1.5e-2  # fp16 autocast against the fp32 reference run
+# The golden is the reference's context-cache API on the raw columns: a one-member inference
+# configuration with no steps (only constant columns dropped; config 1 has none).
+RAW = [{}]
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "regressor_goldens.npz")
 
@@ -58,7 +61,8 @@ def spread_note(got, exp, what):
 def test_predictions_match_the_reference(gold, model, cuda, mix_precision):
     tag = "fp16 autocast" if mix_precision else "fp32"
     bar = AUTOCAST_BAR if mix_precision else PREDICTION_BAR
-    reg = api.NoriRegressor(model=model, device=cuda, memory_policy="max_context", mix_precision=mix_precision)
+    reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, memory_policy="max_context",
+                            mix_precision=mix_precision)
     reg.fit(gold["case/x_train"], gold["case/y_train"])
     with warnings.catch_warnings(record=True) as caught:
         warnings.simplefilter("always")
@@ -88,7 +92,8 @@ def test_predictions_match_the_reference(gold, model, cuda, mix_precision):
 
 def test_int8_cache_codes_and_context_reuse(gold, model, cuda):
     # fp32, as the reference's CPU run: the K/V the codes come from are then fp32 on both sides
-    reg = api.NoriRegressor(model=model, device=cuda, memory_policy={"cache_dtype": "int8"}, mix_precision=False)
+    reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, memory_policy={"cache_dtype": "int8"},
+                            mix_precision=False)
     reg.fit(gold["case/x_train"], gold["case/y_train"])
     first = reg.predict(gold["case/x_test"])
     assert reg.memory_report_["context_reused"] is False
@@ -98,7 +103,7 @@ def test_int8_cache_codes_and_context_reuse(gold, model, cuda):
     # layer 0's int8 codes: the K/V of the context's first layer come from the inputs through one
     # norm and one projection; device and host sums differ in order, so a code may sit one step
     # away where a value lies on a rounding boundary
-    codes, scales = reg._context[3].caches[0]["seq_kv"].device_payload()
+    codes, scales = reg._contexts[0][3].caches[0]["seq_kv"].device_payload()
     d = codes[:, :128].cpu().numpy().astype(np.int32) - gold["case/codes0"].astype(np.int32)
     print(f"[parity] layer-0 int8 codes: {np.mean(d != 0):.2e} differ by one, max {np.abs(d).max()}", flush=True)
     assert np.abs(d).max() <= 1 and np.mean(d != 0) < 0.01
@@ -111,7 +116,8 @@ def test_int8_cache_codes_and_context_reuse(gold, model, cuda):
 
 def test_bf16_rung_and_exact_preset(gold, model, cuda):
     for policy, rung, dtype in ((None, "resident_bf16", "bf16"), ("exact", "resident_bf16", "bf16")):
-        reg = api.NoriRegressor(model=model, device=cuda, memory_policy=policy, mix_precision=False)
+        reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, memory_policy=policy,
+                                mix_precision=False)
         reg.fit(gold["case/x_train"], gold["case/y_train"])
         with warnings.catch_warnings():
             warnings.simplefilter("error", CacheQuantizedWarning)  # the full-precision rung does not quantize
@@ -119,3 +125,46 @@ def test_bf16_rung_and_exact_preset(gold, model, cuda):
         assert reg.memory_report_["rung"] == rung and reg.memory_report_["cache_dtype"] == dtype
         # the int8 golden against the full-precision cache: the int8 rounding is inside the bar
         check_relative(point, gold["case/point"], PREDICTION_BAR, f"nori-6m point predictions, {rung} cache")
+
+
+def test_default_ensemble_members(gold, model, cuda):
+    # the reference's default inference configuration: eight members, each with its own
+    # features and context cache, banks averaged; every member's context is reused by a second
+    # call on the same context, which then returns the same predictions
+    reg = api.NoriRegressor(model=model, device=cuda, memory_policy={"cache_dtype": "int8"})
+    reg.fit(gold["case/x_train"], gold["case/y_train"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", CacheQuantizedWarning)
+        first = reg.predict(gold["case/x_test"])
+        assert reg.memory_report_["ensemble_members"] == 8 and reg.memory_report_["context_reused"] is False
+        second = reg.predict(gold["case/x_test"])
+        assert reg.memory_report_["context_reused"] is True
+        qs = reg.predict(gold["case/x_test"], output_type="quantiles", quantiles=[0.1, 0.5, 0.9])
+    assert np.all(np.isfinite(first)) and np.array_equal(first, second)
+    assert np.all(np.diff(qs, axis=0) >= 0)
+    # the raw-column member is not the ensemble: the members' features differ from the raw ones
+    raw = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, memory_policy={"cache_dtype": "int8"})
+    raw.fit(gold["case/x_train"], gold["case/y_train"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", CacheQuantizedWarning)
+        assert not np.allclose(raw.predict(gold["case/x_test"]), first)
+
+
+def test_yeo_johnson_pass_on_a_skewed_target(gold, model, cuda):
+    # a target with skew above the threshold adds the Yeo-Johnson pass: its point predictions
+    # differ from the plain pass's and stay finite; below the threshold nothing changes
+    x_tr, x_te = gold["case/x_train"], gold["case/x_test"]
+    rng = np.random.default_rng(5)
+    y_skewed = np.exp(3.0 * rng.standard_normal(len(x_tr)))
+    out = {}
+    for aug in ((), ("yj",)):
+        reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, augmentations=aug,
+                                memory_policy={"cache_dtype": "int8"}, mix_precision=False)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore", CacheQuantizedWarning)
+            out[aug] = reg.fit(x_tr, y_skewed).predict(x_te)
+            if aug:
+                plain = reg.fit(x_tr, gold["case/y_train"]).predict(x_te)
+                reg.augmentations = ()
+                assert np.array_equal(plain, reg.predict(x_te))
+    assert np.all(np.isfinite(out[("yj",)])) and not np.allclose(out[()], out[("yj",)])
