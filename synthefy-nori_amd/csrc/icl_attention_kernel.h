@@ -242,14 +242,21 @@ struct Geometry {
     // f16 per V row: the transposed reads of a 16-lane group take 32 bytes from each of 4
     // rows, which land in distinct banks when the row stride is an odd multiple of 32 bytes
     static constexpr int VPITCH = DP % 32 == 0 ? DP + 16 : DP;
+    // A transposed read serves 32 lanes at a time from the 64 banks (256 bytes): lanes 0-15
+    // read rows 0-3 (+4: 4-7) of a 32-row step and lanes 16-31 rows 16-19 (20-23), and
+    // 16 * VPITCH bytes is a multiple of 256, so rows 16-31 of every step sit 128 bytes
+    // further on (4 * VPITCH bytes is 128 modulo 256: they take the banks of rows 4-7).
+    static constexpr int VSTEP = 32 * VPITCH + 64;  // f16 per 32-row step of a V buffer
     static constexpr int KBUF = KB * KPITCH;
-    static constexpr int VBUF = KB * VPITCH;
+    static constexpr int VBUF = (KB / 32) * VSTEP;
+    // f16 offset of row r of a V buffer
+    static constexpr __host__ __device__ int vrow(int r) { return (r >> 5) * VSTEP + (r & 31) * VPITCH + ((r & 16) ? 64 : 0); }
     // LDS buffers in the K/V ring: three let a block be staged while the previous block's V
     // and the next block's K are both being read (one barrier per block); wide heads, whose
     // buffers are large, use two and a second barrier. The budget keeps two 8-wave or three
     // 5-wave workgroups on a CU (a 16-wave workgroup has the CU to itself).
     static constexpr int BUF_BYTES = (KBUF + VBUF) * 2 + KB * 4;
-    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : (NW == 5 ? 52 : 64)) * 1024 ? 3 : 2;
+    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : (NW == 5 ? 52 : 72)) * 1024 ? 3 : 2;
 };
 
 // Shapes with a 16-wave workgroup: narrow heads, where 32 query rows per wavefront fit in
@@ -327,7 +334,7 @@ icl_attention_kernel(const Args a) {
         if (col >= d) {
             *reinterpret_cast<u32x2*>(&Ks[(row / KB) * G::KBUF + (row % KB) * G::KPITCH + col]) =
                 u32x2{(FOLD && col == d) ? 0x3c00u : 0u, 0u};
-            *reinterpret_cast<u32x2*>(&Vs[(row / KB) * G::VBUF + (row % KB) * G::VPITCH + col]) =
+            *reinterpret_cast<u32x2*>(&Vs[(row / KB) * G::VBUF + G::vrow(row % KB) + col]) =
                 u32x2{0u, (FOLD && col == DP - 4) ? 0x3c000000u : 0u};
         }
     }
@@ -381,7 +388,7 @@ icl_attention_kernel(const Args a) {
         u_c0[u] = c == 0;
         u_off[u] = row * row_bytes + (uint32_t)(((half ? a.kv_half : 0) + hk * d + 16 * c) * ES);
         u_soff[u] = row * srow_bytes + (uint32_t)(((half ? a.sc_half : 0) + hk) * 4);
-        u_lds[u] = (uint32_t)(row * (half ? G::VPITCH : G::KPITCH) + 16 * c);
+        u_lds[u] = (uint32_t)((half ? G::vrow(row) : row * G::KPITCH) + 16 * c);
     }
     const char* kv_bg_base = reinterpret_cast<const char*>(a.kv) + b * a.kv_bg * ES;
     const char* sc_bg_base = reinterpret_cast<const char*>(a.kvs) + b * a.sc_bg * 4;
@@ -477,7 +484,7 @@ icl_attention_kernel(const Args a) {
     // sigma(g, j) = 16(g%2) + 4(g/2) + 8(j/4) + j%4 -- the key the swapped probability
     // registers hold in that slot. The second read (slots 4..7) is 8 key rows further.
     const int vg = lane >> 4, vt = lane & 15;
-    const int v_lane = (16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) * G::VPITCH + 4 * (vt & 3);
+    const int v_lane = G::vrow(16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) + 4 * (vt & 3);
     const lds_f16* const KsL = (const lds_f16*)Ks;
     const lds_f16* const VsL = (const lds_f16*)Vs;
     auto read_v = [&](const lds_f16* Vl, f16x8 (&vf)[G::VT]) {
@@ -722,7 +729,7 @@ icl_attention_kernel(const Args a) {
                 }
             }
             step(checked_scan || blk == 0, s_cur, kfr, st + 1 < G::SPB ? Kc + 32 * (st + 1) * G::KPITCH : Kn,
-                 kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + 32 * st * G::VPITCH, blk * KB + 32 * st,
+                 kf + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st), Vc + st * G::VSTEP, blk * KB + 32 * st,
                  blk == 0 && st == 0);
             // K operands of the step after next: this block's rows, or the next block's (a
             // stale buffer after the last block, unused)
