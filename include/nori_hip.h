@@ -195,6 +195,24 @@ int nori_silu_mul(const void* gu, int dtype, int64_t rows, int32_t hidden, int64
                   int64_t out_row_stride, void* stream);
 
 /*
+ * The whole SwiGLU feed-forward sublayer in one kernel, for fp16 rows (the fp16-autocast
+ * SwiGLUMLP.forward, src/synthefy_nori/model/layer.py:261-274, without biases):
+ *     y[r] = T(T(T(silu(T(x[r] Wg^T))) * T(x[r] Wu^T)) Wd^T)
+ * with T the rounding to fp16 and fp32 sums. x: [rows, width] at x_row_stride elements;
+ * w_gate_up: [2 * hidden, width] contiguous, the gate rows then the up rows; w_down:
+ * [width, hidden] contiguous; y: [rows, width] at y_row_stride. width (the sublayer's in and
+ * out features) is 128, 256 or 352; hidden is the gate/up width padded to a multiple of 8
+ * with zero gate/up rows and zero down columns. Strides are multiples of 8 and the four
+ * pointers 16-byte aligned. The projections sum in their own order (a value may differ from
+ * the unfused GEMMs by one fp16 ulp) and silu uses the hardware exp2 and reciprocal; the
+ * hidden activations never leave the CU. Other widths or dtypes: NORI_ERR_UNSUPPORTED
+ * (the caller keeps the unfused projections and nori_silu_mul).
+ */
+int nori_swiglu_mlp(const void* x, int dtype, int64_t rows, int32_t width, int64_t x_row_stride,
+                    const void* w_gate_up, const void* w_down, int32_t hidden, void* y, int64_t y_row_stride,
+                    void* stream);
+
+/*
  * What the two-phase encoder's attentions do to q and k between the projection and the
  * attention (layer.py:1122-1134 with qk_norm and QASS "log_only", layer.py:433-456), applied
  * by nori_icl_attention_qk to each query row and key row as it is loaded:

@@ -38,7 +38,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention, short_context
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
-from .norm import RMSNorm, projection_operand, rms_norm_, silu_mul
+from .norm import FUSED_MLP_WIDTHS, RMSNorm, projection_operand, rms_norm_, silu_mul, swiglu_mlp
 
 ACTIVATION_FN = {"gelu": nn.GELU(), "relu": nn.ReLU(), "silu": nn.SiLU()}
 _SDPA_BACKENDS_WITHOUT_CUDNN = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]
@@ -102,6 +102,10 @@ class QASSMaxScaling(nn.Module):
 class SwiGLUMLP(nn.Module):
     """(SiLU(x W_gate) * x W_up) W_down (reference layer.py:261-274)."""
 
+    # fp16 sublayers of a width the fused kernel covers run as one HIP kernel; False keeps the
+    # stacked projection, nori_silu_mul and the down projection
+    fused = True
+
     def __init__(self, in_features, hidden_size, out_features, has_bias, device, dtype):
         super().__init__()
         hidden = int(2 * hidden_size / 3)
@@ -118,6 +122,18 @@ class SwiGLUMLP(nn.Module):
         # The hidden width is padded to a multiple of 8 with zero gate/up rows and zero down
         # columns, so every row is 16-byte aligned; the padding contributes exact zeros.
         gate_up, gate_up_bias, down, hidden = self._stacked_weights(x)
+        width = x.shape[-1]
+        if (
+            self.fused
+            and gate_up.dtype == torch.float16
+            and gate_up_bias is None
+            and self.w_down.bias is None
+            and width == self.w_down.out_features
+            and width in FUSED_MLP_WIDTHS
+        ):
+            # the whole sublayer in one kernel: its operand as the projections would take it
+            # (autocast casts to fp16), the hidden activations kept on the CU
+            return swiglu_mlp(x.to(torch.float16), gate_up, down, hidden)
         gu = nn.functional.linear(x, gate_up, gate_up_bias)
         return nn.functional.linear(silu_mul(gu, hidden), down, self.w_down.bias)
 

@@ -295,6 +295,37 @@ def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMS
     return out
 
 
+# Widths (in = out features) the fused SwiGLU kernel is built for.
+FUSED_MLP_WIDTHS = (128, 256, 352)
+
+
+def swiglu_mlp(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, hidden: int) -> torch.Tensor:
+    """The whole fp16 SwiGLU feed-forward ``(silu(x Wg^T) * (x Wu^T)) Wd^T`` in one HIP kernel
+    (``nori_swiglu_mlp``): ``gate_up`` [2 * hidden, width] (gate rows, then up rows) and
+    ``down`` [width, hidden], fp16 and contiguous, ``hidden`` padded to a multiple of 8 with
+    zero rows/columns; x [..., width] fp16 with width in FUSED_MLP_WIDTHS. SwiGLUMLP.forward
+    under fp16 autocast (layer.py:261-274) without writing the hidden activations out."""
+    width = x.shape[-1]
+    if gate_up.shape != (2 * hidden, width) or down.shape != (width, hidden):
+        raise ValueError(
+            f"swiglu_mlp: weights {tuple(gate_up.shape)} / {tuple(down.shape)} do not match width {width}, hidden {hidden}"
+        )
+    device = nat.require_device(x, gate_up, down)
+    x2 = x.reshape(-1, width)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    gate_up, down = gate_up.contiguous(), down.contiguous()
+    out = torch.empty((x2.shape[0], width), dtype=x.dtype, device=device)
+    nat.check(
+        nat.lib().nori_swiglu_mlp(
+            x2.data_ptr(), nat.dtype_code(x.dtype), x2.shape[0], width, x2.stride(0), gate_up.data_ptr(),
+            down.data_ptr(), hidden, out.data_ptr(), width, nat.stream_of(device),
+        ),
+        "swiglu_mlp",
+    )
+    return out.view(*x.shape[:-1], width)
+
+
 def silu_mul(gu: torch.Tensor, hidden: int) -> torch.Tensor:
     """``F.silu(gu[..., :hidden]) * gu[..., hidden:]`` for the [gate | up] output of a stacked
     projection, in gu's dtype with torch's rounding of the two ops, one HIP pass

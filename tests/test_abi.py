@@ -34,6 +34,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_rms_norm_to",
             "nori_residual_add",
             "nori_silu_mul",
+            "nori_swiglu_mlp",
             "nori_residual_add_rms_norm",
             "nori_icl_attention",
             "nori_icl_attention_qk",
@@ -99,6 +100,20 @@ def test_argument_errors_map_to_reference_exceptions():
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F32, 3, 5, 44, 1) == 15 * 64 * 2
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 0) == 0
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 1) == 15 * 64 * 2
+    # fused SwiGLU feed-forward: fp16 only, widths 128 / 256 / 352, hidden a multiple of 8
+    mlp = [None, nat.NORI_F16, 4, 128, 128, None, None, 256, None, 128, None]
+    bad = list(mlp); bad[1] = nat.NORI_BF16
+    assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(mlp); bad[3] = bad[4] = bad[9] = 560
+    assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"width 560" in lib.nori_last_error()
+    bad = list(mlp); bad[7] = 20
+    assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_INVALID
+    bad = list(mlp); bad[4] = 100
+    assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_INVALID
+    bad = list(mlp); bad[2] = 0
+    assert lib.nori_swiglu_mlp(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_swiglu_mlp(*mlp) == nat.NORI_ERR_INVALID  # null pointers
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
