@@ -201,7 +201,7 @@ int nori_silu_mul(const void* gu, int dtype, int64_t rows, int32_t hidden, int64
  * with T the rounding to fp16 and fp32 sums. x: [rows, width] at x_row_stride elements;
  * w_gate_up: [2 * hidden, width] contiguous, the gate rows then the up rows; w_down:
  * [width, hidden] contiguous; y: [rows, width] at y_row_stride. width (the sublayer's in and
- * out features) is 128, 256 or 352; hidden is the gate/up width padded to a multiple of 8
+ * out features) is 128, 256 or 352; hidden is the gate/up width padded to a multiple of 32
  * with zero gate/up rows and zero down columns. Strides are multiples of 8 and the four
  * pointers 16-byte aligned. The projections sum in their own order (a value may differ from
  * the unfused GEMMs by one fp16 ulp) and silu uses the hardware exp2 and reciprocal; the

@@ -5,182 +5,167 @@
 // back for the gate and writes [rows, h], and the down projection reads that again; here the
 // hidden activations of a row tile never leave the CU.
 //
-// Workgroup: 4 wavefronts; a wavefront owns 32 * RT rows. Per chunk of 32 hidden units:
+// Workgroup: NW wavefronts of 32 rows each. Per chunk of 32 hidden units:
 //   1. up:   G^T, U^T [32 hidden x 32 rows] = W{g,u}[chunk] . X^T on v_mfma_f32_32x32x16_f16
 //            (A: weight rows staged in LDS; B: the wavefront's X fragments, held in registers
 //            for the whole kernel);
 //   2. gate: a = f16(f16(silu(f16(g))) * f16(u)) in registers; one v_permlane32_swap per word
 //            pair turns the C layout into the B operand of step 3;
 //   3. down: Y^T [width x 32 rows] += Wd[:, chunk] . a^T, accumulated over every chunk.
-// The weight chunks (gate and up rows [64, width], down columns [width, 32]) are staged into a
-// double-buffered LDS ring by the whole workgroup, the next chunk's global loads in flight
-// while the current chunk computes; one barrier per chunk.
+// The weight chunks (gate and up rows [64, width], down columns [width, 32]) go global -> LDS
+// directly (global_load_lds_dwordx4: no staging registers, no LDS write instructions) into a
+// double-buffered ring, the next chunk's loads in flight while the current chunk computes; one
+// barrier per chunk. The weight chunks stream through every workgroup: at width 256 the
+// staging costs about a third of the kernel's time (measured by leaving it out), the gate's
+// VALU work about an eighth.
 //
 // Rounding: the projections sum in fp32 and round to fp16 as hipBLASLt's fp16 GEMMs do, but in
 // their own order, so a value can differ from the unfused sequence's by one fp16 ulp where the
-// fp32 sum sits at a rounding boundary. The gate uses the hardware exp2 and reciprocal
-// (silu(g) = g * rcp(1 + 2^(-g log2 e))), within a few fp32 ulp of torch's g / (1 + exp(-g))
-// before the rounding to fp16.
+// fp32 sum sits at a rounding boundary. silu(g) = g * rcp(1 + 2^(-g log2 e)) with the hardware
+// exp2 and reciprocal, within a few fp32 ulp of torch's g / (1 + exp(-g)) before its rounding
+// to fp16; the product of two fp16 values is exact in fp32, so f16(s * u) is one packed fp16
+// multiply.
 #include "nori_common.h"
 
 namespace {
 
 using namespace nori;
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int HC = 32;  // hidden units per chunk
 constexpr float kLog2eF = 1.4426950408889634f;
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Wavefronts per workgroup: eight (two per SIMD) at width 128, whose Y^T accumulators
+// (width / 2 registers), X fragments (width / 4) and chunk G^T, U^T (32) leave the compiler
+// room in 256 registers; four above (at width 256 an eight-wavefront build spills and runs
+// 4-6 % slower).
+constexpr int waves_for(int e) { return e <= 128 ? 8 : 4; }
 
 template <int E>
 struct MlpGeom {
     static_assert(E % 32 == 0, "width is a multiple of 32");
-    static constexpr int KS = E / 16;         // k-steps of the up projection
-    static constexpr int OT = E / 32;         // 32-row tiles of Y^T
-    static constexpr int GPITCH = E + 8;      // f16 per staged gate/up row (+16 B: the 16 lanes of a
-                                              // b128 read land on distinct banks)
-    static constexpr int DPITCH = HC + 8;     // f16 per staged down row (80 B, likewise)
-    static constexpr int GBUF = 2 * HC * GPITCH;  // gate rows 0-31, then up rows 0-31
-    static constexpr int DBUF = E * DPITCH;
-    static constexpr int GPIECES = 2 * HC * E / 8;  // 16-byte pieces of a chunk
-    static constexpr int DPIECES = E * HC / 8;
-    static constexpr int PIECES = GPIECES + DPIECES;
-    static constexpr int PPT = (PIECES + kThreads - 1) / kThreads;  // pieces per thread
+    static constexpr int NW = waves_for(E);
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int KS = E / 16;  // k-steps of the up projection
+    static constexpr int OT = E / 32;  // 32-row tiles of Y^T
+    // A chunk in LDS, in 16-byte granules: gate rows 0-31 then up rows 0-31, each E/8 granules
+    // and one of padding (the 16 lanes of a b128 read then land on distinct banks), then the
+    // down rows [E, 32 hidden], 4 granules and one of padding each.
+    static constexpr int GROW = E / 8 + 1;
+    static constexpr int NG = 2 * HC * GROW;
+    static constexpr int NDG = E * 5;
+    static constexpr int LOADS = (NG + NDG + 63) / 64;  // wavefront loads of 64 granules
+    static constexpr int BUF = LOADS * 64 * 8;           // f16 per ring buffer
 };
-
-// Rows per wavefront (32 * RT): two row tiles share each weight fragment where the registers
-// allow it (width 128).
-constexpr int row_tiles(int e) { return e <= 128 ? 2 : 1; }
-
-__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)pin_f32(v); }
-
-// f16(f16(silu(g)) * u) for g, u already fp16 values
-__device__ __forceinline__ float gate_value(float g, float u) {
-    const float s = round_f16(g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2eF)));
-    return s * u;
-}
 
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     const f16x2 h = f16x2{(_Float16)pin_f32(a), (_Float16)pin_f32(b)};
     return __builtin_bit_cast(uint32_t, h);
 }
 
-template <int E, int RT>
-__global__ void __launch_bounds__(kThreads, 1)
+// The gate of two hidden units: f16(f16(silu(f16(g))) * f16(u)) as one packed word.
+__device__ __forceinline__ uint32_t gate_pair(float g0, float g1, float u0, float u1) {
+    const f16x2 gh = f16x2{(_Float16)g0, (_Float16)g1};
+    const f16x2 uh = f16x2{(_Float16)u0, (_Float16)u1};
+    const float a = (float)gh[0], b = (float)gh[1];
+    const float s0 = a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -kLog2eF));
+    const float s1 = b * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(b * -kLog2eF));
+    const f16x2 sh = f16x2{(_Float16)s0, (_Float16)s1};
+    return __builtin_bit_cast(uint32_t, sh * uh);
+}
+
+template <int E>
+__global__ void __launch_bounds__(MlpGeom<E>::THREADS)
 swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, const uint16_t* __restrict__ wgu,
                   const uint16_t* __restrict__ wd, int hp, uint16_t* __restrict__ y, int64_t ys) {
     using G = MlpGeom<E>;
-    __shared__ __attribute__((aligned(16))) _Float16 Gs[2 * G::GBUF];
-    __shared__ __attribute__((aligned(16))) _Float16 Ds[2 * G::DBUF];
+    __shared__ __attribute__((aligned(16))) _Float16 ring[2 * G::BUF];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-    const int64_t r0 = (int64_t)blockIdx.x * (kWaves * 32 * RT) + wave * 32 * RT;
-    const int nch = (hp + HC - 1) / HC;
+    const int64_t r0 = (int64_t)blockIdx.x * (G::NW * 32) + wave * 32;
+    const int nch = hp / HC;
 
-    // ---- staging plan: piece p = tid + i * kThreads of a chunk whose first hidden unit is h0
-    auto fetch = [&](int h0, u32x4 (&buf)[G::PPT]) {
+    // ---- staging: wavefront load i (i = wave, wave + NW, ...) fills granules [64i, 64i + 64)
+    // of a buffer, lane l granule 64i + l; padding granules (and the tail past the chunk) load
+    // a valid weight granule that nothing reads
+    auto fetch = [&](int h0, int b) {
 #pragma unroll
-        for (int i = 0; i < G::PPT; ++i) {
-            const int p = tid + i * kThreads;
-            u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if (p < G::GPIECES) {
-                const int row = p / (E / 8), cp = p % (E / 8);
-                const int h = h0 + row % HC;
-                if (h < hp) v = *reinterpret_cast<const u32x4*>(wgu + ((int64_t)(row / HC) * hp + h) * E + 8 * cp);
-            } else if (p < G::PIECES) {
-                const int q = p - G::GPIECES, e = q / (HC / 8), cp = q % (HC / 8);
-                const int h = h0 + 8 * cp;  // hp is a multiple of 8: a piece is valid whole or not at all
-                if (h < hp) v = *reinterpret_cast<const u32x4*>(wd + (int64_t)e * hp + h);
+        for (int k = 0; k < (G::LOADS + G::NW - 1) / G::NW; ++k) {
+            const int i = wave + k * G::NW;
+            if (i >= G::LOADS) break;  // uniform over the wavefront
+            const int q = 64 * i + lane;
+            const uint16_t* src;
+            if (q < G::NG) {
+                const int row = q / G::GROW, cp = min(q % G::GROW, E / 8 - 1);
+                src = wgu + ((int64_t)(row / HC) * hp + h0 + row % HC) * E + 8 * cp;
+            } else {
+                const int qd = min(q - G::NG, G::NDG - 1), e = qd / 5, cp = min(qd % 5, 3);
+                src = wd + (int64_t)e * hp + h0 + 8 * cp;
             }
-            buf[i] = v;
-        }
-    };
-    auto store = [&](int b, const u32x4 (&buf)[G::PPT]) {
-#pragma unroll
-        for (int i = 0; i < G::PPT; ++i) {
-            const int p = tid + i * kThreads;
-            if (p < G::GPIECES) {
-                const int row = p / (E / 8), cp = p % (E / 8);
-                *reinterpret_cast<u32x4*>(&Gs[b * G::GBUF + row * G::GPITCH + 8 * cp]) = buf[i];
-            } else if (p < G::PIECES) {
-                const int q = p - G::GPIECES, e = q / (HC / 8), cp = q % (HC / 8);
-                *reinterpret_cast<u32x4*>(&Ds[b * G::DBUF + e * G::DPITCH + 8 * cp]) = buf[i];
-            }
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)(ring + b * G::BUF + 512 * i), 16, 0, 0);
         }
     };
 
     // ---- X fragments (B operand of the up projection): lane holds x[row][16s + 8hh + 0..7]
-    f16x8 xf[RT][G::KS];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const int64_t row = r0 + 32 * rt + l32;
+    f16x8 xf[G::KS];
+    {
+        const int64_t row = r0 + l32;
         const bool ok = row < rows;
 #pragma unroll
         for (int s = 0; s < G::KS; ++s) {
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
             if (ok) v = *reinterpret_cast<const u32x4*>(x + row * xs + 16 * s + 8 * hh);
-            xf[rt][s] = __builtin_bit_cast(f16x8, v);
+            xf[s] = __builtin_bit_cast(f16x8, v);
         }
     }
 
-    f32x16 yt[RT][G::OT];
+    f32x16 yt[G::OT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int t = 0; t < G::OT; ++t) yt[rt][t] = f32x16{};
+    for (int t = 0; t < G::OT; ++t) yt[t] = f32x16{};
 
-    u32x4 buf[G::PPT];
-    fetch(0, buf);
-    store(0, buf);
+    fetch(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
     for (int c = 0; c < nch; ++c) {
         const int cur = c & 1;
-        if (c + 1 < nch) fetch(HC * (c + 1), buf);  // lands while this chunk computes
-        const _Float16* Gc = Gs + cur * G::GBUF;
-        const _Float16* Dc = Ds + cur * G::DBUF;
+        // the next chunk into the other buffer, whose last reads were in chunk c-1 (before the
+        // previous barrier); it lands while this chunk computes
+        if (c + 1 < nch) fetch(HC * (c + 1), cur ^ 1);
+        const _Float16* Gc = ring + cur * G::BUF;
+        const _Float16* Dc = Gc + 8 * G::NG;
 
         // 1. G^T and U^T of the chunk
-        f32x16 gt[RT], ut[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) gt[rt] = ut[rt] = f32x16{};
+        f32x16 gt = f32x16{}, ut = f32x16{};
 #pragma unroll
         for (int s = 0; s < G::KS; ++s) {
-            const f16x8 ag = *reinterpret_cast<const f16x8*>(Gc + l32 * G::GPITCH + 16 * s + 8 * hh);
-            const f16x8 au = *reinterpret_cast<const f16x8*>(Gc + (HC + l32) * G::GPITCH + 16 * s + 8 * hh);
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                gt[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, xf[rt][s], gt[rt], 0, 0, 0);
-                ut[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(au, xf[rt][s], ut[rt], 0, 0, 0);
-            }
+            const f16x8 ag = *reinterpret_cast<const f16x8*>(Gc + 8 * (l32 * G::GROW + 2 * s + hh));
+            const f16x8 au = *reinterpret_cast<const f16x8*>(Gc + 8 * ((HC + l32) * G::GROW + 2 * s + hh));
+            gt = __builtin_amdgcn_mfma_f32_32x32x16_f16(ag, xf[s], gt, 0, 0, 0);
+            ut = __builtin_amdgcn_mfma_f32_32x32x16_f16(au, xf[s], ut, 0, 0, 0);
         }
 
         // 2. the gate, as words w[j][p] = hidden 8j + 4hh + 2p + {0, 1} of row l32, then the
         //    B operands of the down projection: k-step ks holds hidden 16ks + 8hh + 0..7
-        f16x8 af[RT][2];
+        uint32_t w[4][2];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            uint32_t w[4][2];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    const int i0 = 4 * j + 2 * p;
-                    const float v0 = gate_value(round_f16(gt[rt][i0]), round_f16(ut[rt][i0]));
-                    const float v1 = gate_value(round_f16(gt[rt][i0 + 1]), round_f16(ut[rt][i0 + 1]));
-                    w[j][p] = pack_f16(v0, v1);
-                }
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                // lanes 0-31 keep their words of hidden 16ks + 0..3 and take 4..7 from lane +32;
-                // lanes 32-63 keep 16ks + 12..15 and take 8..11 from lane -32
-                const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * ks][0], w[2 * ks + 1][0], false, false);
-                const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * ks][1], w[2 * ks + 1][1], false, false);
-                af[rt][ks] = __builtin_bit_cast(f16x8, u32x4{s0[0], s1[0], s0[1], s1[1]});
+            for (int p = 0; p < 2; ++p) {
+                const int i0 = 4 * j + 2 * p;
+                w[j][p] = gate_pair(gt[i0], gt[i0 + 1], ut[i0], ut[i0 + 1]);
             }
+        f16x8 af[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            // lanes 0-31 keep their words of hidden 16ks + 0..3 and take 4..7 from lane +32;
+            // lanes 32-63 keep 16ks + 12..15 and take 8..11 from lane -32
+            const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * ks][0], w[2 * ks + 1][0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * ks][1], w[2 * ks + 1][1], false, false);
+            af[ks] = __builtin_bit_cast(f16x8, u32x4{s0[0], s1[0], s0[1], s1[1]});
         }
 
         // 3. Y^T += Wd[:, chunk] a^T
@@ -188,32 +173,26 @@ swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, cons
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int t = 0; t < G::OT; ++t) {
-                const f16x8 ad = *reinterpret_cast<const f16x8*>(Dc + (32 * t + l32) * G::DPITCH + 16 * ks + 8 * hh);
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    yt[rt][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ad, af[rt][ks], yt[rt][t], 0, 0, 0);
+                const f16x8 ad = *reinterpret_cast<const f16x8*>(Dc + 8 * ((32 * t + l32) * 5 + 2 * ks + hh));
+                yt[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ad, af[ks], yt[t], 0, 0, 0);
             }
 
-        // the next chunk into the other buffer, whose last reads were in chunk c-1 (before the
-        // previous barrier)
         if (c + 1 < nch) {
-            store(cur ^ 1, buf);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's loads are in LDS
             __syncthreads();
         }
     }
 
     // ---- y[row][e .. e+3] from Y^T: element 4j + i of tile t is e = 32t + 8j + 4hh + i
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const int64_t row = r0 + 32 * rt + l32;
-        if (row >= rows) continue;
+    const int64_t row = r0 + l32;
+    if (row < rows) {
         uint16_t* yr = y + row * ys;
 #pragma unroll
         for (int t = 0; t < G::OT; ++t)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int e = 32 * t + 8 * j + 4 * hh;
-                const f32x16& v = yt[rt][t];
+                const f32x16& v = yt[t];
                 *reinterpret_cast<u32x2*>(yr + e) = u32x2{pack_f16(v[4 * j], v[4 * j + 1]), pack_f16(v[4 * j + 2], v[4 * j + 3])};
             }
     }
@@ -222,10 +201,10 @@ swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, cons
 template <int E>
 void launch(const uint16_t* x, int64_t rows, int64_t xs, const uint16_t* wgu, const uint16_t* wd, int hp, uint16_t* y,
             int64_t ys, hipStream_t stream) {
-    constexpr int RT = row_tiles(E);
-    const int64_t per = kWaves * 32 * RT;
+    using G = MlpGeom<E>;
+    const int64_t per = G::NW * 32;
     const dim3 grid((unsigned)((rows + per - 1) / per));
-    hipLaunchKernelGGL((swiglu_mlp_kernel<E, RT>), grid, dim3(kThreads), 0, stream, x, rows, xs, wgu, wd, hp, y, ys);
+    hipLaunchKernelGGL((swiglu_mlp_kernel<E>), grid, dim3(G::THREADS), 0, stream, x, rows, xs, wgu, wd, hp, y, ys);
 }
 
 }  // namespace
@@ -237,8 +216,8 @@ extern "C" int nori_swiglu_mlp(const void* x, int dtype, int64_t rows, int32_t w
     if (dtype != NORI_F16) return fail(NORI_ERR_UNSUPPORTED, "swiglu_mlp: unsupported dtype %s (float16 only)", dtype_name(dtype));
     if (width != 128 && width != 256 && width != 352)
         return fail(NORI_ERR_UNSUPPORTED, "swiglu_mlp: no kernel for width %d (128, 256 or 352)", width);
-    if (rows < 0 || rows > 0x7fffffffLL || hidden <= 0 || hidden % 8 != 0)
-        return fail(NORI_ERR_INVALID, "swiglu_mlp: bad shape (%lld rows, hidden %d: a positive multiple of 8)",
+    if (rows < 0 || rows > 0x7fffffffLL || hidden <= 0 || hidden % 32 != 0)
+        return fail(NORI_ERR_INVALID, "swiglu_mlp: bad shape (%lld rows, hidden %d: a positive multiple of 32)",
                     (long long)rows, hidden);
     if (x_row_stride < width || y_row_stride < width || x_row_stride % 8 != 0 || y_row_stride % 8 != 0)
         return fail(NORI_ERR_INVALID, "swiglu_mlp: row strides (%lld, %lld) must be multiples of 8 and at least %d",

@@ -121,34 +121,39 @@ class SwiGLUMLP(nn.Module):
         # silu(g) * u with torch's rounding in the projection dtype, then the down projection.
         # The hidden width is padded to a multiple of 8 with zero gate/up rows and zero down
         # columns, so every row is 16-byte aligned; the padding contributes exact zeros.
-        gate_up, gate_up_bias, down, hidden = self._stacked_weights(x)
         width = x.shape[-1]
         if (
             self.fused
-            and gate_up.dtype == torch.float16
-            and gate_up_bias is None
+            and self._projection_dtype() == torch.float16
+            and self.w_gate.bias is None
             and self.w_down.bias is None
             and width == self.w_down.out_features
             and width in FUSED_MLP_WIDTHS
         ):
             # the whole sublayer in one kernel: its operand as the projections would take it
             # (autocast casts to fp16), the hidden activations kept on the CU
+            gate_up, _, down, hidden = self._stacked_weights(x, multiple=32)
             return swiglu_mlp(x.to(torch.float16), gate_up, down, hidden)
+        gate_up, gate_up_bias, down, hidden = self._stacked_weights(x)
         gu = nn.functional.linear(x, gate_up, gate_up_bias)
         return nn.functional.linear(silu_mul(gu, hidden), down, self.w_down.bias)
 
-    def _stacked_weights(self, x: torch.Tensor):
+    def _projection_dtype(self) -> torch.dtype:
+        return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.w_gate.weight.dtype
+
+    def _stacked_weights(self, x: torch.Tensor, multiple: int = 8):
         """(gate|up weight [2 hp, in], its bias, down weight [out, hp], hp) in the dtype the
-        projections compute in, rebuilt when a weight changes."""
-        dtype = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.w_gate.weight.dtype
+        projections compute in, hp the hidden width padded to ``multiple``; rebuilt when a
+        weight changes."""
+        dtype = self._projection_dtype()
         params = [self.w_gate.weight, self.w_up.weight, self.w_down.weight]
         if self.w_gate.bias is not None:
             params += [self.w_gate.bias, self.w_up.bias]
-        key = (dtype, x.device) + tuple((p.data_ptr(), p._version) for p in params)
+        key = (dtype, x.device, multiple) + tuple((p.data_ptr(), p._version) for p in params)
         cached = getattr(self, "_stacked", None)
         if cached is None or cached[0] != key:
             h = self.w_gate.out_features
-            hp = (h + 7) // 8 * 8
+            hp = (h + multiple - 1) // multiple * multiple
             with torch.no_grad():
                 gate_up = torch.zeros((2 * hp, self.w_gate.in_features), device=x.device, dtype=dtype)
                 gate_up[:h] = self.w_gate.weight

@@ -302,7 +302,7 @@ FUSED_MLP_WIDTHS = (128, 256, 352)
 def swiglu_mlp(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, hidden: int) -> torch.Tensor:
     """The whole fp16 SwiGLU feed-forward ``(silu(x Wg^T) * (x Wu^T)) Wd^T`` in one HIP kernel
     (``nori_swiglu_mlp``): ``gate_up`` [2 * hidden, width] (gate rows, then up rows) and
-    ``down`` [width, hidden], fp16 and contiguous, ``hidden`` padded to a multiple of 8 with
+    ``down`` [width, hidden], fp16 and contiguous, ``hidden`` padded to a multiple of 32 with
     zero rows/columns; x [..., width] fp16 with width in FUSED_MLP_WIDTHS. SwiGLUMLP.forward
     under fp16 autocast (layer.py:261-274) without writing the hidden activations out."""
     width = x.shape[-1]

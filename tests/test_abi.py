@@ -100,14 +100,14 @@ def test_argument_errors_map_to_reference_exceptions():
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F32, 3, 5, 44, 1) == 15 * 64 * 2
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 0) == 0
     assert lib.nori_kv_project_quantize_int8_workspace_size(nat.NORI_F16, 3, 5, 64, 1) == 15 * 64 * 2
-    # fused SwiGLU feed-forward: fp16 only, widths 128 / 256 / 352, hidden a multiple of 8
+    # fused SwiGLU feed-forward: fp16 only, widths 128 / 256 / 352, hidden a multiple of 32
     mlp = [None, nat.NORI_F16, 4, 128, 128, None, None, 256, None, 128, None]
     bad = list(mlp); bad[1] = nat.NORI_BF16
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_UNSUPPORTED
     bad = list(mlp); bad[3] = bad[4] = bad[9] = 560
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_UNSUPPORTED
     assert b"width 560" in lib.nori_last_error()
-    bad = list(mlp); bad[7] = 20
+    bad = list(mlp); bad[7] = 40
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_INVALID
     bad = list(mlp); bad[4] = 100
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_ERR_INVALID

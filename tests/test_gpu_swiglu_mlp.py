@@ -10,8 +10,8 @@ checks here:
   |y - y_ref| <= 2^-8 * max|y_ref| (measured: at most 3.6e-4, about 2^-11.5);
 * against the unfused GPU sequence (hipBLASLt projections + nori_silu_mul), same bound
   (measured: at most 5.9e-4; 99.96 % of the outputs bit-identical);
-* shapes: every width the kernel is built for, hidden widths that leave a partial 32-unit
-  chunk (8, 40, 688), ragged row counts, a strided operand, zero rows;
+* shapes: every width the kernel is built for, hidden widths padded up to whole 32-unit chunks
+  (8, 40, 682), ragged row counts, a strided operand, zero rows;
 * the module: SwiGLUMLP under autocast takes the kernel, and matches its unfused path.
 """
 import pytest
@@ -26,10 +26,11 @@ DEV = torch.device("cuda", 0)
 
 
 def _weights(width: int, hidden: int, seed: int):
-    """Stacked fp16 weights as SwiGLUMLP._stacked_weights lays them out: [gate | up] rows
-    [2 hp, width] and down [width, hp], hp = hidden padded to a multiple of 8 with zeros."""
+    """Stacked fp16 weights as SwiGLUMLP._stacked_weights lays them out for the kernel: [gate |
+    up] rows [2 hp, width] and down [width, hp], hp = hidden padded to a multiple of 32 with
+    zeros."""
     g = torch.Generator().manual_seed(seed)
-    hp = (hidden + 7) // 8 * 8
+    hp = (hidden + 31) // 32 * 32
     gate_up = torch.zeros(2 * hp, width)
     gate_up[:hidden] = torch.randn(hidden, width, generator=g) / width**0.5
     gate_up[hp : hp + hidden] = torch.randn(hidden, width, generator=g) / width**0.5
@@ -90,7 +91,7 @@ def test_against_unfused_sequence(width):
 
 
 def test_strided_operand_and_empty_rows():
-    gate_up, down, hp = _weights(256, 688, seed=11)
+    gate_up, down, hp = _weights(256, 682, seed=11)
     base = torch.randn(400, 264, generator=torch.Generator().manual_seed(5)).half().to(DEV)
     x = base[:, :256]  # row stride 264
     print("swiglu_mlp strided operand", flush=True)
