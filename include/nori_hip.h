@@ -184,6 +184,20 @@ int nori_residual_add_rms_norm(const float* x, const void* u, int u_dtype, const
                                int64_t y_group, int64_t y_group_stride, int64_t y_row_stride, void* stream);
 
 /*
+ * LayerNorm over rows of `cols` elements: y = (x - mean) * rsqrt(var + eps) * weight + bias,
+ * then max(y, 0) when `relu` is non-zero, written as `y_dtype`. Replaces the nn.LayerNorm
+ * calls of the cell encoder under the dtype rules of fp16 autocast (the RBF numeric
+ * embedding's norm, src/synthefy_nori/model/encoders.py:118-276, and the fusion MLP
+ * Linear -> LayerNorm -> ReLU -> Linear -> LayerNorm, :432-585): statistics in fp32 (mean,
+ * biased variance), fp32 weight and bias (either may be NULL), the fp32 result rounded once
+ * to y_dtype -- the fp16 operand an autocast F.linear makes of it, or fp32. cols is a
+ * multiple of 4; rows at x_row_stride / y_row_stride elements (multiples of 4), x and y
+ * aligned to 4 elements.
+ */
+int nori_layer_norm(const void* x, int x_dtype, int64_t rows, int32_t cols, int64_t x_row_stride, const float* weight,
+                    const float* bias, float eps, int relu, void* y, int y_dtype, int64_t y_row_stride, void* stream);
+
+/*
  * SwiGLU gate over the [gate | up] output of one fused projection (gate and up weights stacked,
  * so the operand is read once): out[r, j] = T(T(silu(gu[r, j])) * gu[r, hidden + j]) with
  * silu(x) = x / (1 + exp(-x)) in fp32 and T the rounding to `dtype` (NORI_F32 / NORI_F16 /

@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     ),
     "nori_residual_add": (ctypes.c_int, [_vp, _vp, _i32, _f32, _i64, _vp, _vp]),
     "nori_silu_mul": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _i64, _vp]),
+    "nori_layer_norm": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _f32, _i32, _vp, _i32, _i64, _vp]),
     "nori_swiglu_mlp": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
     "nori_residual_add_rms_norm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _f32, _i64, _i32, _f32, _vp, _vp, _i32, _i64, _i64,
                                                   _i64, _vp]),

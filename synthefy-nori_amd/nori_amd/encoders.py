@@ -33,6 +33,8 @@ import torch
 import torch.nn as nn
 from torch.nn.init import orthogonal_
 
+from .norm import layer_norm
+
 __all__ = [
     "EmbYEncoderStep",
     "LinearEncoder",
@@ -147,6 +149,12 @@ class LinearEncoder(nn.Module):
         return input
 
 
+def _operand_dtype(dtype: torch.dtype) -> torch.dtype:
+    """The dtype an F.linear on the current device computes in: the autocast dtype when
+    autocast is on, else the given one."""
+    return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else dtype
+
+
 class RBFembedding(nn.Module):
     """Scientific-notation RBF embedding of a scalar (:118-276).
 
@@ -242,10 +250,17 @@ class RBFembedding(nn.Module):
                 parts.append(self.exp_digit_embedding((mag // (10**p)) % 10))
             gb = self.gate_mlp(torch.cat(parts, dim=-1).to(self.dtype))
             gamma, beta = torch.split(gb, self.n_kernels, dim=-1)
-            rbf = self.norm(rbf * torch.sigmoid(gamma) + torch.tanh(beta))
+            pre = rbf * torch.sigmoid(gamma) + torch.tanh(beta)
+            if pre.is_cuda:
+                # the norm on the HIP kernel, written as the operand out_layer computes with
+                # (fp16 under fp16 autocast: the same rounding of the same fp32 value)
+                op = _operand_dtype(pre.dtype) if not self.use_original_features else pre.dtype
+                rbf = layer_norm(pre, self.norm.weight, self.norm.bias, self.norm.eps, out_dtype=op)
+            else:
+                rbf = self.norm(pre)
         if self.use_original_features:
             rbf = torch.cat([rbf, x.unsqueeze(-1)], dim=-1)
-        out = self.out_layer(rbf.to(self.dtype))
+        out = self.out_layer(rbf if rbf.dtype == _operand_dtype(self.dtype) else rbf.to(self.dtype))
         return out if self.as_tokenizer else out.reshape(rows, -1)
 
 
@@ -417,8 +432,20 @@ class MaskEmbEncoder(nn.Module):
             emb = torch.cat((emb, PromptQuantilePLEEncoder.encode(x.squeeze(-1), reference).to(emb.dtype)), dim=-1)
         if not self.nan_to_zero:
             emb = torch.where(missing, self.mask_embedding.expand_as(emb), emb)
-        input[self.out_key] = self.fusion_network(emb.flatten(3)).view(b, s, g, -1)
+        h = emb.flatten(3)
+        input[self.out_key] = (self._fusion_on_device(h) if h.is_cuda else self.fusion_network(h)).view(b, s, g, -1)
         return input
+
+    def _fusion_on_device(self, h: torch.Tensor) -> torch.Tensor:
+        """fusion_network (Linear -> LayerNorm -> ReLU -> Linear -> LayerNorm) with the norms on
+        the HIP kernel: the first writes the ReLU'd operand of the second Linear in the dtype it
+        computes in, the second the fp32 (autocast) or input-dtype output torch's would."""
+        lin1, ln1, _, lin2, ln2 = self.fusion_network
+        h = lin1(h)
+        h = layer_norm(h, ln1.weight, ln1.bias, ln1.eps, relu=True, out_dtype=_operand_dtype(h.dtype))
+        h = lin2(h)
+        autocast = torch.is_autocast_enabled("cuda")
+        return layer_norm(h, ln2.weight, ln2.bias, ln2.eps, out_dtype=torch.float32 if autocast else h.dtype)
 
 
 class NanEncoder(nn.Module):

@@ -295,6 +295,38 @@ def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMS
     return out
 
 
+def layer_norm(
+    x: torch.Tensor,
+    weight: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    eps: float,
+    relu: bool = False,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """``F.layer_norm`` over the last axis (then ``relu`` when asked) in one HIP pass
+    (``nori_layer_norm``): fp32 statistics and affine, the result rounded once to
+    ``out_dtype`` (default: x's dtype) -- under fp16 autocast the fp16 operand of the F.linear
+    that follows (ref encoders.py:118-276, 432-585)."""
+    cols = x.shape[-1]
+    out_dtype = out_dtype or x.dtype
+    device = nat.require_device(x)
+    x2 = x.reshape(-1, cols)
+    if x2.stride(-1) != 1 or x2.stride(0) % 4 or x2.data_ptr() % (4 * x2.element_size()):
+        x2 = x2.contiguous()
+    w = None if weight is None else weight.detach().to(device=device, dtype=torch.float32).contiguous()
+    b = None if bias is None else bias.detach().to(device=device, dtype=torch.float32).contiguous()
+    out = torch.empty((x2.shape[0], cols), dtype=out_dtype, device=device)
+    nat.check(
+        nat.lib().nori_layer_norm(
+            x2.data_ptr(), nat.dtype_code(x.dtype), x2.shape[0], cols, x2.stride(0),
+            None if w is None else w.data_ptr(), None if b is None else b.data_ptr(), float(eps), int(relu),
+            out.data_ptr(), nat.dtype_code(out_dtype), cols, nat.stream_of(device),
+        ),
+        "layer_norm",
+    )
+    return out.view(*x.shape[:-1], cols)
+
+
 # Widths (in = out features) the fused SwiGLU kernel is built for.
 FUSED_MLP_WIDTHS = (128, 256, 352)
 

@@ -35,6 +35,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_residual_add",
             "nori_silu_mul",
             "nori_swiglu_mlp",
+            "nori_layer_norm",
             "nori_residual_add_rms_norm",
             "nori_icl_attention",
             "nori_icl_attention_qk",
@@ -114,6 +115,17 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(mlp); bad[2] = 0
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_swiglu_mlp(*mlp) == nat.NORI_ERR_INVALID  # null pointers
+    # layer norm: float dtypes only, width a multiple of 4, eps a non-negative number
+    ln = [None, nat.NORI_F16, 4, 128, 128, None, None, 1e-5, 0, None, nat.NORI_F32, 128, None]
+    bad = list(ln); bad[1] = nat.NORI_I8
+    assert lib.nori_layer_norm(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(ln); bad[3] = bad[4] = bad[11] = 126
+    assert lib.nori_layer_norm(*bad) == nat.NORI_ERR_INVALID
+    bad = list(ln); bad[7] = float("nan")
+    assert lib.nori_layer_norm(*bad) == nat.NORI_ERR_INVALID
+    bad = list(ln); bad[2] = 0
+    assert lib.nori_layer_norm(*bad) == nat.NORI_OK
+    assert lib.nori_layer_norm(*ln) == nat.NORI_ERR_INVALID  # null pointers
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
