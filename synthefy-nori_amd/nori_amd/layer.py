@@ -38,7 +38,8 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention, short_context
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
-from .norm import FUSED_MLP_WIDTHS, RMSNorm, projection_operand, rms_norm_, silu_mul, swiglu_mlp
+from .norm import (FUSED_MLP_WIDTHS, RMSNorm, operand_dtype, projection_operand, residual_add, residual_add_norm,
+                   rms_norm_, silu_mul, swiglu_mlp)
 
 ACTIVATION_FN = {"gelu": nn.GELU(), "relu": nn.ReLU(), "silu": nn.SiLU()}
 _SDPA_BACKENDS_WITHOUT_CUDNN = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]
@@ -750,6 +751,58 @@ class EncoderBaseLayer(nn.Module):
             return residual + self.deepnorm_alpha * update
         return residual + update
 
+    def _alpha_value(self, update: torch.Tensor) -> float:
+        """The deep-norm factor as ``residual + deepnorm_alpha * update`` applies it to this
+        update (1 without deep norm): a 0-dim fp32 buffer on the update's device is cast to the
+        update's dtype before the multiply; one left on the host enters a device op as a scalar,
+        at fp32. Read from the device once per case."""
+        if self.deepnorm_alpha is None:
+            return 1.0
+        a = self.deepnorm_alpha
+        host_scalar = a.device.type == "cpu" and update.device.type != "cpu"
+        cache = self.__dict__.setdefault("_alpha_values", {})
+        key = (update.dtype, host_scalar, a.device, a._version)
+        if key not in cache:
+            cache[key] = float(a.detach().float().cpu()) if host_scalar else float(a.detach().to(update.dtype).float().cpu())
+        return cache[key]
+
+    def _step_output(self, step_idx, operand, feature_atten_mask, eval_pos):
+        sublayer = self.layer_steps[step_idx]
+        out = sublayer(operand, feature_atten_mask, eval_pos) if isinstance(sublayer, functools.partial) else sublayer(operand)
+        return out[0] if isinstance(out, tuple) else out
+
+    def _add_then_steps(self, x, update, steps, feature_atten_mask, eval_pos, then_norm=None):
+        """Pre-norm: ``x + alpha * update``, then the non-sequence ``steps``; each residual update
+        is formed in the same pass as the normalized operand of what follows (the next step's
+        norm, or ``then_norm``), bit for bit the separate residual add and norm
+        (``residual_add_norm``). x is left as it is; returns the new stream (and, with
+        ``then_norm``, its operand)."""
+        fused = self.pre_norm and x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+        if not fused:
+            x = self._residual_add(x, update)
+            for step in steps:
+                x = self._run_non_sequence_step(x, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
+            if then_norm is None:
+                return x
+            return x, (projection_operand(then_norm, x) if self.pre_norm else x)
+        stream = torch.empty_like(x, memory_format=torch.contiguous_format)
+        src = x
+        for step in steps:
+            operand = residual_add_norm(src, update, self._alpha_value(update), self.layer_norms[step],
+                                        out_dtype=operand_dtype(x), x_out=stream)
+            src = stream
+            update = self._step_output(step, operand, feature_atten_mask, eval_pos)
+            del operand
+        if then_norm is not None:
+            operand = residual_add_norm(src, update, self._alpha_value(update), then_norm,
+                                        out_dtype=operand_dtype(x), x_out=stream)
+            return stream, operand
+        if src is stream:
+            residual_add(stream, update, self._alpha_value(update), inplace=True)
+        else:
+            stream.copy_(residual_add(src, update, self._alpha_value(update)))
+        return stream
+
     def _run_non_sequence_step(self, x, *, step_idx, feature_atten_mask, eval_pos):
         sublayer, norm = self.layer_steps[step_idx], self.layer_norms[step_idx]
         if self.pre_norm:
@@ -995,14 +1048,11 @@ class EncoderBaseLayer(nn.Module):
                 quantize_kv_cache, offload_kv_cache, device, exact=exact_cache_write,
             )
         eval_pos = x_train.shape[1]
-        for step in pre_steps:
-            x_train = self._run_non_sequence_step(x_train, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
         seq_attn_train = self.sequence_attentions[index1]
         seq_attn_test = self.sequence_attentions[index2]
         seq_norm = self.layer_norms[seq_step]
+        x_train, src = self._pre_steps_then_operand(x_train, pre_steps, seq_norm, feature_atten_mask, eval_pos)
         residual = x_train
-        # src feeds only projections: under autocast the norm writes their fp16 operand directly
-        src = projection_operand(seq_norm, x_train) if self.pre_norm else x_train
         train_attn = seq_attn_train(
             x=src.transpose(1, 2), x_kv=src.transpose(1, 2), copy_first_head_kv=self.self_share_all_kv_heads
         )[0].transpose(1, 2)
@@ -1019,26 +1069,46 @@ class EncoderBaseLayer(nn.Module):
         else:
             seq_kv_cache = seq_attn_test.project_kv_cache(kv_source, copy_first_head_kv=self.cross_share_all_kv_heads)
         del kv_source
-        x_train = self._residual_add(residual, train_attn) if self.pre_norm else seq_norm(train_attn + residual)
-        for step in post_steps:
-            x_train = self._run_non_sequence_step(x_train, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
+        if self.pre_norm:
+            x_train = self._add_then_steps(residual, train_attn, post_steps, feature_atten_mask, eval_pos)
+        else:
+            x_train = seq_norm(train_attn + residual)
+            for step in post_steps:
+                x_train = self._run_non_sequence_step(x_train, step_idx=step, feature_atten_mask=feature_atten_mask,
+                                                      eval_pos=eval_pos)
         return x_train, {"seq_kv": seq_kv_cache}
+
+    def _pre_steps_then_operand(self, x, pre_steps, seq_norm, feature_atten_mask, eval_pos):
+        """The steps before the sequence attention, then the attention's input: its normalized
+        operand under pre-norm (written in the projection dtype; the last residual update of
+        the steps formed in the same pass), else the stream itself."""
+        if not self.pre_norm:
+            for step in pre_steps:
+                x = self._run_non_sequence_step(x, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
+            return x, x
+        if not pre_steps:
+            # src feeds only projections: under autocast the norm writes their fp16 operand directly
+            return x, projection_operand(seq_norm, x)
+        first = self._step_output(pre_steps[0], projection_operand(self.layer_norms[pre_steps[0]], x), feature_atten_mask,
+                                  eval_pos)
+        return self._add_then_steps(x, first, pre_steps[1:], feature_atten_mask, eval_pos, then_norm=seq_norm)
 
     def forward_test_with_cache(self, x_test: torch.Tensor, cache: dict, feature_atten_mask: torch.Tensor | None = None):
         """Query rows through one layer against the layer's context cache (layer.py:1915-1967)."""
         pre_steps, seq_step, post_steps, seq_index = self._cache_steps()
         eval_pos = x_test.shape[1]
-        for step in pre_steps:
-            x_test = self._run_non_sequence_step(x_test, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
         index1 = seq_index * 2 if self.seq_attn_isolated else seq_index
         index2 = index1 + 1 if self.seq_attn_isolated else index1
         seq_attn_test = self.sequence_attentions[index2]
         seq_norm = self.layer_norms[seq_step]
+        x_test, src = self._pre_steps_then_operand(x_test, pre_steps, seq_norm, feature_atten_mask, eval_pos)
         residual = x_test
-        src = projection_operand(seq_norm, x_test) if self.pre_norm else x_test
         test_attn, _ = seq_attn_test.forward_with_kv_cache(src.transpose(1, 2), cache["seq_kv"])
+        del src
         test_attn = test_attn.transpose(1, 2)
-        x_test = self._residual_add(residual, test_attn) if self.pre_norm else seq_norm(test_attn + residual)
+        if self.pre_norm:
+            return self._add_then_steps(residual, test_attn, post_steps, feature_atten_mask, eval_pos)
+        x_test = seq_norm(test_attn + residual)
         for step in post_steps:
             x_test = self._run_non_sequence_step(x_test, step_idx=step, feature_atten_mask=feature_atten_mask, eval_pos=eval_pos)
         return x_test

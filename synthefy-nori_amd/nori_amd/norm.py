@@ -246,9 +246,12 @@ def _row_levels(t: torch.Tensor) -> tuple[int, int, int, int, int] | None:
 
 
 def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMSNorm", *,
-                      out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                      out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
+                      x_out: torch.Tensor | None = None) -> torch.Tensor:
     """``x += alpha * u`` in place (``residual_add``'s rounding), then ``norm`` of the updated x,
     in one HIP pass (``nori_residual_add_rms_norm``), bit for bit the two separate calls.
+    ``x_out`` (contiguous fp32, x's shape) takes the sum instead of x, which is then left as
+    it is.
 
     ``norm`` is an ``RMSNorm`` without weight over x's trailing width. The result is written in
     ``out_dtype`` (default x's; a projection operand under autocast passes ``operand_dtype(x)``,
@@ -261,9 +264,11 @@ def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMS
     for n in ns:
         cols *= int(n)
     dt = (out.dtype if out is not None else (x.dtype if out_dtype is None else out_dtype))
+    xo = x if x_out is None else x_out
     fused = (
         isinstance(norm, RMSNorm) and norm.weight is None and x.is_cuda and x.dtype == torch.float32
         and x.is_contiguous() and tuple(u.shape) == tuple(x.shape) and u.device == x.device
+        and xo.dtype == torch.float32 and xo.is_contiguous() and tuple(xo.shape) == tuple(x.shape)
         and u.dtype in (torch.float32, torch.float16, torch.bfloat16) and dt in (torch.float32, torch.float16, torch.bfloat16)
         and tuple(x.shape[-len(ns):]) == ns and cols % 4 == 0 and cols <= 1024
     )
@@ -276,14 +281,18 @@ def residual_add_norm(x: torch.Tensor, u: torch.Tensor, alpha: float, norm: "RMS
             levels = None if u_levels is None else (ctypes.c_int64 * 5)(*u_levels)
             rc = nat.lib().nori_residual_add_rms_norm(
                 x.data_ptr(), u.data_ptr(), nat.dtype_code(u.dtype), levels, float(alpha), rows, cols,
-                float(norm.eps), x.data_ptr(), y.data_ptr(), nat.dtype_code(dt), group, gstride, rstride,
+                float(norm.eps), xo.data_ptr(), y.data_ptr(), nat.dtype_code(dt), group, gstride, rstride,
                 nat.stream_of(x.device),
             )
             if rc == nat.NORI_OK:
                 return y
             if rc != nat.NORI_ERR_UNSUPPORTED:
                 nat.check(rc, "residual_add_rms_norm")
-    residual_add(x, u, alpha, inplace=True)
+    if x_out is None:
+        residual_add(x, u, alpha, inplace=True)
+    else:
+        x_out.copy_(residual_add(x, u, alpha))
+        x = x_out
     if out is None:
         if dt == x.dtype:
             return norm(x)

@@ -105,3 +105,53 @@ def test_swiglu_module_matches_separate_projections(cuda):
             results.append((mlp(x), mlp.w_down(torch.nn.functional.silu(mlp.w_gate(x)) * mlp.w_up(x))))
     for a, b in results:
         check_relative(a, b, 2e-3, "stacked SwiGLU vs separate gate/up projections (fp16 autocast)")
+
+
+@pytest.mark.parametrize("layer_arch,alpha", [("smf", 18**-0.5), ("fmfmsm", None)])
+def test_dense_layer_residual_chain_is_bit_exact(cuda, layer_arch, alpha):
+    """The dense layer's pre-norm residual updates formed in the same pass as the next norm's
+    operand (``_add_then_steps``, ``nori_residual_add_rms_norm``) against the separate
+    ``residual + deepnorm_alpha * update`` (the fp32 buffer cast to the update's dtype, as
+    torch applies it) and norm of each step (layer.py:1444-1445), under fp16 autocast and in
+    fp32. alpha 18^-1/2 is not an fp16 value, so the cast matters.
+
+    * bit-identical streams when the sublayers are deterministic functions of their operands
+      (the library GEMMs may pick split-K kernels whose sums are not reproducible run to run);
+    * with the layer's own sublayers, the two orders agree to a relative 1e-3."""
+    from nori_amd.layer import EncoderBaseLayer
+
+    torch.manual_seed(5)
+    layer = EncoderBaseLayer(
+        nhead=4, embed_dim=128, hid_dim=384, pre_norm=True, activation="swiglu", norm_type="rmsnorm",
+        layer_arch=layer_arch, deepnorm_alpha=alpha, device=cuda,
+    ).eval()
+    pre_steps, seq_step, post_steps, _ = layer._cache_steps()
+    steps = list(pre_steps) or list(post_steps)
+    assert layer.deepnorm_alpha is None or layer.deepnorm_alpha.device.type == "cpu"
+    _chain_cases(layer, steps, cuda, layer_arch)
+    layer.to(cuda)  # the buffer on the device: torch casts it to the update's dtype first
+    _chain_cases(layer, steps, cuda, layer_arch)
+
+
+def _chain_cases(layer, steps, cuda, layer_arch):
+    x = torch.randn(2, 40, 9, 128, device=cuda)
+    update = torch.randn(2, 40, 9, 128, device=cuda) * 2.0
+    own_steps = list(layer.layer_steps)
+    synthetic = [lambda op, k=k: (torch.tanh(op.float() * (1.1 + 0.3 * k)) * 3.0).to(op.dtype) for k in range(len(own_steps))]
+    for sublayers, exact in ((synthetic, True), (own_steps, False)):
+        layer.layer_steps = sublayers
+        for autocast in (True, False):
+            with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+                u = update.half() if autocast else update
+                ref = layer._residual_add(x, u)
+                for step in steps:
+                    ref = layer._run_non_sequence_step(ref, step_idx=step, feature_atten_mask=None, eval_pos=40)
+                x0 = x.clone()
+                got = layer._add_then_steps(x, u, steps, None, 40)
+            torch.cuda.synchronize()
+            assert torch.equal(x, x0), "the input stream was modified"
+            if exact:
+                assert torch.equal(got, ref), f"{layer_arch} autocast={autocast}: max diff {float((got - ref).abs().max())}"
+            else:
+                check_relative(got, ref, 1e-3, f"{layer_arch} residual chain with the layer's sublayers")
+    layer.layer_steps = own_steps
