@@ -820,6 +820,11 @@ struct Prologue {
 // The short-context kernel (icl_attention_short.hip): one launch over every (b, h, query) row.
 int launch_short(int kv_dtype, const Args& a, const Prologue& pro, hipStream_t stream);
 
+// The few-token MFMA kernel (icl_attention_tile.hip): a wavefront per (b, h, 32-query tile)
+// over the unit's whole context; tile_shape() says which calls it takes.
+bool tile_shape(int q_dtype, int kv_dtype, int64_t nq, int64_t nk, int d, uint32_t flags);
+int launch_tile(Args a, hipStream_t stream);
+
 // Few queries attending to few keys: the VALU kernel, whose cost grows with nq * nk, beats the
 // MFMA kernel's fixed cost per (b, h) unit (a 64-query tile over a staged 64-key block).
 constexpr bool short_context(int64_t nq, int64_t nk) { return nq <= 64 && nk <= 128 && nq * nk <= 2048; }

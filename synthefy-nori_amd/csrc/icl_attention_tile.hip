@@ -1,0 +1,195 @@
+// Attention among few tokens on the MFMA units: up to 64 queries over up to 64 keys per (b, h)
+// unit, head width up to 64, fp16 queries and keys/values. This is the feature attention over
+// a row's tokens (MultiheadAttention.forward with combined QKV, src/synthefy_nori/model/
+// layer.py:1062-1162) at widths past the short-context kernel's (51 tokens of nori-100m's
+// tables: 51 x 51 query-key pairs, heads of 56): hundreds of thousands of (row, head) units
+// of a few thousand pairs each.
+//
+// One wavefront owns a (b, h, 32-query tile) unit and the unit's whole context (two 32-key
+// steps at most), so there is no online rescaling and no block pipeline:
+//   * S^T [keys x 32 queries] on v_mfma_f32_32x32x16_f16, K rows (A) and Q rows (B) loaded
+//     from global straight into operand registers;
+//   * an exact softmax per query over the lane's logits and its partner lane's (l ^ 32);
+//   * V staged row-major into the wavefront's LDS region and read back transposed
+//     (ds_read_b64_tr_b16) as the A operand of v_mfma_f32_16x16x32_f16, the probabilities
+//     swapped into its B operand (v_permlane16_swap) -- the long-context kernel's PV step;
+//   * O divided by the denominator and written in the output dtype (and the natural-log LSE
+//     when asked).
+// Wavefronts share nothing, so the workgroup has no barrier.
+#include "icl_attention_kernel.h"
+
+namespace nori {
+namespace attn {
+namespace {
+
+constexpr int kTileWaves = 4;
+
+__device__ __forceinline__ f16x8 load_row8(const uint16_t* p, int c0, int d) {
+    // 8 consecutive fp16 from element c0 of a row of d (d a multiple of 4): two 8-byte loads,
+    // zero past d
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    u32x2_t lo = u32x2_t{0u, 0u}, hi = u32x2_t{0u, 0u};
+    if (c0 < d) lo = *reinterpret_cast<const u32x2_t*>(p + c0);
+    if (c0 + 4 < d) hi = *reinterpret_cast<const u32x2_t*>(p + c0 + 4);
+    return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+
+template <int DP>
+__global__ void __launch_bounds__(64 * kTileWaves)
+icl_attention_tile_kernel(const Args a, int64_t nunits) {
+    using G = Geometry<DP, 16>;
+    constexpr int KS = DP / 16;  // logit k-steps
+    constexpr int VT = DP / 16;  // 16-row tiles of O^T
+    constexpr int VREG = 2 * G::VSTEP;  // f16 of a wavefront's V rows (64 keys)
+    __shared__ __attribute__((aligned(16))) _Float16 vbuf[kTileWaves * VREG];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int64_t unit = (int64_t)blockIdx.x * kTileWaves + wave;
+    if (unit >= nunits) return;  // whole wavefronts; no barrier follows
+    const int nqt = a.nqt;
+    const int qt = (int)(unit % nqt);
+    const int h = (int)((unit / nqt) % a.heads);
+    const int64_t b = unit / nqt / a.heads;
+    const int hk = h / a.hgroup;
+    const int d = a.d, nq = (int)a.nq, nk = (int)a.nk;
+    const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q) + b * a.q_bg + (int64_t)h * a.q_head;
+    const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.kv) + b * a.kv_bg + (int64_t)hk * d;
+    const uint16_t* vb = kb + a.kv_half;
+
+    // ---- V rows [0, 64) of the unit into this wavefront's LDS region (zeros past nk and d),
+    // 4 elements a lane per pass, in the long-context kernel's V row layout
+    _Float16* vw = vbuf + wave * VREG;
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    for (int p = lane; p < 64 * (DP / 4); p += 64) {
+        const int r = p / (DP / 4), c = 4 * (p % (DP / 4));
+        u32x2_t v = u32x2_t{0u, 0u};
+        if (r < nk && c < d) v = *reinterpret_cast<const u32x2_t*>(vb + (int64_t)r * a.kv_row + c);
+        *reinterpret_cast<u32x2_t*>(&vw[G::vrow(r) + c]) = v;
+    }
+
+    // ---- S^T for the (at most two) 32-key steps: lane holds keys 32kt + 8j + 4hh + i of
+    // query 32qt + l32
+    f16x8 qf[KS];
+    {
+        const int qr = 32 * qt + l32;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            qf[s] = qr < nq ? load_row8(qb + (int64_t)qr * a.q_row, 16 * s + 8 * hh, d) : f16x8{};
+    }
+    const int nks = (nk + 31) / 32;  // 1 or 2, uniform
+    f32x16 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+        st[kt] = f32x16{};
+        if (kt >= nks) break;
+        const int kr = 32 * kt + l32;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const f16x8 kf = kr < nk ? load_row8(kb + (int64_t)kr * a.kv_row, 16 * s + 8 * hh, d) : f16x8{};
+            st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st[kt], 0, 0, 0);
+        }
+    }
+
+    // ---- exact softmax in base 2 over the lane's 32 logits and its partner's
+    float x[2][16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+            x[kt][e] = key < nk ? st[kt][e] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, x[kt][e]);
+        }
+    mx = fmaxf(mx, other_half(mx));  // key 0 is valid: finite
+    float lsum = 0.f;
+    uint32_t pw[2][8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float p0 = __builtin_amdgcn_exp2f(x[kt][2 * t] - mx), p1 = __builtin_amdgcn_exp2f(x[kt][2 * t + 1] - mx);
+            const f16x2 pp = f16x2{(_Float16)p0, (_Float16)p1};
+            lsum += (float)pp[0] + (float)pp[1];  // the probabilities PV sums, as rounded
+            pw[kt][t] = __builtin_bit_cast(uint32_t, pp);
+        }
+    lsum += other_half(lsum);
+
+    // ---- O^T += V^T P^T per 32-key step (the long-context kernel's operand layouts)
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's V rows are in LDS
+    __builtin_amdgcn_wave_barrier();
+    const int vg = lane >> 4, vt = lane & 15;
+    const int v_lane = G::vrow(16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) + 4 * (vt & 3);
+    const lds_f16* vl0 = (const lds_f16*)vw + v_lane;
+    f32x4 o[VT][2];
+#pragma unroll
+    for (int t = 0; t < VT; ++t) o[t][0] = o[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+        if (kt >= nks) break;
+        u32x4 pa, pb;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const auto r = __builtin_amdgcn_permlane16_swap(pw[kt][t], pw[kt][t + 4], false, false);
+            pa[t] = r[0];
+            pb[t] = r[1];
+        }
+        const f16x8 p0 = __builtin_bit_cast(f16x8, pa), p1 = __builtin_bit_cast(f16x8, pb);
+        const lds_f16* vl = vl0 + kt * G::VSTEP;
+#pragma unroll
+        for (int t = 0; t < VT; ++t) {
+            const f16x4 lo = read_tr16(vl + 16 * t);
+            const f16x4 hi = read_tr16(vl + 8 * G::VPITCH + 16 * t);
+            const f16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            o[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p0, o[t][0], 0, 0, 0);
+            o[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, p1, o[t][1], 0, 0, 0);
+        }
+    }
+
+    // ---- epilogue: tile (t, qb) holds rows 16t + 4(lane/16) + 0..3 of query 16qb + lane%16
+#pragma unroll
+    for (int qbk = 0; qbk < 2; ++qbk) {
+        const int src = 16 * qbk + (lane & 15);  // the S^T lane holding this query's sums
+        const float l = lane_value(lsum, src), m = lane_value(mx, src);
+        const int qo = 32 * qt + src;
+        if (qo >= nq) continue;
+        const float inv = 1.0f / l;
+        const int64_t obase = b * a.o_bg + (int64_t)qo * a.o_row + (int64_t)h * a.o_head;
+#pragma unroll
+        for (int t = 0; t < VT; ++t) {
+            const int d0 = 16 * t + 4 * (lane >> 4);
+            if (d0 < d) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_from_f32(a.out, a.out_dtype, obase + d0 + i, o[t][qbk][i] * inv);
+            }
+        }
+        if (a.lse && (lane >> 4) == 0) a.lse[(b * a.heads + h) * a.nq + qo] = (m + __log2f(l)) * kLn2;
+    }
+}
+
+}  // namespace
+
+// Shapes the tile kernel takes: fp16 queries and cache, at most 64 queries over at most 64
+// keys, heads up to 64 wide, no running-output merge.
+bool tile_shape(int q_dtype, int kv_dtype, int64_t nq, int64_t nk, int d, uint32_t flags) {
+    return q_dtype == NORI_F16 && kv_dtype == NORI_F16 && nq <= 64 && nk <= 64 && d <= 64 && !(flags & NORI_ATTN_MERGE);
+}
+
+int launch_tile(Args a, hipStream_t stream) {
+    a.nqt = (int)((a.nq + 31) / 32);
+    const int64_t nunits = a.bg * a.heads * (int64_t)a.nqt;
+    const int64_t grid = (nunits + kTileWaves - 1) / kTileWaves;
+    if (grid > 0x7fffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: too many (b, h) units for one launch");
+    const int dp = (a.d + 15) / 16 * 16;
+    const dim3 g((unsigned)grid), blk(64 * kTileWaves);
+    switch (dp) {
+        case 16: hipLaunchKernelGGL(icl_attention_tile_kernel<16>, g, blk, 0, stream, a, nunits); break;
+        case 32: hipLaunchKernelGGL(icl_attention_tile_kernel<32>, g, blk, 0, stream, a, nunits); break;
+        case 48: hipLaunchKernelGGL(icl_attention_tile_kernel<48>, g, blk, 0, stream, a, nunits); break;
+        default: hipLaunchKernelGGL(icl_attention_tile_kernel<64>, g, blk, 0, stream, a, nunits); break;
+    }
+    return NORI_OK;
+}
+
+}  // namespace attn
+}  // namespace nori

@@ -506,3 +506,39 @@ def test_int8_scales_outside_the_f16_range(cuda):
                                             offload=True)
     with pytest.raises(NotImplementedError, match="fp16 range"):
         nori_amd.compute_attention_blockwise(q, blocks)
+
+
+@pytest.mark.parametrize("d", [8, 16, 44, 56, 64])
+@pytest.mark.parametrize("nq,nk", [(51, 51), (33, 64), (64, 64), (40, 60), (64, 33)])
+def test_few_token_tile_path(cuda, d, nq, nk):
+    """Up to 64 fp16 queries over up to 64 fp16 keys past the short-context kernel's 2048
+    query-key pairs take the few-token MFMA kernel (a wavefront per (b, h, 32-query tile),
+    exact softmax over the unit's whole context): the feature attention over a row's tokens of
+    a 100-feature table (51 tokens). GQA (4 query heads on 2 K/V heads) and the LSE output
+    against the float64 oracle; a running-output merge keeps the long-context kernel."""
+    assert not attn.short_context(nq, nk)
+    bg, heads, kv_heads = 29, 4, 2
+    kv = make_cache(bg, nk, kv_heads, d, cuda, seed=3 * d + nk)
+    q = make_queries(bg, nq, heads, d, cuda, seed=d + nq, dtype=torch.float16, gain=2.0)
+    lse = torch.empty(bg, heads, nq, device=cuda)
+    got = nori_amd.icl_attention(q, kv, lse=lse)
+    exp, exp_lse = reference(q, kv.double())
+    check(got, exp)
+    assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, kv.double(), heads // kv_heads)).all()
+    run = torch.zeros(bg, nq, heads, d, device=cuda)
+    lse2 = torch.full((bg, heads, nq), float("-inf"), device=cuda)
+    for sl in (slice(0, nk // 2), slice(nk // 2, nk)):
+        nori_amd.icl_attention(q, kv[:, sl], out=run, lse=lse2, merge=True)
+    check(run, exp)
+
+
+def test_few_token_tile_path_on_a_qkv_projection(cuda):
+    """The feature attention's own layout: q and K/V as strided views into one [rows, tokens,
+    3, heads, d] projection (nori-100m dims: 51 tokens, 10 heads of 56), fp16 output."""
+    rows, tokens, heads, d = 700, 51, 10, 56
+    g = torch.Generator().manual_seed(9)
+    qkv = torch.randn(rows, tokens, 3, heads, d, generator=g).half().to(cuda)
+    got = nori_amd.icl_attention(qkv[:, :, 0], qkv[:, :, 1:])
+    assert got.dtype == torch.float16
+    exp, _ = reference(qkv[:, :, 0], qkv[:, :, 1:].double())
+    check(got.float(), exp)
