@@ -5,17 +5,17 @@
 // tables: 51 x 51 query-key pairs, heads of 56): hundreds of thousands of (row, head) units
 // of a few thousand pairs each.
 //
-// One wavefront owns a (b, h, 32-query tile) unit and the unit's whole context (two 32-key
-// steps at most), so there is no online rescaling and no block pipeline:
+// One wavefront owns a (b, h, 32-query tile) and the unit's whole context (two 32-key steps at
+// most), so there is no online rescaling and no block pipeline:
 //   * S^T [keys x 32 queries] on v_mfma_f32_32x32x16_f16, K rows (A) and Q rows (B) loaded
 //     from global straight into operand registers;
 //   * an exact softmax per query over the lane's logits and its partner lane's (l ^ 32);
-//   * V staged row-major into the wavefront's LDS region and read back transposed
+//   * V staged row-major into the unit's LDS region (by both query tiles' wavefronts, one
+//     workgroup barrier) and read back transposed
 //     (ds_read_b64_tr_b16) as the A operand of v_mfma_f32_16x16x32_f16, the probabilities
 //     swapped into its B operand (v_permlane16_swap) -- the long-context kernel's PV step;
 //   * O divided by the denominator and written in the output dtype (and the natural-log LSE
 //     when asked).
-// Wavefronts share nothing, so the workgroup has no barrier.
 #include "icl_attention_kernel.h"
 
 namespace nori {
@@ -24,48 +24,67 @@ namespace {
 
 constexpr int kTileWaves = 4;
 
-__device__ __forceinline__ f16x8 load_row8(const uint16_t* p, int c0, int d) {
-    // 8 consecutive fp16 from element c0 of a row of d (d a multiple of 4): two 8-byte loads,
-    // zero past d
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    u32x2_t lo = u32x2_t{0u, 0u}, hi = u32x2_t{0u, 0u};
-    if (c0 < d) lo = *reinterpret_cast<const u32x2_t*>(p + c0);
-    if (c0 + 4 < d) hi = *reinterpret_cast<const u32x2_t*>(p + c0 + 4);
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// 4 fp16 at element c of row r of a [rows, d] matrix with row stride rs, zero when r >= rows
+// or c >= d (d a multiple of 4). The load always happens, at a clamped address inside the
+// matrix, and the value is selected away: no branch, so the loads of a row block issue
+// back to back.
+__device__ __forceinline__ u32x2_t load4(const uint16_t* base, int64_t rs, int r, int rows, int c, int d) {
+    const bool ok = r < rows && c < d;
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(base + (int64_t)min(r, rows - 1) * rs + min(c, d - 4));
+    return ok ? v : u32x2_t{0u, 0u};
+}
+
+// 8 consecutive fp16 from element c0 of row r (zeros past d or past the rows)
+__device__ __forceinline__ f16x8 load_row8(const uint16_t* base, int64_t rs, int r, int rows, int c0, int d) {
+    const u32x2_t lo = load4(base, rs, r, rows, c0, d), hi = load4(base, rs, r, rows, c0 + 4, d);
     return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
 
-template <int DP>
+template <int DP, int NQT>
 __global__ void __launch_bounds__(64 * kTileWaves)
-icl_attention_tile_kernel(const Args a, int64_t nunits) {
+icl_attention_tile_kernel(const Args a, int64_t nbh) {
     using G = Geometry<DP, 16>;
     constexpr int KS = DP / 16;  // logit k-steps
     constexpr int VT = DP / 16;  // 16-row tiles of O^T
-    constexpr int VREG = 2 * G::VSTEP;  // f16 of a wavefront's V rows (64 keys)
-    __shared__ __attribute__((aligned(16))) _Float16 vbuf[kTileWaves * VREG];
+    constexpr int VREG = 2 * G::VSTEP;  // f16 of a unit's V rows (64 keys)
+    constexpr int UPW = kTileWaves / NQT;  // (b, h) units per workgroup, NQT wavefronts each
+    __shared__ __attribute__((aligned(16))) _Float16 vbuf[UPW * VREG];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-    const int64_t unit = (int64_t)blockIdx.x * kTileWaves + wave;
-    if (unit >= nunits) return;  // whole wavefronts; no barrier follows
-    const int nqt = a.nqt;
-    const int qt = (int)(unit % nqt);
-    const int h = (int)((unit / nqt) % a.heads);
-    const int64_t b = unit / nqt / a.heads;
+    const int lu = wave / NQT, qt = wave % NQT;
+    const int64_t unit = (int64_t)blockIdx.x * UPW + lu;  // (b, h)
+    const bool active = unit < nbh;                        // uniform over the wavefront
+    const int64_t uc = active ? unit : nbh - 1;            // a valid unit for inactive wavefronts
+    const int h = (int)(uc % a.heads);
+    const int64_t b = uc / a.heads;
     const int hk = h / a.hgroup;
     const int d = a.d, nq = (int)a.nq, nk = (int)a.nk;
     const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q) + b * a.q_bg + (int64_t)h * a.q_head;
     const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.kv) + b * a.kv_bg + (int64_t)hk * d;
     const uint16_t* vb = kb + a.kv_half;
 
-    // ---- V rows [0, 64) of the unit into this wavefront's LDS region (zeros past nk and d),
-    // 4 elements a lane per pass, in the long-context kernel's V row layout
-    _Float16* vw = vbuf + wave * VREG;
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    for (int p = lane; p < 64 * (DP / 4); p += 64) {
-        const int r = p / (DP / 4), c = 4 * (p % (DP / 4));
-        u32x2_t v = u32x2_t{0u, 0u};
-        if (r < nk && c < d) v = *reinterpret_cast<const u32x2_t*>(vb + (int64_t)r * a.kv_row + c);
-        *reinterpret_cast<u32x2_t*>(&vw[G::vrow(r) + c]) = v;
+    // ---- V rows [0, 64) of the unit into its LDS region (zeros past nk and d), in the
+    // long-context kernel's V row layout; the unit's NQT wavefronts share the rows, each
+    // loading every NQT-th 4-element piece, all loads issued before the first LDS write
+    _Float16* vw = vbuf + lu * VREG;
+    constexpr int VP = DP / 4;  // pieces per row: 64 * VP pieces, VP / NQT per lane
+    {
+        u32x2_t vr[VP / NQT];
+#pragma unroll
+        for (int k = 0; k < VP / NQT; ++k) {
+            const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
+            vr[k] = load4(vb, a.kv_row, r, nk, c, d);
+        }
+#pragma unroll
+        for (int k = 0; k < VP / NQT; ++k) {
+            const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
+            *reinterpret_cast<u32x2_t*>(&vw[G::vrow(r) + c]) = vr[k];
+        }
     }
+    __syncthreads();  // the unit's V rows from both of its wavefronts; the only barrier
+    if (!active) return;
 
     // ---- S^T for the (at most two) 32-key steps: lane holds keys 32kt + 8j + 4hh + i of
     // query 32qt + l32
@@ -74,7 +93,7 @@ icl_attention_tile_kernel(const Args a, int64_t nunits) {
         const int qr = 32 * qt + l32;
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-            qf[s] = qr < nq ? load_row8(qb + (int64_t)qr * a.q_row, 16 * s + 8 * hh, d) : f16x8{};
+            qf[s] = load_row8(qb, a.q_row, qr, nq, 16 * s + 8 * hh, d);
     }
     const int nks = (nk + 31) / 32;  // 1 or 2, uniform
     f32x16 st[2];
@@ -85,7 +104,7 @@ icl_attention_tile_kernel(const Args a, int64_t nunits) {
         const int kr = 32 * kt + l32;
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            const f16x8 kf = kr < nk ? load_row8(kb + (int64_t)kr * a.kv_row, 16 * s + 8 * hh, d) : f16x8{};
+            const f16x8 kf = load_row8(kb, a.kv_row, kr, nk, 16 * s + 8 * hh, d);
             st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st[kt], 0, 0, 0);
         }
     }
@@ -116,8 +135,6 @@ icl_attention_tile_kernel(const Args a, int64_t nunits) {
     lsum += other_half(lsum);
 
     // ---- O^T += V^T P^T per 32-key step (the long-context kernel's operand layouts)
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's V rows are in LDS
-    __builtin_amdgcn_wave_barrier();
     const int vg = lane >> 4, vt = lane & 15;
     const int v_lane = G::vrow(16 * (vg & 1) + 4 * (vg >> 1) + (vt >> 2)) + 4 * (vt & 3);
     const lds_f16* vl0 = (const lds_f16*)vw + v_lane;
@@ -175,19 +192,24 @@ bool tile_shape(int q_dtype, int kv_dtype, int64_t nq, int64_t nk, int d, uint32
     return q_dtype == NORI_F16 && kv_dtype == NORI_F16 && nq <= 64 && nk <= 64 && d <= 64 && !(flags & NORI_ATTN_MERGE);
 }
 
+template <int NQT>
+void launch_nqt(const Args& a, int64_t nbh, int dp, hipStream_t stream) {
+    const dim3 g((unsigned)((nbh + kTileWaves / NQT - 1) / (kTileWaves / NQT))), blk(64 * kTileWaves);
+    switch (dp) {
+        case 16: hipLaunchKernelGGL((icl_attention_tile_kernel<16, NQT>), g, blk, 0, stream, a, nbh); break;
+        case 32: hipLaunchKernelGGL((icl_attention_tile_kernel<32, NQT>), g, blk, 0, stream, a, nbh); break;
+        case 48: hipLaunchKernelGGL((icl_attention_tile_kernel<48, NQT>), g, blk, 0, stream, a, nbh); break;
+        default: hipLaunchKernelGGL((icl_attention_tile_kernel<64, NQT>), g, blk, 0, stream, a, nbh); break;
+    }
+}
+
 int launch_tile(Args a, hipStream_t stream) {
     a.nqt = (int)((a.nq + 31) / 32);
-    const int64_t nunits = a.bg * a.heads * (int64_t)a.nqt;
-    const int64_t grid = (nunits + kTileWaves - 1) / kTileWaves;
-    if (grid > 0x7fffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: too many (b, h) units for one launch");
+    const int64_t nbh = a.bg * a.heads;
+    if (nbh > 0x7fffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: too many (b, h) units for one launch");
     const int dp = (a.d + 15) / 16 * 16;
-    const dim3 g((unsigned)grid), blk(64 * kTileWaves);
-    switch (dp) {
-        case 16: hipLaunchKernelGGL(icl_attention_tile_kernel<16>, g, blk, 0, stream, a, nunits); break;
-        case 32: hipLaunchKernelGGL(icl_attention_tile_kernel<32>, g, blk, 0, stream, a, nunits); break;
-        case 48: hipLaunchKernelGGL(icl_attention_tile_kernel<48>, g, blk, 0, stream, a, nunits); break;
-        default: hipLaunchKernelGGL(icl_attention_tile_kernel<64>, g, blk, 0, stream, a, nunits); break;
-    }
+    if (a.nqt == 1) launch_nqt<1>(a, nbh, dp, stream);
+    else launch_nqt<2>(a, nbh, dp, stream);
     return NORI_OK;
 }
 
