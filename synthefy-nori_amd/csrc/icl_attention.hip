@@ -238,7 +238,7 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     if (args.grid * plan.nw * 64 > 0xffffffffLL) return fail(NORI_ERR_UNSUPPORTED, "icl_attention: grid too large");
 
     hipStream_t stream = (hipStream_t)stream_v;
-    if (!plan.short_ctx && tile_shape(q_dtype, kv_dtype, nq, nk, d, flags)) {
+    if (tile_shape(q_dtype, kv_dtype, nq, nk, d, flags) && !pro && (!plan.short_ctx || nq > 16)) {
         const int st = launch_tile(args, stream);
         return st != NORI_OK ? st : launch_status("icl_attention tile");
     }

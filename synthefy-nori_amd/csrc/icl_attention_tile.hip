@@ -43,8 +43,8 @@ __device__ __forceinline__ f16x8 load_row8(const uint16_t* base, int64_t rs, int
 }
 
 template <int DP, int NQT>
-__global__ void __launch_bounds__(64 * kTileWaves)
-icl_attention_tile_kernel(const Args a, int64_t nbh) {
+__global__ void __launch_bounds__(64 * kTileWaves, 3)
+icl_attention_tile_kernel(const Args a, int64_t nbh, int vec_f16) {
     using G = Geometry<DP, 16>;
     constexpr int KS = DP / 16;  // logit k-steps
     constexpr int VT = DP / 16;  // 16-row tiles of O^T
@@ -65,48 +65,45 @@ icl_attention_tile_kernel(const Args a, int64_t nbh) {
     const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.kv) + b * a.kv_bg + (int64_t)hk * d;
     const uint16_t* vb = kb + a.kv_half;
 
-    // ---- V rows [0, 64) of the unit into its LDS region (zeros past nk and d), in the
-    // long-context kernel's V row layout; the unit's NQT wavefronts share the rows, each
-    // loading every NQT-th 4-element piece, all loads issued before the first LDS write
-    _Float16* vw = vbuf + lu * VREG;
+    // ---- every global load of the wavefront issued before its first wait: its share of the
+    // unit's V rows [0, 64) (zeros past nk and d; the unit's NQT wavefronts each load every
+    // NQT-th 4-element piece), its 32 Q rows and the K rows of both 32-key steps (rows past
+    // nk clamped to row nk - 1: their logits are masked)
     constexpr int VP = DP / 4;  // pieces per row: 64 * VP pieces, VP / NQT per lane
-    {
-        u32x2_t vr[VP / NQT];
+    u32x2_t vr[VP / NQT];
 #pragma unroll
-        for (int k = 0; k < VP / NQT; ++k) {
-            const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
-            vr[k] = load4(vb, a.kv_row, r, nk, c, d);
-        }
-#pragma unroll
-        for (int k = 0; k < VP / NQT; ++k) {
-            const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
-            *reinterpret_cast<u32x2_t*>(&vw[G::vrow(r) + c]) = vr[k];
-        }
+    for (int k = 0; k < VP / NQT; ++k) {
+        const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
+        vr[k] = load4(vb, a.kv_row, r, nk, c, d);
     }
-    __syncthreads();  // the unit's V rows from both of its wavefronts; the only barrier
+    f16x8 qf[KS], kf[2][KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = load_row8(qb, a.q_row, 32 * qt + l32, nq, 16 * s + 8 * hh, d);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kf[kt][s] = load_row8(kb, a.kv_row, 32 * kt + l32, nk, 16 * s + 8 * hh, d);
+
+    // ---- V into the unit's LDS region, in the long-context kernel's V row layout
+    _Float16* vw = vbuf + lu * VREG;
+#pragma unroll
+    for (int k = 0; k < VP / NQT; ++k) {
+        const int p = lane + 64 * (qt + NQT * k), r = p / VP, c = 4 * (p % VP);
+        *reinterpret_cast<u32x2_t*>(&vw[G::vrow(r) + c]) = vr[k];
+    }
+    __syncthreads();  // the unit's V rows from all of its wavefronts; the only barrier
     if (!active) return;
 
     // ---- S^T for the (at most two) 32-key steps: lane holds keys 32kt + 8j + 4hh + i of
     // query 32qt + l32
-    f16x8 qf[KS];
-    {
-        const int qr = 32 * qt + l32;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-            qf[s] = load_row8(qb, a.q_row, qr, nq, 16 * s + 8 * hh, d);
-    }
     const int nks = (nk + 31) / 32;  // 1 or 2, uniform
     f32x16 st[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
         st[kt] = f32x16{};
         if (kt >= nks) break;
-        const int kr = 32 * kt + l32;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const f16x8 kf = load_row8(kb, a.kv_row, kr, nk, 16 * s + 8 * hh, d);
-            st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st[kt], 0, 0, 0);
-        }
+        for (int s = 0; s < KS; ++s) st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kt][s], qf[s], st[kt], 0, 0, 0);
     }
 
     // ---- exact softmax in base 2 over the lane's 32 logits and its partner's
@@ -175,7 +172,13 @@ icl_attention_tile_kernel(const Args a, int64_t nbh) {
 #pragma unroll
         for (int t = 0; t < VT; ++t) {
             const int d0 = 16 * t + 4 * (lane >> 4);
-            if (d0 < d) {
+            if (d0 >= d) continue;
+            if (vec_f16) {  // the lane's 4 consecutive elements in one 8-byte store
+                const f16x2 lo = {(_Float16)(o[t][qbk][0] * inv), (_Float16)(o[t][qbk][1] * inv)};
+                const f16x2 hi = {(_Float16)(o[t][qbk][2] * inv), (_Float16)(o[t][qbk][3] * inv)};
+                *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(a.out) + obase + d0) =
+                    u32x2_t{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+            } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) store_from_f32(a.out, a.out_dtype, obase + d0 + i, o[t][qbk][i] * inv);
             }
@@ -194,12 +197,15 @@ bool tile_shape(int q_dtype, int kv_dtype, int64_t nq, int64_t nk, int d, uint32
 
 template <int NQT>
 void launch_nqt(const Args& a, int64_t nbh, int dp, hipStream_t stream) {
+    // fp16 output whose rows and heads start on 8-byte boundaries: 4-element stores
+    const int vec_f16 = a.out_dtype == NORI_F16 && (uintptr_t)a.out % 8 == 0 && a.o_bg % 4 == 0 && a.o_row % 4 == 0 &&
+                        a.o_head % 4 == 0;
     const dim3 g((unsigned)((nbh + kTileWaves / NQT - 1) / (kTileWaves / NQT))), blk(64 * kTileWaves);
     switch (dp) {
-        case 16: hipLaunchKernelGGL((icl_attention_tile_kernel<16, NQT>), g, blk, 0, stream, a, nbh); break;
-        case 32: hipLaunchKernelGGL((icl_attention_tile_kernel<32, NQT>), g, blk, 0, stream, a, nbh); break;
-        case 48: hipLaunchKernelGGL((icl_attention_tile_kernel<48, NQT>), g, blk, 0, stream, a, nbh); break;
-        default: hipLaunchKernelGGL((icl_attention_tile_kernel<64, NQT>), g, blk, 0, stream, a, nbh); break;
+        case 16: hipLaunchKernelGGL((icl_attention_tile_kernel<16, NQT>), g, blk, 0, stream, a, nbh, vec_f16); break;
+        case 32: hipLaunchKernelGGL((icl_attention_tile_kernel<32, NQT>), g, blk, 0, stream, a, nbh, vec_f16); break;
+        case 48: hipLaunchKernelGGL((icl_attention_tile_kernel<48, NQT>), g, blk, 0, stream, a, nbh, vec_f16); break;
+        default: hipLaunchKernelGGL((icl_attention_tile_kernel<64, NQT>), g, blk, 0, stream, a, nbh, vec_f16); break;
     }
 }
 
