@@ -227,6 +227,22 @@ int nori_swiglu_mlp(const void* x, int dtype, int64_t rows, int32_t width, int64
                     void* stream);
 
 /*
+ * QASS "full" query scaling in one pass (replaces QASSMaxScaling.forward's gate branch,
+ * src/synthefy_nori/model/layer.py:316-456, as it runs under fp16 autocast):
+ *     out[r, h] = T(T(q[r, h] * base_scale[h]) * T(1 + T(tanh(T(T(gelu(T(q[r, h] W1^T + b1))) W2^T + b2)))))
+ * with T the rounding to fp16, fp32 sums and gelu the erf form. q: [rows, heads, d] fp16 with
+ * rows q_row_stride elements apart and heads contiguous; w1: [hidden, d], b1: [hidden], w2:
+ * [d, hidden], b2: [d], base_scale: [heads, d] (log n * (1 + tanh(base_mlp(log n))), formed by
+ * the caller), all fp16 and contiguous; out like q at out_row_stride. hidden is 64; d a
+ * multiple of 4 up to 64; strides multiples of 4; q, base_scale and out 8-byte aligned. The two
+ * GEMMs sum in their own order (a value may differ from the separate ops by one fp16 ulp).
+ * Other shapes or dtypes: NORI_ERR_UNSUPPORTED (the caller keeps the separate ops).
+ */
+int nori_qass_gate(const void* q, int dtype, int64_t rows, int32_t heads, int32_t d, int64_t q_row_stride,
+                   const void* w1, const void* b1, const void* w2, const void* b2, int32_t hidden,
+                   const void* base_scale, void* out, int64_t out_row_stride, void* stream);
+
+/*
  * What the two-phase encoder's attentions do to q and k between the projection and the
  * attention (layer.py:1122-1134 with qk_norm and QASS "log_only", layer.py:433-456), applied
  * by nori_icl_attention_qk to each query row and key row as it is loaded:

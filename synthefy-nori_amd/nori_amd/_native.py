@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "nori_silu_mul": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _i64, _vp]),
     "nori_layer_norm": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _f32, _i32, _vp, _i32, _i64, _vp]),
     "nori_swiglu_mlp": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
+    "nori_qass_gate": (ctypes.c_int, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp]),
     "nori_residual_add_rms_norm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _f32, _i64, _i32, _f32, _vp, _vp, _i32, _i64, _i64,
                                                   _i64, _vp]),
     "nori_kv_project_quantize_int8": (

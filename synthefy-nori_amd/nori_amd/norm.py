@@ -367,6 +367,36 @@ def swiglu_mlp(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, hidde
     return out.view(*x.shape[:-1], width)
 
 
+QASS_GATE_HIDDEN = 64
+
+
+def qass_gate(q: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor,
+              base_scale: torch.Tensor) -> torch.Tensor:
+    """QASS "full" scaling ``q * base_scale * (1 + tanh(gate_mlp(q)))`` in one HIP pass
+    (``nori_qass_gate``): q [..., H, D] fp16, the gate MLP's weights w1 [64, D], b1 [64], w2
+    [D, 64], b2 [D] and base_scale [H, D], all fp16. QASSMaxScaling.forward under fp16
+    autocast (layer.py:316-456), with each op's fp16 rounding."""
+    h, d = q.shape[-2], q.shape[-1]
+    if w1.shape != (QASS_GATE_HIDDEN, d) or w2.shape != (d, QASS_GATE_HIDDEN) or b1.shape != (QASS_GATE_HIDDEN,) \
+            or b2.shape != (d,) or base_scale.numel() != h * d:
+        raise ValueError(f"qass_gate: weights do not match {h} heads of {d}")
+    device = nat.require_device(q, w1, b1, w2, b2, base_scale)
+    q3 = q.reshape(-1, h, d)
+    if q3.stride(-1) != 1 or q3.stride(-2) != d or q3.stride(0) % 4 or q3.data_ptr() % 8:
+        q3 = q3.contiguous()
+    w1, b1, w2, b2 = w1.contiguous(), b1.contiguous(), w2.contiguous(), b2.contiguous()
+    bs = base_scale.reshape(h, d).contiguous()
+    out = torch.empty((q3.shape[0], h, d), dtype=q.dtype, device=device)
+    nat.check(
+        nat.lib().nori_qass_gate(
+            q3.data_ptr(), nat.dtype_code(q.dtype), q3.shape[0], h, d, q3.stride(0), w1.data_ptr(), b1.data_ptr(),
+            w2.data_ptr(), b2.data_ptr(), QASS_GATE_HIDDEN, bs.data_ptr(), out.data_ptr(), h * d, nat.stream_of(device),
+        ),
+        "qass_gate",
+    )
+    return out.view(q.shape)
+
+
 def silu_mul(gu: torch.Tensor, hidden: int) -> torch.Tensor:
     """``F.silu(gu[..., :hidden]) * gu[..., hidden:]`` for the [gate | up] output of a stacked
     projection, in gu's dtype with torch's rounding of the two ops, one HIP pass

@@ -35,6 +35,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_residual_add",
             "nori_silu_mul",
             "nori_swiglu_mlp",
+            "nori_qass_gate",
             "nori_layer_norm",
             "nori_residual_add_rms_norm",
             "nori_icl_attention",
@@ -115,6 +116,22 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(mlp); bad[2] = 0
     assert lib.nori_swiglu_mlp(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_swiglu_mlp(*mlp) == nat.NORI_ERR_INVALID  # null pointers
+    # fused QASS gate: fp16 only, hidden 64, d a multiple of 4 up to 64
+    qg = [None, nat.NORI_F16, 4, 10, 56, 560, None, None, None, None, 64, None, None, 560, None]
+    bad = list(qg); bad[1] = nat.NORI_F32
+    assert lib.nori_qass_gate(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(qg); bad[10] = 32
+    assert lib.nori_qass_gate(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"hidden width 32" in lib.nori_last_error()
+    bad = list(qg); bad[4] = 68
+    assert lib.nori_qass_gate(*bad) == nat.NORI_ERR_INVALID
+    bad = list(qg); bad[4] = 54
+    assert lib.nori_qass_gate(*bad) == nat.NORI_ERR_INVALID
+    bad = list(qg); bad[5] = 500
+    assert lib.nori_qass_gate(*bad) == nat.NORI_ERR_INVALID
+    bad = list(qg); bad[2] = 0
+    assert lib.nori_qass_gate(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_qass_gate(*qg) == nat.NORI_ERR_INVALID  # null pointers
     # layer norm: float dtypes only, width a multiple of 4, eps a non-negative number
     ln = [None, nat.NORI_F16, 4, 128, 128, None, None, 1e-5, 0, None, nat.NORI_F32, 128, None]
     bad = list(ln); bad[1] = nat.NORI_I8
