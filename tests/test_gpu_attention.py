@@ -532,6 +532,23 @@ def test_few_token_tile_path(cuda, d, nq, nk):
     check(run, exp)
 
 
+def test_few_token_tile_path_at_the_config4_launch(cuda):
+    """The 51 x 51 feature attention at the size one config-4 build launch has (65,536 rows =
+    8 tables x 8,192 context rows, 10 heads of 56, q and K/V read out of one [rows, 51, 3, 10,
+    56] fp16 projection, fp16 output): 96 sampled rows against the float64 oracle, and the rows
+    bit for bit what a launch over those rows alone gives."""
+    rows, tokens, heads, d = 65536, 51, 10, 56
+    torch.manual_seed(4)
+    qkv = torch.randn(rows, tokens, 3, heads, d, device=cuda, dtype=torch.float16)
+    print(f"few-token attention at [{rows}, {tokens}, 3, {heads}, {d}]", flush=True)
+    got = nori_amd.icl_attention(qkv[:, :, 0], qkv[:, :, 1:])
+    pick = torch.randperm(rows, generator=torch.Generator().manual_seed(5))[:96].to(cuda)
+    sub = qkv[pick]
+    exp, _ = reference(sub[:, :, 0], sub[:, :, 1:].double())
+    check(got[pick].float(), exp)
+    assert torch.equal(nori_amd.icl_attention(sub[:, :, 0], sub[:, :, 1:]), got[pick])
+
+
 def test_few_token_tile_path_on_a_qkv_projection(cuda):
     """The feature attention's own layout: q and K/V as strided views into one [rows, tokens,
     3, heads, d] projection (nori-100m dims: 51 tokens, 10 heads of 56), fp16 output."""

@@ -87,6 +87,29 @@ def test_fused_gate_against_the_separate_ops(monkeypatch, heads, d):
     assert err <= 1e-2
 
 
+def test_fused_gate_at_the_config4_launch():
+    """One config-4 build sub-batch's queries (8.4 M vectors: 102 x 8192 rows, 10 heads of 56):
+    every output against the separate ops within the same bound, and the bit-identical share."""
+    m = _module(10, 56, seed=7).to(DEV)
+    q = torch.randn(102, 8192, 10, 56, device=DEV, dtype=torch.float16) * 2.0
+    print("qass gate at [102, 8192, 10, 56]", flush=True)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        m.fused = True
+        got = m(q, 8192)
+        m.fused = False
+        ref = m(q, 8192)
+        m.qass_mode = "base_only"
+        qbs = m(q, 8192)
+        m.qass_mode = "full"
+    torch.cuda.synchronize()
+    worst, same = 0.0, 0
+    for i in range(0, 102, 17):  # in slices: the float64 bound of the whole tensor is 6 GB per term
+        w, sm = _compare(got[i:i + 17], ref[i:i + 17], qbs[i:i + 17])
+        worst, same = max(worst, w), same + sm * 17 / 102
+    print(f"  vs separate ops: worst {worst:.2f} of the bound, {same:.4f} bit-identical", flush=True)
+    assert worst <= 1.0 and same >= 0.9
+
+
 def test_single_key_and_fp32_queries_keep_the_torch_path(monkeypatch):
     m = _module(2, 32, seed=5).to(DEV)
     monkeypatch.setattr(layer_mod, "qass_gate", lambda *a: pytest.fail("fused gate taken"))
