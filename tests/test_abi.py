@@ -166,6 +166,13 @@ def test_operators_refuse_cpu_tensors():
         nori_amd.icl_attention(torch.randn(2, 3, 1, 8), t)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         nori_amd.project_quantize_kv(torch.randn(5, 32), torch.randn(64, 32), 2, 16)
+    from nori_amd.norm import qass_gate
+
+    h16 = lambda *shape: torch.randn(*shape).half()  # noqa: E731
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        qass_gate(h16(1, 8, 2, 56), h16(64, 56), h16(64), h16(56, 64), h16(56), h16(2, 56))
+    with pytest.raises(ValueError, match="do not match"):  # the gate's hidden width is 64
+        qass_gate(h16(1, 8, 2, 56), h16(32, 56), h16(32), h16(56, 32), h16(56), h16(2, 56))
 
 
 def test_fused_projection_shape_errors():
