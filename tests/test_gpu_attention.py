@@ -125,8 +125,8 @@ SHORT_CACHES = {"i8": torch.float16, "f16": torch.float16, "bf16": torch.bfloat1
 @pytest.mark.parametrize("nq,nk", [(5, 7), (1, 1), (64, 32), (16, 128)])
 def test_short_context_path(cuda, d, kv_kind, nq, nk):
     """Few queries over few keys (nq <= 64, nk <= 128, nq * nk <= 2048) take the VALU kernel:
-    the in-row attentions of the two-phase encoder (fp16 caches with more than 16 queries and
-    at most 64 keys take the few-token MFMA kernel instead). GQA (4 query heads on 2 K/V
+    the in-row attentions of the two-phase encoder (fp16 caches with 8 or more queries and at
+    most 64 keys take the few-token MFMA kernel instead). GQA (4 query heads on 2 K/V
     heads), the LSE output, and the running-output merge of two context halves."""
     bg, heads, kv_heads = 37, 4, 2
     kv = make_cache(bg, nk, kv_heads, d, cuda, seed=d + nk, dtype=SHORT_CACHES[kv_kind])
@@ -510,9 +510,9 @@ def test_int8_scales_outside_the_f16_range(cuda):
 
 
 @pytest.mark.parametrize("d", [8, 16, 44, 56, 64])
-@pytest.mark.parametrize("nq,nk", [(51, 51), (33, 64), (64, 64), (40, 60), (64, 33), (33, 33), (17, 5)])
+@pytest.mark.parametrize("nq,nk", [(51, 51), (33, 64), (64, 64), (40, 60), (64, 33), (33, 33), (17, 5), (9, 9), (8, 10)])
 def test_few_token_tile_path(cuda, d, nq, nk):
-    """17 to 64 fp16 queries over up to 64 fp16 keys take the few-token MFMA kernel (a
+    """8 to 64 fp16 queries over up to 64 fp16 keys take the few-token MFMA kernel (a
     wavefront per (b, h, 32-query tile), exact softmax over the unit's whole context): the
     feature attention over a row's tokens (33 tokens at 32 features, 51 at 50). GQA (4 query
     heads on 2 K/V heads) and the LSE output against the float64 oracle; a running-output
