@@ -239,8 +239,12 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
 
     hipStream_t stream = (hipStream_t)stream_v;
     // few-token MFMA kernel from 8 queries up (8 x 10 tokens, 2 heads of 64: 0.69 against 0.84 ms
-    // on the short-context kernel, which stays ahead at 4 queries and fewer: 0.36 against 0.68)
-    if (tile_shape(q_dtype, kv_dtype, nq, nk, d, flags) && !pro && (!plan.short_ctx || nq >= 8)) {
+    // on the short-context kernel, which stays ahead at 4 queries and fewer: 0.36 against 0.68).
+    // It reads queries 4 elements (8 bytes) at a time, so their rows and heads must start on
+    // 4-element boundaries; other query views take the kernels below, which read them one
+    // element at a time.
+    const bool q_vec4 = (uintptr_t)q % 8 == 0 && q_bg_stride % 4 == 0 && q_row_stride % 4 == 0 && q_head_stride % 4 == 0;
+    if (tile_shape(q_dtype, kv_dtype, nq, nk, d, flags) && q_vec4 && !pro && (!plan.short_ctx || nq >= 8)) {
         const int st = launch_tile(args, stream);
         return st != NORI_OK ? st : launch_status("icl_attention tile");
     }

@@ -74,7 +74,7 @@ __device__ __forceinline__ void finish(float (&v)[4], float mean, float rstd, co
         float o = (v[k] - mean) * rstd;
         if (w) o = o * w[c0 + k];
         if (b) o = o + b[c0 + k];
-        v[k] = relu ? fmaxf(o, 0.0f) : o;
+        v[k] = relu ? (o < 0.0f ? 0.0f : o) : o;  // NaN passes through, as torch.relu keeps it
     }
 }
 

@@ -43,7 +43,8 @@ from . import ensemble
 from .memory_policy import MemoryPolicy, estimate_cache_gb, warn_quantized
 from .transformer import FeaturesTransformer
 
-__all__ = ["NORI_6M_CONFIG", "NoriRegressor", "build_model", "load_model", "quantile_dist_mean"]
+__all__ = ["NORI_6M_CONFIG", "NoriRegressor", "build_model", "context_device_bytes", "load_model", "quantile_dist_mean",
+           "retain_context"]
 
 # nori-6m, the released base model: configs/model_base.json with the tier-1 training flags of
 # scripts/train.sh:146-148 (embed 128, hidden 384, 2 heads, 16 layers, "model v2 lite": SwiGLU,
@@ -152,6 +153,65 @@ def _numeric_matrix(X, name: str) -> np.ndarray:
     return arr
 
 
+def context_device_bytes(obj) -> int:
+    """Device bytes a retained context holds: the sizes of the distinct GPU storages reachable
+    from it (tensors, dicts, lists, tuples and object attributes, 8 levels deep), each storage
+    counted once however many views of it the cache keeps (row slices of one payload, a payload
+    and its codes/scales views). Host tensors do not count: they are not what runs the GPU out
+    of memory. predictor.py:2151-2189 walks a bundle the same way."""
+    storages: dict[int, int] = {}
+    seen: set[int] = set()
+
+    def walk(o, depth: int) -> None:
+        if depth > 8 or id(o) in seen:
+            return
+        seen.add(id(o))
+        if isinstance(o, torch.Tensor):
+            if o.device.type == "cuda":
+                st = o.untyped_storage()
+                storages[st.data_ptr()] = st.nbytes()
+            return
+        if isinstance(o, dict):
+            for v in o.values():
+                walk(v, depth + 1)
+        elif isinstance(o, (list, tuple, set)):
+            for v in o:
+                walk(v, depth + 1)
+        elif hasattr(o, "__dict__"):
+            for v in vars(o).values():
+                walk(v, depth + 1)
+
+    try:
+        walk(obj, 0)
+    except Exception:  # accounting must never break a predict
+        return 0
+    return sum(storages.values())
+
+
+def retain_context(contexts: dict, slot, entry, budget: int | None, size_of=context_device_bytes) -> bool:
+    """Keep ``entry`` (whose last element is the context) in ``contexts`` under ``slot`` within a
+    byte budget across every retained context (predictor.py:2110-2261): with no budget (no
+    measurable device memory) it is kept; a context larger than the whole budget empties the
+    store and is not kept (reuse is worth nothing if holding it leaves no room to run the
+    model); otherwise the least recently used contexts (the dict's insertion order; a reuse hit
+    moves its slot to the end) are dropped until the new one fits. Returns whether it was kept."""
+    contexts.pop(slot, None)
+    if budget is None:
+        contexts[slot] = entry
+        return True
+    incoming = size_of(entry[-1])
+    if incoming > budget:
+        contexts.clear()
+        return False
+    total = sum(size_of(e[-1]) for e in contexts.values())
+    for old in list(contexts):
+        if total + incoming <= budget:
+            break
+        total -= size_of(contexts.pop(old)[-1])
+    contexts[slot] = entry
+    return True
+
+
 def _device(device) -> torch.device:
     if device is not None:
         return torch.device(device)
@@ -171,7 +231,13 @@ class NoriRegressor:
     None, a preset ("exact", "max_context", "off"), a dict of ``MemoryPolicy`` fields, or a
     ``MemoryPolicy``. ``mix_precision``: run the cached path under fp16 autocast (the reference
     predictor's GPU default).
+
+    Context caches are kept for reuse across calls, one per member slot, within
+    ``context_cache_budget_frac`` (0.25, the reference's share) of the device's memory in all
+    (``retain_context``).
     """
+
+    context_cache_budget_frac = 0.25
 
     def __init__(self, model_path: str | None = None, *, model=None, device=None, inference_config=None,
                  augmentations=("yj",), yj_skew_threshold: float = 10.0, seed: int = 0, quantile_collapse: str = "mean",
@@ -315,29 +381,46 @@ class NoriRegressor:
         ``yj_skew_threshold`` in magnitude: the ensemble again on the Yeo-Johnson-transformed
         target, its point prediction clipped to the transformed context range +/- 3 widths and
         mapped back, averaged with the plain one (rows whose inverse is not finite keep the plain
-        one) -- predictor.py:1880-1990."""
+        one) -- predictor.py:1880-1990. The pass is an augmentation: if the skew test or the pass
+        itself raises, the plain prediction is returned (predictor.py:1934-1943, 1995-2003), and
+        the power transform's warnings are silenced as the reference silences them."""
         if "yj" not in self.augmentations:
             return point
-        from scipy import stats
-        from sklearn.preprocessing import PowerTransformer
+        try:
+            from scipy import stats
 
-        y = np.asarray(y_norm, dtype=np.float64)
-        y = y[np.isfinite(y)]
-        if len(y) < 10:
+            y = np.asarray(y_norm, dtype=np.float64)
+            y = y[np.isfinite(y)]
+            if len(y) < 10:
+                return point
+            skew = float(stats.skew(y, bias=False))
+        except Exception:
             return point
-        skew = float(stats.skew(y, bias=False))
         if not np.isfinite(skew) or abs(skew) < self.yj_skew_threshold:
             return point
-        pt = PowerTransformer(method="yeo-johnson", standardize=True)
-        y_yj = pt.fit_transform(np.asarray(y_norm, dtype=np.float64).reshape(-1, 1)).ravel()
-        bank = self._ensemble_bank(net, x_test, y_yj.astype(np.float32), slot0=1000)
-        p_yj = self._collapse(bank, taus, collapse)
-        lo, hi = y_yj.min(), y_yj.max()
-        width = (hi - lo) * 3.0 + 1e-6
-        back = pt.inverse_transform(np.clip(p_yj, lo - width, hi + width).reshape(-1, 1)).ravel()
-        bad = ~np.isfinite(back)
-        back[bad] = point[bad]
-        return 0.5 * (point + back)
+        try:
+            import warnings
+
+            from sklearn.preprocessing import PowerTransformer
+
+            pt = PowerTransformer(method="yeo-johnson", standardize=True)
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore")
+                y_yj = pt.fit_transform(np.asarray(y_norm, dtype=np.float64).reshape(-1, 1)).ravel()
+            bank = self._ensemble_bank(net, x_test, y_yj.astype(np.float32), slot0=1000)
+            p_yj = self._collapse(bank, taus, collapse)
+            lo, hi = y_yj.min(), y_yj.max()
+            width = (hi - lo) * 3.0 + 1e-6
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore")
+                back = pt.inverse_transform(np.clip(p_yj, lo - width, hi + width).reshape(-1, 1)).ravel()
+            bad = ~np.isfinite(back)
+            back[bad] = point[bad]
+            return 0.5 * (point + back)
+        except Exception as exc:
+            print(f"  [YJ] augmentation failed ({type(exc).__name__}: {exc}), "
+                  "falling back to identity-only prediction")
+            return point
 
     def _network(self) -> FeaturesTransformer:
         if self._net is None:
@@ -398,7 +481,8 @@ class NoriRegressor:
                 yc = torch.from_numpy(y_norm).to(home)[None]
                 context = net.build_context_cache(xc, yc, **build)
                 if policy.reuse_context_cache and not streaming:
-                    self._contexts[slot] = (key, x_ctx.tobytes(), y_norm.tobytes(), context)
+                    retain_context(self._contexts, slot, (key, x_ctx.tobytes(), y_norm.tobytes(), context),
+                                   self._context_budget_bytes())
             xq = torch.from_numpy(x_test).to(torch.device("cpu") if streaming else dev)[None]
             bank = net.apply_context_cache(xq, context)[0].float()
         if not bool(torch.isfinite(bank).all()):
@@ -414,7 +498,15 @@ class NoriRegressor:
             return None
         k, xb, yb, context = held
         if k == key and xb == x_ctx.tobytes() and yb == y_norm.tobytes():
+            self._contexts[slot] = self._contexts.pop(slot)  # most recently used: evicted last
             return context
         del self._contexts[slot]
         return None
+
+    def _context_budget_bytes(self) -> int | None:
+        """Device bytes all retained contexts may hold together: a minority share of the GPU's
+        memory (predictor.py:2191-2216), None off the GPU."""
+        if self.device_.type != "cuda":
+            return None
+        return int(torch.cuda.get_device_properties(self.device_).total_memory * float(self.context_cache_budget_frac))
 

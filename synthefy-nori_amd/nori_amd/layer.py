@@ -860,7 +860,7 @@ class EncoderBaseLayer(nn.Module):
     # -------------------------------------------------------------- cache build / apply
     def _project_kv_cache_rowchunked(
         self, attn_mod, x_kv_src, copy_kv, row_chunk, *, norm=None, offload=False, quantize=False, device=None,
-        streaming=False, exact=False,
+        streaming=False, fused_write=False,
     ):
         """``attn_mod``'s K/V cache of ``x_kv_src`` [B, N, G, E], projected ``row_chunk`` rows at a
         time (reference layer.py:1482-1572).
@@ -874,7 +874,7 @@ class EncoderBaseLayer(nn.Module):
         n_rows = x_kv_src.shape[1]
         batch, groups = x_kv_src.shape[0], x_kv_src.shape[2]
         compute_device = torch.device(device) if device is not None else attn_mod.qkv_proj_weight.device
-        fused = _fused_cache_write(attn_mod, norm, copy_kv, compute_device) if quantize and not exact else None
+        fused = _fused_cache_write(attn_mod, norm, copy_kv, compute_device) if quantize and fused_write else None
 
         def host_rows():
             if x_kv_src.device != compute_device and compute_device.type == "cuda" and x_kv_src.device.type == "cpu":
@@ -921,7 +921,7 @@ class EncoderBaseLayer(nn.Module):
 
     def _forward_train_cache_memsaving(
         self, x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, row_chunk, quantize,
-        offload, device, exact=False,
+        offload, device, fused_write=False,
     ):
         """Row-bounded cache build (reference layer.py:1694-1769). Only the self-attention K/V is
         full-N and resident; the per-row steps, the self-attention queries and the stored cross
@@ -947,7 +947,7 @@ class EncoderBaseLayer(nn.Module):
         )
         test_cache = self._project_kv_cache_rowchunked(
             seq_attn_test, x_train, self.cross_share_all_kv_heads, row_chunk, norm=norm, device=device,
-            quantize=quantize, offload=offload, exact=exact,
+            quantize=quantize, offload=offload, fused_write=fused_write,
         )
         for r0 in range(0, n_rows, row_chunk):
             sl = slice(r0, min(r0 + row_chunk, n_rows))
@@ -958,7 +958,7 @@ class EncoderBaseLayer(nn.Module):
 
     def _forward_train_cache_streaming(
         self, x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, row_chunk, quantize,
-        device, *, cross_cache_offload=True, exact=False,
+        device, *, cross_cache_offload=True, fused_write=False,
     ):
         """One context layer with only ``row_chunk``-row tensors on the device (reference
         layer.py:1574-1692).
@@ -1018,7 +1018,7 @@ class EncoderBaseLayer(nn.Module):
         )
         test_cache = self._project_kv_cache_rowchunked(
             seq_attn_test, prepared, self.cross_share_all_kv_heads, row_chunk, norm=norm, device=compute_device,
-            quantize=quantize, offload=cross_cache_offload, streaming=True, exact=exact,
+            quantize=quantize, offload=cross_cache_offload, streaming=True, fused_write=fused_write,
         )
         output = write_host(
             prepared, lambda rows: run_rows(self._seq_attention_rows(rows, seq_attn_train, seq_norm, train_cache), post_steps)
@@ -1035,7 +1035,7 @@ class EncoderBaseLayer(nn.Module):
         device=None,
         stream_context: bool = False,
         _hybrid_resident_int8_prefill: bool = False,
-        exact_cache_write: bool = False,
+        fused_cache_write: bool = False,
     ):
         """Context rows through one layer, returning (x_train, {"seq_kv": cache}) (layer.py:1771-1913).
 
@@ -1045,12 +1045,13 @@ class EncoderBaseLayer(nn.Module):
         row-bounded build, ``stream_context`` / ``_hybrid_resident_int8_prefill`` the host-streamed
         one (non-serial attention only, as in the reference).
 
-        An int8 cross cache under the fp16 autocast of GPU inference is written by the fused
-        kernel (``kv_project.project_quantize_kv``: projection and quantizer in one pass, the
-        fp16 K/V never stored): its sums run in MFMA order, so a code can differ by one from the
-        separate projection-then-quantize steps where a K/V value sits on an fp16 rounding
-        boundary. ``exact_cache_write`` keeps those separate steps (the library GEMM's K/V, then
-        the exact quantizer) instead.
+        An int8 cross cache is written by the reference's separate steps -- the projection
+        (the library GEMM), then the exact quantizer -- so its codes and scales are bit for bit
+        the reference expression's on the same device. ``fused_cache_write`` (fp16 autocast of
+        GPU inference) writes it with the fused kernel instead
+        (``kv_project.project_quantize_kv``: projection and quantizer in one pass, the fp16 K/V
+        never stored), whose sums run in MFMA order, so a code can differ by one where a K/V
+        value sits on an fp16 rounding boundary.
         """
         pre_steps, seq_step, post_steps, seq_index = self._cache_steps()
         index1 = seq_index * 2 if self.seq_attn_isolated else seq_index
@@ -1076,12 +1077,12 @@ class EncoderBaseLayer(nn.Module):
             return self._forward_train_cache_streaming(
                 x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, fit_row_chunk,
                 quantize_kv_cache, device, cross_cache_offload=not _hybrid_resident_int8_prefill,
-                exact=exact_cache_write,
+                fused_write=fused_cache_write,
             )
         if fit_row_chunk:
             return self._forward_train_cache_memsaving(
                 x_train, feature_atten_mask, pre_steps, seq_step, post_steps, index1, index2, fit_row_chunk,
-                quantize_kv_cache, offload_kv_cache, device, exact=exact_cache_write,
+                quantize_kv_cache, offload_kv_cache, device, fused_write=fused_cache_write,
             )
         eval_pos = x_train.shape[1]
         seq_attn_train = self.sequence_attentions[index1]
@@ -1094,7 +1095,7 @@ class EncoderBaseLayer(nn.Module):
         )[0].transpose(1, 2)
         kv_source = (train_attn if self.seq_attn_serial else src).transpose(1, 2)
         fused = None
-        if quantize_kv_cache and not exact_cache_write:
+        if quantize_kv_cache and fused_cache_write:
             fused = _fused_cache_write(seq_attn_test, None, self.cross_share_all_kv_heads, kv_source.device)
         if fused is not None and kv_project.fusable(kv_source, fused[0], seq_attn_test.head_dim):
             # the int8 cross cache written straight from the operand rows (offloaded after)
@@ -1177,7 +1178,7 @@ class LayerStack(nn.Module):
                 device=device,
                 stream_context=stream_context,
                 _hybrid_resident_int8_prefill=hybrid,
-                exact_cache_write=kwargs.get("exact_cache_write", False),
+                fused_cache_write=kwargs.get("fused_cache_write", False),
             )
             if (quantize or offload) and not stream_context and not hybrid:
                 scale_caches([layer_cache], quantize=quantize, offload=offload, device=device)

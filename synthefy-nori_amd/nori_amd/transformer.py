@@ -533,14 +533,16 @@ class FeaturesTransformer(nn.Module):
         quantize_kv_cache: bool | None = None,
         stream_context: bool = False,
         _hybrid_resident_int8_prefill: bool = False,
-        exact_cache_write: bool = False,
+        fused_cache_write: bool = False,
     ) -> ContextCache:
         """Encode the context table once into a ``ContextCache`` (:813-959).
 
-        ``exact_cache_write`` (int8 caches under fp16 autocast): project the K/V with the
-        library GEMM and quantize them in a second pass, as the reference's separate steps do,
-        instead of the fused projection + quantizer kernel, whose MFMA summation order can move a
-        code by one where a K/V value sits on an fp16 rounding boundary.
+        int8 caches are written as the reference writes them: the K/V projection (the library
+        GEMM), then the exact quantizer, so codes and scales are bit for bit the reference
+        expression's on the same device. ``fused_cache_write`` (int8 caches under fp16 autocast)
+        opts into the fused projection + quantizer kernel instead: one pass, the fp16 K/V never
+        stored, but its MFMA summation order can move a code by one where a K/V value sits on an
+        fp16 rounding boundary.
         """
         self._require_context_cache()
         if quantize_kv_cache is not None and cache_dtype == "bf16":
@@ -581,7 +583,7 @@ class FeaturesTransformer(nn.Module):
                 raise ValueError(f"{what} requires a concrete context_row_chunk")
             return self._build_context_cache_streaming(
                 x_train, y_train[:, :eval_pos], cache_dtype=cache_dtype, fit_row_chunk=fit_row_chunk,
-                _hybrid_resident_int8_prefill=_hybrid_resident_int8_prefill, exact_cache_write=exact_cache_write,
+                _hybrid_resident_int8_prefill=_hybrid_resident_int8_prefill, fused_cache_write=fused_cache_write,
             )
 
         x_dict, _ = self._build_x_preprocess_inputs(x_train, eval_pos)
@@ -606,7 +608,7 @@ class FeaturesTransformer(nn.Module):
             offload_kv_cache=offload_kv_cache,
             fit_row_chunk=fit_row_chunk,
             device=data.device,
-            exact_cache_write=exact_cache_write,
+            fused_cache_write=fused_cache_write,
         )
         return ContextCache(
             caches=caches,
@@ -620,7 +622,7 @@ class FeaturesTransformer(nn.Module):
 
     def _build_context_cache_streaming(
         self, x_train: torch.Tensor, y_train: torch.Tensor, *, cache_dtype: str, fit_row_chunk: int,
-        _hybrid_resident_int8_prefill: bool = False, exact_cache_write: bool = False,
+        _hybrid_resident_int8_prefill: bool = False, fused_cache_write: bool = False,
     ) -> ContextCache:
         """Context cache with no full-N tensor on the device (reference transformer.py:1169-1301).
 
@@ -692,7 +694,7 @@ class FeaturesTransformer(nn.Module):
             device=device,
             stream_context=not _hybrid_resident_int8_prefill,
             _hybrid_resident_int8_prefill=_hybrid_resident_int8_prefill,
-            exact_cache_write=exact_cache_write,
+            fused_cache_write=fused_cache_write,
         )
         return ContextCache(
             caches=caches,

@@ -3,8 +3,8 @@
 The reference's module (src/synthefy_nori/inference/preprocess.py) cannot be imported here: it
 imports ``kditransform``, which this image does not have, so no member's features could be
 written as golden vectors from the reference itself. Each step is pinned instead by what fixes
-it independently of this code: the default configuration against the reference's own
-configuration file (tests/golden/default_inference_members.json), the seed draws against
+it independently of this code: the default configuration against the SHA-256 digest of the
+reference's own configuration file (tests/golden/default_inference_digest.json), the seed draws against
 Python's and numpy's generators as the reference calls them, the column operations by closed
 forms (which columns a step keeps, which products it forms, what a permutation does), the
 distribution steps by the sklearn / scipy routines the reference builds them from, and the
@@ -27,12 +27,16 @@ from sklearn.preprocessing import QuantileTransformer
 import regressor_case as case
 from nori_amd import ensemble as en
 
-GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "default_inference_members.json")
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "default_inference_digest.json")
 
 
 def test_default_members_are_the_reference_configuration():
+    # the digest of the canonical JSON form (sorted keys) of the reference's member list
     with open(GOLDEN) as f:
-        assert json.loads(json.dumps(list(en.DEFAULT_MEMBERS), sort_keys=True)) == json.load(f)
+        gold = json.load(f)
+    members = json.loads(json.dumps(list(en.DEFAULT_MEMBERS)))
+    assert len(members) == gold["members"]
+    assert hashlib.sha256(json.dumps(members, sort_keys=True).encode()).hexdigest() == gold["sha256"]
 
 
 def test_seed_slots_follow_the_reference_draws():

@@ -559,3 +559,23 @@ def test_few_token_tile_path_on_a_qkv_projection(cuda):
     assert got.dtype == torch.float16
     exp, _ = reference(qkv[:, :, 0], qkv[:, :, 1:].double())
     check(got.float(), exp)
+
+
+@pytest.mark.parametrize("offset", [1, 2])
+def test_few_token_shape_with_a_query_view_off_the_4_element_grid(cuda, offset):
+    """Few-token shapes whose query rows do not start on 4-element (8-byte) boundaries -- here
+    heads of 44 read out of rows of 44 + offset elements at element offset 1 or 2 -- are
+    routed to the kernels that read queries one element at a time (the few-token kernel reads
+    them 8 bytes at a time) and still match the float64 oracle."""
+    bg, nq, nk, heads, kv_heads, d = 13, 33, 33, 4, 2, 44
+    kv = make_cache(bg, nk, kv_heads, d, cuda, seed=77)
+    base = make_queries(bg, nq, heads, d + offset, cuda, seed=78, dtype=torch.float16, gain=2.0)
+    q = base[..., offset:]
+    assert q.stride(2) % 4 != 0 or q.storage_offset() % 4 != 0
+    lse = torch.empty(bg, heads, nq, device=cuda)
+    got = nori_amd.icl_attention(q, kv, lse=lse)
+    exp, exp_lse = reference(q, kv.double())
+    check(got, exp)
+    assert ((lse.double().cpu() - exp_lse).abs().numpy() <= lse_bound(q, kv.double(), heads // kv_heads)).all()
+    # the same values in an aligned view give the same answer to the bar
+    check(nori_amd.icl_attention(q.contiguous(), kv), exp)

@@ -12,10 +12,14 @@ codes them. Bars:
     0.5% of them different, scales within one fp16 ulp;
   * row slices written through strided views equal the whole-tensor call bit for bit;
   * the layer's int8 cache builds under autocast -- the plain whole-context build and the
-    bounded ones -- take the fused write by default and give the same caches (codes within
-    one, at most 1% of them different) and outputs as the unfused build that
-    ``exact_cache_write=True`` selects, and the reference's fp32 outputs (its own run of
-    the same stack, tests/golden/layer_cache_goldens.npz) to their tolerance.
+    bounded ones -- write the cache by the reference's separate steps by default, and take the
+    fused write only with ``fused_cache_write=True``, which gives the same caches (codes within
+    one, at most 1% of them different) and outputs as the default build, and the reference's
+    fp32 outputs (its own run of the same stack, tests/golden/layer_cache_goldens.npz) to
+    their tolerance;
+  * the default build of a nori-30m layer (embed 352, 8 heads of 44) under autocast writes
+    codes and scales equal (torch.equal) to torch's F.linear of the layer's own cache operand
+    quantized by the reference expression on the same device.
 """
 
 from __future__ import annotations
@@ -206,7 +210,7 @@ def test_int8_builds_fuse_the_cache_write(cuda, monkeypatch, tag, mode):
         x_train = torch.from_numpy(gold[f"{tag}/x_train"]).clone()
         if mode in ("plain", "rowchunk"):
             x_train = x_train.to(cuda)
-        kwargs = dict(quantize_kv_cache=True, device=cuda, exact_cache_write=not fused)
+        kwargs = dict(quantize_kv_cache=True, device=cuda, fused_cache_write=fused)
         if mode != "plain":
             kwargs.update(fit_row_chunk=ROW_CHUNK)
         if mode == "stream":
@@ -221,10 +225,10 @@ def test_int8_builds_fuse_the_cache_write(cuda, monkeypatch, tag, mode):
         return out, caches, test_out
 
     f_out, f_caches, f_test = build(True)
-    assert calls, "the int8 build did not take the fused cache write"
+    assert calls, "fused_cache_write=True did not take the fused cache write"
     calls.clear()
     u_out, u_caches, u_test = build(False)
-    assert not calls, "exact_cache_write=True still took the fused cache write"
+    assert not calls, "the default int8 build took the fused cache write"
     for fc, uc in zip(f_caches, u_caches):
         fk, uk = fc["seq_kv"], uc["seq_kv"]
         assert type(fk) is type(uk) and isinstance(fk, (ScalableSeqKV, BlockwiseSeqKV))
@@ -241,3 +245,42 @@ def test_int8_builds_fuse_the_cache_write(cuda, monkeypatch, tag, mode):
     sfx = "int8" if mode == "plain" else f"{mode}_int8"
     check(f_test, gold[f"{tag}/test_out_{sfx}"])
     check(f_out, gold[f"{tag}/train_out_{sfx}"])
+
+
+def test_default_int8_build_codes_equal_the_reference_expression_at_nori30m_dims(cuda, monkeypatch):
+    # one nori-30m layer (embed 352, 8 heads of 44, hidden 1056) over 33 tokens x 1,024 context
+    # rows: the default int8 build projects the cross cache with F.linear under fp16 autocast and
+    # codes it with the HIP quantizer; codes and scales must be torch.equal to the reference
+    # expression (kv_cache_scaling.py:29-37) applied by torch on this device to the fp16 K/V of
+    # the same operand rows (layer.py:651-683)
+    torch.manual_seed(0)
+    layer = NL.EncoderBaseLayer(
+        nhead=8, embed_dim=352, hid_dim=1056, pre_norm=True, activation="swiglu", layer_arch="smf",
+        seq_attn_isolated=True, use_qassmax=True, norm_type="rmsnorm", deepnorm_alpha=12 ** -0.5, qass_mode="full",
+    ).eval().to(cuda)
+    stack = NL.LayerStack([layer]).eval()
+    operands = []
+    real = NL.MultiheadAttention.project_kv_cache
+
+    def capture(self, x_kv, **kw):
+        operands.append((self, x_kv.detach().clone()))
+        return real(self, x_kv, **kw)
+
+    monkeypatch.setattr(NL.MultiheadAttention, "project_kv_cache", capture)
+    fused_calls = []
+    monkeypatch.setattr(nori_amd.kv_project, "project_quantize_kv", lambda *a, **k: fused_calls.append(1))
+    x = torch.randn(1, 1024, 33, 352, device=cuda)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
+        _, caches = stack.build_train_cache(x, quantize_kv_cache=True, device=cuda)
+        assert not fused_calls and len(operands) == 1
+        mod, src = operands[0]
+        w = mod.qkv_proj_weight[1:].reshape(2 * 8 * 44, 352)
+        kv = F.linear(src.reshape(-1, *src.shape[-2:]), w).view(33, 1024, 2, 8, 44)
+    assert kv.dtype == torch.float16
+    exp_q, exp_s = torch_quantize(kv)
+    got_q, got_s = caches[0]["seq_kv"].device_payload()
+    assert got_q.shape == exp_q.shape and got_s.shape == exp_s.shape
+    assert torch.equal(got_q, exp_q), f"{(got_q != exp_q).sum().item()} codes differ"
+    assert torch.equal(got_s, exp_s), f"{(got_s != exp_s).sum().item()} scales differ"
+    print(f"[parity] nori-30m default int8 build: {got_q.numel()} codes and {got_s.numel()} scales equal torch's",
+          flush=True)

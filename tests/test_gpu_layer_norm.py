@@ -111,3 +111,21 @@ def test_cell_encoder_under_autocast():
     err = float((out.cpu() - ref).abs().max() / ref.abs().max())
     print(f"cell encoder under autocast vs fp32 CPU: {err:.3e}", flush=True)
     assert err <= 2e-2  # fp16 projections against fp32 ones
+
+
+@pytest.mark.parametrize("cols", [128, 96])
+def test_relu_keeps_nan_rows(cols):
+    # an inf or NaN cell (an fp16 projection that overflowed) makes its row's statistics NaN;
+    # the fused ReLU keeps NaN as torch.relu does, so predict still sees the non-finite output
+    x = torch.randn(40, cols, device=DEV)
+    x[3, 5] = float("inf")
+    x[7, 0] = float("nan")
+    w = torch.rand(cols, device=DEV) + 0.5
+    b = torch.randn(cols, device=DEV)
+    y = layer_norm(x, w, b, 1e-5, relu=True, out_dtype=torch.float32)
+    ref = torch.relu(torch.nn.functional.layer_norm(x, (cols,), w, b, 1e-5))
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(y[3]).all()) and bool(torch.isnan(y[7]).all())
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    ok = ~torch.isnan(ref)
+    assert float((y[ok] - ref[ok]).abs().max()) <= 4e-6 * float(ref[ok].abs().max())

@@ -157,3 +157,51 @@ def test_fit_and_predict_argument_errors():
         reg.predict(x_te[:, :5])
     with pytest.raises(ValueError, match="memory preset"):
         api.NoriRegressor(model=object(), memory_policy="nope").fit(x_tr, y_tr)
+
+
+def test_retained_contexts_stay_within_the_byte_budget():
+    # predictor.py:2110-2261: retained contexts are bounded by bytes across every slot, the
+    # least recently used dropped first; one larger than the whole budget empties the store and
+    # is not kept; no budget keeps everything
+    sizes = {"a": 40, "b": 30, "c": 20, "d": 50, "huge": 101}
+    size_of = sizes.__getitem__
+    store: dict = {}
+    for slot, name in enumerate("abc"):
+        assert api.retain_context(store, slot, ("key", name), 100, size_of)
+    assert [e[-1] for e in store.values()] == ["a", "b", "c"]  # 90 of 100
+    store[0] = store.pop(0)  # a reuse hit on slot 0 ("a") makes it the most recent
+    assert api.retain_context(store, 3, ("key", "d"), 100, size_of)  # needs 50: drops "b", then "c"
+    assert [e[-1] for e in store.values()] == ["a", "d"]
+    assert api.retain_context(store, 0, ("key", "c"), 100, size_of)  # a slot's new context replaces its old one
+    assert sorted(e[-1] for e in store.values()) == ["c", "d"]
+    assert not api.retain_context(store, 5, ("key", "huge"), 100, size_of)
+    assert store == {}
+    for slot, name in enumerate("abcd"):
+        assert api.retain_context(store, slot, ("key", name), None, size_of)
+    assert len(store) == 4
+
+
+def test_context_device_bytes_counts_each_device_storage_once():
+    # host tensors do not count; views of one storage count once (CPU here: every figure is 0)
+    t = torch.zeros(10, 4)
+    assert api.context_device_bytes({"kv": t, "views": [t[:5], t[5:]]}) == 0
+    assert api.context_device_bytes(object()) == 0
+
+
+def test_yeo_johnson_pass_falls_back_to_the_plain_prediction(monkeypatch):
+    # predictor.py:1934-1957, 1995-2003: a failure inside the augmentation returns the plain
+    # prediction instead of ending predict
+    reg = api.NoriRegressor(augmentations=("yj",), yj_skew_threshold=0.5)
+    point = np.arange(5.0)
+    y = np.exp(3.0 * np.random.default_rng(0).standard_normal(200)).astype(np.float32)
+
+    def boom(*a, **k):
+        raise RuntimeError("member failed")
+
+    monkeypatch.setattr(reg, "_ensemble_bank", boom)
+    out = reg._yeo_johnson_pass(None, None, y, point, None, "mean")
+    assert out is point
+    # too few finite targets, or a skew below the threshold: the plain prediction, unchanged
+    assert reg._yeo_johnson_pass(None, None, y[:5], point, None, "mean") is point
+    reg.yj_skew_threshold = 1e9
+    assert reg._yeo_johnson_pass(None, None, y, point, None, "mean") is point
