@@ -16,7 +16,15 @@ script is the .npz data beside it, never the reference's code):
 * the ladder: the reference's ``MemoryPolicy.resolve`` (inference/memory_policy.py:1173-1300)
   over presets, fields and cache sizes, with the report keys (``model_dump``).
 
-Usage: python tests/golden/make_regressor_golden.py   (writes tests/golden/regressor_goldens.npz)
+A second fixture, tests/golden/regressor_autocast_goldens.npz, holds the same case run by the
+reference under ``torch.autocast("cpu", dtype=torch.float16)`` -- its predictor's own GPU mode
+(predictor.py:3208-3217) -- and its spread: the largest relative change of each output (point
+predictions, the 0.1 / 0.5 / 0.9 quantiles, the median, the whole bank) when the same fp16 run
+takes the context rows in three other orders (the outputs do not depend on that order except
+through the order of the sums), next to its distance from the fp32 run.
+
+Usage: python tests/golden/make_regressor_golden.py
+(writes tests/golden/regressor_goldens.npz and tests/golden/regressor_autocast_goldens.npz)
 """
 
 from __future__ import annotations
@@ -32,6 +40,7 @@ import torch
 REFERENCE_SRC = "/root/reference/src"
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "regressor_goldens.npz")
+OUT_AUTOCAST = os.path.join(HERE, "regressor_autocast_goldens.npz")
 sys.path[:0] = [os.path.dirname(HERE), os.path.join(os.path.dirname(os.path.dirname(HERE)), "synthefy-nori_amd")]
 
 import regressor_case as case  # noqa: E402
@@ -103,6 +112,43 @@ def main():
     out["case/point"] = point.numpy() * y_std + y_mean
     out["case/codes0"] = codes0[:, :128].numpy()  # layer 0's cache, first 128 context rows
     out["case/scales0"] = scales0[:, :128].numpy()
+
+    # ---- the same case under the reference's fp16 autocast, and its spread over context orders
+    def autocast_run(rows):
+        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16):
+            c = ref.build_context_cache(torch.from_numpy(x_tr[rows])[None], torch.from_numpy(y_norm[rows])[None],
+                                        cache_dtype="int8")
+            b = ref.apply_context_cache(torch.from_numpy(x_te)[None], c)[0].float()
+        p = qd.quantile_dist_mean_simple(b.double(), taus, enforce_monotone_first=True).numpy() * y_std + y_mean
+        srt = np.sort(b.numpy().astype(np.float64), axis=1) * y_std + y_mean
+        outs = {"point": p, "bank": srt, "median": 0.5 * (srt[:, 498] + srt[:, 499]) if srt.shape[1] % 2 == 0
+                else srt[:, srt.shape[1] // 2]}
+        for level in case.QUANTILE_LEVELS:
+            outs[f"q{level}"] = srt[:, int(round(level * 1000)) - 1]
+        return b.numpy(), outs
+
+    def rel(a, b):
+        return float(np.abs(np.asarray(a, np.float64) - b).max() / np.abs(b).max())
+
+    ac: dict[str, np.ndarray] = {}
+    bank_ac, outs = autocast_run(np.arange(len(x_tr)))
+    ac["bank_norm"] = bank_ac
+    ac["point"] = outs["point"]
+    fp32_sorted = np.sort(bank.numpy().astype(np.float64), axis=1) * y_std + y_mean
+    fp32_outs = {"point": out["case/point"], "bank": fp32_sorted,
+                 "median": 0.5 * (fp32_sorted[:, 498] + fp32_sorted[:, 499])}
+    for level in case.QUANTILE_LEVELS:
+        fp32_outs[f"q{level}"] = fp32_sorted[:, int(round(level * 1000)) - 1]
+    spread = {k: 0.0 for k in outs}
+    for seed in range(3):
+        _, outs_p = autocast_run(np.random.default_rng(300 + seed).permutation(len(x_tr)))
+        for k in outs:
+            spread[k] = max(spread[k], rel(outs_p[k], outs[k]))
+    for k in outs:
+        ac[f"spread/{k}"] = np.array(spread[k])
+        ac[f"vs_fp32/{k}"] = np.array(rel(outs[k], fp32_outs[k]))
+    np.savez_compressed(OUT_AUTOCAST, **ac)
+    print("fp16 autocast: spread over context orders " + ", ".join(f"{k} {v:.2e}" for k, v in spread.items()))
 
     # ---- the ladder
     rows = []

@@ -256,7 +256,8 @@ def test_default_int8_build_codes_equal_the_reference_expression_at_nori30m_dims
     torch.manual_seed(0)
     layer = NL.EncoderBaseLayer(
         nhead=8, embed_dim=352, hid_dim=1056, pre_norm=True, activation="swiglu", layer_arch="smf",
-        seq_attn_isolated=True, use_qassmax=True, norm_type="rmsnorm", deepnorm_alpha=12 ** -0.5, qass_mode="full",
+        seq_attn_isolated=True, cross_share_all_kv_heads=False, use_qassmax=True, norm_type="rmsnorm",
+        deepnorm_alpha=12 ** -0.5, qass_mode="full",
     ).eval().to(cuda)
     stack = NL.LayerStack([layer]).eval()
     operands = []

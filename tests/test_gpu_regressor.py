@@ -1,15 +1,23 @@
-"""NoriRegressor on the GPU against the reference's own nori-6m run (tests/golden/regressor_goldens.npz).
+"""NoriRegressor on the GPU against the reference's own nori-6m runs (tests/golden/regressor_goldens.npz,
+tests/golden/regressor_autocast_goldens.npz).
 
 The case (tests/regressor_case.py): a seeded random-init nori-6m model, 1024 context + 256
 query rows of 16 features, the int8 context cache. The reference ran its context-cache API on
-the CPU in fp32 with the same weights (hash-checked); here the whole path runs on the HIP
-kernels. Predictions are held to the prediction bar, max|got - exp| / max|exp| <= 1e-3, in
-fp32 (mix_precision=False). Under fp16 autocast -- the reference predictor's own GPU mode --
-every projection and the 999-level head compute and round in fp16 (so does the reference's GPU
-path), and the bank's upper levels (~9 in standardized units here) are resolved to 2^-7, so that
-mode is held to 1.5e-2 against the fp32 golden (measured: 3.1e-3 on the point predictions, up to
-9.3e-3 on the 0.9 quantile). Each check prints its figure, and the error relative to the predictions' spread
-across rows is printed beside it.
+the CPU with the same weights (hash-checked) in fp32, and again under fp16 autocast (its
+predictor's own GPU mode, predictor.py:3208-3217); here the whole path runs on the HIP kernels.
+
+* fp32 (mix_precision=False) is held to the prediction bar, max|got - exp| / max|exp| <= 1e-3,
+  against the reference's fp32 run.
+* fp16 autocast (mix_precision=True, the default) is held to the reference's fp16 autocast run.
+  Every projection and the 999-level head round to fp16 there (the bank's upper levels, ~9 in
+  standardized units, to 2^-7), and the reference's own fp16 outputs move by 3.6e-3 (0.1
+  quantile) to 1.5e-2 (0.9 quantile) when only the order of the context rows -- so of its sums --
+  changes (the golden recipe measures it over three orders and stores it). No fp16 run can be
+  held closer than that to another; each output's bar is the prediction bar or 1.5 times that
+  spread, whichever is larger. Against the fp32 run, the same factor times the reference's own
+  fp16-to-fp32 distance.
+Each check prints its figure, and the error relative to the predictions' spread across rows is
+printed beside it.
 """
 
 from __future__ import annotations
@@ -30,18 +38,22 @@ from parity import PREDICTION_BAR, check_relative
 
 pytestmark = pytest.mark.gpu
 
-AUTOCAST_BAR = 1.5e-2  # fp16 autocast against the fp32 reference run
+SPREAD_FACTOR = 1.5
 # The golden is the reference's context-cache API on the raw columns: a one-member inference
 # configuration with no steps (only constant columns dropped; config 1 has none).
 RAW = [{}]
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "regressor_goldens.npz")
+GOLDEN_AUTOCAST = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "regressor_autocast_goldens.npz")
 
 
 @pytest.fixture(scope="module")
 def gold():
     with np.load(GOLDEN, allow_pickle=False) as f:
-        return {k: f[k] for k in f.files}
+        g = {k: f[k] for k in f.files}
+    with np.load(GOLDEN_AUTOCAST, allow_pickle=False) as f:
+        g.update({f"ac/{k}": f[k] for k in f.files})
+    return g
 
 
 @pytest.fixture(scope="module")
@@ -60,7 +72,6 @@ def spread_note(got, exp, what):
 @pytest.mark.parametrize("mix_precision", [True, False])
 def test_predictions_match_the_reference(gold, model, cuda, mix_precision):
     tag = "fp16 autocast" if mix_precision else "fp32"
-    bar = AUTOCAST_BAR if mix_precision else PREDICTION_BAR
     reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, memory_policy="max_context",
                             mix_precision=mix_precision)
     reg.fit(gold["case/x_train"], gold["case/y_train"])
@@ -68,22 +79,34 @@ def test_predictions_match_the_reference(gold, model, cuda, mix_precision):
         warnings.simplefilter("always")
         point = reg.predict(gold["case/x_test"])
     assert any(issubclass(w.category, CacheQuantizedWarning) for w in caught)
-    check_relative(point, gold["case/point"], bar, f"nori-6m point predictions ({tag})")
-    spread_note(point, gold["case/point"], f"nori-6m point predictions ({tag})")
-
     y_mean, y_std = reg.y_mean_, reg.y_std_
-    ref_sorted = np.sort(gold["case/bank_norm"].astype(np.float64), axis=1) * y_std + y_mean
+    fp32_sorted = np.sort(gold["case/bank_norm"].astype(np.float64), axis=1) * y_std + y_mean
+    if mix_precision:
+        ac_sorted = np.sort(gold["ac/bank_norm"].astype(np.float64), axis=1) * y_std + y_mean
+        # each output against the reference's fp16 run (bar from its own spread over context
+        # orders) and its fp32 run (bar from its own fp16-to-fp32 distance)
+        goldens = [(ac_sorted, gold["ac/point"], lambda k: max(PREDICTION_BAR, SPREAD_FACTOR * float(gold[f"ac/spread/{k}"])),
+                    "reference fp16 autocast run"),
+                   (fp32_sorted, gold["case/point"],
+                    lambda k: max(PREDICTION_BAR, SPREAD_FACTOR * float(gold[f"ac/vs_fp32/{k}"])), "reference fp32 run")]
+    else:
+        goldens = [(fp32_sorted, gold["case/point"], lambda k: PREDICTION_BAR, "reference fp32 run")]
     qs = reg.predict(gold["case/x_test"], output_type="quantiles", quantiles=list(case.QUANTILE_LEVELS))
     assert qs.shape == (3, case.N_QUERY)
-    for i, level in enumerate(case.QUANTILE_LEVELS):
-        check_relative(qs[i], ref_sorted[:, int(round(level * 1000)) - 1], bar,
-                       f"nori-6m quantile {level} ({tag})")
     full = reg.predict(gold["case/x_test"], output_type="full")
-    check_relative(full["quantiles"], ref_sorted, bar, f"nori-6m 999-level bank ({tag})")
     np.testing.assert_allclose(full["mean"], point, rtol=1e-12, atol=1e-12)
     median = reg.predict(gold["case/x_test"], output_type="median")
-    check_relative(median, 0.5 * (ref_sorted[:, 498] + ref_sorted[:, 499]) if ref_sorted.shape[1] % 2 == 0
-                   else ref_sorted[:, ref_sorted.shape[1] // 2], bar, f"nori-6m median ({tag})")
+    for ref_sorted, ref_point, bar, against in goldens:
+        check_relative(point, ref_point, bar("point"), f"nori-6m point predictions ({tag}) vs the {against}")
+        spread_note(point, ref_point, f"nori-6m point predictions ({tag}) vs the {against}")
+        for i, level in enumerate(case.QUANTILE_LEVELS):
+            check_relative(qs[i], ref_sorted[:, int(round(level * 1000)) - 1], bar(f"q{level}"),
+                           f"nori-6m quantile {level} ({tag}) vs the {against}")
+        check_relative(full["quantiles"], ref_sorted, bar("bank"), f"nori-6m 999-level bank ({tag}) vs the {against}")
+        n_levels = ref_sorted.shape[1]
+        ref_median = (0.5 * (ref_sorted[:, n_levels // 2 - 1] + ref_sorted[:, n_levels // 2]) if n_levels % 2 == 0
+                      else ref_sorted[:, n_levels // 2])
+        check_relative(median, ref_median, bar("median"), f"nori-6m median ({tag}) vs the {against}")
 
     report = reg.memory_report_
     assert report["rung"] == "resident_int8" and report["cache_dtype"] == "int8" and report["cache"] is True
