@@ -114,6 +114,10 @@ def main():
     out["case/scales0"] = scales0[:, :128].numpy()
 
     # ---- the same case under the reference's fp16 autocast, and its spread over context orders
+    def median_of(srt):
+        n = srt.shape[1]
+        return 0.5 * (srt[:, n // 2 - 1] + srt[:, n // 2]) if n % 2 == 0 else srt[:, n // 2]
+
     def autocast_run(rows):
         with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16):
             c = ref.build_context_cache(torch.from_numpy(x_tr[rows])[None], torch.from_numpy(y_norm[rows])[None],
@@ -121,8 +125,7 @@ def main():
             b = ref.apply_context_cache(torch.from_numpy(x_te)[None], c)[0].float()
         p = qd.quantile_dist_mean_simple(b.double(), taus, enforce_monotone_first=True).numpy() * y_std + y_mean
         srt = np.sort(b.numpy().astype(np.float64), axis=1) * y_std + y_mean
-        outs = {"point": p, "bank": srt, "median": 0.5 * (srt[:, 498] + srt[:, 499]) if srt.shape[1] % 2 == 0
-                else srt[:, srt.shape[1] // 2]}
+        outs = {"point": p, "bank": srt, "median": median_of(srt)}
         for level in case.QUANTILE_LEVELS:
             outs[f"q{level}"] = srt[:, int(round(level * 1000)) - 1]
         return b.numpy(), outs
@@ -135,8 +138,7 @@ def main():
     ac["bank_norm"] = bank_ac
     ac["point"] = outs["point"]
     fp32_sorted = np.sort(bank.numpy().astype(np.float64), axis=1) * y_std + y_mean
-    fp32_outs = {"point": out["case/point"], "bank": fp32_sorted,
-                 "median": 0.5 * (fp32_sorted[:, 498] + fp32_sorted[:, 499])}
+    fp32_outs = {"point": out["case/point"], "bank": fp32_sorted, "median": median_of(fp32_sorted)}
     for level in case.QUANTILE_LEVELS:
         fp32_outs[f"q{level}"] = fp32_sorted[:, int(round(level * 1000)) - 1]
     spread = {k: 0.0 for k in outs}
