@@ -17,8 +17,9 @@ script is the .npz data beside it, never the reference's code):
   over presets, fields and cache sizes, with the report keys (``model_dump``).
 
 A second fixture, tests/golden/regressor_autocast_goldens.npz, holds the same case run by the
-reference under ``torch.autocast("cpu", dtype=torch.float16)`` -- its predictor's own GPU mode
-(predictor.py:3208-3217) -- and its spread: the largest relative change of each output (point
+reference under ``torch.autocast("cpu", dtype=torch.float16)`` with CUDA autocast's op policy
+(tests/golden/cuda_autocast_policy.py) -- its predictor's own GPU mode (predictor.py:3208-3217)
+-- and its spread: the largest relative change of each output (point
 predictions, the 0.1 / 0.5 / 0.9 quantiles, the median, the whole bank) when the same fp16 run
 takes the context rows in three other orders (the outputs do not depend on that order except
 through the order of the sums), next to its distance from the fp32 run.
@@ -44,6 +45,7 @@ OUT_AUTOCAST = os.path.join(HERE, "regressor_autocast_goldens.npz")
 sys.path[:0] = [os.path.dirname(HERE), os.path.join(os.path.dirname(os.path.dirname(HERE)), "synthefy-nori_amd")]
 
 import regressor_case as case  # noqa: E402
+from cuda_autocast_policy import cuda_policy  # noqa: E402
 
 # (label, policy request, est_cache_gb, bytes_per_element, head_dim, vram_gb, ram_gb)
 LADDER_CASES = [
@@ -119,7 +121,7 @@ def main():
         return 0.5 * (srt[:, n // 2 - 1] + srt[:, n // 2]) if n % 2 == 0 else srt[:, n // 2]
 
     def autocast_run(rows):
-        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16):
+        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16), cuda_policy():
             c = ref.build_context_cache(torch.from_numpy(x_tr[rows])[None], torch.from_numpy(y_norm[rows])[None],
                                         cache_dtype="int8")
             b = ref.apply_context_cache(torch.from_numpy(x_te)[None], c)[0].float()

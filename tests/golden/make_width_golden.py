@@ -6,8 +6,9 @@ transformer.py: ``FeaturesTransformer`` build_context_cache / apply_context_cach
 the CPU, twice per case:
 
 * in fp32, with a full-precision and an int8 cache;
-* under ``torch.autocast("cpu", dtype=torch.float16)`` with an int8 cache -- the reference's
-  own fp16 autocast run, the mode its predictor uses on a GPU (predictor.py:3208-3217) -- and
+* under ``torch.autocast("cpu", dtype=torch.float16)`` with CUDA autocast's op policy
+  (tests/golden/cuda_autocast_policy.py) and an int8 cache -- the reference's own fp16
+  autocast run, the mode its predictor uses on a GPU (predictor.py:3208-3217) -- and
   again with the context rows in three other orders. The outputs do not depend on the order of
   the context rows, except through the order of the sums; the largest relative change over the
   three orders is stored as ``spread_*``: how far the reference's own fp16 run moves when only
@@ -37,6 +38,7 @@ sys.path[:0] = [HERE, os.path.dirname(HERE)]
 
 import regressor_case as case  # noqa: E402
 import width_cases as wc  # noqa: E402
+from cuda_autocast_policy import cuda_policy  # noqa: E402
 from make_golden import load_reference  # noqa: E402
 
 CPU = torch.device("cpu")
@@ -60,7 +62,7 @@ def stack_case(L, idx: int, tag: str, out: dict) -> None:
     x_train, x_test = (torch.from_numpy(a) for a in wc.stack_inputs(tag))
 
     def run(xt, quant, autocast):
-        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16, enabled=autocast):
+        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16, enabled=autocast), cuda_policy():
             tr_out, caches = stack.build_train_cache(xt.clone(), quantize_kv_cache=quant, device=CPU)
             te_out = stack.forward_test_with_cache(x_test.clone(), caches)
         return f32(tr_out), f32(te_out), caches
@@ -103,7 +105,7 @@ def model_case(L, T, idx: int, tag: str, out: dict) -> None:
     n_ctx = c["n_ctx"]
 
     def run(xc, yc, cache_dtype, autocast):
-        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16, enabled=autocast):
+        with torch.inference_mode(), torch.autocast("cpu", dtype=torch.float16, enabled=autocast), cuda_policy():
             ctx = model.build_context_cache(xc, yc, cache_dtype=cache_dtype)
             return f32(model.apply_context_cache(x[:, n_ctx:], ctx))
 

@@ -12,7 +12,8 @@ at those widths, and the fused cache write (``fused_cache_write=True``).
 
 Bars (max|got - exp| / max|exp|, printed by every check):
 * fp32 on the GPU against the reference's fp32 run: 1e-3, the prediction bar;
-* fp16 autocast on the GPU against the reference's fp16 autocast run: the prediction bar, or
+* fp16 autocast on the GPU against the reference's fp16 autocast run (made on the CPU with CUDA
+  autocast's op policy, tests/golden/cuda_autocast_policy.py): the prediction bar, or
   1.5 times the reference's own spread if that is larger -- the largest change of the
   reference's fp16 outputs when only the order of the context rows (so of its sums) changes,
   measured by the golden recipe over three orders and stored beside the outputs. An fp16 run
