@@ -40,7 +40,7 @@ import numpy as np
 import torch
 
 from . import ensemble
-from .memory_policy import MemoryPolicy, estimate_cache_gb, warn_quantized
+from .memory_policy import RUNGS, MemoryPolicy, estimate_cache_gb, fit_row_chunk_attempts, memory_attempt, warn_quantized
 from .transformer import FeaturesTransformer
 
 __all__ = ["NORI_6M_CONFIG", "NoriRegressor", "build_model", "context_device_bytes", "load_model", "quantile_dist_mean",
@@ -212,6 +212,93 @@ def retain_context(contexts: dict, slot, entry, budget: int | None, size_of=cont
     return True
 
 
+def _query_trace(execution: MemoryPolicy, events, *, history: list, pipeline_id: int, context_row_chunk,
+                 reason: str) -> MemoryPolicy:
+    """One ``attempt_history`` entry per decode event of an attempt (the query-chunk halvings of
+    ``apply_context_cache``), returning the policy of the last (predictor.py:1387-1421)."""
+    final = execution
+    for i, (query_chunk, outcome) in enumerate(events):
+        final = execution.escalated(execution.rung, dropped_context_rows=0, query_chunk=query_chunk)
+        history.append(memory_attempt(final, pipeline_ids=[pipeline_id], path="cached", rung=final.rung,
+                                      context_row_chunk=context_row_chunk, query_chunk=query_chunk, outcome=outcome,
+                                      reason=reason if i == 0 else "oom_retry"))
+    return final
+
+
+def run_cache_attempts(requested: MemoryPolicy, resolved: MemoryPolicy, attempt, *, bytes_per_element: int,
+                       head_dim: int, history: list, pipeline_id: int = 0, query_chunk: int | None = None,
+                       evict=lambda: None):
+    """The cached path's out-of-memory retries (predictor.py:3142-3400): the opening rung, then
+    every budget-feasible precision / placement rung after it (``runtime_fallbacks``), then the
+    last of those with the bounded context-row chunk ladder (``fit_row_chunk_attempts``).
+
+    ``attempt(policy, fit_row_chunk, hybrid, on_query_event, state)`` builds (or reuses) the
+    context cache for one rung and applies it, calling ``on_query_event(query_chunk, outcome)``
+    per decode attempt and setting ``state["context"] = True`` once it holds a context. An
+    ``torch.cuda.OutOfMemoryError`` records the attempt, runs ``evict`` (the failed rung's
+    retained context), frees torch's cached blocks and moves to the next rung; the last rung's
+    error propagates (the reference then falls back to its uncached plain loop, which this
+    package does not have; a streamed context never does). A ``NotImplementedError`` is recorded
+    as "unsupported" and propagates. Every attempt is appended to ``history`` as the reference's
+    ``MemoryAttempt``. Returns (what ``attempt`` returned, the policy of the successful attempt,
+    with the rung it reached and its last query chunk)."""
+    pinned = requested.context_row_chunk
+    initial = resolved.context_row_chunk if resolved.stream_context else pinned
+    placements = requested.runtime_fallbacks(resolved, bytes_per_element=bytes_per_element, head_dim=head_dim)
+    if not placements:
+        raise NotImplementedError(f"memory policy rung {resolved.rung!r} has no cached path to attempt")
+    attempts = [(p, initial) for p in placements] + [(placements[-1], c) for c in fit_row_chunk_attempts(initial)]
+    for index, (policy, chunk) in enumerate(attempts):
+        reason = "resolved" if index == 0 else "oom_retry"
+        execution = policy
+        if chunk is not None and chunk != initial:
+            execution = policy.escalated(policy.rung if policy.stream_context else "context_row_chunk",
+                                         context_row_chunk=chunk)
+        hybrid = (policy.rung == "resident_int8" and policy.cache_dtype == "int8" and not policy.offload_to_host
+                  and not policy.stream_context and chunk is not None)
+        events: list = []
+        state: dict = {}
+        try:
+            result = attempt(policy, chunk, hybrid, lambda q, outcome: events.append((q, outcome)), state)
+        except NotImplementedError:
+            history.append(memory_attempt(policy, pipeline_ids=[pipeline_id], path="cached", rung=policy.rung,
+                                          context_row_chunk=chunk, outcome="unsupported", reason=reason))
+            evict()
+            raise
+        except torch.cuda.OutOfMemoryError:
+            if events or state.get("context"):
+                failed = list(events) or [(query_chunk, "oom")]
+                if failed[-1][1] == "success":  # decoded, then ran out of memory afterwards
+                    failed[-1] = (failed[-1][0], "oom")
+                _query_trace(execution, failed, history=history, pipeline_id=pipeline_id, context_row_chunk=chunk,
+                             reason=reason)
+            else:
+                history.append(memory_attempt(policy, pipeline_ids=[pipeline_id], path="cached", rung=policy.rung,
+                                              context_row_chunk=chunk, outcome="oom", reason=reason))
+            evict()
+            if torch.cuda.is_available():
+                torch.cuda.empty_cache()
+            if index + 1 < len(attempts):
+                continue
+            raise
+        if not events:
+            events.append((query_chunk, "success"))
+        final = _query_trace(execution, events, history=history, pipeline_id=pipeline_id, context_row_chunk=chunk,
+                             reason=reason)
+        return result, final
+    raise AssertionError("unreachable: the attempt list is never empty")
+
+
+def _severity(policy: MemoryPolicy) -> tuple:
+    """How degraded an outcome is (predictor.py:1307-1331): rung, then dropped rows, then a
+    smaller context-row chunk, then a smaller query chunk."""
+    rank = RUNGS.index(policy.rung) if policy.rung in RUNGS else -1
+    chunk = policy.context_row_chunk
+    query = policy.query_chunk
+    return (rank, int(policy.dropped_context_rows or 0), -chunk if chunk is not None else float("-inf"),
+            -query if query is not None else float("-inf"))
+
+
 def _device(device) -> torch.device:
     if device is not None:
         return torch.device(device)
@@ -255,6 +342,8 @@ class NoriRegressor:
         self._net = None
         self._contexts = {}  # member slot -> (cache key, x bytes, y bytes, ContextCache)
         self._report = None
+        self._attempt_history: list = []
+        self._outcome_policy = None
 
     # ------------------------------------------------------------------ sklearn surface
     def get_params(self, deep: bool = True) -> dict:
@@ -328,6 +417,9 @@ class NoriRegressor:
             raise ValueError(f"X has {x_test.shape[1]} features, the context has {self.n_features_in_}")
         net = self._network()
         y_norm = ((self.y_train_ - self.y_mean_) / self.y_std_).astype(np.float32)
+        # one call's memory outcome: its attempts and its most degraded rung (predictor.py:1333-1351)
+        self._attempt_history = []
+        self._outcome_policy = None
         bank = self._ensemble_bank(net, x_test, y_norm)  # [rows, K] in standardized target units, fp32
         taus = torch.tensor(net.regression_quantiles, dtype=torch.float64, device=bank.device)
         if output_type in ("mean", "median", "mode"):
@@ -453,42 +545,60 @@ class NoriRegressor:
     def _quantile_bank(self, net: FeaturesTransformer, x_ctx: np.ndarray, x_test: np.ndarray, y_norm: np.ndarray,
                        slot: int) -> tuple[torch.Tensor, bool]:
         """One member's bank: its context cache (built, or the one an earlier call built from the
-        same bytes) applied to its query rows."""
+        same bytes) applied to its query rows, on the rung the memory policy opens with or, after
+        an out-of-memory error, the next one the retry ladder allows (``run_cache_attempts``)."""
         dev = self.device_
         if dev.type != "cuda":
             raise RuntimeError("NoriRegressor runs on a ROCm GPU: the nori_amd kernels have no CPU path")
         amp = bool(self.mix_precision)
         n_groups = math.ceil(x_ctx.shape[1] / net.features_per_group) + 1
-        policy = self._policy(net, n_groups, 2 if amp else 4)
-        if not policy.cache:
+        compute_bytes = 2 if amp else 4
+        requested = MemoryPolicy.coerce(self.memory_policy)
+        resolved = self._policy(net, n_groups, compute_bytes)
+        if not resolved.cache:
             raise NotImplementedError(
-                f"memory policy resolved to rung {policy.rung!r}: the uncached forward is not part of this build; "
+                f"memory policy resolved to rung {resolved.rung!r}: the uncached forward is not part of this build; "
                 "allow the cache (the int8 rungs hold about 1.9x more context than bf16)"
             )
-        build = dict(cache_dtype=policy.cache_dtype, offload_kv_cache=policy.offload_to_host,
-                     fit_row_chunk=policy.context_row_chunk)
-        streaming = policy.rung.startswith("stream_")
-        if streaming:
-            build["stream_context"] = True
-        key = (tuple(sorted(build.items())), amp, str(dev))
-        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16, enabled=amp):
-            context = self._reused_context(slot, key, x_ctx, y_norm) if policy.reuse_context_cache and not streaming \
-                else None
-            reused = context is not None
-            if context is None:
-                home = torch.device("cpu") if streaming else dev
-                xc = torch.from_numpy(x_ctx).to(home)[None]
-                yc = torch.from_numpy(y_norm).to(home)[None]
-                context = net.build_context_cache(xc, yc, **build)
-                if policy.reuse_context_cache and not streaming:
-                    retain_context(self._contexts, slot, (key, x_ctx.tobytes(), y_norm.tobytes(), context),
-                                   self._context_budget_bytes())
-            xq = torch.from_numpy(x_test).to(torch.device("cpu") if streaming else dev)[None]
-            bank = net.apply_context_cache(xq, context)[0].float()
-        if not bool(torch.isfinite(bank).all()):
-            raise RuntimeError("the model produced non-finite predictions")  # predictor.py:731-765
-        self._report = policy.with_outcome(query_chunk=int(x_test.shape[0])).as_report()
-        return bank, reused, policy
+
+        def attempt(policy: MemoryPolicy, fit_row_chunk, hybrid, on_query, state):
+            build = dict(cache_dtype=policy.cache_dtype, offload_kv_cache=policy.offload_to_host,
+                         fit_row_chunk=fit_row_chunk)
+            streaming = policy.stream_context
+            if streaming:
+                build["stream_context"] = True
+            if hybrid:
+                build["_hybrid_resident_int8_prefill"] = True
+            key = (tuple(sorted(build.items())), amp, str(dev))
+            reuse = policy.reuse_context_cache and not streaming
+            with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16, enabled=amp):
+                context = self._reused_context(slot, key, x_ctx, y_norm) if reuse else None
+                reused = context is not None
+                if context is None:
+                    home = torch.device("cpu") if streaming else dev
+                    xc = torch.from_numpy(x_ctx).to(home)[None]
+                    yc = torch.from_numpy(y_norm).to(home)[None]
+                    context = net.build_context_cache(xc, yc, **build)
+                    if reuse:
+                        retain_context(self._contexts, slot, (key, x_ctx.tobytes(), y_norm.tobytes(), context),
+                                       self._context_budget_bytes())
+                state["context"] = True
+                xq = torch.from_numpy(x_test).to(torch.device("cpu") if streaming else dev)[None]
+                bank = net.apply_context_cache(xq, context, adaptive_query_chunk=policy.adaptive_query_chunk,
+                                               query_chunk_attempt_callback=on_query)[0].float()
+            if not bool(torch.isfinite(bank).all()):
+                raise RuntimeError("the model produced non-finite predictions")  # predictor.py:731-765
+            return bank, reused
+
+        (bank, reused), final = run_cache_attempts(
+            requested, resolved, attempt, bytes_per_element=compute_bytes, head_dim=net.embed_dim // net.nhead,
+            history=self._attempt_history, pipeline_id=slot, query_chunk=int(x_test.shape[0]),
+            evict=lambda: self._contexts.pop(slot, None))
+        if self._outcome_policy is None or _severity(final) > _severity(self._outcome_policy):
+            self._outcome_policy = final
+        self._report = self._outcome_policy.as_report()
+        self._report["attempt_history"] = list(self._attempt_history)
+        return bank, reused, final
 
     def _reused_context(self, slot: int, key, x_ctx: np.ndarray, y_norm: np.ndarray):
         """The context a member encoded in an earlier call, when its cache parameters, its context

@@ -7,8 +7,13 @@ Restates the decision half of ``synthefy_nori.inference.memory_policy``
 placement candidates (:1085-1137) and ``resolve`` (:1173-1300). It is pure arithmetic: the
 cache it chooses is built by ``FeaturesTransformer.build_context_cache``, whose int8 rungs run
 the HIP quantizer. The report (``as_report``) carries the reference's ``memory_report_`` keys.
-Not restated: the serving-process coercion (``coerce_for_service``), the runtime OOM retry
-ladder and the element-budget subsampling, which belong to the reference's control plane.
+The runtime half is restated too: ``runtime_fallbacks`` (:1304-1375) lists the precision /
+placement rungs an out-of-memory retry may step to, ``fit_row_chunk_attempts`` the bounded
+prefill retry ladder below them (:175; predictor.py:1287-1291), ``escalated`` (:1377-1409)
+records a rung the retry reached, and ``memory_attempt`` one entry of ``attempt_history``
+(``MemoryAttempt``, :480-530); ``NoriRegressor`` drives them (predictor.py:3142-3400).
+Not restated: the serving-process coercion (``coerce_for_service``) and the element-budget
+subsampling, which belong to the reference's control plane.
 """
 
 from __future__ import annotations
@@ -19,7 +24,10 @@ import warnings
 from dataclasses import dataclass, field
 
 __all__ = [
+    "ATTEMPT_OUTCOMES",
+    "ATTEMPT_REASONS",
     "CACHE_DTYPES",
+    "FIT_ROW_CHUNK_RETRY_LADDER",
     "MEMORY_PRESETS",
     "RUNGS",
     "CacheQuantizedWarning",
@@ -28,7 +36,9 @@ __all__ = [
     "MemoryPolicy",
     "default_stream_context_row_chunk",
     "estimate_cache_gb",
+    "fit_row_chunk_attempts",
     "int8_footprint_gb",
+    "memory_attempt",
 ]
 
 MEMORY_PRESETS = ("exact", "max_context", "off")
@@ -38,6 +48,13 @@ RUNGS = ("no_cache", "resident_bf16", "resident_int8", "offload_bf16", "offload_
          "stream_int8", "context_row_chunk", "plain_loop")
 STREAM_RUNGS = ("stream_bf16", "stream_int8")
 DEGRADED_RUNGS = ("offload_bf16", "offload_int8", "stream_bf16", "stream_int8", "context_row_chunk", "plain_loop")
+
+# Bounded prefill retries after the last placement rung (memory_policy.py:175): a context-row
+# chunk ladder, never below 256 rows, so an out-of-memory build cannot retry forever.
+FIT_ROW_CHUNK_RETRY_LADDER = (2048, 1024, 512, 256)
+ATTEMPT_OUTCOMES = ("success", "oom", "unsupported")
+ATTEMPT_REASONS = ("resolved", "oom_retry", "fallback_after_oom", "fallback_after_unsupported")
+DEFAULT_STREAM_CONTEXT_ROW_CHUNK = 2048
 
 GIB = 1024**3
 ASSUMED_VRAM_GB = 24.0  # when the device cannot be asked (memory_policy.py: ASSUMED_VRAM_GB)
@@ -72,6 +89,34 @@ def int8_footprint_gb(est_cache_gb: float, *, bytes_per_element: int, head_dim: 
 def default_stream_context_row_chunk(total_vram_gb: float | None) -> int:
     vram = ASSUMED_VRAM_GB if total_vram_gb is None else total_vram_gb
     return next(rows for floor, rows in _STREAM_ROW_CHUNKS if vram >= floor)
+
+
+def fit_row_chunk_attempts(pinned: int | None) -> list[int]:
+    """The prefill retry chunks smaller than ``pinned`` (all of them when nothing is pinned); the
+    pinned value itself is the attempt that already failed (predictor.py:1287-1291)."""
+    return [c for c in FIT_ROW_CHUNK_RETRY_LADDER if pinned is None or c < pinned]
+
+
+def memory_attempt(policy: "MemoryPolicy", *, pipeline_ids: list[int], path: str, rung: str,
+                   context_row_chunk: int | None, outcome: str, reason: str, dropped_context_rows: int = 0,
+                   query_chunk: int | None = None) -> dict:
+    """One ``attempt_history`` entry, with the fields and checks of the reference's
+    ``MemoryAttempt`` (memory_policy.py:480-530)."""
+    if outcome not in ATTEMPT_OUTCOMES:
+        raise ValueError(f"unknown attempt outcome {outcome!r}")
+    if reason not in ATTEMPT_REASONS:
+        raise ValueError(f"unknown attempt reason {reason!r}")
+    if rung not in RUNGS:
+        raise ValueError(f"unknown rung {rung!r}")
+    for name, value in (("context_row_chunk", context_row_chunk), ("query_chunk", query_chunk)):
+        if value is not None and value <= 0:
+            raise ValueError(f"{name} must be positive, got {value!r}")
+    if dropped_context_rows < 0:
+        raise ValueError("dropped_context_rows must be >= 0")
+    return {"pipeline_ids": list(pipeline_ids), "path": path, "rung": rung, "cache_dtype": policy.cache_dtype,
+            "offload_to_host": policy.offload_to_host, "context_row_chunk": context_row_chunk,
+            "query_chunk": query_chunk, "outcome": outcome, "reason": reason,
+            "dropped_context_rows": dropped_context_rows}
 
 
 def host_ram_gb() -> float:
@@ -248,6 +293,60 @@ class MemoryPolicy:
         dtype, gb = self.precisions(est_cache_gb=est_cache_gb, bytes_per_element=bytes_per_element,
                                     head_dim=head_dim)[-1]
         return decided("plain_loop", dtype, False, gb, cache=False)
+
+    # ------------------------------------------------------------------ runtime retries
+    def runtime_fallbacks(self, resolved: "MemoryPolicy", *, bytes_per_element: int,
+                          head_dim: int) -> list["MemoryPolicy"]:
+        """The precision / placement rungs an out-of-memory retry walks, starting at
+        ``resolved``'s own (memory_policy.py:1304-1375): for a streamed context the host-feasible
+        stream precisions; for the resident and offloaded rungs the budget-feasible placements,
+        recomputed from ``resolved``'s stored estimate and budgets; nothing for the others.
+        ``self`` is the request ``resolved`` came from (its reuse and chunk settings carry over)."""
+        est = resolved.est_cache_gb or 0.0
+        if resolved.rung in STREAM_RUNGS:
+            attempts = [
+                dataclasses.replace(resolved, cache=True, reuse_context_cache=False, cache_dtype=dtype,
+                                    offload_to_host=True, rung=f"stream_{dtype}", resident_gb=gb,
+                                    context_row_chunk=resolved.context_row_chunk or DEFAULT_STREAM_CONTEXT_ROW_CHUNK)
+                for dtype, gb in self.precisions(est_cache_gb=est, bytes_per_element=bytes_per_element,
+                                                 head_dim=head_dim)
+                if gb <= (resolved.host_budget_absolute_gb or 0.0)
+            ]
+            labels = [a.rung for a in attempts]
+            return attempts[labels.index(resolved.rung):]
+        if resolved.rung not in ("resident_bf16", "resident_int8", "offload_bf16", "offload_int8"):
+            return []
+        attempts = [
+            dataclasses.replace(resolved, cache=True, reuse_context_cache=self.reuse_context_cache, cache_dtype=dtype,
+                                offload_to_host=offload, rung=rung, resident_gb=gb,
+                                context_row_chunk=self.context_row_chunk)
+            for rung, dtype, offload, gb in self.placements(
+                est_cache_gb=est, bytes_per_element=bytes_per_element, head_dim=head_dim,
+                gpu_budget_gb=resolved.gpu_budget_absolute_gb or 0.0,
+                host_budget_gb=resolved.host_budget_absolute_gb or 0.0)
+        ]
+        labels = [a.rung for a in attempts]
+        if resolved.rung not in labels:
+            return [resolved]
+        return attempts[labels.index(resolved.rung):]
+
+    def escalated(self, rung: str, *, context_row_chunk: int | None = None, dropped_context_rows: int | None = None,
+                  query_chunk: int | None = None) -> "MemoryPolicy":
+        """A copy recording the rung a retry reached (memory_policy.py:1377-1409); a streamed
+        context never leaves the stream rungs, and the plain loop drops the cache."""
+        if self.stream_context and rung not in STREAM_RUNGS:
+            raise ValueError(f"stream_context=True cannot escalate to rung={rung!r}; it remains on one of "
+                             f"{STREAM_RUNGS} or raises instead of silently using plain_loop.")
+        updates: dict = {"rung": rung}
+        if context_row_chunk is not None:
+            updates["context_row_chunk"] = context_row_chunk
+        if dropped_context_rows is not None:
+            updates["dropped_context_rows"] = dropped_context_rows
+        if query_chunk is not None:
+            updates["query_chunk"] = query_chunk
+        if rung == "plain_loop":
+            updates.update(cache=False, reuse_context_cache=False, offload_to_host=False)
+        return dataclasses.replace(self, **updates)
 
     # ------------------------------------------------------------------ report
     @property

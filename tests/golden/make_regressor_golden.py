@@ -168,8 +168,31 @@ def main():
             dump = resolved.model_dump()
             row["report"] = {k: dump[k] for k in dump if k != "attempt_history"}
             row["report_keys"] = sorted(dump)
+            # the runtime out-of-memory retries from that opening rung (memory_policy.py:1304-1375)
+            fallbacks = mp.MemoryPolicy.coerce(request).runtime_fallbacks(resolved, bytes_per_element=bpe, head_dim=hd)
+            row["fallbacks"] = [{k: v for k, v in f.model_dump().items() if k != "attempt_history"} for f in fallbacks]
+            # a retry's escalation records (memory_policy.py:1377-1409)
+            try:
+                esc = resolved.escalated("context_row_chunk", context_row_chunk=512, query_chunk=64)
+                row["escalated_chunk"] = {k: v for k, v in esc.model_dump().items() if k != "attempt_history"}
+            except Exception as exc:
+                row["escalated_chunk"] = type(exc).__name__
+            try:
+                esc = resolved.escalated("plain_loop", dropped_context_rows=7)
+                row["escalated_plain"] = {k: v for k, v in esc.model_dump().items() if k != "attempt_history"}
+            except Exception as exc:
+                row["escalated_plain"] = type(exc).__name__
         rows.append(row)
     out["ladder/json"] = np.array(json.dumps(rows))
+    out["ladder/fit_row_chunk_retry"] = np.array(mp.FIT_ROW_CHUNK_RETRY_LADDER, dtype=np.int64)
+    # one attempt_history entry as the reference's MemoryAttempt writes it (memory_policy.py:480-530)
+    resolved = mp.MemoryPolicy.coerce({"cache_dtype": "int8"}).resolve(
+        est_cache_gb=2.0, bytes_per_element=2, head_dim=64, total_vram_gb=24.0, total_ram_gb=64.0)
+    attempt = mp.MemoryAttempt(pipeline_ids=[3], path="cached", rung="context_row_chunk",
+                               cache_dtype=resolved.cache_dtype, offload_to_host=resolved.offload_to_host,
+                               context_row_chunk=512, query_chunk=None, outcome="oom", reason="oom_retry",
+                               dropped_context_rows=0).model_dump()
+    out["ladder/attempt_json"] = np.array(json.dumps(attempt))
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: point predictions {out['case/point'][:4]}, ladder {[r.get('report', {}).get('rung', r.get('error')) for r in rows]}")
 

@@ -194,3 +194,30 @@ def test_yeo_johnson_pass_on_a_skewed_target(gold, model, cuda):
                 reg.augmentations = ()
                 assert np.array_equal(plain, reg.predict(x_te))
     assert np.all(np.isfinite(out[("yj",)])) and not np.allclose(out[()], out[("yj",)])
+
+
+def test_out_of_memory_on_the_opening_rung_retries_the_next(gold, model, cuda, monkeypatch):
+    # predictor.py:3142-3400: a build that runs out of device memory on the opening rung
+    # (resident bf16 here) is retried on the next the policy allows (resident int8), and both
+    # attempts are in memory_report_["attempt_history"]
+    reg = api.NoriRegressor(model=model, device=cuda, inference_config=RAW, mix_precision=False)
+    reg.fit(gold["case/x_train"], gold["case/y_train"])
+    real = FeaturesTransformer.build_context_cache
+    calls = []
+
+    def flaky(self, *a, **k):
+        calls.append(k.get("cache_dtype"))
+        if len(calls) == 1:
+            raise torch.cuda.OutOfMemoryError("synthetic out-of-memory on the first build")
+        return real(self, *a, **k)
+
+    monkeypatch.setattr(FeaturesTransformer, "build_context_cache", flaky)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", CacheQuantizedWarning)
+        point = reg.predict(gold["case/x_test"])
+    report = reg.memory_report_
+    assert calls == ["bf16", "int8"]
+    assert [(a["rung"], a["outcome"], a["reason"]) for a in report["attempt_history"]] == [
+        ("resident_bf16", "oom", "resolved"), ("resident_int8", "success", "oom_retry")]
+    assert report["rung"] == "resident_int8" and report["cache_dtype"] == "int8"
+    check_relative(point, gold["case/point"], PREDICTION_BAR, "nori-6m point predictions after the retry (fp32)")

@@ -113,6 +113,71 @@ def test_memory_ladder_matches_the_reference(gold):
         assert not missing, f"report lacks the reference's keys {sorted(missing)}"
 
 
+POLICY_KEYS = ("rung", "cache", "cache_dtype", "offload_to_host", "reuse_context_cache", "context_row_chunk",
+               "stream_context", "allow_quantization", "query_chunk", "dropped_context_rows")
+GB_KEYS = ("est_cache_gb", "resident_gb", "gpu_budget_absolute_gb", "host_budget_absolute_gb")
+
+
+def _same_policy(got: dict, exp: dict, label: str) -> None:
+    for key in POLICY_KEYS:
+        assert got[key] == exp[key], (label, key, got[key], exp[key])
+    for key in GB_KEYS:
+        if exp[key] is None:
+            assert got[key] is None, (label, key)
+        else:
+            assert math.isclose(got[key], exp[key], rel_tol=1e-12), (label, key, got[key], exp[key])
+
+
+def test_runtime_fallbacks_and_escalations_match_the_reference(gold):
+    # memory_policy.py:1304-1409: the rungs an out-of-memory retry walks from each opening rung,
+    # and the records a retry's escalation writes, as the reference computed them
+    rows = json.loads(str(gold["ladder/json"]))
+    seen = 0
+    for row in rows:
+        if "error" in row:
+            continue
+        request = MemoryPolicy.coerce(row["request"])
+        resolved = request.resolve(est_cache_gb=row["est"], bytes_per_element=row["bpe"], head_dim=row["head_dim"],
+                                   total_vram_gb=row["vram"], total_ram_gb=row["ram"])
+        got = request.runtime_fallbacks(resolved, bytes_per_element=row["bpe"], head_dim=row["head_dim"])
+        assert [f.rung for f in got] == [f["rung"] for f in row["fallbacks"]], row["label"]
+        for g, e in zip(got, row["fallbacks"]):
+            _same_policy(g.as_report(), e, row["label"])
+        seen += len(got)
+        for rung, kwargs, key in (("context_row_chunk", dict(context_row_chunk=512, query_chunk=64), "escalated_chunk"),
+                                  ("plain_loop", dict(dropped_context_rows=7), "escalated_plain")):
+            if isinstance(row[key], str):
+                assert row[key] == "ValueError"
+                with pytest.raises(ValueError):
+                    resolved.escalated(rung, **kwargs)
+            else:
+                _same_policy(resolved.escalated(rung, **kwargs).as_report(), row[key], row["label"] + " " + rung)
+    assert seen >= 15
+
+
+def test_fit_row_chunk_retry_ladder_and_attempt_records(gold):
+    from nori_amd import memory_policy as M
+
+    assert M.FIT_ROW_CHUNK_RETRY_LADDER == tuple(int(v) for v in gold["ladder/fit_row_chunk_retry"])
+    # the retries are the ladder's chunks below the pinned one (predictor.py:1287-1291)
+    assert M.fit_row_chunk_attempts(None) == [2048, 1024, 512, 256]
+    assert M.fit_row_chunk_attempts(2048) == [1024, 512, 256]
+    assert M.fit_row_chunk_attempts(600) == [512, 256]
+    assert M.fit_row_chunk_attempts(256) == []
+    exp = json.loads(str(gold["ladder/attempt_json"]))
+    resolved = MemoryPolicy.coerce({"cache_dtype": "int8"}).resolve(
+        est_cache_gb=2.0, bytes_per_element=2, head_dim=64, total_vram_gb=24.0, total_ram_gb=64.0)
+    got = M.memory_attempt(resolved, pipeline_ids=[3], path="cached", rung="context_row_chunk", context_row_chunk=512,
+                           outcome="oom", reason="oom_retry")
+    assert got == exp
+    for bad in (dict(outcome="maybe"), dict(reason="why"), dict(rung="nowhere"), dict(context_row_chunk=0)):
+        kwargs = dict(pipeline_ids=[0], path="cached", rung="resident_int8", context_row_chunk=None, outcome="oom",
+                      reason="resolved")
+        kwargs.update(bad)
+        with pytest.raises(ValueError):
+            M.memory_attempt(resolved, **kwargs)
+
+
 def test_policy_coercion_and_refusals():
     assert MemoryPolicy.coerce("exact").allow_quantization is False
     assert MemoryPolicy.coerce("max_context").cache_dtype == "int8"
@@ -205,3 +270,118 @@ def test_yeo_johnson_pass_falls_back_to_the_plain_prediction(monkeypatch):
     assert reg._yeo_johnson_pass(None, None, y[:5], point, None, "mean") is point
     reg.yj_skew_threshold = 1e9
     assert reg._yeo_johnson_pass(None, None, y, point, None, "mean") is point
+
+
+def _retry_request():
+    return MemoryPolicy(gpu_budget_absolute_gb=1.0, host_budget_absolute_gb=2.0, elements_budget=1_072)
+
+
+def _resolve(request):
+    return request.resolve(est_cache_gb=0.1, bytes_per_element=2, head_dim=4, total_vram_gb=8.0, total_ram_gb=16.0)
+
+
+def test_runtime_oom_walks_every_allowed_rung_then_bounded_fit_chunks():
+    # predictor.py:3142-3400 as the reference's own test drives it
+    # (tests/test_inference_pipeline_batching.py:758-794): every budget-feasible precision /
+    # placement rung, then the last one with the context-row chunk ladder, each failure recorded
+    request = _retry_request()
+    resolved = _resolve(request)
+    assert resolved.rung == "resident_bf16"
+    tried, evicted, history = [], [], []
+
+    def attempt(policy, chunk, hybrid, on_query, state):
+        tried.append((policy.cache_dtype, policy.offload_to_host, chunk))
+        if (policy.cache_dtype, policy.offload_to_host, chunk) != ("int8", True, 512):
+            raise torch.cuda.OutOfMemoryError("synthetic build OOM")
+        state["context"] = True
+        on_query(300, "success")
+        return "bank"
+
+    result, final = api.run_cache_attempts(request, resolved, attempt, bytes_per_element=2, head_dim=4,
+                                           history=history, pipeline_id=0, query_chunk=300,
+                                           evict=lambda: evicted.append(1))
+    expected = [("bf16", False, None), ("int8", False, None), ("bf16", True, None), ("int8", True, None),
+                ("int8", True, 2048), ("int8", True, 1024), ("int8", True, 512)]
+    assert tried == expected and result == "bank" and len(evicted) == 6
+    assert final.rung == "context_row_chunk" and final.context_row_chunk == 512 and final.query_chunk == 300
+    assert [a["outcome"] for a in history] == ["oom"] * 6 + ["success"]
+    assert [(a["cache_dtype"], a["offload_to_host"], a["context_row_chunk"]) for a in history] == expected
+    assert [a["reason"] for a in history] == ["resolved"] + ["oom_retry"] * 6
+    assert all(a["dropped_context_rows"] == 0 for a in history)
+    assert history[-1]["rung"] == "context_row_chunk" and history[0]["query_chunk"] is None
+
+
+def test_runtime_oom_records_decode_halvings_and_propagates_when_exhausted():
+    request = _retry_request()
+    resolved = _resolve(request)
+    history = []
+
+    def decode_oom_once(policy, chunk, hybrid, on_query, state):
+        # the first rung's build succeeds and its decode halves once (apply_context_cache's
+        # callback), then succeeds
+        state["context"] = True
+        on_query(300, "oom")
+        on_query(150, "success")
+        return "bank"
+
+    _, final = api.run_cache_attempts(request, resolved, decode_oom_once, bytes_per_element=2, head_dim=4,
+                                      history=history, query_chunk=300)
+    assert [(a["query_chunk"], a["outcome"], a["reason"]) for a in history] == [
+        (300, "oom", "resolved"), (150, "success", "oom_retry")]
+    assert final.rung == "resident_bf16" and final.query_chunk == 150
+
+    history = []
+
+    def always_oom(policy, chunk, hybrid, on_query, state):
+        raise torch.cuda.OutOfMemoryError("synthetic build OOM")
+
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        api.run_cache_attempts(request, resolved, always_oom, bytes_per_element=2, head_dim=4, history=history)
+    assert len(history) == 4 + 4 and all(a["outcome"] == "oom" for a in history)
+    assert [a["context_row_chunk"] for a in history[4:]] == [2048, 1024, 512, 256]
+
+    history = []
+
+    def unsupported(policy, chunk, hybrid, on_query, state):
+        raise NotImplementedError("no bounded build for serial attention")
+
+    with pytest.raises(NotImplementedError):
+        api.run_cache_attempts(request, resolved, unsupported, bytes_per_element=2, head_dim=4, history=history)
+    assert [a["outcome"] for a in history] == ["unsupported"]
+
+
+def test_runtime_oom_retries_a_streamed_context_on_stream_rungs_only():
+    request = MemoryPolicy(stream_context=True, host_budget_absolute_gb=2.0)
+    resolved = request.resolve(est_cache_gb=0.1, bytes_per_element=2, head_dim=4, total_vram_gb=8.0,
+                               total_ram_gb=16.0)
+    assert resolved.rung == "stream_bf16" and resolved.context_row_chunk == 2048
+    tried, history = [], []
+
+    def attempt(policy, chunk, hybrid, on_query, state):
+        tried.append((policy.rung, chunk, hybrid))
+        raise torch.cuda.OutOfMemoryError("synthetic build OOM")
+
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        api.run_cache_attempts(request, resolved, attempt, bytes_per_element=2, head_dim=4, history=history)
+    # both stream precisions at the resolved cap, then the smaller caps on the last one; never a
+    # resident rung, never the hybrid prefill
+    assert tried == [("stream_bf16", 2048, False), ("stream_int8", 2048, False), ("stream_int8", 1024, False),
+                     ("stream_int8", 512, False), ("stream_int8", 256, False)]
+    assert {a["rung"] for a in history} == {"stream_bf16", "stream_int8"}
+
+
+def test_hybrid_prefill_only_on_the_resident_int8_rung_with_a_chunk():
+    request = MemoryPolicy(cache_dtype="int8", gpu_budget_absolute_gb=1.0, host_budget_absolute_gb=2.0,
+                           offload_to_host=False)
+    resolved = _resolve(request)
+    assert resolved.rung == "resident_int8"
+    tried = []
+
+    def attempt(policy, chunk, hybrid, on_query, state):
+        tried.append((chunk, hybrid))
+        if chunk != 1024:
+            raise torch.cuda.OutOfMemoryError("synthetic build OOM")
+        return "bank"
+
+    api.run_cache_attempts(request, resolved, attempt, bytes_per_element=2, head_dim=4, history=[])
+    assert tried == [(None, False), (2048, True), (1024, True)]
