@@ -243,3 +243,167 @@ def test_wide_table_projection_gate():
     np.testing.assert_allclose(np.linalg.norm(out, axis=0), sv, rtol=1e-4)
     with pytest.raises(NotImplementedError):
         en.WideTableProjection(strategy="corr")
+
+
+# ---- the reference's own fingerprint tests (tests/test_fingerprint_feature_encoder.py:16-68)
+def _float_hash(row: np.ndarray) -> float:
+    # float_hash_arr (preprocess.py:1225-1248): SHA-256 of the row's bytes as an integer, modulo
+    # 10^12, over 10^12
+    return (int(hashlib.sha256(row.tobytes()).hexdigest(), 16) % 10**12) / 10**12
+
+
+def _fit_fingerprint(x):
+    step = en.RowFingerprint()
+    step.fit(x, [1], 42)
+    return step
+
+
+def test_fingerprint_context_and_query_use_single_and_double_salt():
+    x = np.array([[1.0, 2.0], [3.5, -4.0]], dtype=np.float32)
+    step = _fit_fingerprint(x)
+    context, context_cat = step.apply(x, is_test=False)
+    query, query_cat = step.apply(x.copy(), is_test=True)
+    exp_context = np.asarray([_float_hash(row + step.salt) for row in x], dtype=x.dtype)
+    exp_query = np.asarray([_float_hash(row + 2 * step.salt) for row in x], dtype=x.dtype)
+    np.testing.assert_array_equal(context[:, :-1], x)
+    np.testing.assert_array_equal(query[:, :-1], x)
+    np.testing.assert_array_equal(context[:, -1], exp_context)
+    np.testing.assert_array_equal(query[:, -1], exp_query)
+    assert np.all(context[:, -1] != query[:, -1])
+    assert context_cat == query_cat == [1]
+
+
+def test_fingerprint_duplicate_context_rows_are_rehashed_but_query_duplicates_are_not():
+    row = np.array([[1.0, 2.0]], dtype=np.float32)
+    rows = np.repeat(row, repeats=2, axis=0)
+    step = _fit_fingerprint(rows)
+    context, _ = step.apply(rows, is_test=False)
+    query, _ = step.apply(rows, is_test=True)
+    first = _float_hash(row[0] + step.salt)
+    second = _float_hash(row[0] + step.salt + 1)  # the duplicate: rehashed as row + salt + 1
+    np.testing.assert_array_equal(context[:, -1], np.asarray([first, second], dtype=row.dtype))
+    q = _float_hash(row[0] + 2 * step.salt)
+    np.testing.assert_array_equal(query[:, -1], np.asarray([q, q], dtype=row.dtype))
+
+
+def test_fingerprint_unseen_query_uses_the_query_namespace():
+    step = _fit_fingerprint(np.array([[1.0, 2.0]], dtype=np.float32))
+    query_rows = np.array([[3.0, 4.0]], dtype=np.float32)
+    query, _ = step.apply(query_rows, is_test=True)
+    np.testing.assert_array_equal(query[:, -1], np.asarray([_float_hash(query_rows[0] + 2 * step.salt)],
+                                                           dtype=query_rows.dtype))
+
+
+# ---- the reference's SVD rank rules (tests/test_preprocess_svd_rank.py:35-102)
+def _svd_fit(x, **kw):
+    step = en.WideTableProjection(strategy="svd_all", n_features_threshold=256, device="cpu", **kw)
+    step.fit(x, [], 0)
+    return step
+
+
+def _svd_rank(step):
+    return None if step.svd is None else int(step.svd.components_.shape[0])
+
+
+def test_short_wide_table_is_reduced_not_rotated():
+    x = np.random.default_rng(0).normal(size=(190, 1901))
+    k = _svd_rank(_svd_fit(x, svd_components=512, svd_rows_per_component=3))
+    assert k is not None and k <= 190 // 3 and k < min(x.shape) - 1
+
+
+def test_tall_table_still_capped_by_svd_components():
+    x = np.random.default_rng(1).normal(size=(6234, 2000))
+    assert _svd_rank(_svd_fit(x, svd_components=512, svd_rows_per_component=3)) == 512
+
+
+def test_default_rows_per_component_keeps_the_previous_rank():
+    x = np.random.default_rng(5).normal(size=(300, 400))
+    assert _svd_rank(_svd_fit(x, svd_components=256)) == 256
+
+
+def test_rows_per_component_one_restores_the_previous_rank():
+    x = np.random.default_rng(2).normal(size=(190, 1901))
+    assert _svd_rank(_svd_fit(x, svd_components=512, svd_rows_per_component=1)) == 189
+
+
+def test_narrow_table_is_untouched_by_the_gate():
+    x = np.random.default_rng(3).normal(size=(5000, 10))
+    assert _svd_fit(x, svd_components=512).svd is None
+
+
+@pytest.mark.parametrize("n", [2, 3, 7])
+def test_tiny_row_counts_stay_valid(n):
+    x = np.random.default_rng(4).normal(size=(n, 400))
+    k = _svd_rank(_svd_fit(x, svd_components=512))
+    assert k is None or k >= 1
+
+
+def test_shipped_configuration_enables_the_rank_rule_and_the_transductive_fit():
+    sels = [m["HighDimFeatureSelector"] for m in en.DEFAULT_MEMBERS if "HighDimFeatureSelector" in m]
+    assert sels
+    for h in sels:
+        assert h.get("svd_rows_per_component") == 3 and h.get("svd_components") == 512
+        assert h.get("fit_on_test") is True
+
+
+# ---- the reference's transductive wide-table fit (tests/test_hdf_selector_transductive_fit.py:28-75)
+def _shifted_split(seed=0, n_train=400, n_test=100, n_features=40, n_shifted=10, shift=8.0):
+    rng = np.random.default_rng(seed)
+    x_train = rng.standard_normal((n_train, n_features))
+    x_test = rng.standard_normal((n_test, n_features))
+    x_test[:, :n_shifted] += shift  # test values far outside the context range
+    return x_train.astype(np.float32), x_test.astype(np.float32)
+
+
+def _selector(**kw):
+    return en.WideTableProjection(strategy="svd_all", svd_components=8, n_features_threshold=16, device="cpu", **kw)
+
+
+def test_transductive_flag_defaults_off_and_is_stored():
+    assert _selector().fit_on_test is False
+    assert _selector(fit_on_test=True).fit_on_test is True
+
+
+def test_member_fits_the_projection_on_context_plus_test_only_when_enabled(monkeypatch):
+    x_train, x_test = _shifted_split()
+    seen = {}
+    real_fit = en.WideTableProjection.fit
+
+    def recording_fit(self, x, categorical, seed, y=None):
+        seen["rows"] = len(x)
+        seen["y"] = y
+        return real_fit(self, x, categorical, seed, y=y)
+
+    monkeypatch.setattr(en.WideTableProjection, "fit", recording_fit)
+    for flag, rows in ((True, len(x_train) + len(x_test)), (False, len(x_train))):
+        seen.clear()
+        member = en.Member({"HighDimFeatureSelector": {"strategy": "svd_all", "svd_components": 8,
+                                                       "n_features_threshold": 16, "fit_on_test": flag}},
+                           list(range(en.SEED_SLOTS)), 0, "cpu")
+        member.features(x_train, x_test, [], np.zeros(len(x_train), dtype=np.float32))
+        assert seen["rows"] == rows
+        if flag:
+            assert seen["y"] is None  # labels are never part of the transductive fit
+
+
+def test_transductive_projection_reconstructs_shifted_test_rows_better():
+    x_train, x_test = _shifted_split()
+    ctx_only, both = _selector(), _selector()
+    ctx_only.fit(x_train, [], 0)
+    both.fit(np.vstack([x_train, x_test]), [], 0)
+    assert ctx_only.svd is not None and both.svd is not None
+
+    def recon_error(step):
+        comps = np.asarray(step.svd.components_, dtype=np.float64)
+        x = x_test.astype(np.float64)
+        return float(np.mean((x - x @ comps.T @ comps) ** 2))
+
+    assert recon_error(both) < 0.5 * recon_error(ctx_only)
+
+
+def test_disabled_transductive_flag_is_byte_identical():
+    x_train, x_test = _shifted_split()
+    a, b = _selector(), _selector(fit_on_test=False)
+    a.fit(x_train, [], 0)
+    b.fit(x_train, [], 0)
+    np.testing.assert_array_equal(a.apply(x_test)[0], b.apply(x_test)[0])

@@ -1,0 +1,75 @@
+"""The default preprocessing ensemble on config 1's table with its SVDs on the GPU.
+
+Each of the reference's eight default members (configs/default_inference.json;
+preprocess.py:916-1222 for the redistribution step) is run on the nori-6m case's table
+(tests/regressor_case.py: 1024 context + 256 query rows, 16 features) with the device SVD on
+the GPU, and checked by what fixes it independently of this code:
+
+* feature shapes: quantile members 66 columns (16 + 10 pair products, kept; their uniform
+  quantile transform; a 13-column SVD block; the fingerprint), adaptive members 27;
+* the quantile block of each quantile member: sklearn's QuantileTransformer with the capped
+  settings, fitted on the same context rows, to 1e-12;
+* the SVD block: column norms equal the singular values of the scaled block it is taken from
+  (numpy's LAPACK SVD), the components orthonormal, and the block the projection on them;
+* the whole member's features: the GPU run equals the CPU run (float64 SVDs) to 1e-9.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from sklearn.preprocessing import QuantileTransformer
+
+import regressor_case as case
+from nori_amd import ensemble as en
+
+pytestmark = pytest.mark.gpu
+
+
+def _redistribute_io(member, x_tr, x_te, y):
+    """Run the member's steps on the context rows up to its redistribution step: (input, output)."""
+    cat = []
+    for step, seed in zip(member.steps, member.seeds):
+        if isinstance(step, en.WideTableProjection) and step.fit_on_test:
+            cat = step.fit(np.vstack([x_tr, x_te]), cat, seed)
+        else:
+            cat = step.fit(x_tr, cat, seed, y=y)
+        if isinstance(step, en.Redistribute):
+            return x_tr, step.apply(x_tr, is_test=False)[0], step, seed
+        x_tr, _ = step.apply(x_tr, is_test=False)
+        x_te, cat = step.apply(x_te, is_test=True)
+    raise AssertionError("member has no redistribution step")
+
+
+def test_default_members_on_config1_table(cuda):
+    x_tr, y_tr, x_te, _ = case.table()
+    y = ((y_tr - y_tr.mean()) / y_tr.std()).astype(np.float32)
+    gpu = en.build_members(en.DEFAULT_MEMBERS, 0, cuda)
+    cpu = en.build_members(en.DEFAULT_MEMBERS, 0, "cpu")
+    for i, (mg, mc) in enumerate(zip(gpu, cpu)):
+        a, b, cat = mg.features(x_tr, x_te, [], y)
+        print(f"member {i}: features {a.shape} / {b.shape}", flush=True)
+        assert a.shape == (1024, 66 if i < 4 else 27) and b.shape == (256, a.shape[1]) and cat == []
+        a_cpu, b_cpu, _ = mc.features(x_tr, x_te, [], y)
+        np.testing.assert_allclose(a, a_cpu, rtol=1e-9, atol=1e-9)
+        np.testing.assert_allclose(b, b_cpu, rtol=1e-9, atol=1e-9)
+        if i >= 4:
+            continue
+        x_in, out, step, seed = _redistribute_io(en.build_members(en.DEFAULT_MEMBERS, 0, cuda)[i], x_tr, x_te, y)
+        n, p = x_in.shape
+        static_seed, _ = en._rng(seed)
+        k = max(1, min(n // 10 + 1, p // 2))  # from the step's input width
+        assert out.shape == (n, 2 * p + k)
+        np.testing.assert_array_equal(out[:, :p], x_in)
+        qt = QuantileTransformer(output_distribution="uniform", n_quantiles=max(2, min(max(n // 5, 2), n, 256)),
+                                 subsample=min(n, 10000), random_state=static_seed).fit(x_in)
+        np.testing.assert_allclose(out[:, p:2 * p], qt.transform(x_in), rtol=0, atol=1e-12)
+        block = np.hstack([out[:, :p], out[:, p:2 * p]]).astype(np.float64)
+        scaled = block / block.std(axis=0)
+        svd = out[:, 2 * p:]
+        sv = np.linalg.svd(scaled, compute_uv=False)[:k]
+        np.testing.assert_allclose(np.linalg.norm(svd, axis=0), sv, rtol=1e-9)
+        comps = step.worker.named_steps["svd_worker"].transformer_list[1][1].named_steps["svd"].components_
+        np.testing.assert_allclose(comps @ comps.T, np.eye(k), atol=1e-10)
+        np.testing.assert_allclose(svd, scaled @ comps.T, rtol=1e-9, atol=1e-9)
+        print(f"member {i}: quantile block and {k}-column SVD block pinned", flush=True)
