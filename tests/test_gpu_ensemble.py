@@ -11,7 +11,8 @@ the GPU, and checked by what fixes it independently of this code:
   settings, fitted on the same context rows, to 1e-12;
 * the SVD block: column norms equal the singular values of the scaled block it is taken from
   (numpy's LAPACK SVD), the components orthonormal, and the block the projection on them;
-* the whole member's features: the GPU run equals the CPU run (float64 SVDs) to 1e-9.
+* the whole member's features: the GPU run equals the CPU run (float64 SVDs) to 1e-9, except
+  the row fingerprint, whose hash of a row's bytes changes with any last-bit difference.
 """
 
 from __future__ import annotations
@@ -51,8 +52,17 @@ def test_default_members_on_config1_table(cuda):
         print(f"member {i}: features {a.shape} / {b.shape}", flush=True)
         assert a.shape == (1024, 66 if i < 4 else 27) and b.shape == (256, a.shape[1]) and cat == []
         a_cpu, b_cpu, _ = mc.features(x_tr, x_te, [], y)
-        np.testing.assert_allclose(a, a_cpu, rtol=1e-9, atol=1e-9)
-        np.testing.assert_allclose(b, b_cpu, rtol=1e-9, atol=1e-9)
+        # every column but the row fingerprint equals the CPU run's; the fingerprint hashes a row's
+        # bytes, so a last-bit difference of the GPU SVD anywhere in a row changes it (the
+        # reference's hash on two devices behaves the same): it is held to its own contract, a
+        # unique value in [0, 1) per context row
+        order = mg.steps[-1].order
+        fp = int(np.where(order == len(order) - 1)[0][0])
+        rest = [j for j in range(a.shape[1]) if j != fp]
+        np.testing.assert_allclose(a[:, rest], a_cpu[:, rest], rtol=1e-9, atol=1e-9)
+        np.testing.assert_allclose(b[:, rest], b_cpu[:, rest], rtol=1e-9, atol=1e-9)
+        assert len(np.unique(a[:, fp])) == len(a) and ((a[:, fp] >= 0) & (a[:, fp] < 1)).all()
+        assert ((b[:, fp] >= 0) & (b[:, fp] < 1)).all()
         if i >= 4:
             continue
         x_in, out, step, seed = _redistribute_io(en.build_members(en.DEFAULT_MEMBERS, 0, cuda)[i], x_tr, x_te, y)
