@@ -212,14 +212,16 @@ def retain_context(contexts: dict, slot, entry, budget: int | None, size_of=cont
     return True
 
 
-def _query_trace(execution: MemoryPolicy, events, *, history: list, pipeline_id: int, context_row_chunk,
-                 reason: str) -> MemoryPolicy:
+def _query_trace(execution: MemoryPolicy, events, *, history: list, pipeline_id, context_row_chunk,
+                 reason: str, path: str = "cached") -> MemoryPolicy:
     """One ``attempt_history`` entry per decode event of an attempt (the query-chunk halvings of
-    ``apply_context_cache``), returning the policy of the last (predictor.py:1387-1421)."""
+    ``apply_context_cache``), returning the policy of the last (predictor.py:1387-1421).
+    ``pipeline_id``: the member, or the list of members of a batched attempt."""
+    ids = list(pipeline_id) if isinstance(pipeline_id, (list, tuple)) else [pipeline_id]
     final = execution
     for i, (query_chunk, outcome) in enumerate(events):
         final = execution.escalated(execution.rung, dropped_context_rows=0, query_chunk=query_chunk)
-        history.append(memory_attempt(final, pipeline_ids=[pipeline_id], path="cached", rung=final.rung,
+        history.append(memory_attempt(final, pipeline_ids=ids, path=path, rung=final.rung,
                                       context_row_chunk=context_row_chunk, query_chunk=query_chunk, outcome=outcome,
                                       reason=reason if i == 0 else "oom_retry"))
     return final
@@ -289,6 +291,12 @@ def run_cache_attempts(requested: MemoryPolicy, resolved: MemoryPolicy, attempt,
     raise AssertionError("unreachable: the attempt list is never empty")
 
 
+# Members scored together in one batched cache build and apply: at most this many, and only
+# when their feature matrices are at most this wide (predictor.py:58-67).
+MEMBER_BATCH = 4
+MEMBER_BATCH_MAX_FEATURES = 256
+
+
 def _severity(policy: MemoryPolicy) -> tuple:
     """How degraded an outcome is (predictor.py:1307-1331): rung, then dropped rows, then a
     smaller context-row chunk, then a smaller query chunk."""
@@ -344,6 +352,7 @@ class NoriRegressor:
         self._report = None
         self._attempt_history: list = []
         self._outcome_policy = None
+        self._member_fits: dict = {}  # member slot -> (fit key, fitted member, its context features)
 
     # ------------------------------------------------------------------ sklearn surface
     def get_params(self, deep: bool = True) -> dict:
@@ -391,6 +400,7 @@ class NoriRegressor:
         std = float(y_arr.std())
         self.y_std_ = std if std >= 1e-12 else 1.0
         self._contexts = {}
+        self._member_fits = {}
         return self
 
     # ------------------------------------------------------------------ predict
@@ -447,26 +457,114 @@ class NoriRegressor:
 
     def _ensemble_bank(self, net: FeaturesTransformer, x_test: np.ndarray, y_norm: np.ndarray, slot0: int = 0):
         """The mean of the members' quantile banks (predictor.py:2972-3000, 3533): each member's
-        features from the context and query rows, scored through that member's context cache."""
+        features from the context and query rows, scored through that member's context cache.
+
+        Members whose context and query matrices have the same shapes are scored together, up to
+        ``MEMBER_BATCH`` at a time and at most ``MEMBER_BATCH_MAX_FEATURES`` features wide, as
+        the tables of one batched cache build and apply (predictor.py:2325-2359, 2497-2700) when
+        the memory policy keeps the caches resident; the rest, and a batch that runs out of
+        device memory, one member at a time. A member whose preprocessing fit did not read the
+        query rows keeps that fit for later calls on the same context and only transforms the
+        new query rows (the fit depends on the context rows, the targets and its seeds alone)."""
         config = ensemble.DEFAULT_MEMBERS if self.inference_config is None else self.inference_config
         members = ensemble.build_members(config, self.seed, self.device_)
         categorical = ensemble.categorical_columns(self.X_train_)
-        total = None
+        fit_key = (repr(ensemble.read_members(config)), self.seed, y_norm.tobytes(), str(self.device_))
+        feats = []
+        for i, member in enumerate(members):
+            held = self._member_fits.get(slot0 + i)
+            if held is not None and held[0] == fit_key and not held[1].reads_queries:
+                x_ctx, x_q = held[2], held[1].query_features(x_test)
+            else:
+                x_ctx, x_q, _ = member.features(self.X_train_, x_test, categorical, y_norm)
+                self._member_fits[slot0 + i] = (fit_key, member, x_ctx)
+            feats.append((np.ascontiguousarray(x_ctx, dtype=np.float32), np.ascontiguousarray(x_q, dtype=np.float32)))
+        groups: dict = {}
+        for i, (x_ctx, x_q) in enumerate(feats):
+            groups.setdefault((x_ctx.shape, x_q.shape), []).append(i)
+        batches = []
+        for idx in groups.values():
+            size = MEMBER_BATCH if feats[idx[0]][0].shape[1] <= MEMBER_BATCH_MAX_FEATURES else 1
+            batches += [idx[j:j + size] for j in range(0, len(idx), size)]
+        banks: list = [None] * len(members)
         reused = True
         quantized = None
-        for i, member in enumerate(members):
-            x_ctx, x_q, _ = member.features(self.X_train_, x_test, categorical, y_norm)
-            bank, was_reused, policy = self._quantile_bank(net, np.ascontiguousarray(x_ctx, dtype=np.float32),
-                                                           np.ascontiguousarray(x_q, dtype=np.float32), y_norm, slot0 + i)
+        for batch in batches:
+            got = None
+            if len(batch) > 1:
+                got = self._batched_banks(net, [feats[i][0] for i in batch], [feats[i][1] for i in batch], y_norm,
+                                          tuple(slot0 + i for i in batch))
+            if got is not None:
+                out, was_reused, policy = got
+                for j, i in enumerate(batch):
+                    banks[i] = out[j]
+            else:
+                for i in batch:
+                    banks[i], was_reused, policy = self._quantile_bank(net, feats[i][0], feats[i][1], y_norm, slot0 + i)
             reused &= was_reused
             if policy.cache_dtype == "int8":
                 quantized = policy
-            total = bank if total is None else total + bank
+        total = banks[0]
+        for b in banks[1:]:
+            total = total + b
         self._report["context_reused"] = reused
         self._report["ensemble_members"] = len(members)
         if quantized is not None:
             warn_quantized(quantized)  # once per predict, as the reference warns once per call
         return total / len(members)
+
+    def _batched_banks(self, net: FeaturesTransformer, xs_ctx: list, xs_q: list, y_norm: np.ndarray, slots: tuple):
+        """Several members' banks from one cache build and apply over their feature matrices
+        stacked as tables, or None where the batch does not apply: a policy rung other than a
+        resident cache without row chunks (the reference batches only those), or a batch that
+        runs out of device memory (recorded; its members are then scored one at a time)."""
+        dev = self.device_
+        if dev.type != "cuda":
+            raise RuntimeError("NoriRegressor runs on a ROCm GPU: the nori_amd kernels have no CPU path")
+        amp = bool(self.mix_precision)
+        n_groups = math.ceil(xs_ctx[0].shape[1] / net.features_per_group) + 1
+        policy = self._policy(net, n_groups, 2 if amp else 4, tables=len(slots))
+        if (policy.rung not in ("resident_bf16", "resident_int8") or policy.offload_to_host
+                or policy.context_row_chunk is not None or policy.stream_context):
+            return None
+        slot = ("batch",) + slots
+        x_ctx = np.stack(xs_ctx)
+        y_ctx = np.broadcast_to(y_norm, (len(slots), len(y_norm))).copy()
+        build = dict(cache_dtype=policy.cache_dtype, offload_kv_cache=False, fit_row_chunk=None)
+        key = (tuple(sorted(build.items())), amp, str(dev))
+        events: list = []
+        context = None
+        try:
+            with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16, enabled=amp):
+                context = self._reused_context(slot, key, x_ctx, y_ctx) if policy.reuse_context_cache else None
+                reused = context is not None
+                if context is None:
+                    context = net.build_context_cache(torch.from_numpy(x_ctx).to(dev), torch.from_numpy(y_ctx).to(dev),
+                                                      **build)
+                    if policy.reuse_context_cache:
+                        retain_context(self._contexts, slot, (key, x_ctx.tobytes(), y_ctx.tobytes(), context),
+                                       self._context_budget_bytes())
+                xq = torch.from_numpy(np.stack(xs_q)).to(dev)
+                bank = net.apply_context_cache(xq, context, adaptive_query_chunk=policy.adaptive_query_chunk,
+                                               query_chunk_attempt_callback=lambda q, o: events.append((q, o))).float()
+        except torch.cuda.OutOfMemoryError:
+            self._attempt_history.append(memory_attempt(
+                policy, pipeline_ids=list(slots), path="pipeline_batch", rung=policy.rung, context_row_chunk=None,
+                query_chunk=events[-1][0] if events else None, outcome="oom", reason="resolved"))
+            self._contexts.pop(slot, None)
+            del context
+            torch.cuda.empty_cache()
+            return None
+        if not bool(torch.isfinite(bank).all()):
+            raise RuntimeError("the model produced non-finite predictions")  # predictor.py:731-765
+        final = _query_trace(policy, events or [(int(xs_q[0].shape[0]), "success")], history=self._attempt_history,
+                             pipeline_id=list(slots), context_row_chunk=None, reason="resolved",
+                             path="pipeline_batch")
+        if self._outcome_policy is None or _severity(final) > _severity(self._outcome_policy):
+            self._outcome_policy = final
+        self._report = self._outcome_policy.as_report()
+        self._report["attempt_history"] = list(self._attempt_history)
+        return [bank[j] for j in range(len(slots))], reused, final
 
     def _yeo_johnson_pass(self, net, x_test, y_norm, point, taus, collapse) -> np.ndarray:
         """With "yj" among the augmentations and a target skew (unbiased) of at least
@@ -532,13 +630,13 @@ class NoriRegressor:
             self._net = net.to(self.device_).eval()
         return self._net
 
-    def _policy(self, net: FeaturesTransformer, n_groups: int, compute_bytes: int) -> MemoryPolicy:
+    def _policy(self, net: FeaturesTransformer, n_groups: int, compute_bytes: int, tables: int = 1) -> MemoryPolicy:
         policy = MemoryPolicy.coerce(self.memory_policy)
         vram = None
         if self.device_.type == "cuda":
             vram = torch.cuda.get_device_properties(self.device_).total_memory / 1024**3
-        est = estimate_cache_gb(n_context_rows=self.X_train_.shape[0], n_groups=n_groups, nlayers=net.nlayers,
-                                embed_dim=net.embed_dim, bytes_per_element=compute_bytes)
+        est = tables * estimate_cache_gb(n_context_rows=self.X_train_.shape[0], n_groups=n_groups,
+                                         nlayers=net.nlayers, embed_dim=net.embed_dim, bytes_per_element=compute_bytes)
         return policy.resolve(est_cache_gb=est, bytes_per_element=compute_bytes,
                               head_dim=net.embed_dim // net.nhead, total_vram_gb=vram)
 

@@ -199,6 +199,13 @@ class WideTableProjection:
         x = np.asarray(x, dtype=np.float64)
         return self.svd.transform(np.where(np.isnan(x), 0.0, x)).astype(np.float32), []
 
+    def depends_on_rows(self) -> bool:
+        """Whether the fit's outcome depends on the rows' values, not only on the column count:
+        an active projection does, and so does the gate when binary columns can open it."""
+        if self.strategy == "passthrough":
+            return False
+        return self.svd is not None or self.binary_threshold <= 1.0
+
 
 class FeatureCap:
     """MaxFeatureSubsampler (preprocess.py:1685-1731): at most ``max_features`` columns, a sorted
@@ -629,14 +636,27 @@ class Member:
         """The member's (context, query) feature matrices: each step fitted on the context
         (the wide-table projection with ``fit_on_test`` on both splits) and applied to both."""
         cat = list(categorical)
+        self.reads_queries = False
         for step, seed in zip(self.steps, self.seeds):
             if isinstance(step, WideTableProjection) and step.fit_on_test and len(x_test):
                 cat = step.fit(np.vstack([x_train, x_test]), cat, seed)
+                self.reads_queries |= step.depends_on_rows()
             else:
                 cat = step.fit(x_train, cat, seed, y=y_train)
             x_train, _ = step.apply(x_train, is_test=False)
             x_test, cat = step.apply(x_test, is_test=True)
+        self.categorical = cat
         return np.asarray(x_train), np.asarray(x_test), cat
+
+    def query_features(self, x_test: np.ndarray) -> np.ndarray:
+        """Other query rows through the steps ``features`` fitted, for a member whose fit did not
+        read the query rows (``reads_queries`` False): the same matrix ``features`` would give
+        for them, since every other step is fitted on the context alone."""
+        if getattr(self, "reads_queries", True):
+            raise RuntimeError("this member's fit read its query rows; fit it again with features()")
+        for step in self.steps:
+            x_test, _ = step.apply(x_test, is_test=True)
+        return np.asarray(x_test)
 
 
 def build_members(config, seed: int, device) -> list[Member]:

@@ -407,3 +407,28 @@ def test_disabled_transductive_flag_is_byte_identical():
     a.fit(x_train, [], 0)
     b.fit(x_train, [], 0)
     np.testing.assert_array_equal(a.apply(x_test)[0], b.apply(x_test)[0])
+
+
+def test_a_fitted_member_transforms_new_query_rows_as_a_fresh_fit_would():
+    # every default step is fitted on the context alone (the transductive projection is a
+    # pass-through below 257 columns, whatever the rows), so a member fitted once transforms
+    # other query rows to exactly what fitting it again with them gives
+    x_tr, y_tr, x_te, _ = case.table()
+    y = ((y_tr - y_tr.mean()) / y_tr.std()).astype(np.float32)
+    other = np.random.default_rng(9).standard_normal((40, x_tr.shape[1])).astype(np.float32)
+    for i, (fitted, fresh) in enumerate(zip(en.build_members(en.DEFAULT_MEMBERS, 0, "cpu"),
+                                            en.build_members(en.DEFAULT_MEMBERS, 0, "cpu"))):
+        a, _, _ = fitted.features(x_tr, x_te, [], y)
+        assert fitted.reads_queries is False
+        a2, b2, _ = fresh.features(x_tr, other, [], y)
+        np.testing.assert_array_equal(a, a2)
+        np.testing.assert_array_equal(fitted.query_features(other), b2)
+    # an active transductive projection reads the query rows: no reuse
+    wide = np.random.default_rng(1).standard_normal((90, 300)).astype(np.float32)
+    member = en.Member({"HighDimFeatureSelector": {"strategy": "svd_all", "svd_components": 8,
+                                                   "n_features_threshold": 256, "fit_on_test": True}},
+                       list(range(en.SEED_SLOTS)), 0, "cpu")
+    member.features(wide[:60], wide[60:], [], np.zeros(60, dtype=np.float32))
+    assert member.reads_queries is True
+    with pytest.raises(RuntimeError):
+        member.query_features(wide[60:])

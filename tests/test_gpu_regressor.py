@@ -221,3 +221,22 @@ def test_out_of_memory_on_the_opening_rung_retries_the_next(gold, model, cuda, m
         ("resident_bf16", "oom", "resolved"), ("resident_int8", "success", "oom_retry")]
     assert report["rung"] == "resident_int8" and report["cache_dtype"] == "int8"
     check_relative(point, gold["case/point"], PREDICTION_BAR, "nori-6m point predictions after the retry (fp32)")
+
+
+def test_same_shaped_members_are_scored_in_batches(gold, model, cuda, monkeypatch):
+    # the default ensemble's two groups of four same-shaped members each run as one batched
+    # cache build and apply (predictor.py:2325-2359, 2497-2700); the predictions equal scoring
+    # the members one at a time, and a second call reuses both the batched caches and the
+    # members' preprocessing fits, giving the same bits
+    kwargs = dict(model=model, device=cuda, memory_policy={"cache_dtype": "int8"}, mix_precision=False)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", CacheQuantizedWarning)
+        reg = api.NoriRegressor(**kwargs).fit(gold["case/x_train"], gold["case/y_train"])
+        batched = reg.predict(gold["case/x_test"])
+        history = reg.memory_report_["attempt_history"]
+        assert [a["pipeline_ids"] for a in history if a["path"] == "pipeline_batch"] == [[0, 1, 2, 3], [4, 5, 6, 7]]
+        again = reg.predict(gold["case/x_test"])
+        assert reg.memory_report_["context_reused"] is True and np.array_equal(batched, again)
+        monkeypatch.setattr(api, "MEMBER_BATCH", 1)
+        one = api.NoriRegressor(**kwargs).fit(gold["case/x_train"], gold["case/y_train"]).predict(gold["case/x_test"])
+    check_relative(batched, one, PREDICTION_BAR, "default ensemble, batched members vs one at a time (fp32)")
