@@ -39,7 +39,7 @@ import math
 import numpy as np
 import torch
 
-from . import ensemble
+from . import ensemble, graphs
 from .memory_policy import RUNGS, MemoryPolicy, estimate_cache_gb, fit_row_chunk_attempts, memory_attempt, warn_quantized
 from .transformer import FeaturesTransformer
 
@@ -426,6 +426,11 @@ class NoriRegressor:
         if x_test.shape[1] != self.n_features_in_:
             raise ValueError(f"X has {x_test.shape[1]} features, the context has {self.n_features_in_}")
         net = self._network()
+        # exact graph replay of the cached query layers (predictor.py:2394-2482), on request
+        if graphs.cached_graphs_requested():
+            graphs.enable_cached_graphs(net)
+        else:
+            graphs.disable_cached_graphs(net)
         y_norm = ((self.y_train_ - self.y_mean_) / self.y_std_).astype(np.float32)
         # one call's memory outcome: its attempts and its most degraded rung (predictor.py:1333-1351)
         self._attempt_history = []
@@ -463,7 +468,8 @@ class NoriRegressor:
         ``MEMBER_BATCH`` at a time and at most ``MEMBER_BATCH_MAX_FEATURES`` features wide, as
         the tables of one batched cache build and apply (predictor.py:2325-2359, 2497-2700) when
         the memory policy keeps the caches resident; the rest, and a batch that runs out of
-        device memory, one member at a time. A member whose preprocessing fit did not read the
+        device memory, one member at a time (always, when exact graph replay is requested:
+        ``SYNTHEFY_EXACT_CACHED_CUDAGRAPHS=1``). A member whose preprocessing fit did not read the
         query rows keeps that fit for later calls on the same context and only transforms the
         new query rows (the fit depends on the context rows, the targets and its seeds alone)."""
         config = ensemble.DEFAULT_MEMBERS if self.inference_config is None else self.inference_config
@@ -484,7 +490,10 @@ class NoriRegressor:
             groups.setdefault((x_ctx.shape, x_q.shape), []).append(i)
         batches = []
         for idx in groups.values():
+            # exact graph replay keeps every member at one table, as the reference's exact mode does
             size = MEMBER_BATCH if feats[idx[0]][0].shape[1] <= MEMBER_BATCH_MAX_FEATURES else 1
+            if graphs.cached_graphs_requested():
+                size = 1
             batches += [idx[j:j + size] for j in range(0, len(idx), size)]
         banks: list = [None] * len(members)
         reused = True

@@ -88,8 +88,9 @@ class QASSMaxScaling(nn.Module):
     def forward(self, q: torch.Tensor, key_len: int) -> torch.Tensor:
         if key_len <= 1:
             return q
-        # log n in double, cast once: an fp16 key count overflows at 65520 rows
-        log_n = torch.tensor(math.log(float(max(key_len, 2))), device=q.device, dtype=q.dtype)
+        # log n in double, cast once: an fp16 key count overflows at 65520 rows (a fill on the
+        # device, not a host copy, so the pass can be captured into a graph)
+        log_n = torch.full((), math.log(float(max(key_len, 2))), device=q.device, dtype=q.dtype)
         if self.qass_mode == "log_only":
             return q * log_n.view(1, 1, 1, 1)
         base_delta = self.base_mlp(log_n.view(1, 1)).view(1, 1, self.num_heads, self.head_dim)
