@@ -15,11 +15,16 @@ from .attention import attend_dense, compute_attention_blockwise, icl_attention
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, dequantize_int8, quantize_int8, scale_caches
 from .kv_project import project_quantize_kv
 from .api import NoriRegressor
+from .degradation import CacheQuantizedWarning, DegradedPipelineWarning, SvdFallbackWarning, strict_pipeline
 from .norm import RMSNorm, rms_norm
 from .transformer import ContextCache, FeaturesTransformer
 
 __all__ = [
     "BlockwiseSeqKV",
+    "CacheQuantizedWarning",
+    "DegradedPipelineWarning",
+    "SvdFallbackWarning",
+    "strict_pipeline",
     "ContextCache",
     "FeaturesTransformer",
     "NoriRegressor",

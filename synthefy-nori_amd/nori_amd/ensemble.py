@@ -17,13 +17,15 @@ same inputs and seed. The steps:
 =============================  ==============================================================
 config key                     here
 =============================  ==============================================================
-HighDimFeatureSelector         ``WideTableProjection`` (the gate and the ``svd_all`` strategy)
+HighDimFeatureSelector         ``WideTableProjection`` (the gate; SVD, correlation, mutual
+                               information and extra-trees strategies)
 MaxFeatureSubsampler           ``FeatureCap``
 PolynomialInteractionGenerator ``PairProducts``
 (always)                       ``DropConstantColumns``
 MADWinsorizer                  ``MadClip``
-RebalanceFeatureDistribution   ``Redistribute`` (+ ``PerColumnTransform`` for "adaptive")
-CategoricalFeatureEncoder      ``CategoryCodes``
+RebalanceFeatureDistribution   ``Redistribute`` (+ ``PerColumnTransform`` for "adaptive",
+                               ``RevertingPowerTransform`` for "power")
+CategoricalFeatureEncoder      ``CategoryCodes`` (ordinal codes or one-hot columns)
 FingerprintFeatureEncoder      ``RowFingerprint``
 FeatureShuffler                ``ColumnOrder``
 =============================  ==============================================================
@@ -38,22 +40,29 @@ import copy
 import hashlib
 import json
 import random
+import warnings
 
 import numpy as np
 import torch
 from sklearn.base import BaseEstimator, TransformerMixin
 from sklearn.compose import ColumnTransformer
+from sklearn.decomposition import TruncatedSVD
+from sklearn.ensemble import ExtraTreesRegressor
+from sklearn.feature_selection import mutual_info_regression
 from sklearn.impute import SimpleImputer
 from sklearn.pipeline import FeatureUnion, Pipeline
 from sklearn.preprocessing import (
     FunctionTransformer,
     MinMaxScaler,
+    OneHotEncoder,
     OrdinalEncoder,
     PowerTransformer,
     QuantileTransformer,
     RobustScaler,
     StandardScaler,
 )
+
+from .degradation import SvdFallbackWarning
 
 __all__ = ["DEFAULT_MEMBERS", "Member", "build_members", "categorical_columns", "read_members"]
 
@@ -79,6 +88,8 @@ SEED_SLOTS = 10  # seeds per member (predictor.py:219); the wide-table projectio
 MIN_ROWS_FOR_CATEGORIES = 100  # predictor.py:216
 MIN_UNIQUE_FOR_NUMERIC = 4  # predictor.py:218
 QUANTILE_CAP, QUANTILE_SUBSAMPLE_CAP = 256, 10000  # preprocess.py:63-70 (their defaults)
+QUANTILE_SUBSAMPLE_DEFAULT = 10000  # sklearn's QuantileTransformer default subsample
+ONE_HOT_MAX_ELEMENTS = 1_000_000  # preprocess.py:729-731: a wider one-hot matrix is not built
 ADAPTIVE_FIT_ROWS = 2000  # preprocess.py:380-384
 _MAX_SEED = int(np.iinfo(np.int32).max)
 
@@ -113,9 +124,29 @@ def categorical_columns(x: np.ndarray) -> list[int]:
 
 # ---------------------------------------------------------------------------------- helpers
 def _inf_to_nan(x):
-    x = np.array(x, dtype=np.float64, copy=True)
-    x[np.isinf(x)] = np.nan
-    return x
+    """Infinities to NaN, in the input's own float type (float32 stays float32)."""
+    out = np.array(x, copy=True)
+    if out.dtype.kind == "f":
+        out[np.isinf(out)] = np.nan
+    return out
+
+
+def _nonfinite_to_nan():
+    return FunctionTransformer(func=_inf_to_nan, inverse_func=_identity, check_inverse=False)
+
+
+def _mean_fill():
+    return SimpleImputer(missing_values=np.nan, strategy="mean", keep_empty_features=True)
+
+
+def _shift_nonnegative(x):
+    """The matrix moved up by the magnitude of its smallest entry. Stateless, as the reference's
+    step is (preprocess.py:45-46): the query matrix is moved by its own minimum."""
+    return x + np.abs(np.nanmin(x))
+
+
+def _plus_epsilon(x):
+    return x + 1e-10
 
 
 def _identity(x):
@@ -133,18 +164,34 @@ class DeviceSVD(BaseEstimator, TransformerMixin):
     """The exact truncated SVD of the context (torch.linalg.svd in float64 on the model's
     device), signs fixed so each component's largest-magnitude entry of U is positive (sklearn's
     u-based svd_flip): ``fit_transform`` is U*S, ``transform`` projects on the components
-    (preprocess.py:86-156)."""
+    (preprocess.py:86-156). When the device solver raises (out of memory, no convergence),
+    sklearn's TruncatedSVD with ``algorithm`` (default randomized) and ``random_state`` takes
+    over, as the reference falls back (preprocess.py:107-112); the projection runs on the GPU
+    when the device is one, else in numpy."""
 
-    def __init__(self, n_components: int, device):
+    def __init__(self, n_components: int, device, random_state=None, algorithm=None):
         self.n_components = int(n_components)
         self.device = device
+        self.random_state = random_state
+        self.algorithm = algorithm
 
     def fit(self, x, y=None):
         self.fit_transform(x)
         return self
 
     def fit_transform(self, x, y=None):
-        xt = torch.from_numpy(np.asarray(x, dtype=np.float64)).to(self.device)
+        x = np.asarray(x, dtype=np.float64)
+        try:
+            return self._device_fit(x)
+        except Exception:
+            svd = TruncatedSVD(n_components=self.n_components, algorithm=self.algorithm or "randomized",
+                               random_state=self.random_state)
+            out = svd.fit_transform(x)
+            self.components_ = svd.components_
+            return out
+
+    def _device_fit(self, x):
+        xt = torch.from_numpy(x).to(self.device)
         n, p = xt.shape
         k = max(1, min(self.n_components, p, n))
         u, s, vh = torch.linalg.svd(xt, full_matrices=False)
@@ -155,54 +202,171 @@ class DeviceSVD(BaseEstimator, TransformerMixin):
         return (u * (s * signs)[None, :]).cpu().numpy()
 
     def transform(self, x):
-        xt = torch.from_numpy(np.asarray(x, dtype=np.float64)).to(self.device)
-        return (xt @ torch.from_numpy(self.components_).to(self.device).T).cpu().numpy()
+        x = np.asarray(x, dtype=np.float64)
+        if torch.device(self.device).type == "cuda":
+            try:
+                xt = torch.from_numpy(x).to(self.device)
+                return (xt @ torch.from_numpy(self.components_).to(self.device).T).cpu().numpy()
+            except torch.cuda.OutOfMemoryError:
+                pass
+        return x @ self.components_.T
 
 
 # ---------------------------------------------------------------------------------- steps
 class WideTableProjection:
     """HighDimFeatureSelector (preprocess.py:1323-1684): a pass-through unless the table has
     more than ``n_features_threshold`` columns or at least ``binary_threshold`` of them are
-    binary; then (strategy "svd_all") the NaN-zeroed columns are replaced by their first
-    min(svd_components, p - 1, n - 1, n // svd_rows_per_component) SVD coordinates."""
+    binary (exactly two distinct finite values); then, by strategy:
+
+    * ``svd_all``: the NaN-zeroed columns replaced by their first
+      min(svd_components, p - 1, n - 1, n // svd_rows_per_component) SVD coordinates;
+    * ``svd_binary``: when the binary columns are at least ``binary_threshold`` of the table and
+      at least two, they are replaced by the first min(svd_components, n_binary - 1, n - 1) SVD
+      coordinates of their NaN-zeroed block, placed after the other columns;
+    * ``corr`` / ``mi`` / ``extratrees``: the ``top_k`` columns with the largest |Pearson
+      correlation| with the target, sklearn's mutual information, or an extra-trees forest's
+      impurity importances (the last two on NaN-zeroed rows with a finite target, at most
+      ``subsample_rows`` of them drawn without replacement), kept in table order.
+
+    The target-driven strategies pass through when there is no target (the fit on context +
+    query rows, ``fit_on_test``, has none), when it has the wrong length or fewer than
+    max(10, top_k // 4) finite values, or when the scorer raises; so does any other strategy
+    name. An SVD that raises warns with ``SvdFallbackWarning`` and degrades as the reference
+    does: at fit, to a pass-through; at transform, to one all-zero column (``svd_all``) or to
+    the non-binary columns (``svd_binary``)."""
 
     def __init__(self, *, strategy="passthrough", top_k=256, n_features_threshold=128, binary_threshold=0.5,
                  svd_components=64, svd_rows_per_component=1, extratrees_n_estimators=100, subsample_rows=5000,
                  fit_on_test=False, device=None):
-        if strategy not in ("passthrough", "svd_all"):
-            raise NotImplementedError(f"HighDimFeatureSelector strategy {strategy!r} is not part of this build")
         self.strategy, self.fit_on_test = strategy, bool(fit_on_test)
+        self.top_k = int(top_k)
         self.n_features_threshold, self.binary_threshold = int(n_features_threshold), float(binary_threshold)
         self.svd_components, self.rows_per_component = int(svd_components), max(1, int(svd_rows_per_component))
+        self.n_trees, self.subsample_rows = int(extratrees_n_estimators), int(subsample_rows)
         self.device = device
-        self.svd = None
+        self.svd, self.selected, self.categorical = None, None, []
+
+    @staticmethod
+    def binary_columns(x) -> np.ndarray:
+        """Columns with exactly two distinct finite values."""
+        return np.array([len(np.unique(c[np.isfinite(c)])) == 2 for c in x.T], dtype=bool)
+
+    @staticmethod
+    def correlations(x, y) -> np.ndarray:
+        """|Pearson r| of each column with the target over the rows where both are finite; 0 for a
+        column with fewer than 3 such rows or a (near-)constant side (preprocess.py:1434-1451)."""
+        scores = np.zeros(x.shape[1], dtype=np.float64)
+        for j in range(x.shape[1]):
+            ok = np.isfinite(x[:, j]) & np.isfinite(y)
+            if ok.sum() < 3:
+                continue
+            a, b = x[ok, j], y[ok]
+            if a.std() < 1e-8 or b.std() < 1e-8:
+                continue
+            r = np.corrcoef(a, b)[0, 1]
+            scores[j] = abs(r) if np.isfinite(r) else 0.0
+        return scores
+
+    def _passthrough(self, categorical):
+        self.svd, self.selected, self.categorical = None, None, list(categorical)
+        return list(self.categorical)
+
+    def _degraded(self, stage, exc, fallback):
+        warnings.warn(f"HighDimFeatureSelector(strategy={self.strategy!r}): SVD {stage} failed "
+                      f"({type(exc).__name__}: {str(exc)[:120]}) -> {fallback}. Predictions are degraded, not "
+                      f"the configured pipeline; strict_pipeline() makes this an error.", SvdFallbackWarning,
+                      stacklevel=3)
+
+    @staticmethod
+    def _remap(kept, categorical):
+        position = {int(old): new for new, old in enumerate(kept)}
+        return sorted(position[int(c)] for c in categorical if int(c) in position)
 
     def fit(self, x, categorical, seed, y=None):
         x = np.asarray(x, dtype=np.float64)
         n, p = x.shape
-        self.svd = None
         if self.strategy == "passthrough" or p == 0:
-            self.categorical = list(categorical)
-            return self.categorical
-        binary = np.array([len(np.unique(c[np.isfinite(c)])) == 2 for c in x.T])
-        if not (p > self.n_features_threshold or float(binary.mean()) >= self.binary_threshold):
-            self.categorical = list(categorical)
-            return self.categorical
-        k = max(1, min(self.svd_components, p - 1, n - 1, n // self.rows_per_component))
-        self.svd = DeviceSVD(k, self.device).fit(np.where(np.isnan(x), 0.0, x))
-        self.categorical = []
-        return []
+            return self._passthrough(categorical)
+        binary = self.binary_columns(x)
+        frac = float(binary.mean())
+        if not (p > self.n_features_threshold or frac >= self.binary_threshold):
+            return self._passthrough(categorical)
+        seed_int = int(seed) % 2**31
+        if self.strategy in ("svd_all", "svd_binary"):
+            if self.strategy == "svd_binary":
+                if frac < self.binary_threshold or int(binary.sum()) < 2:
+                    return self._passthrough(categorical)
+                mask = binary
+                k = max(1, min(self.svd_components, int(binary.sum()) - 1, n - 1))
+                fallback = f"passthrough of all {p} raw columns ({int(binary.sum())} binary columns left unprojected)"
+            else:
+                mask = np.ones(p, dtype=bool)
+                k = max(1, min(self.svd_components, p - 1, n - 1, n // self.rows_per_component))
+                fallback = f"passthrough of all {p} raw columns (no reduction to {k} components)"
+            try:
+                svd = DeviceSVD(k, self.device, random_state=seed_int)
+                svd.fit(np.where(np.isnan(x[:, mask]), 0.0, x[:, mask]))
+            except Exception as exc:
+                self._degraded("fit", exc, fallback)
+                return self._passthrough(categorical)
+            self.svd, self.selected, self.mask, self.keep = svd, None, mask, np.where(~mask)[0]
+            self.categorical = self._remap(self.keep, categorical) if self.strategy == "svd_binary" else []
+            return list(self.categorical)
+        if y is None or self.strategy not in ("corr", "mi", "extratrees"):
+            return self._passthrough(categorical)
+        y = np.asarray(y, dtype=np.float64).ravel()
+        if y.size != n:
+            return self._passthrough(categorical)
+        finite = np.isfinite(y)
+        if int(finite.sum()) < max(10, self.top_k // 4):
+            return self._passthrough(categorical)
+        if self.strategy == "corr":
+            scores = self.correlations(x, y)
+        else:
+            xs, ys = x[finite], y[finite]
+            if len(xs) > self.subsample_rows:
+                rows = np.random.default_rng(int(seed) % 2**32).choice(len(xs), size=self.subsample_rows, replace=False)
+                xs, ys = xs[rows], ys[rows]
+            xs = np.where(np.isnan(xs), 0.0, xs)
+            try:
+                if self.strategy == "mi":
+                    scores = mutual_info_regression(xs, ys, random_state=seed_int)
+                else:
+                    forest = ExtraTreesRegressor(n_estimators=self.n_trees, random_state=seed_int, n_jobs=-1)
+                    scores = forest.fit(xs, ys).feature_importances_
+            except Exception:
+                return self._passthrough(categorical)
+        top = max(1, min(self.top_k, p))
+        self.svd, self.selected = None, np.sort(np.argsort(-np.asarray(scores), kind="stable")[:top])
+        self.categorical = self._remap(self.selected, categorical)
+        return list(self.categorical)
 
     def apply(self, x, is_test=False):
+        if self.selected is not None:
+            return x[:, self.selected], list(self.categorical)
         if self.svd is None:
-            return x, self.categorical
+            return x, list(self.categorical)
         x = np.asarray(x, dtype=np.float64)
-        return self.svd.transform(np.where(np.isnan(x), 0.0, x)).astype(np.float32), []
+        block = np.where(np.isnan(x[:, self.mask]), 0.0, x[:, self.mask])
+        try:
+            coords = self.svd.transform(block)
+        except Exception as exc:
+            if self.strategy == "svd_all":
+                self._degraded("transform", exc, f"a single all-zero column for {x.shape[0]} rows "
+                                                 f"(all {block.shape[1]} features dropped)")
+                return np.zeros((x.shape[0], 1), dtype=np.float32), []
+            self._degraded("transform", exc, f"dropping the {block.shape[1]} SVD-projected columns, keeping the "
+                                             f"{len(self.keep)} non-binary ones")
+            return x[:, self.keep].astype(np.float32), list(self.categorical)
+        if self.strategy == "svd_all":
+            return coords.astype(np.float32), []
+        return np.concatenate([x[:, self.keep], coords], axis=1).astype(np.float32), list(self.categorical)
 
     def depends_on_rows(self) -> bool:
         """Whether the fit's outcome depends on the rows' values, not only on the column count:
-        an active projection does, and so does the gate when binary columns can open it."""
-        if self.strategy == "passthrough":
+        an active projection does, and so does the gate when binary columns can open it. The
+        target-driven strategies pass through on a fit without a target."""
+        if self.strategy not in ("svd_all", "svd_binary"):
             return False
         return self.svd is not None or self.binary_threshold <= 1.0
 
@@ -417,13 +581,77 @@ class PerColumnTransform(BaseEstimator, TransformerMixin):
         return np.nan_to_num(out, nan=0.0, posinf=0.0, neginf=0.0)
 
 
+class RevertingPowerTransform(PowerTransformer):
+    """RobustPowerTransformer (preprocess.py:185-236): a per-column Yeo-Johnson transform, each
+    column standardized, that hands a column back unchanged when the fit-time output of that
+    column has a variance more than ``var_tolerance`` away from 1 or any value above
+    ``max_abs_value`` (a constant column, or one with a far outlier). A column whose lambda
+    search raises keeps lambda NaN and is left as it is.
+
+    Standardized, although the reference constructs its worker with ``standardize=False``: it
+    takes that through ``**kwargs``, which sklearn's ``clone`` cannot see, and ColumnTransformer
+    fits a clone, rebuilt with PowerTransformer's default ``standardize=True``. As there, the
+    fit returns the transformed (not reverted) columns, so the steps after this one are fitted
+    on them while ``transform`` feeds them the reverted columns."""
+
+    def __init__(self, var_tolerance: float = 1e-3, max_abs_value: float = 100.0, *, method="yeo-johnson",
+                 standardize=True, copy=True):
+        super().__init__(method=method, standardize=standardize, copy=copy)
+        self.var_tolerance, self.max_abs_value = var_tolerance, max_abs_value
+
+    def fit(self, x, y=None):
+        super().fit(x, y)
+        self.revert_ = np.array([], dtype=int)
+        return self
+
+    def fit_transform(self, x, y=None):
+        z = super().fit_transform(x, y)
+        off = np.abs(np.nanvar(z, axis=0) - 1.0) > self.var_tolerance
+        large = np.any(z > self.max_abs_value, axis=0)
+        self.revert_ = np.flatnonzero(off | large)
+        return z
+
+    def transform(self, x):
+        z = super().transform(x)
+        if len(self.revert_):
+            z[:, self.revert_] = np.asarray(x)[:, self.revert_]
+        return z
+
+    def _yeo_johnson_optimize(self, x):
+        try:
+            with warnings.catch_warnings():
+                warnings.filterwarnings("ignore", message=r"overflow encountered", category=RuntimeWarning)
+                return super()._yeo_johnson_optimize(x)
+        except Exception:
+            return np.nan
+
+    def _yeo_johnson_transform(self, x, lmbda):
+        return x if np.isnan(lmbda) else super()._yeo_johnson_transform(x, lmbda)
+
+
 class Redistribute:
     """RebalanceFeatureDistribution (preprocess.py:916-1222): the numeric columns through each
     worker transform, next to either all original columns (``original_flag``) or the categorical
     ones, and optionally an SVD block of the result (``svd_tag="svd"``: mean-imputed columns
-    scaled to unit variance, min(n // 10 + 1, p // 2) components). Worker tags here:
-    quantile_uniform_10 / _5 / _all_data, quantile_norm_all_data, adaptive, robust, squash and
-    None (identity)."""
+    scaled to unit variance, min(n // 10 + 1, p // 2) components). Worker tags:
+
+    * quantile_uniform_10 / _5 / _all_data, quantile_norm_all_data: sklearn's quantile transform,
+      capped at 256 quantiles and 10000 fitting rows;
+    * quantile_norm_10 / _5: what the reference's fitted worker is -- a uniform (not normal)
+      quantile transform with min(n // 10 or n // 5, n, 10000) quantiles, unseeded: its QTx takes
+      output_distribution and random_state through ``**kwargs``, which sklearn's ``clone`` (the
+      ColumnTransformer fits a clone) cannot see;
+    * power: ``RevertingPowerTransform`` -> infinities to NaN -> mean fill -> standardize ->
+      infinities to NaN -> mean fill;
+    * logNormal: infinities to NaN -> mean fill -> shift by the matrix's smallest magnitude ->
+      + 1e-10 -> log -> infinities to NaN -> mean fill;
+    * adaptive: ``PerColumnTransform``; robust and squash: sklearn's RobustScaler(unit_variance);
+    * None and any other name (the reference's fallback, which takes the default "quantile"
+      too): the identity.
+
+    The kernel-density-integral tags (kdi*, norm_and_kdi) need the third-party ``kditransform``
+    package (the reference's pyproject asks for kditransform>=1.0), which this environment does
+    not have; they raise NotImplementedError."""
 
     def __init__(self, *, worker_tags=None, discrete_flag=False, original_flag=False, svd_tag=None,
                  joined_svd_feature=True, joined_log_normal=True, device=None):
@@ -440,13 +668,29 @@ class Redistribute:
             return _capped_quantiles("uniform", max(n // 5, 2), seed, n, n)
         if tag == "quantile_norm_all_data":
             return _capped_quantiles("normal", max(n // 5, 2), seed, n, n)
+        if tag in ("quantile_norm_10", "quantile_norm_5"):
+            wanted = max(n // (10 if tag.endswith("_10") else 5), 2)
+            return QuantileTransformer(output_distribution="uniform", random_state=None,
+                                       n_quantiles=max(1, min(wanted, n, QUANTILE_SUBSAMPLE_DEFAULT)),
+                                       subsample=QUANTILE_SUBSAMPLE_DEFAULT)
+        if tag == "power":
+            return Pipeline([("power", RevertingPowerTransform()), ("inf_a", _nonfinite_to_nan()),
+                             ("fill_a", _mean_fill()), ("scale", StandardScaler()),
+                             ("inf_b", _nonfinite_to_nan()), ("fill_b", _mean_fill())])
+        if tag == "logNormal":
+            return Pipeline([("inf_a", _nonfinite_to_nan()), ("fill_a", _mean_fill()),
+                             ("shift", FunctionTransformer(func=_shift_nonnegative)),
+                             ("epsilon", FunctionTransformer(func=_plus_epsilon)),
+                             ("log", FunctionTransformer(np.log, validate=False)),
+                             ("inf_b", _nonfinite_to_nan()), ("fill_b", _mean_fill())])
         if tag == "adaptive":
             return PerColumnTransform(random_state=seed, n_quantiles=max(n // 10, 2))
         if tag in ("robust", "squash"):
             return RobustScaler(unit_variance=True)
-        if tag is None:
-            return FunctionTransformer(_identity)
-        raise NotImplementedError(f"RebalanceFeatureDistribution worker tag {tag!r} is not part of this build")
+        if isinstance(tag, str) and (tag.startswith("kdi") or tag == "norm_and_kdi"):
+            raise NotImplementedError(f"RebalanceFeatureDistribution worker tag {tag!r} needs the kditransform "
+                                      "package, which is not installed")
+        return FunctionTransformer(_identity)
 
     def fit(self, x, categorical, seed, y=None):
         static_seed, _ = _rng(seed)
@@ -467,13 +711,15 @@ class Redistribute:
         columns = ColumnTransformer(workers, remainder="drop", sparse_threshold=0.0)
         if self.svd_tag == "svd" and p >= 2:
             scaled = Pipeline([
-                ("i2n_pre", FunctionTransformer(func=_inf_to_nan, inverse_func=_identity, check_inverse=False)),
-                ("fill_missing_pre", SimpleImputer(missing_values=np.nan, strategy="mean", keep_empty_features=True)),
+                ("i2n_pre", _nonfinite_to_nan()),
+                ("fill_missing_pre", _mean_fill()),
                 ("standard", StandardScaler(with_mean=False)),
-                ("i2n_post", FunctionTransformer(func=_inf_to_nan, inverse_func=_identity, check_inverse=False)),
-                ("fill_missing_post", SimpleImputer(missing_values=np.nan, strategy="mean", keep_empty_features=True)),
+                ("i2n_post", _nonfinite_to_nan()),
+                ("fill_missing_post", _mean_fill()),
             ])
-            svd = Pipeline([("save_standard", scaled), ("svd", DeviceSVD(max(1, min(n // 10 + 1, p // 2)), self.device))])
+            svd = Pipeline([("save_standard", scaled),
+                            ("svd", DeviceSVD(max(1, min(n // 10 + 1, p // 2)), self.device, random_state=static_seed,
+                                              algorithm="arpack"))])
             self.worker = Pipeline([("worker", columns),
                                     ("svd_worker", FeatureUnion([("default", FunctionTransformer(func=_identity)),
                                                                  ("svd", svd)]))])
@@ -491,11 +737,17 @@ class CategoryCodes:
     columns that qualify (the "*feature_shuffled" strategies keep columns whose rarest level
     appears at least 10 times; "strict" also needs fewer than rows / 10 levels), moved to the
     front, with each column's levels relabelled by a seeded permutation for the "_shuffled"
-    strategies; "numeric" / "none" leave the matrix as it is."""
+    strategies; "onehot" puts sklearn's one-hot columns of every categorical column first (one
+    column for a two-level one, all-zero for a level the context did not have) -- unless that
+    matrix would hold a million entries or more on the context rows, when the matrix is left
+    as it is; "numeric" / "none" leave the matrix as it is."""
+
+    STRATEGIES = ("ordinal", "ordinal_strict_feature_shuffled", "ordinal_shuffled", "ordinal_feature_shuffled",
+                  "onehot", "numeric", "none")
 
     def __init__(self, *, encoding_strategy="ordinal"):
-        if encoding_strategy not in ("ordinal", "ordinal_strict_feature_shuffled", "ordinal_shuffled", "numeric", "none"):
-            raise NotImplementedError(f"CategoricalFeatureEncoder strategy {encoding_strategy!r} is not part of this build")
+        if encoding_strategy not in self.STRATEGIES and not str(encoding_strategy).startswith("ordinal"):
+            raise ValueError(f"Unsupported encoding strategy: {encoding_strategy}")
         self.strategy = encoding_strategy
 
     def _qualifies(self, col, strict):
@@ -509,6 +761,17 @@ class CategoryCodes:
         if self.strategy in ("numeric", "none"):
             self.categorical = list(categorical)
             return self.categorical
+        if self.strategy == "onehot":
+            columns = ColumnTransformer([("one_hot_encoder", OneHotEncoder(drop="if_binary", sparse_output=False,
+                                                                           handle_unknown="ignore"), list(categorical))],
+                                        remainder="passthrough").fit(x)
+            width = columns.transform(x).shape[1]
+            if x.shape[0] * width >= ONE_HOT_MAX_ELEMENTS:
+                self.categorical = list(categorical)
+            else:
+                self.columns = columns
+                self.categorical = list(range(width))[columns.output_indices_["one_hot_encoder"]]
+            return list(self.categorical)
         suffix = self.strategy[len("ordinal"):]
         cats = list(categorical)
         if "feature_shuffled" in suffix:

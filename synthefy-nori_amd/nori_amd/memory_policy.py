@@ -23,6 +23,8 @@ import os
 import warnings
 from dataclasses import dataclass, field
 
+from .degradation import CacheQuantizedWarning, DegradedPipelineWarning
+
 __all__ = [
     "ATTEMPT_OUTCOMES",
     "ATTEMPT_REASONS",
@@ -60,14 +62,6 @@ GIB = 1024**3
 ASSUMED_VRAM_GB = 24.0  # when the device cannot be asked (memory_policy.py: ASSUMED_VRAM_GB)
 # staged-row caps of the streamed context by accelerator size (memory_policy.py:157-168, 201-215)
 _STREAM_ROW_CHUNKS = ((80.0, 16384), (40.0, 8192), (0.0, 2048))
-
-
-class DegradedPipelineWarning(UserWarning):
-    """The model was handed less than the configured pipeline promised (inference/degradation.py)."""
-
-
-class CacheQuantizedWarning(DegradedPipelineWarning):
-    """The context K/V cache was stored int8 (inference/degradation.py, raised at predictor.py:3286-3305)."""
 
 
 class ContextTooLargeError(RuntimeError):

@@ -241,8 +241,6 @@ def test_wide_table_projection_gate():
     assert out.shape == (90, k) and cat == []
     sv = np.linalg.svd(wide, compute_uv=False)[:k]
     np.testing.assert_allclose(np.linalg.norm(out, axis=0), sv, rtol=1e-4)
-    with pytest.raises(NotImplementedError):
-        en.WideTableProjection(strategy="corr")
 
 
 # ---- the reference's own fingerprint tests (tests/test_fingerprint_feature_encoder.py:16-68)

@@ -17,6 +17,9 @@ the GPU, and checked by what fixes it independently of this code:
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import pytest
 from sklearn.preprocessing import QuantileTransformer
@@ -25,6 +28,8 @@ import regressor_case as case
 from nori_amd import ensemble as en
 
 pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "regressor_goldens.npz")
 
 
 def _redistribute_io(member, x_tr, x_te, y):
@@ -83,3 +88,61 @@ def test_default_members_on_config1_table(cuda):
         np.testing.assert_allclose(comps @ comps.T, np.eye(k), atol=1e-10)
         np.testing.assert_allclose(svd, scaled @ comps.T, rtol=1e-9, atol=1e-9)
         print(f"member {i}: quantile block and {k}-column SVD block pinned", flush=True)
+
+
+# members built from the steps the shipped configurations do not use: the svd_binary and
+# correlation projections, the power / logNormal / quantile_norm_10 redistributions and one-hot
+# codes (preprocess.py:686-832, 970-1222, 1323-1684)
+OTHER_MEMBERS = [
+    {"HighDimFeatureSelector": {"strategy": "corr", "top_k": 10, "n_features_threshold": 12},
+     "RebalanceFeatureDistribution": {"worker_tags": ["power"], "original_flag": True},
+     "CategoricalFeatureEncoder": {"encoding_strategy": "onehot"}, "FeatureShuffler": {"mode": "shuffle"}},
+    {"HighDimFeatureSelector": {"strategy": "svd_binary", "binary_threshold": 0.1, "svd_components": 8},
+     "RebalanceFeatureDistribution": {"worker_tags": ["logNormal"], "svd_tag": "svd"},
+     "FingerprintFeatureEncoder": True},
+    {"RebalanceFeatureDistribution": {"worker_tags": ["quantile_norm_10"], "original_flag": True},
+     "CategoricalFeatureEncoder": {"encoding_strategy": "onehot"}, "FeatureShuffler": {"mode": "rotate"}},
+]
+
+
+def _other_table():
+    x_tr, y_tr, x_te, _ = case.table()
+    x_tr, x_te = x_tr.copy(), x_te.copy()
+    # two binary columns and a three-level one, so the binary projection and one-hot codes engage
+    for j, levels in ((0, 2), (1, 2), (2, 3)):
+        x_tr[:, j] = np.floor(np.abs(x_tr[:, j]) * 7) % levels
+        x_te[:, j] = np.floor(np.abs(x_te[:, j]) * 7) % levels
+    return x_tr, y_tr, x_te
+
+
+def test_other_members_features_and_predictions(cuda):
+    import warnings
+
+    from nori_amd import api
+    from nori_amd.memory_policy import CacheQuantizedWarning
+    from nori_amd.transformer import FeaturesTransformer
+
+    x_tr, y_tr, x_te = _other_table()
+    y = ((y_tr - y_tr.mean()) / y_tr.std()).astype(np.float32)
+    cat = en.categorical_columns(x_tr)
+    assert cat == [0, 1, 2]
+    for i, (mg, mc) in enumerate(zip(en.build_members(OTHER_MEMBERS, 0, cuda), en.build_members(OTHER_MEMBERS, 0, "cpu"))):
+        a, b, _ = mg.features(x_tr, x_te, cat, y)
+        a_cpu, b_cpu, _ = mc.features(x_tr, x_te, cat, y)
+        print(f"other member {i}: features {a.shape} / {b.shape}", flush=True)
+        assert a.shape == a_cpu.shape and np.isfinite(a).all() and np.isfinite(b).all()
+        keep = list(range(a.shape[1] - 1)) if i == 1 else list(range(a.shape[1]))  # member 1 ends in the fingerprint
+        np.testing.assert_allclose(a[:, keep], a_cpu[:, keep], rtol=1e-9, atol=1e-9)
+        np.testing.assert_allclose(b[:, keep], b_cpu[:, keep], rtol=1e-9, atol=1e-9)
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        scales = json.loads(str(f["case/weight_scales"]))
+    model = case.seeded_model(FeaturesTransformer, api.NORI_6M_CONFIG, scales).to(cuda)
+    kwargs = dict(model=model, device=cuda, inference_config=OTHER_MEMBERS, memory_policy={"cache_dtype": "int8"},
+                  mix_precision=False)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", CacheQuantizedWarning)
+        reg = api.NoriRegressor(**kwargs).fit(x_tr, y_tr)
+        point = reg.predict(x_te)
+        qs = reg.predict(x_te, output_type="quantiles", quantiles=[0.1, 0.5, 0.9])
+        assert reg.memory_report_["ensemble_members"] == 3
+    assert point.shape == (len(x_te),) and np.isfinite(point).all() and np.all(np.diff(qs, axis=0) >= 0)
