@@ -94,11 +94,27 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     p.dp = (d + 15) / 16 * 16;
     p.mode = mode_for(d);
     p.nw = (nq > 256 && has_16_waves(p.dp, p.mode)) ? 16 : (nq > 96 ? 8 : 2);
+    auto padded = [&](int nw) { return (nq + nw * QPW - 1) / (nw * QPW) * nw * QPW; };
     // a 160-row tile where it covers the queries with fewer padded rows (320 queries: two
     // exact tiles instead of two 256-row ones)
     if (p.nw != 2 && has_5_waves(p.dp)) {
-        auto padded = [&](int nw) { return (nq + nw * QPW - 1) / (nw * QPW) * nw * QPW; };
         if (padded(5) * 5 < padded(p.nw) * 4) p.nw = 5;
+    }
+    // resident-context workgroups for contexts of up to 256 keys read by more than 160 queries
+    // per (b, h), where their 320-row tiles pad the queries no more than the ring's tiles and
+    // there are at least two units per CU: each unit stages its whole context once (320 x 256
+    // keys, 2048 (b, h) units, d 64: 308 -> 274 us)
+    if (!p.short_ctx && nk <= kResidentKeys && nq > 5 * QPW && has_resident(p.dp) && padded(10) <= padded(p.nw)) {
+        const int nqt = (int)((nq + 10 * QPW - 1) / (10 * QPW));
+        if (bg * heads * (int64_t)nqt >= 2 * (int64_t)device_cu_count()) {
+            p.nw = 10;
+            p.nqt = nqt;
+            p.nunits = bg * heads * (int64_t)nqt;
+            p.n_whole = p.nunits;
+            p.nsplit = 1;
+            p.kps = kResidentKeys;
+            return p;
+        }
     }
     p.nqt = (int)((nq + p.nw * QPW - 1) / (p.nw * QPW));
     p.nunits = bg * heads * (int64_t)p.nqt;
@@ -191,6 +207,7 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported output dtype %s", dtype_name(out_dtype));
     if (kv_dtype != NORI_I8 && kv_dtype != NORI_F16 && kv_dtype != NORI_BF16 && kv_dtype != NORI_F32)
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: unsupported cache dtype %s", dtype_name(kv_dtype));
+    if (flags & ~NORI_ATTN_MERGE) return fail(NORI_ERR_INVALID, "icl_attention: unknown flags 0x%x", flags);
     if ((flags & NORI_ATTN_MERGE) && (out_dtype != NORI_F32 || !lse))
         return fail(NORI_ERR_INVALID, "icl_attention: merging needs an fp32 running output and an LSE buffer");
     if (kv_dtype == NORI_I8 && !kv_scales) return fail(NORI_ERR_INVALID, "icl_attention: int8 cache without scales");
@@ -202,9 +219,9 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     if (((uintptr_t)kv) % (4 * es) || kv_row_stride % 4 || kv_bg_stride % 4 || kv_half_stride % 4)
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: cache rows must start on 4-element boundaries");
     if (kv_half_stride < (int64_t)kv_heads * d || kv_row_stride < kv_half_stride + (int64_t)kv_heads * d ||
-        (double)block_keys(16) * kv_row_stride * es >= 2147483647.0)
+        (double)kResidentKeys * kv_row_stride * es >= 2147483647.0)
         return fail(NORI_ERR_UNSUPPORTED,
-                    "icl_attention: cache rows must be [K heads | V heads] within one row stride of < 16 MiB");
+                    "icl_attention: cache rows must be [K heads | V heads] within one row stride of < 8 MiB");
     if (kv_dtype == NORI_I8 && (sc_half_stride < kv_heads || sc_row_stride < sc_half_stride + kv_heads))
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: scale rows must be [K heads | V heads] within one row stride");
 
@@ -244,6 +261,14 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     // 4-element boundaries; other query views take the kernels below, which read them one
     // element at a time.
     const bool q_vec4 = (uintptr_t)q % 8 == 0 && q_bg_stride % 4 == 0 && q_row_stride % 4 == 0 && q_head_stride % 4 == 0;
+    const bool q16 = q_dtype == NORI_F16 || q_dtype == NORI_BF16;
+    if (q16 && q_vec4) args.flags |= kQVec4;
+    if (q16 && d % 8 == 0 && (uintptr_t)q % 16 == 0 && q_bg_stride % 8 == 0 && q_row_stride % 8 == 0 &&
+        q_head_stride % 8 == 0)
+        args.flags |= kQVec8;
+    if ((out_dtype == NORI_F16 || out_dtype == NORI_BF16) && !(flags & NORI_ATTN_MERGE) && (uintptr_t)out % 8 == 0 &&
+        out_bg_stride % 4 == 0 && out_row_stride % 4 == 0 && out_head_stride % 4 == 0)
+        args.flags |= kOutVec4;
     if (tile_shape(q_dtype, kv_dtype, nq, nk, d, flags) && q_vec4 && !pro && (!plan.short_ctx || nq >= 8)) {
         const int st = launch_tile(args, stream);
         return st != NORI_OK ? st : launch_status("icl_attention tile");

@@ -42,9 +42,18 @@
 namespace nori {
 namespace attn {
 
+// Resident-context workgroups: 10 wavefronts (320 query rows of one (b, h)) that stage the
+// unit's whole context, at most kResidentKeys rows, into LDS once, behind one barrier, and then
+// scan it with no further staging. For contexts this short the ring's per-block load latency
+// and barriers dominate: the 256-key column attention of many small tables spends 90 % of a
+// wavefront's life waiting in the ring kernel. The scan's arithmetic is the ring kernel's.
+constexpr int kResidentKeys = 256;
+constexpr bool resident(int nw) { return nw == 10; }
+
 // Context rows (keys) per block, the unit of staging and of the one barrier per block:
-// 128 for 16-wave workgroups (a barrier over 16 wavefronts is the costlier one), 64 otherwise.
-constexpr int block_keys(int nw) { return nw == 16 ? 128 : 64; }
+// 128 for 16-wave workgroups (a barrier over 16 wavefronts is the costlier one), the whole
+// context for resident workgroups, 64 otherwise.
+constexpr int block_keys(int nw) { return nw == 16 ? 128 : (resident(nw) ? kResidentKeys : 64); }
 constexpr int QPW = 32;  // query rows per wavefront
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -74,6 +83,15 @@ __device__ __forceinline__ const lds_f16* opaque_lds(const lds_f16* p) {
 __device__ __forceinline__ f16x4 read_tr16(const lds_f16* p) {
     return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
 }
+
+// Layout facts the host has checked, passed in the high bits of Args::flags (the C ABI's
+// flags use the low bits): 16-bit queries whose pointer, row, head and batch strides are
+// multiples of 8 elements with d a multiple of 8 (16-byte fragment loads) or of 4 elements
+// (8-byte loads), and a 16-bit output with 4-element aligned pointer and strides written
+// without a merge (8-byte stores).
+constexpr uint32_t kQVec8 = 1u << 31;
+constexpr uint32_t kQVec4 = 1u << 30;
+constexpr uint32_t kOutVec4 = 1u << 29;
 
 struct Args {
     const void* q; int q_dtype; int64_t nq; int heads; int d;
@@ -254,9 +272,11 @@ struct Geometry {
     // LDS buffers in the K/V ring: three let a block be staged while the previous block's V
     // and the next block's K are both being read (one barrier per block); wide heads, whose
     // buffers are large, use two and a second barrier. The budget keeps two 8-wave or three
-    // 5-wave workgroups on a CU (a 16-wave workgroup has the CU to itself).
+    // 5-wave workgroups on a CU (a 16-wave workgroup has the CU to itself). A resident
+    // workgroup holds one buffer, the whole context (two fit on a CU at head widths up to 64).
     static constexpr int BUF_BYTES = (KBUF + VBUF) * 2 + KB * 4;
-    static constexpr int NBUF = 3 * BUF_BYTES <= (NW == 16 ? 120 : (NW == 5 ? 52 : 72)) * 1024 ? 3 : 2;
+    static constexpr int NBUF =
+        resident(NW) ? 1 : (3 * BUF_BYTES <= (NW == 16 ? 120 : (NW == 5 ? 52 : 72)) * 1024 ? 3 : 2);
 };
 
 // Shapes with a 16-wave workgroup: narrow heads, where 32 query rows per wavefront fit in
@@ -269,12 +289,19 @@ constexpr bool has_16_waves(int dp, int mode) { return dp <= 32 || ((dp == 48 ||
 // exact tiles instead of two 256-row tiles).
 constexpr bool has_5_waves(int dp) { return dp <= 64; }
 
+// Shapes with a resident-context workgroup (10 wavefronts, two per CU): heads up to 64 wide,
+// whose 256-key K and V buffers (80 KB) leave room for a second workgroup.
+constexpr bool has_resident(int dp) { return dp <= 64; }
+
 // Register budget: heads up to 64 wide keep 4 wavefronts per SIMD (two 8-wave workgroups per
 // CU). Without the bound the 64-wide 8-wave fold kernel takes 135 VGPRs and only one workgroup
 // fits; with it, it (and the 48-wide VALU-mode kernel) spills 6 registers to scratch and still
 // runs faster (nori-100m layer shape on 8-wave workgroups: 94.4 ms unbounded, 80.7 ms bounded).
 template <int DP, int NW>
-struct WavesPerEU { static constexpr int value = (NW == 16 || ((NW == 8 || NW == 5) && DP <= 64)) ? 4 : 1; };
+struct WavesPerEU {
+    // two resident 10-wave workgroups per CU: five wavefronts per SIMD
+    static constexpr int value = resident(NW) ? 5 : ((NW == 16 || ((NW == 8 || NW == 5) && DP <= 64)) ? 4 : 1);
+};
 
 template <int DP, int KVT, int MODE, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DP, NW>::value)))
@@ -346,18 +373,38 @@ icl_attention_kernel(const Args a) {
     {
         const float qmul = FOLD ? a.scale_log2 : 1.0f;
         const bool qok = qi < a.nq;
-        const int64_t qbase = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head;
+        // Every element is loaded, at an index clamped into a valid row (the last query for the
+        // padding rows of a tile, element d - 1 past the head), and the value is selected away:
+        // with no branch around a load, the fragment's loads issue back to back and share one
+        // wait instead of costing one memory round trip each.
+        const int64_t qbase = b * a.q_bg + min<int64_t>(qi, a.nq - 1) * a.q_row + (int64_t)h * a.q_head;
         auto fill = [&](auto load) {
 #pragma unroll
             for (int ks = 0; ks < G::KSTEPS; ++ks) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int dd = 16 * ks + 8 * hh + j;
-                    qf[ks][j] = (qok && dd < d) ? (_Float16)(load(qbase + dd) * qmul) : (_Float16)0.0f;
+                    const float v = load(qbase + min(dd, d - 1));
+                    qf[ks][j] = (qok && dd < d) ? (_Float16)(v * qmul) : (_Float16)0.0f;
                 }
             }
         };
-        if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+        if (a.flags & kQVec8) {
+            // one 16-byte load per 8-element chunk (a chunk past the head is zero)
+            const uint16_t* q16 = reinterpret_cast<const uint16_t*>(a.q);
+            const bool bf = a.q_dtype == NORI_BF16;
+#pragma unroll
+            for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                const int dd = 16 * ks + 8 * hh;
+                const u32x4 w = *reinterpret_cast<const u32x4*>(q16 + qbase + min(dd, d - 8));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t e = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+                    const float v = bf ? bf16_to_f32(e) : f16_to_f32(e);
+                    qf[ks][j] = (qok && dd < d) ? (_Float16)(v * qmul) : (_Float16)0.0f;
+                }
+            }
+        } else if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
         else if (a.q_dtype == NORI_BF16) fill([&](int64_t i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
         else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
     }
@@ -673,6 +720,31 @@ icl_attention_kernel(const Args a) {
     // test on every step (pass 1, the lazy-rescale scan). The two scans do the same arithmetic
     // otherwise. (The VALU-mode kernels scan once with the test on: at DP 64 the second pass's
     // live state spills inside their loop and costs more than the test.)
+    if constexpr (resident(NW)) {
+        // the whole context range (klen <= KB keys, checked on the host) in one staged buffer,
+        // then one checked 32-key step after another; rows past klen are staged as zeros and
+        // masked out of the partial last step
+        {
+            Raw<KVT> raw[NU];
+            load_block(k_begin, raw);
+            store_block(0, raw);
+        }
+        __syncthreads();
+        const int nsteps = (klen + 31) >> 5;
+        const lds_f16* Kr = opaque_lds(KsL + k_lane);
+        const lds_f16* Vr = opaque_lds(VsL + v_lane);
+        f16x8 kfr[G::KSTEPS];
+        read_k(Kr, kfr);
+        f32x16 s_cur = logits(kfr);
+        read_k(Kr + 32 * min(1, G::SPB - 1) * G::KPITCH, kfr);  // the K operands of step 1
+        for (int st = 0; st < nsteps; ++st) {
+            // the following step's K rows (a valid buffer row past the last step, unused)
+            const int nx = min(st + 1, G::SPB - 1);
+            step(true, s_cur, kfr, Kr + 32 * nx * G::KPITCH, kfac + ((FOLD || KVT != NORI_I8) ? 0 : 32 * st),
+                 Vr + st * G::VSTEP, 32 * st, st == 0);
+            if constexpr (PREFETCH) read_k(Kr + 32 * min(st + 2, G::SPB - 1) * G::KPITCH, kfr);
+        }
+    } else {
     __shared__ int rescan;
     if (tid == 0) rescan = 0;  // ordered before its readers by the barriers of the scan
     constexpr int PASSES = FOLD ? 2 : 1;
@@ -753,6 +825,7 @@ icl_attention_kernel(const Args a) {
     __syncthreads();  // every flag written; every read of the ring done before pass 1 restages it
     if (!rescan) break;
     }
+    }  // ring scan
 
     // ---------------- epilogue: per query, its denominator and running max in the O^T layout
     // (lane holds query 16qb + lane%16)
@@ -791,6 +864,27 @@ icl_attention_kernel(const Args a) {
         const int64_t lse_idx = (b * a.heads + h) * a.nq + qo;
         float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
         if (merge) merge_weights(a.lse[lse_idx], lse_part, w_old, w_new, lse_out);
+        if (a.flags & kOutVec4) {
+            // the lane's 4 consecutive head elements in one 8-byte store
+            const bool bf = a.out_dtype == NORI_BF16;
+#pragma unroll
+            for (int t = 0; t < G::VT; ++t) {
+                const int d0 = 16 * t + 4 * (lane >> 4);
+                if (d0 < d) {
+                    uint32_t w[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const float v0 = o[t][qb][2 * i] * inv, v1 = o[t][qb][2 * i + 1] * inv;
+                        const uint32_t h0 = bf ? f32_to_bf16(v0) : f32_to_f16(v0);
+                        const uint32_t h1 = bf ? f32_to_bf16(v1) : f32_to_f16(v1);
+                        w[i] = h0 | (h1 << 16);
+                    }
+                    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d0) = u32x2{w[0], w[1]};
+                }
+            }
+            if (a.lse && (lane >> 4) == 0) a.lse[lse_idx] = lse_out;
+            continue;
+        }
 #pragma unroll
         for (int t = 0; t < G::VT; ++t) {
             const int d0 = 16 * t + 4 * (lane >> 4);
@@ -843,6 +937,12 @@ int launch_shape(int nw, const Args& a, hipStream_t stream) {
     if constexpr (has_5_waves(DP)) {
         if (nw == 5) {
             hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 5>), grid, dim3(5 * 64), 0, stream, a);
+            return NORI_OK;
+        }
+    }
+    if constexpr (has_resident(DP)) {
+        if (nw == 10) {
+            hipLaunchKernelGGL((icl_attention_kernel<DP, KVT, MODE, 10>), grid, dim3(10 * 64), 0, stream, a);
             return NORI_OK;
         }
     }

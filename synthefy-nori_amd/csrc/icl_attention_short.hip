@@ -113,8 +113,17 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
     f32x4 q = {0.f, 0.f, 0.f, 0.f}, kw = {1.f, 1.f, 1.f, 1.f};
     if (live) {
         const int64_t qb = b * a.q_bg + qi * a.q_row + (int64_t)h * a.q_head + c0;
+        if (a.flags & kQVec4) {  // 16-bit, 4-element aligned: one 8-byte load
+            const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(a.q) + qb);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = load_as_f32(a.q, a.q_dtype, qb + e);
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t x = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                q[e] = a.q_dtype == NORI_BF16 ? bf16_to_f32(x) : f16_to_f32(x);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = load_as_f32(a.q, a.q_dtype, qb + e);
+        }
     }
     if (pro.qw) {
         f32x4 qw = {0.f, 0.f, 0.f, 0.f};
@@ -197,7 +206,17 @@ __global__ void __launch_bounds__(kThreads) icl_attention_short_kernel(const Arg
     const bool merge = a.flags & NORI_ATTN_MERGE;
     float w_old = 0.f, w_new = 1.f, lse_out = lse_part;
     if (merge) merge_weights(a.lse[row], lse_part, w_old, w_new, lse_out);
-    if (live) {
+    if (live && (a.flags & kOutVec4)) {  // 16-bit output, no merge: one 8-byte store
+        const int64_t ob = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head + c0;
+        const bool bf = a.out_dtype == NORI_BF16;
+        uint32_t w[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float v0 = o[2 * i] * inv, v1 = o[2 * i + 1] * inv;
+            w[i] = (uint32_t)(bf ? f32_to_bf16(v0) : f32_to_f16(v0)) | ((uint32_t)(bf ? f32_to_bf16(v1) : f32_to_f16(v1)) << 16);
+        }
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + ob) = u32x2{w[0], w[1]};
+    } else if (live) {
         const int64_t ob = b * a.o_bg + qi * a.o_row + (int64_t)h * a.o_head + c0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {

@@ -141,6 +141,21 @@ def test_quantile_member_blocks():
     assert all(u[np.argmax(np.abs(u[:, j])), j] > 0 for j in range(k))
     sv = np.linalg.svd(scaled, compute_uv=False)[:k]
     np.testing.assert_allclose(np.linalg.norm(svd, axis=0), sv, rtol=1e-9)
+    # a float32 member matrix stays float32 through the scaling, as the reference's
+    # float-preserving steps keep it (np.nan_to_num, SimpleImputer, StandardScaler); the SVD is
+    # then taken in float64 of those float32 values
+    x32 = x.astype(np.float32)
+    step32 = en.Redistribute(worker_tags=["quantile_uniform_all_data"], original_flag=True, svd_tag="svd",
+                             device="cpu")
+    step32.fit(x32, [], 42)
+    out32 = step32.apply(x32)[0]
+    columns = step32.worker.named_steps["worker"].transform(x32)
+    branch = step32.worker.named_steps["svd_worker"].transformer_list[1][1]
+    scaled32 = branch.named_steps["save_standard"].transform(columns)
+    assert columns.dtype == np.float32 and scaled32.dtype == np.float32
+    np.testing.assert_allclose(scaled32, columns / columns.astype(np.float64).std(axis=0), rtol=2e-7, atol=1e-6)
+    np.testing.assert_allclose(out32[:, 2 * p:], scaled32.astype(np.float64) @ branch.named_steps["svd"].components_.T,
+                               rtol=1e-9, atol=1e-9)
 
 
 def test_per_column_kinds():

@@ -561,6 +561,37 @@ def test_few_token_tile_path_on_a_qkv_projection(cuda):
     check(got.float(), exp)
 
 
+@pytest.mark.parametrize("d,kv_kind", [(64, "f16"), (64, "i8"), (32, "bf16"), (48, "f16")])
+@pytest.mark.parametrize("nq,nk", [(320, 256), (300, 200), (640, 97)])
+def test_resident_context_path(cuda, d, kv_kind, nq, nk):
+    """Contexts of up to 256 keys read by more than 160 queries per (b, h), with at least two
+    (b, h) units per CU, take the resident-context workgroups (10 wavefronts that stage the
+    unit's whole context once): here 384 tables x 2 heads. They match the float64 oracle on a
+    sample of tables; where the head width is a multiple of 16 (the VALU-mode scan, the same
+    arithmetic as the ring kernel's) they give the ring kernel's bits, which a slice of two
+    tables -- too few units for the resident path -- takes on the same rows."""
+    bg, heads = 384, 2
+    kv = make_cache(bg, nk, heads, d, cuda, seed=nq + nk + d, dtype=SHORT_CACHES[kv_kind])
+    q = make_queries(bg, nq, heads, d, cuda, seed=nq + d, dtype=torch.float16, gain=2.0)
+    print(f"resident path: d {d} {kv_kind} nq {nq} nk {nk}", flush=True)
+    if kv_kind == "i8":
+        codes, scales = nori_amd.quantize_int8(kv)
+        got = nori_amd.icl_attention(q, codes, scales)
+        ring = nori_amd.icl_attention(q[:2], codes[:2], scales[:2])
+        values = codes[:3].double() * scales[:3].double()
+    else:
+        got = nori_amd.icl_attention(q, kv)
+        ring = nori_amd.icl_attention(q[:2], kv[:2])
+        values = kv[:3].double()
+    exp, _ = reference(q[:3], values)
+    check(got[:3], exp)
+    assert torch.isfinite(got).all()
+    if d % 16 == 0:
+        assert torch.equal(got[:2], ring)
+    else:
+        check(got[:2], ring.float())
+
+
 @pytest.mark.parametrize("offset", [1, 2])
 def test_few_token_shape_with_a_query_view_off_the_4_element_grid(cuda, offset):
     """Few-token shapes whose query rows do not start on 4-element (8-byte) boundaries -- here

@@ -9,8 +9,9 @@ the GPU, and checked by what fixes it independently of this code:
   quantile transform; a 13-column SVD block; the fingerprint), adaptive members 27;
 * the quantile block of each quantile member: sklearn's QuantileTransformer with the capped
   settings, fitted on the same context rows, to 1e-12;
-* the SVD block: column norms equal the singular values of the scaled block it is taken from
-  (numpy's LAPACK SVD), the components orthonormal, and the block the projection on them;
+* the SVD block: taken from the member's float32 columns scaled in float32 (the closed form to
+  float32 rounding); its column norms equal that block's singular values (numpy's LAPACK SVD)
+  to 1e-8, the components are orthonormal, and the block is the projection on them;
 * the whole member's features: the GPU run equals the CPU run (float64 SVDs) to 1e-9, except
   the row fingerprint, whose hash of a row's bytes changes with any last-bit difference.
 """
@@ -79,12 +80,21 @@ def test_default_members_on_config1_table(cuda):
         qt = QuantileTransformer(output_distribution="uniform", n_quantiles=max(2, min(max(n // 5, 2), n, 256)),
                                  subsample=min(n, 10000), random_state=static_seed).fit(x_in)
         np.testing.assert_allclose(out[:, p:2 * p], qt.transform(x_in), rtol=0, atol=1e-12)
+        # the block the SVD is taken from: the member's float32 columns scaled to unit variance in
+        # float32, as the reference's float-preserving steps leave them (closed form to float32
+        # rounding); the SVD identities are checked on that block itself
+        columns = step.worker.named_steps["worker"].transform(x_in)
+        branch = step.worker.named_steps["svd_worker"].transformer_list[1][1]
+        scaled = branch.named_steps["save_standard"].transform(columns)
+        assert columns.dtype == np.float32 and scaled.dtype == np.float32
         block = np.hstack([out[:, :p], out[:, p:2 * p]]).astype(np.float64)
-        scaled = block / block.std(axis=0)
+        np.testing.assert_allclose(scaled, block / block.std(axis=0), rtol=2e-7, atol=1e-6)
+        scaled = scaled.astype(np.float64)
         svd = out[:, 2 * p:]
         sv = np.linalg.svd(scaled, compute_uv=False)[:k]
-        np.testing.assert_allclose(np.linalg.norm(svd, axis=0), sv, rtol=1e-9)
-        comps = step.worker.named_steps["svd_worker"].transformer_list[1][1].named_steps["svd"].components_
+        # the device solver's float64 singular values against LAPACK's: 1.5e-9 relative measured
+        np.testing.assert_allclose(np.linalg.norm(svd, axis=0), sv, rtol=1e-8)
+        comps = branch.named_steps["svd"].components_
         np.testing.assert_allclose(comps @ comps.T, np.eye(k), atol=1e-10)
         np.testing.assert_allclose(svd, scaled @ comps.T, rtol=1e-9, atol=1e-9)
         print(f"member {i}: quantile block and {k}-column SVD block pinned", flush=True)
