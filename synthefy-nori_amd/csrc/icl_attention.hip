@@ -147,12 +147,26 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     return p;
 }
 
+// Whether a launch of this shape runs the q/k prologue: the short-context kernel always, a
+// resident-context launch when the key norm (if any) applies to an f16 cache.
+bool takes_prologue(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int kv_dtype, const void* k_weight) {
+    if (short_context(nq, nk)) return true;
+    return make_plan(bg, nq, heads, d, nk).nw == 10 && (!k_weight || kv_dtype == NORI_F16);
+}
+
 int64_t workspace_bytes(const Plan& p, int d) {
     if (p.nsplit <= 1) return 0;
     return (int64_t)p.nsplit * (p.nunits - p.n_whole) * p.nw * QPW * (d + 1) * (int64_t)sizeof(float);
 }
 
 }  // namespace
+
+extern "C" int32_t nori_icl_attention_takes_prologue(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk,
+                                                     int32_t kv_dtype, int32_t with_key_norm) {
+    if (bg <= 0 || nq <= 0 || heads <= 0 || d < 4 || d > 128 || d % 4 || nk <= 0) return 0;
+    static const char one = 0;
+    return takes_prologue(bg, nq, heads, d, nk, kv_dtype, with_key_norm ? &one : nullptr) ? 1 : 0;
+}
 
 extern "C" int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk) {
     if (bg <= 0 || nq <= 0 || heads <= 0 || d < 4 || d > 128 || d % 4 || nk <= 0) return 0;
@@ -186,9 +200,10 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
         prologue.wdt = pro->weight_dtype;
         prologue.eps = pro->eps;
         prologue.qmult = pro->q_mult;
-        if (!short_context(nq, nk))
+        if (bg > 0 && nq > 0 && heads > 0 && d >= 4 && nk > 0 && !takes_prologue(bg, nq, heads, d, nk, kv_dtype, pro->k_weight))
             return fail(NORI_ERR_UNSUPPORTED,
-                        "icl_attention: the q/k prologue runs only with few queries over few keys (%lld x %lld)",
+                        "icl_attention: the q/k prologue runs only on the short-context kernel (few queries over few "
+                        "keys) and on resident-context launches (%lld x %lld here)",
                         (long long)nq, (long long)nk);
     }
     if (bg < 0 || nq < 0)
@@ -236,6 +251,13 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     args.out = out; args.out_dtype = out_dtype; args.o_bg = out_bg_stride; args.o_row = out_row_stride;
     args.o_head = out_head_stride; args.lse = lse; args.flags = flags;
     args.bg = bg;
+    if (pro && plan.nw == 10 && !plan.short_ctx) {
+        args.pqw = prologue.qw;
+        args.pkw = prologue.kw;
+        args.pwdt = prologue.wdt;
+        args.peps = prologue.eps;
+        args.pqmult = prologue.qmult;
+    }
     args.nqt = plan.nqt;
     args.qrows = plan.nw * QPW;
     args.nunits = plan.nunits;

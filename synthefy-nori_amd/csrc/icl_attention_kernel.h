@@ -101,6 +101,10 @@ struct Args {
     float scale_log2;  // logit scale * log2(e)
     void* out; int out_dtype; int64_t o_bg, o_row, o_head;
     float* lse; uint32_t flags;
+    // The q/k prologue of resident-context launches (null gains: none): the per-head RMS norms
+    // of the query rows and of the staged key rows with their gains (dtype pwdt) and eps, then
+    // the query multiply pqmult, each step rounded to its operand's dtype.
+    const void* pqw = nullptr; const void* pkw = nullptr; int pwdt = NORI_F32; float peps = 0.f; float pqmult = 1.f;
     // Work items are (b, h, query tile) units, numbered with the query tile fastest. Units
     // [0, n_whole) scan the whole context; each of the tail units [n_whole, nunits) is split
     // into nsplit ranges of keys_per_split keys whose partial (O, LSE) pairs a second kernel
@@ -175,6 +179,20 @@ __device__ __forceinline__ float lane_value(float v, int src) {
 
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+
+// v rounded to a runtime dtype, as torch rounds an op's result in that dtype
+__device__ __forceinline__ float round_to_dtype(float v, int dt) {
+    if (dt == NORI_F16) return round_to<NORI_F16>(v);
+    if (dt == NORI_BF16) return round_to<NORI_BF16>(v);
+    return v;
+}
+
+// sum over the 4 lanes of a quad (DPP quad permutations), every lane gets it
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));  // lane ^ 1
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));  // lane ^ 2
+    return v;
 }
 
 __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
@@ -378,17 +396,7 @@ icl_attention_kernel(const Args a) {
         // with no branch around a load, the fragment's loads issue back to back and share one
         // wait instead of costing one memory round trip each.
         const int64_t qbase = b * a.q_bg + min<int64_t>(qi, a.nq - 1) * a.q_row + (int64_t)h * a.q_head;
-        auto fill = [&](auto load) {
-#pragma unroll
-            for (int ks = 0; ks < G::KSTEPS; ++ks) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int dd = 16 * ks + 8 * hh + j;
-                    const float v = load(qbase + min(dd, d - 1));
-                    qf[ks][j] = (qok && dd < d) ? (_Float16)(v * qmul) : (_Float16)0.0f;
-                }
-            }
-        };
+        float qv[G::KSTEPS][8];
         if (a.flags & kQVec8) {
             // one 16-byte load per 8-element chunk (a chunk past the head is zero)
             const uint16_t* q16 = reinterpret_cast<const uint16_t*>(a.q);
@@ -400,13 +408,58 @@ icl_attention_kernel(const Args a) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint16_t e = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-                    const float v = bf ? bf16_to_f32(e) : f16_to_f32(e);
-                    qf[ks][j] = (qok && dd < d) ? (_Float16)(v * qmul) : (_Float16)0.0f;
+                    qv[ks][j] = dd < d ? (bf ? bf16_to_f32(e) : f16_to_f32(e)) : 0.0f;
                 }
             }
-        } else if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
-        else if (a.q_dtype == NORI_BF16) fill([&](int64_t i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
-        else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
+        } else {
+            auto fill = [&](auto load) {
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int dd = 16 * ks + 8 * hh + j;
+                        const float v = load(qbase + min(dd, d - 1));
+                        qv[ks][j] = dd < d ? v : 0.0f;
+                    }
+                }
+            };
+            if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+            else if (a.q_dtype == NORI_BF16) fill([&](int64_t i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+            else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
+        }
+        if constexpr (resident(NW)) {
+            if (a.pqw) {
+                // the query row's RMS norm with its gain, T(T(q * rsqrt(mean(q^2) + eps)) * w),
+                // then T(q * qmult), T rounding to the query dtype as the separate passes do;
+                // the row's other half is in lane ^ 32
+                float ss = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) ss = fmaf(qv[ks][j], qv[ks][j], ss);
+                ss += other_half(ss);
+                const float inv = rsqrtf(ss / (float)d + a.peps);
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int dd = 16 * ks + 8 * hh + j;
+                        if (dd < d) {
+                            const float w = load_as_f32(a.pqw, a.pwdt, dd);
+                            float v = round_to_dtype(round_to_dtype(qv[ks][j] * inv, a.q_dtype) * w, a.q_dtype);
+                            if (a.pqmult != 1.0f) v = round_to_dtype(v * a.pqmult, a.q_dtype);
+                            qv[ks][j] = v;
+                        }
+                    }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int dd = 16 * ks + 8 * hh + j;
+                qf[ks][j] = (qok && dd < d) ? (_Float16)(qv[ks][j] * qmul) : (_Float16)0.0f;
+            }
     }
 
     // ---- staging plan of this thread. Unit idx = tid + u * THREADS covers elements
@@ -730,6 +783,43 @@ icl_attention_kernel(const Args a) {
             store_block(0, raw);
         }
         __syncthreads();
+        if constexpr (KVT == NORI_F16) {
+            if (a.pkw) {
+                // each staged key row's RMS norm with its gain, rounded to f16 (the cache dtype)
+                // as the separate pass rounds it: 4 lanes per row, DP / 4 elements each
+                constexpr int EPL = DP / 4;
+                const int part = tid & 3;
+                for (int r = tid >> 2; r < klen; r += THREADS / 4) {
+                    _Float16* row = Ks + r * G::KPITCH + part * EPL;
+                    float v[EPL];
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPL; e += 4) {
+                        const f16x4 x = *reinterpret_cast<const f16x4*>(row + e);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            v[e + i] = part * EPL + e + i < d ? (float)x[i] : 0.0f;
+                            ss = fmaf(v[e + i], v[e + i], ss);
+                        }
+                    }
+                    ss = quad_sum(ss);
+                    const float inv = rsqrtf(ss / (float)d + a.peps);
+#pragma unroll
+                    for (int e = 0; e < EPL; e += 4) {
+                        if (part * EPL + e < d) {  // d is a multiple of 4
+                            f16x4 x;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float w = load_as_f32(a.pkw, a.pwdt, part * EPL + e + i);
+                                x[i] = (_Float16)round_to<NORI_F16>(round_to<NORI_F16>(v[e + i] * inv) * w);
+                            }
+                            *reinterpret_cast<f16x4*>(row + e) = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
         const int nsteps = (klen + 31) >> 5;
         const lds_f16* Kr = opaque_lds(KsL + k_lane);
         const lds_f16* Vr = opaque_lds(VsL + v_lane);

@@ -39,6 +39,15 @@ def workspace_bytes(bg: int, nq: int, heads: int, d: int, nk: int) -> int:
     return int(nat.lib().nori_icl_attention_workspace_size(bg, nq, heads, d, nk))
 
 
+def takes_prologue(bg: int, nq: int, heads: int, d: int, nk: int, kv_dtype: torch.dtype, key_norm: bool) -> bool:
+    """Whether ``icl_attention(..., qk_prologue=...)`` runs for these sizes: on the short-context
+    kernel (few queries over few keys) and on resident-context launches (up to 256 keys read by
+    many queries; a key norm there needs an fp16 cache) -- the launch planner's answer
+    (``nori_icl_attention_takes_prologue``)."""
+    return bool(nat.lib().nori_icl_attention_takes_prologue(bg, nq, heads, d, nk, nat.dtype_code(kv_dtype),
+                                                            1 if key_norm else 0))
+
+
 def short_context(nq: int, nk: int) -> bool:
     """Whether the attention runs on the short-context kernel: few queries over few keys (the
     planner's rule, short_context() in csrc/icl_attention_kernel.h)."""
@@ -69,8 +78,8 @@ def icl_attention(
     qk_prologue: ``{"q_weight", "k_weight", "eps", "q_mult"}`` -- per-head RMS norms of the
     raw q and K rows (gains of d elements, or None) and a multiply of the normed q, applied
     as the kernel loads them, rounded as the separate passes round them
-    (``nori_icl_attention_qk``). Only for ``short_context(Q, N)`` shapes and full-precision
-    caches; raises NotImplementedError elsewhere.
+    (``nori_icl_attention_qk``). Only where ``takes_prologue`` says so (short-context shapes
+    with full-precision caches, resident-context launches); the library refuses it elsewhere.
     """
     if q.dim() != 4:
         raise ValueError(f"query must be [BG, Q, H, D], got {tuple(q.shape)}")

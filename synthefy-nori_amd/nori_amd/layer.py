@@ -35,7 +35,7 @@ import torch
 import torch.nn as nn
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from .attention import attend_dense, compute_attention_blockwise, icl_attention, short_context
+from .attention import attend_dense, compute_attention_blockwise, icl_attention, takes_prologue
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
 from .norm import (FUSED_MLP_WIDTHS, QASS_GATE_HIDDEN, RMSNorm, operand_dtype, projection_operand, qass_gate,
@@ -447,11 +447,13 @@ class MultiheadAttention(nn.Module):
     def _norm_q(self, q):
         return q if self.q_norm is None else self.q_norm(q)
 
-    def _short_prologue(self, q: torch.Tensor, kv: torch.Tensor) -> dict | None:
-        """The q/k steps between projection and attention as a prologue of the short-context
-        kernel, or None where they run as separate passes. Needs the per-head q/k norms (with
-        gains and one eps), QASS off or "log_only" (a multiply by fp16(log n)), no log-n or
-        temperature scale, a full-precision cache on the GPU and a short-context shape."""
+    def _fused_prologue(self, q: torch.Tensor, kv: torch.Tensor) -> dict | None:
+        """The q/k steps between projection and attention as a prologue fused into the
+        attention kernel's loads, or None where they run as separate passes. Needs the per-head
+        q/k norms (with gains and one eps), QASS off or "log_only" (a multiply by fp16(log n)),
+        no log-n or temperature scale, a full-precision cache on the GPU, and a launch that
+        takes the prologue (the short-context kernel, or a resident-context launch over an fp16
+        cache: ``takes_prologue``)."""
         if not (self.qk_norm and q.is_cuda and kv.dtype != torch.int8):
             return None
         if self.use_logn_attention or self.use_learnable_attn_temperature:
@@ -461,7 +463,8 @@ class MultiheadAttention(nn.Module):
         if self.qassmax is not None and self.qassmax.qass_mode != "log_only":
             return None
         n_keys = int(kv.shape[1])
-        if not short_context(int(q.shape[1]), n_keys):
+        bg, nq, heads, d = (int(n) for n in q.shape)
+        if not takes_prologue(bg, nq, heads, d, n_keys, kv.dtype, key_norm=True):
             return None
         q_mult = 1.0
         if self.qassmax is not None and n_keys > 1:  # QASSMaxScaling.forward's factor, in q's dtype
@@ -604,9 +607,9 @@ class MultiheadAttention(nn.Module):
         contiguous head axis, e.g. views into one stacked projection) through the q/k norms,
         QASS and the HIP kernel; returns the attention output [BS, F, H, D] before the output
         projection."""
-        prologue = self._short_prologue(q, kv) if attn_mask is None else None
+        prologue = self._fused_prologue(q, kv) if attn_mask is None else None
         if prologue is not None:
-            # q/k norms and the log-n multiply fused into the short-context kernel's loads
+            # q/k norms and the log-n multiply fused into the attention kernel's loads
             if self._attention_dropout_p() != 0.0:
                 raise RuntimeError("the HIP attention path is inference-only (dropout must be zero)")
             return icl_attention(q, kv, qk_prologue=prologue)

@@ -40,6 +40,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_residual_add_rms_norm",
             "nori_icl_attention",
             "nori_icl_attention_qk",
+            "nori_icl_attention_takes_prologue",
             "nori_icl_attention_workspace_size",
             "nori_icl_attention_noalloc",
             "nori_kv_project_quantize_int8",
@@ -187,10 +188,11 @@ def test_fused_projection_shape_errors():
 
 
 def test_qk_prologue_only_on_the_short_context_path():
-    """nori_icl_attention_qk refuses (NORI_ERR_UNSUPPORTED, nothing launched) exactly the shapes
-    the planner sends to the MFMA kernel -- attention.short_context() mirrors that rule -- and
-    int8 caches with a key norm; otherwise it goes on to the ordinary argument checks (here the
-    null pointers), all before any device call."""
+    """nori_icl_attention_qk refuses (NORI_ERR_UNSUPPORTED, nothing launched) the shapes the
+    planner sends to the ring MFMA kernel -- for one table, every shape but the short-context
+    ones, which attention.short_context() mirrors -- and int8 caches with a key norm; otherwise
+    it goes on to the ordinary argument checks (here the null pointers), all before any device
+    call. nori_icl_attention_takes_prologue gives the same answer without a call."""
     import ctypes
 
     from nori_amd import _native as nat
@@ -204,6 +206,7 @@ def test_qk_prologue_only_on_the_short_context_path():
             None, nat.NORI_F16, 0, 0, 0, None, 0, None, 0, ctypes.addressof(pro), None,
         )
         assert rc == (nat.NORI_ERR_INVALID if short_context(nq, nk) else nat.NORI_ERR_UNSUPPORTED), (nq, nk, rc)
+        assert lib.nori_icl_attention_takes_prologue(1, nq, 2, 64, nk, nat.NORI_F16, 0) == int(short_context(nq, nk))
     keyed = nat.QKPrologue(None, 1, nat.NORI_F32, 1e-6, 1.0)  # any non-null gain pointer
     rc = lib.nori_icl_attention_qk(
         None, nat.NORI_F16, 1, 4, 2, 64, 0, 0, 0, None, nat.NORI_I8, None, 6, 2, 0, 0, 128, 0, 0, 0, 0.125,
