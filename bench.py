@@ -105,6 +105,11 @@ def parse_args():
         help="measure only one layer's prefill self-attention (65536 x 65536, fp16 K/V)",
     )
     p.add_argument(
+        "--mfma-ceiling", action="store_true",
+        help="measure only the dense f16 MFMA rate under the power limit (random vs all-zero operands) and the "
+        "workload's attention launch on its real cache vs an all-zero cache",
+    )
+    p.add_argument(
         "--cache-write", action="store_true",
         help="measure only the fused context-cache write of one layer against the unfused sequence "
         "(also the command its rocprofv3 trace and counters are taken with)",
@@ -251,6 +256,72 @@ def cache_write(torch, dev, codes, scales, reps=5):
         "fused_algorithmic_bytes": fused_bytes,
         "fused_GBps": round(fused_bytes / fused_ms / 1e6, 1),
         "fused_TFLOPs": round(2.0 * rows * EMBED * 2 * HEADS * HEAD_DIM / fused_ms / 1e9, 1),
+    }
+
+
+def mfma_ceiling(torch, dev, codes, scales, att_flop, iters=4096, reps=3):
+    """The dense f16 MFMA rate the GPU sustains under its power limit, on random and on all-zero
+    operands (nori_mfma_f16_probe: nothing but v_mfma_f32_32x32x16_f16, four wavefronts per SIMD),
+    and the workload's attention launch over its real int8 cache against the same launch over an
+    all-zero cache: the kernel's time depends on its data the way the MFMA rate does."""
+    import ctypes
+
+    import nori_amd
+    from nori_amd import _native as nat
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    n_vec = 1 << 20  # 16-byte vectors of f16 pairs: sign and mantissa random, |v| in [0.25, 4)
+    mant = torch.randint(0, 1 << 10, (n_vec * 8,), generator=g, device=dev, dtype=torch.int32)
+    expo = torch.randint(13, 16, (n_vec * 8,), generator=g, device=dev, dtype=torch.int32)
+    sign = torch.randint(0, 2, (n_vec * 8,), generator=g, device=dev, dtype=torch.int32)
+    rnd = ((sign << 15) | (expo << 10) | mant).to(torch.int16)
+    zero = torch.zeros_like(rnd)
+    sink = torch.empty(1 << 20, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    lib = nat.lib()
+    flop = lib.nori_mfma_f16_probe_flop(iters)
+
+    def probe_rate(ops):
+        def call():
+            nat.check(lib.nori_mfma_f16_probe(ctypes.c_void_p(ops.data_ptr()), n_vec, iters,
+                                              ctypes.c_void_p(sink.data_ptr()), sink.numel(),
+                                              nat.stream_of(dev)), "mfma_f16_probe")
+        call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return flop * reps / (e0.elapsed_time(e1) / 1e3)
+
+    rate_rnd, rate_zero = probe_rate(rnd), probe_rate(zero)
+    q = torch.randn((GROUPS, QUERY_ROWS, HEADS, HEAD_DIM), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(nori_amd.attention.workspace_bytes(GROUPS, QUERY_ROWS, HEADS, HEAD_DIM, CONTEXT_ROWS), 1),
+                     dtype=torch.uint8, device=dev)
+
+    def attn_ms(c):
+        nori_amd.icl_attention(q, c, scales, out=out, workspace=ws)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(10):
+            nori_amd.icl_attention(q, c, scales, out=out, workspace=ws)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 10
+
+    ms_real, ms_zero = attn_ms(codes), attn_ms(torch.zeros_like(codes))
+    return {
+        "what": "dense f16 MFMA rate under the power limit (v_mfma_f32_32x32x16_f16 only, 4 wavefronts per SIMD, "
+        "8 operand register sets per wavefront) on random operands (|v| in [0.25, 4), random sign and mantissa) "
+        "and on all-zero operands; the bench's attention launch on its N(0,1) int8 cache and on an all-zero cache",
+        "mfma_f16_random_TFLOPs": round(rate_rnd / 1e12, 1),
+        "mfma_f16_zero_TFLOPs": round(rate_zero / 1e12, 1),
+        "random_frac_of_peak": round(rate_rnd / MFMA_BF16_PEAK, 4),
+        "attention_ms_real_cache": round(ms_real, 4),
+        "attention_ms_zero_cache": round(ms_zero, 4),
+        "attention_frac_of_random_ceiling": round(att_flop / (ms_real / 1e3) / rate_rnd, 4),
     }
 
 
@@ -651,6 +722,16 @@ def main():
         kv16 = torch.randn(shape, generator=torch.Generator(device=dev).manual_seed(2), device=dev, dtype=torch.float16)
         print(json.dumps(prefill_attention(torch, dev, kv16)), flush=True)
         return
+    if args.mfma_ceiling:
+        shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
+        kv16 = torch.randn(shape, generator=torch.Generator(device=dev).manual_seed(2), device=dev, dtype=torch.float16)
+        codes = torch.empty(shape, dtype=torch.int8, device=dev)
+        scales = torch.empty(shape[:-1] + (1,), dtype=torch.float32, device=dev)
+        _quantize_into(kv16, codes, scales)
+        del kv16
+        print(json.dumps(mfma_ceiling(torch, dev, codes, scales,
+                                      4.0 * GROUPS * HEADS * QUERY_ROWS * CONTEXT_ROWS * HEAD_DIM)), flush=True)
+        return
     if args.cache_write:
         shape = (GROUPS, CONTEXT_ROWS, 2, HEADS, HEAD_DIM)
         codes = torch.empty(shape, dtype=torch.int8, device=dev)
@@ -747,6 +828,8 @@ def main():
     torch.cuda.synchronize()
     dequant_ms = [a.elapsed_time(b) for a, b in dq_events]
     del dq_out
+    ceiling = mfma_ceiling(torch, dev, codes[0], scales[0],
+                           4.0 * GROUPS * HEADS * QUERY_ROWS * CONTEXT_ROWS * HEAD_DIM)
     write = cache_write(torch, dev, codes[0], scales[0])
     prefill = prefill_attention(torch, dev, kv[0])
     model_e2e = end_to_end(torch, dev)
@@ -830,6 +913,7 @@ def main():
             "launches": len(dequant_ms),
         },
     }
+    line["mfma_ceiling"] = ceiling
     line["cache_write"] = write
     line["prefill_attention"] = prefill
     line["end_to_end"] = model_e2e

@@ -353,6 +353,23 @@ int nori_icl_attention_noalloc(const void* q, int q_dtype, int64_t bg, int64_t n
                                void* out, int out_dtype, int64_t out_bg_stride, int64_t out_row_stride,
                                int64_t out_head_stride, float* lse, uint32_t flags, void* stream);
 
+/* ---- measurement (no counterpart in the reference) ----
+ *
+ * The dense f16 MFMA rate this GPU sustains on given operand data. Under a dense MFMA load
+ * the engine clock is set by the power limit, and an MFMA's power depends on its operand
+ * bits, so the achievable rate depends on the data (bench.py times random against all-zero
+ * operands beside the attention kernel's figures). nori_mfma_f16_probe runs nothing but
+ * v_mfma_f32_32x32x16_f16 for `iters` iterations of eight MFMAs per wavefront, four
+ * wavefronts per SIMD on every CU, each wavefront cycling through eight operand register sets
+ * read from `operands` (n_vec 16-byte vectors of f16 pairs, indexed modulo n_vec); `sink`
+ * (sink_len floats) takes the accumulators so nothing is optimized away.
+ * nori_mfma_f16_probe_flop gives the FLOP one call performs on the current device (-1 when it
+ * cannot be queried).
+ */
+int nori_mfma_f16_probe(const void* operands, int64_t n_vec, int32_t iters, float* sink, int64_t sink_len,
+                        void* stream);
+int64_t nori_mfma_f16_probe_flop(int64_t iters);
+
 #ifdef __cplusplus
 }
 #endif

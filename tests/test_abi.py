@@ -45,6 +45,8 @@ def test_header_declares_the_expected_entry_points():
             "nori_icl_attention_noalloc",
             "nori_kv_project_quantize_int8",
             "nori_kv_project_quantize_int8_workspace_size",
+            "nori_mfma_f16_probe",
+            "nori_mfma_f16_probe_flop",
         ]
     )
 
@@ -144,6 +146,9 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(ln); bad[2] = 0
     assert lib.nori_layer_norm(*bad) == nat.NORI_OK
     assert lib.nori_layer_norm(*ln) == nat.NORI_ERR_INVALID  # null pointers
+    # the MFMA rate probe (measurement only): operands, a sink and iterations are required
+    assert lib.nori_mfma_f16_probe(None, 0, 1, None, 0, None) == nat.NORI_ERR_INVALID
+    assert b"mfma_f16_probe" in lib.nori_last_error()
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK
