@@ -38,6 +38,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .attention import attend_dense, compute_attention_blockwise, icl_attention, takes_prologue
 from . import kv_project
 from .kv_cache_scaling import BlockwiseSeqKV, ScalableSeqKV, scale_caches
+from .projection import linear as proj_linear
 from .norm import (FUSED_MLP_WIDTHS, QASS_GATE_HIDDEN, RMSNorm, operand_dtype, projection_operand, qass_gate,
                    residual_add, residual_add_norm, rms_norm_, silu_mul, swiglu_mlp)
 
@@ -517,7 +518,7 @@ class MultiheadAttention(nn.Module):
                 f"cache=({kv_cache['batch']}, {kv_cache['groups']}), query=({B}, {S})"
             )
         x_flat = x.reshape(-1, *x.shape[-2:])
-        q = torch.nn.functional.linear(x_flat, self._linear_weights(x.device)[0])
+        q = proj_linear(x_flat, self._linear_weights(x.device)[0])
         q = q.view(*x_flat.shape[:-1], self.num_heads, self.head_dim)
         blockwise = isinstance(kv_cache, BlockwiseSeqKV)
         if blockwise:
@@ -538,7 +539,7 @@ class MultiheadAttention(nn.Module):
         else:
             atten_out = attend_dense(q, kv_cache)
         w_out = self._linear_weights(atten_out.device)[2]
-        out = torch.nn.functional.linear(atten_out.reshape(*atten_out.shape[:-2], -1), w_out.to(atten_out.dtype))
+        out = proj_linear(atten_out.reshape(*atten_out.shape[:-2], -1), w_out.to(atten_out.dtype))
         return out.reshape(B, S, *out.shape[1:]), None
 
     def compute_attention_blockwise(self, q: torch.Tensor, kv_cache: BlockwiseSeqKV, *, sdpa_scale: float | None = None):
@@ -587,14 +588,14 @@ class MultiheadAttention(nn.Module):
             use_linear = self._is_linear_projection_used(x.device)
             if use_linear:
                 w_q, w_kv, _ = self._linear_weights(x.device)
-                q = torch.nn.functional.linear(x, w_q).view(*x.shape[:-1], self.num_heads, self.head_dim)
+                q = proj_linear(x, w_q).view(*x.shape[:-1], self.num_heads, self.head_dim)
             else:
                 q = torch.einsum("... s, h d s -> ... h d", x, self.qkv_proj_weight[0])
             kv_w = self.qkv_proj_weight[1:]
             if copy_first_head_kv:
                 kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w[:, :1])
             elif use_linear:
-                kv = torch.nn.functional.linear(x_kv, w_kv).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
+                kv = proj_linear(x_kv, w_kv).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
             else:
                 kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w)
             atten_out = self.attend_projected(q, kv, attn_mask)
@@ -642,7 +643,7 @@ class MultiheadAttention(nn.Module):
         of the whole attention output into [..., D, H] order before its GEMM (1.95 against
         1.21 ms for 835,584 rows of 10 heads of 56)."""
         if atten_out.is_cuda or self._is_linear_projection_used(atten_out.device):
-            return torch.nn.functional.linear(
+            return proj_linear(
                 atten_out.reshape(*atten_out.shape[:-2], self.num_heads * self.head_dim),
                 self._linear_weights(atten_out.device)[2],
             )

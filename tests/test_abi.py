@@ -45,6 +45,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_icl_attention_noalloc",
             "nori_kv_project_quantize_int8",
             "nori_kv_project_quantize_int8_workspace_size",
+            "nori_linear_f16",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
         ]
@@ -146,6 +147,18 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(ln); bad[2] = 0
     assert lib.nori_layer_norm(*bad) == nat.NORI_OK
     assert lib.nori_layer_norm(*ln) == nat.NORI_ERR_INVALID  # null pointers
+    # fp16 projection: inner width 128 or 256, output width a multiple of 4, aligned rows
+    lin = [None, 1, 4096, 128, 0, 128, None, 128, 64, None, 0, 64, None]
+    bad = list(lin); bad[3] = 96
+    assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"inner width 96" in lib.nori_last_error()
+    bad = list(lin); bad[8] = 62
+    assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(lin); bad[8] = 0
+    assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_INVALID
+    bad = list(lin); bad[2] = 0
+    assert lib.nori_linear_f16(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_linear_f16(*lin) == nat.NORI_ERR_INVALID  # null pointers
     # the MFMA rate probe (measurement only): operands, a sink and iterations are required
     assert lib.nori_mfma_f16_probe(None, 0, 1, None, 0, None) == nat.NORI_ERR_INVALID
     assert b"mfma_f16_probe" in lib.nori_last_error()
