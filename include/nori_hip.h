@@ -358,15 +358,17 @@ int nori_icl_attention_noalloc(const void* q, int q_dtype, int64_t bg, int64_t n
  * (reference model/layer.py:651-683 for the K/V projection, 1114-1160 for the Q, K/V and
  * output projections; model/two_phase.py:53-55, 122-138 for the two-phase attentions): fp32
  * sums of fp16 products, one rounding to fp16 (the library GEMM's result up to the order of
- * its fp32 sums). x holds n_outer * n_inner rows of k fp16 elements, row (o, i) at element
- * offset o * x_outer_stride + i * x_row_stride; weight holds n rows of k elements, w_row_stride
- * apart; output row (o, i) is written at o * y_outer_stride + i * y_row_stride. k is 128 or 256
- * and n a multiple of 4; x and weight rows 16-byte aligned, output rows 8-byte aligned.
- * Built for tall operands (HBM-bound: each x row read once, each output row written once).
+ * its fp32 sums). x holds n_outer * n_mid * n_inner rows of k fp16 elements, row (o, j, i) at
+ * element offset o * x_outer_stride + j * x_mid_stride + i * x_row_stride; weight holds n rows
+ * of k elements, w_row_stride apart; output row (o, j, i) is written at o * y_outer_stride +
+ * j * y_mid_stride + i * y_row_stride. k is 128 or 256 and n a multiple of 4; x and weight
+ * rows 16-byte aligned, output rows 8-byte aligned. Built for tall operands (HBM-bound: each x
+ * row read once, each output row written once).
  */
-int nori_linear_f16(const void* x, int64_t n_outer, int64_t n_inner, int32_t k, int64_t x_outer_stride,
-                    int64_t x_row_stride, const void* weight, int64_t w_row_stride, int32_t n, void* y,
-                    int64_t y_outer_stride, int64_t y_row_stride, void* stream);
+int nori_linear_f16(const void* x, int64_t n_outer, int64_t n_mid, int64_t n_inner, int32_t k,
+                    int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, const void* weight,
+                    int64_t w_row_stride, int32_t n, void* y, int64_t y_outer_stride, int64_t y_mid_stride,
+                    int64_t y_row_stride, void* stream);
 
 /* ---- measurement (no counterpart in the reference) ----
  *

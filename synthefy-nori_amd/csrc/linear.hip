@@ -18,9 +18,10 @@
 //     stored row by row, 16 bytes per lane and 128 contiguous bytes per row (written straight
 //     from the MFMA layout, a store instruction touched 16 rows in 32-byte pieces and the
 //     kernel ran 10-20 % slower at N = 128-256).
-//   * Rows are addressed on a two-level grid, row r = o * n_inner + i (strides x_outer, x_row
-//     and y_outer, y_row), so strided views (a token subset of each row, a slice of a stacked
-//     output) are read and written in place.
+//   * Rows are addressed on a three-level grid, row r = (o * n_mid + j) * n_inner + i (strides
+//     x_outer, x_mid, x_row and y_outer, y_mid, y_row), so strided views (a token subset of
+//     each row, a slice of a stacked output, the [table, group, row] transpose of a
+//     [table, row, group] cell buffer) are read and written in place.
 //   * Workgroups are numbered so that the column chunks of one row block are consecutive on
 //     one XCD (the hardware deals workgroup i to XCD i % 8): the x block is read from HBM once
 //     and served to the other chunks by that XCD's L2.
@@ -36,13 +37,21 @@ constexpr int kNR = 2;                    // 16-row tiles per wavefront
 constexpr int kRows = kWaves * kNR * 16;  // rows per workgroup
 
 struct LinArgs {
-    const _Float16* x; int64_t rows, n_inner, x_outer, x_row;
+    const _Float16* x; int64_t rows, n_mid, n_inner, x_outer, x_mid, x_row;
     const _Float16* w; int64_t w_row;
     int n;
-    _Float16* y; int64_t y_outer, y_row;
+    _Float16* y; int64_t y_outer, y_mid, y_row;
     int nchunks;
     int64_t grid;
 };
+
+// element offsets of row r in x and y on the three-level row grid
+__device__ __forceinline__ void row_offsets(const LinArgs& a, int64_t r, int64_t& xo, int64_t& yo) {
+    const int64_t oj = r / a.n_inner, i = r - oj * a.n_inner;
+    const int64_t o = oj / a.n_mid, j = oj - o * a.n_mid;
+    xo = o * a.x_outer + j * a.x_mid + i * a.x_row;
+    yo = o * a.y_outer + j * a.y_mid + i * a.y_row;
+}
 
 __device__ __forceinline__ uint32_t pack_f16_rn(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, f16x2{(_Float16)lo, (_Float16)hi});
@@ -68,9 +77,9 @@ __global__ void __launch_bounds__(kThreads) linear_f16_kernel(const LinArgs a) {
 #pragma unroll
     for (int nt = 0; nt < kNR; ++nt) {
         const int64_t row = rb * kRows + wave * (kNR * 16) + nt * 16 + (lane & 15);
-        const int64_t rr = row < a.rows ? row : a.rows - 1;
-        const int64_t o = rr / a.n_inner, i = rr - o * a.n_inner;
-        const _Float16* xrow = a.x + o * a.x_outer + i * a.x_row + 8 * g;
+        int64_t xo, yo;
+        row_offsets(a, row < a.rows ? row : a.rows - 1, xo, yo);
+        const _Float16* xrow = a.x + xo + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) xf[nt][ks] = *reinterpret_cast<const f16x8*>(xrow + 32 * ks);
     }
@@ -81,9 +90,8 @@ __global__ void __launch_bounds__(kThreads) linear_f16_kernel(const LinArgs a) {
     for (int p = 0; p < 4; ++p) {
         const int64_t row = rb * kRows + wave * (kNR * 16) + 8 * p + (lane >> 3);
         svalid[p] = row < a.rows;
-        const int64_t rr = svalid[p] ? row : a.rows - 1;
-        const int64_t o = rr / a.n_inner, i = rr - o * a.n_inner;
-        soff[p] = o * a.y_outer + i * a.y_row;
+        int64_t xo;
+        row_offsets(a, svalid[p] ? row : a.rows - 1, xo, soff[p]);
     }
 
     for (int e = tid; e < NC * KS * 4; e += kThreads) {
@@ -139,35 +147,41 @@ int launch(LinArgs a, hipStream_t stream) {
 
 }  // namespace
 
-extern "C" int nori_linear_f16(const void* x, int64_t n_outer, int64_t n_inner, int32_t k, int64_t x_outer_stride,
-                               int64_t x_row_stride, const void* weight, int64_t w_row_stride, int32_t n, void* y,
-                               int64_t y_outer_stride, int64_t y_row_stride, void* stream) {
+extern "C" int nori_linear_f16(const void* x, int64_t n_outer, int64_t n_mid, int64_t n_inner, int32_t k,
+                               int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, const void* weight,
+                               int64_t w_row_stride, int32_t n, void* y, int64_t y_outer_stride, int64_t y_mid_stride,
+                               int64_t y_row_stride, void* stream) {
     clear_error();
-    if (n_outer < 0 || n_inner < 0 || k <= 0 || n <= 0)
-        return fail(NORI_ERR_INVALID, "linear_f16: bad shape n_outer=%lld n_inner=%lld k=%d n=%d", (long long)n_outer,
-                    (long long)n_inner, k, n);
+    if (n_outer < 0 || n_mid < 0 || n_inner < 0 || k <= 0 || n <= 0)
+        return fail(NORI_ERR_INVALID, "linear_f16: bad shape n_outer=%lld n_mid=%lld n_inner=%lld k=%d n=%d",
+                    (long long)n_outer, (long long)n_mid, (long long)n_inner, k, n);
     if (k != 128 && k != 256) return fail(NORI_ERR_UNSUPPORTED, "linear_f16: inner width %d is not 128 or 256", k);
     if (n % 4) return fail(NORI_ERR_UNSUPPORTED, "linear_f16: output width %d is not a multiple of 4", n);
-    if (n_outer == 0 || n_inner == 0) return NORI_OK;
-    if (n_inner > INT64_MAX / n_outer)
-        return fail(NORI_ERR_INVALID, "linear_f16: %lld x %lld rows overflow", (long long)n_outer, (long long)n_inner);
+    if (n_outer == 0 || n_mid == 0 || n_inner == 0) return NORI_OK;
+    if (n_inner > INT64_MAX / n_mid || n_mid * n_inner > INT64_MAX / n_outer)
+        return fail(NORI_ERR_INVALID, "linear_f16: %lld x %lld x %lld rows overflow", (long long)n_outer,
+                    (long long)n_mid, (long long)n_inner);
     if (!x || !weight || !y) return fail(NORI_ERR_INVALID, "linear_f16: null pointer");
     // 16-byte x and W row chunks, 8-byte output pieces
-    if ((uintptr_t)x % 16 || x_row_stride % 8 || x_outer_stride % 8 || (uintptr_t)weight % 16 || w_row_stride % 8 ||
-        w_row_stride < k || (uintptr_t)y % 8 || y_row_stride % 4 || y_outer_stride % 4)
+    if ((uintptr_t)x % 16 || x_row_stride % 8 || x_mid_stride % 8 || x_outer_stride % 8 || (uintptr_t)weight % 16 ||
+        w_row_stride % 8 || w_row_stride < k || (uintptr_t)y % 8 || y_row_stride % 4 || y_mid_stride % 4 ||
+        y_outer_stride % 4)
         return fail(NORI_ERR_UNSUPPORTED,
                     "linear_f16: x and weight rows must be 16-byte aligned, output rows 8-byte aligned");
     LinArgs a;
     a.x = reinterpret_cast<const _Float16*>(x);
-    a.rows = n_outer * n_inner;
+    a.rows = n_outer * n_mid * n_inner;
+    a.n_mid = n_mid;
     a.n_inner = n_inner;
     a.x_outer = x_outer_stride;
+    a.x_mid = x_mid_stride;
     a.x_row = x_row_stride;
     a.w = reinterpret_cast<const _Float16*>(weight);
     a.w_row = w_row_stride;
     a.n = n;
     a.y = reinterpret_cast<_Float16*>(y);
     a.y_outer = y_outer_stride;
+    a.y_mid = y_mid_stride;
     a.y_row = y_row_stride;
     hipStream_t s = (hipStream_t)stream;
     return k == 128 ? launch<4, 128>(a, s) : launch<8, 64>(a, s);

@@ -87,7 +87,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
          _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _vp],
     ),
     "nori_kv_project_quantize_int8_workspace_size": (_i64, [_i32, _i64, _i64, _i32, _i32]),
-    "nori_linear_f16": (ctypes.c_int, [_vp, _i64, _i64, _i32, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _vp]),
+    "nori_linear_f16": (
+        ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _vp],
+    ),
     "nori_mfma_f16_probe": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _vp]),
     "nori_mfma_f16_probe_flop": (_i64, [_i64]),
 }

@@ -564,11 +564,11 @@ class MultiheadAttention(nn.Module):
         projection. Only a masked call takes torch SDPA."""
         if calculate_sample_attention or calculate_feature_attention:
             raise NotImplementedError("attention-score diagnostics are not computed by the HIP attention path")
-        B, S, _, _ = x.shape
+        B, S, F, _ = x.shape
         assert x.shape[-1] == self.embed_dim
-        x = x.reshape(-1, *x.shape[-2:])
-        BS, F, _ = x.shape
+        BS = B * S
         if self.qkv_combined:
+            x = x.reshape(-1, *x.shape[-2:])
             qkv = torch.einsum("... s, j h d s -> ... j h d", x, self.qkv_proj_weight)
             if self.qk_norm:
                 qkv = torch.stack((self.q_norm(qkv[:, :, 0]), self.k_norm(qkv[:, :, 1]), qkv[:, :, 2]), dim=2)
@@ -584,20 +584,23 @@ class MultiheadAttention(nn.Module):
                 atten_out = self._sdpa(q, k, v, attn_mask)
         else:
             assert x_kv is not None, "kv combined attention requires kv input"
-            x_kv = x_kv.reshape(-1, *x_kv.shape[-2:])
+            n_kv = int(x_kv.shape[-2])
             use_linear = self._is_linear_projection_used(x.device)
+            # the projections read x and x_kv as they lie: a strided view such as the column
+            # attention's [table, group, row] transpose of the cells goes through the projection
+            # kernel without the copy its flattening would make (the result is contiguous)
             if use_linear:
                 w_q, w_kv, _ = self._linear_weights(x.device)
-                q = proj_linear(x, w_q).view(*x.shape[:-1], self.num_heads, self.head_dim)
+                q = proj_linear(x, w_q).view(BS, F, self.num_heads, self.head_dim)
             else:
-                q = torch.einsum("... s, h d s -> ... h d", x, self.qkv_proj_weight[0])
+                q = torch.einsum("... s, h d s -> ... h d", x.reshape(BS, F, -1), self.qkv_proj_weight[0])
             kv_w = self.qkv_proj_weight[1:]
             if copy_first_head_kv:
-                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w[:, :1])
+                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w[:, :1])
             elif use_linear:
-                kv = proj_linear(x_kv, w_kv).view(*x_kv.shape[:-1], 2, self.num_heads, self.head_dim)
+                kv = proj_linear(x_kv, w_kv).view(BS, n_kv, 2, self.num_heads, self.head_dim)
             else:
-                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv, kv_w)
+                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w)
             atten_out = self.attend_projected(q, kv, attn_mask)
         out = self.project_out(atten_out.reshape(BS, F, self.num_heads, self.head_dim))
         return out.reshape(B, S, *out.shape[1:]), None, None

@@ -3,13 +3,13 @@
 ``linear(x, weight)`` is ``torch.nn.functional.linear(x, weight)`` for fp16 operands (what the
 reference's projections compute under the GPU's fp16 autocast, layer.py:651-683, 1114-1160):
 fp32 sums of fp16 products, rounded once to fp16. ``nori_linear_f16`` (csrc/linear.hip) reads
-x and writes the output through strides -- a token subset of each row, or a slice of a stacked
-output buffer (``out``) -- without copies. ``linear`` routes to it the shapes where it is the
-faster of the two (same-box A/B against the library GEMM: inner width 128 and up to 256 output
-columns, e.g. 655,360 rows x 128 -> 128 in 78 against 110 us; at inner width 256 or wider
-outputs the library GEMM was as fast or faster); everything else (other dtypes, widths or
-shapes, short operands, CPU tensors) is ``F.linear``. The two differ only in the order of the
-fp32 sums.
+x and writes the output through strides -- a token subset of each row, a slice of a stacked
+output buffer (``out``), the transposed [table, group, row] view of a cell buffer -- without
+copies. ``linear`` routes to it the shapes where it is the faster of the two (same-box A/B
+against the library GEMM: inner width 128 and up to 256 output columns, e.g. 655,360 rows x
+128 -> 128 in 78 against 110 us; at inner width 256 or wider outputs the library GEMM was as
+fast or faster); everything else (other dtypes, widths or shapes, short operands, CPU
+tensors) is ``F.linear``. The two differ only in the order of the fp32 sums.
 """
 
 from __future__ import annotations
@@ -28,7 +28,7 @@ _MIN_ROWS = 4096  # below this the library GEMM's launch is as cheap
 
 
 def _row_levels(t: torch.Tensor) -> list[tuple[int, int]] | None:
-    """The rows of ``t`` [..., C] as at most two (count, stride) levels, outer first (adjacent
+    """The rows of ``t`` [..., C] as at most three (count, stride) levels, outer first (adjacent
     leading dims merged where their strides chain), or None when they need more levels."""
     merged: list[tuple[int, int]] = []
     for size, stride in zip(t.shape[:-1], t.stride()[:-1]):
@@ -39,40 +39,59 @@ def _row_levels(t: torch.Tensor) -> list[tuple[int, int]] | None:
             merged[-1] = (merged[-1][0] * size, stride)
         else:
             merged.append((size, stride))
-    if len(merged) > 2:
+    return merged if len(merged) <= 3 else None
+
+
+def _common_grid(x: torch.Tensor, y: torch.Tensor) -> tuple[tuple[int, ...], tuple[int, ...], tuple[int, ...]] | None:
+    """((n_outer, n_mid, n_inner), x strides, y strides): one three-level row grid addressing the
+    rows of x and of y (same leading shape) in the same order, or None. The grid's levels are
+    the union of both tensors' level boundaries; a tensor level that spans several grid levels
+    gives each of them its stride times the rows inside it."""
+    per = [_row_levels(x), _row_levels(y)]
+    if per[0] is None or per[1] is None:
         return None
-    return merged
-
-
-def _common_grid(x: torch.Tensor, y: torch.Tensor) -> tuple[int, int, int, int, int, int] | None:
-    """(n_outer, n_inner, x outer stride, x row stride, y outer stride, y row stride): one
-    two-level row grid addressing the rows of x and of y (same leading shape) in the same
-    order, or None."""
-    lx, ly = _row_levels(x), _row_levels(y)
-    if lx is None or ly is None:
+    bounds = set()
+    for levels in per:
+        prod = 1
+        for count, _ in reversed(levels):
+            prod *= count
+            bounds.add(prod)
+    counts, prev = [], 1  # inner first
+    for b in sorted(bounds):
+        if b % prev:
+            return None
+        counts.append(b // prev)
+        prev = b
+    if len(counts) > 3:
         return None
-    rows = x.numel() // max(int(x.shape[-1]), 1)
-    grid = lx if len(lx) == 2 else (ly if len(ly) == 2 else [(1, 0), (rows, lx[0][1] if lx else 0)])
-    outer, inner = grid[0][0], grid[1][0]
+    strides = []
+    for levels in per:
+        st, gi = [], 0
+        for count, stride in reversed(levels):
+            inside, mult = 1, 1
+            while gi < len(counts) and inside * counts[gi] <= count:
+                st.append(stride * mult)
+                mult *= counts[gi]
+                inside *= counts[gi]
+                gi += 1
+            if inside != count:
+                return None
+        strides.append(st)
+    pad = 3 - len(counts)
+    grid = tuple([1] * pad + counts[::-1])
+    return grid, tuple([0] * pad + strides[0][::-1]), tuple([0] * pad + strides[1][::-1])
 
-    def on_grid(levels):
-        if len(levels) == 2:
-            return (levels[0][1], levels[1][1]) if (levels[0][0], levels[1][0]) == (outer, inner) else None
-        stride = levels[0][1] if levels else 0
-        return inner * stride, stride
 
-    gx, gy = on_grid(lx), on_grid(ly)
-    if gx is None or gy is None:
-        return None
-    return outer, inner, gx[0], gx[1], gy[0], gy[1]
-
-
-def takes_kernel(x: torch.Tensor, weight: torch.Tensor) -> bool:
-    """Whether ``linear(x, weight)`` runs on the HIP kernel."""
+def takes_kernel(x: torch.Tensor, weight: torch.Tensor, *, any_width: bool = False) -> bool:
+    """Whether ``linear(x, weight)`` runs on the HIP kernel (``any_width``: whether the kernel
+    can take the operands at all, whatever the routing rule says)."""
     if not (x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16 and weight.dim() == 2):
         return False
     k = int(x.shape[-1])
-    if k not in _WIDTHS or int(weight.shape[1]) != k or int(weight.shape[0]) % 4 or int(weight.shape[0]) > _MAX_N:
+    widths = (128, 256) if any_width else _WIDTHS
+    if k not in widths or int(weight.shape[1]) != k or int(weight.shape[0]) % 4:
+        return False
+    if not any_width and int(weight.shape[0]) > _MAX_N:
         return False
     if x.stride(-1) != 1:
         return False
@@ -84,10 +103,12 @@ def takes_kernel(x: torch.Tensor, weight: torch.Tensor) -> bool:
     return levels is not None and all(st % 8 == 0 for _, st in levels)
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None, *,
+           any_width: bool = False) -> torch.Tensor:
     """``F.linear(x, weight)`` (no bias) -> [..., N]; with ``out`` (a view of that shape, any
-    row strides) the result is written there and ``out`` returned."""
-    if not takes_kernel(x, weight):
+    row strides) the result is written there and ``out`` returned. ``any_width`` takes the
+    kernel for every shape it can (a caller whose strided ``out`` would otherwise cost a copy)."""
+    if not takes_kernel(x, weight, any_width=any_width):
         y = torch.nn.functional.linear(x, weight)
         if out is None:
             return y
@@ -98,15 +119,16 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = Non
         out = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=torch.float16, device=x.device)
     elif tuple(out.shape) != tuple(x.shape[:-1]) + (n,) or out.dtype != torch.float16 or out.device != x.device:
         raise ValueError(f"out {tuple(out.shape)} {out.dtype} is not the [..., {n}] fp16 result of x {tuple(x.shape)}")
-    grid = _common_grid(x, out)
-    if grid is None or out.stride(-1) != 1 or out.data_ptr() % 8 or grid[4] % 4 or grid[5] % 4:
+    common = _common_grid(x, out)
+    if common is None or out.stride(-1) != 1 or out.data_ptr() % 8 or any(st % 4 for st in common[2]):
         out.copy_(linear(x, weight))
         return out
+    (no, nm, ni), (xo, xm, xr), (yo, ym, yr) = common
     nat.check(
         nat.lib().nori_linear_f16(
-            ctypes.c_void_p(x.data_ptr()), grid[0], grid[1], int(x.shape[-1]), grid[2], grid[3],
+            ctypes.c_void_p(x.data_ptr()), no, nm, ni, int(x.shape[-1]), xo, xm, xr,
             ctypes.c_void_p(weight.data_ptr()), int(weight.stride(0)), n,
-            ctypes.c_void_p(out.data_ptr()), grid[4], grid[5], nat.stream_of(x.device),
+            ctypes.c_void_p(out.data_ptr()), yo, ym, yr, nat.stream_of(x.device),
         ),
         "linear_f16",
     )

@@ -148,15 +148,15 @@ def test_argument_errors_map_to_reference_exceptions():
     assert lib.nori_layer_norm(*bad) == nat.NORI_OK
     assert lib.nori_layer_norm(*ln) == nat.NORI_ERR_INVALID  # null pointers
     # fp16 projection: inner width 128 or 256, output width a multiple of 4, aligned rows
-    lin = [None, 1, 4096, 128, 0, 128, None, 128, 64, None, 0, 64, None]
-    bad = list(lin); bad[3] = 96
+    lin = [None, 1, 1, 4096, 128, 0, 0, 128, None, 128, 64, None, 0, 0, 64, None]
+    bad = list(lin); bad[4] = 96
     assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_UNSUPPORTED
     assert b"inner width 96" in lib.nori_last_error()
-    bad = list(lin); bad[8] = 62
+    bad = list(lin); bad[10] = 62
     assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_UNSUPPORTED
-    bad = list(lin); bad[8] = 0
+    bad = list(lin); bad[10] = 0
     assert lib.nori_linear_f16(*bad) == nat.NORI_ERR_INVALID
-    bad = list(lin); bad[2] = 0
+    bad = list(lin); bad[3] = 0
     assert lib.nori_linear_f16(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_linear_f16(*lin) == nat.NORI_ERR_INVALID  # null pointers
     # the MFMA rate probe (measurement only): operands, a sink and iterations are required

@@ -44,9 +44,9 @@ def dyadic(shape, step, lim, gen, device):
 def kernel_linear(x, w):
     """The kernel itself on a contiguous [rows, k] x, whatever ``linear`` would route."""
     y = torch.empty(x.shape[0], w.shape[0], dtype=torch.float16, device=x.device)
-    nat.check(nat.lib().nori_linear_f16(ctypes.c_void_p(x.data_ptr()), 1, x.shape[0], x.shape[1], 0, x.stride(0),
+    nat.check(nat.lib().nori_linear_f16(ctypes.c_void_p(x.data_ptr()), 1, 1, x.shape[0], x.shape[1], 0, 0, x.stride(0),
                                         ctypes.c_void_p(w.data_ptr()), w.stride(0), w.shape[0],
-                                        ctypes.c_void_p(y.data_ptr()), 0, y.stride(0), nat.stream_of(x.device)),
+                                        ctypes.c_void_p(y.data_ptr()), 0, 0, y.stride(0), nat.stream_of(x.device)),
               "linear_f16")
     return y
 
@@ -113,6 +113,20 @@ def test_strided_views_in_place(cuda):
     wide = buf[:, :4, :640]
     projection.linear(cells, w, out=wide)
     assert torch.equal(wide, torch.nn.functional.linear(cells, w))
+
+
+def test_transposed_cell_view(cuda):
+    # the column attention's operands: cells [table, row, group, width] read as the transposed
+    # [table, group, row] view (three row levels), and its first rows as the K/V operand
+    g = torch.Generator(device=cuda).manual_seed(12)
+    cells = torch.randn(40, 320, 4, 128, generator=g, device=cuda).to(torch.float16)
+    cols = cells.transpose(1, 2)
+    w = (torch.randn(256, 128, generator=g, device=cuda) / 11.3).to(torch.float16)
+    for x in (cols, cols[:, :, :256]):
+        assert projection.takes_kernel(x, w)
+        y = projection.linear(x, w)
+        assert y.is_contiguous() and y.shape == x.shape[:-1] + (256,)
+        assert torch.equal(y, kernel_linear(x.contiguous().view(-1, 128), w).view(y.shape))
 
 
 def test_falls_back_where_the_kernel_does_not_apply(cuda):
