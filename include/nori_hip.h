@@ -266,9 +266,9 @@ typedef struct {
  * the reference as one call (it replaces the RMSNorm passes over q and K, the q multiply and
  * the attention of MultiheadAttention.forward, layer.py:1062-1162). Taken where the
  * short-context kernel runs (few queries over few keys: the in-row attentions of the
- * two-phase encoder, full-precision caches) and on resident-context launches (contexts of up
- * to 256 keys read by many queries: its column and row attentions; a key norm there needs an
- * fp16 cache); nori_icl_attention_takes_prologue says which. Elsewhere it returns
+ * two-phase encoder, full-precision caches) and on resident-context launches (fp16 queries
+ * over contexts of up to 256 keys read by many queries: its column and row attentions; a key
+ * norm there needs an fp16 cache); nori_icl_attention_takes_prologue says which. Elsewhere it returns
  * NORI_ERR_UNSUPPORTED having done nothing, and the caller runs the separate passes.
  */
 int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t heads, int32_t d,
@@ -318,14 +318,15 @@ int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_oute
                                                      int32_t norm);
 
 /*
- * 1 when nori_icl_attention_qk takes a prologue for these sizes and cache dtype (with a key
- * norm when with_key_norm is nonzero), 0 when it would return NORI_ERR_UNSUPPORTED. Has no
- * counterpart in the reference: it answers, for the caller choosing between the fused
- * prologue and the separate norm passes of MultiheadAttention.forward (layer.py:1122-1134),
- * the launch planner's question without device work.
+ * 1 when nori_icl_attention_qk takes a prologue for these sizes, cache dtype and query dtype
+ * (with a key norm when with_key_norm is nonzero), 0 when it would return
+ * NORI_ERR_UNSUPPORTED. Has no counterpart in the reference: it answers, for the caller
+ * choosing between the fused prologue and the separate norm passes of
+ * MultiheadAttention.forward (layer.py:1122-1134), the launch planner's question without
+ * device work.
  */
 int32_t nori_icl_attention_takes_prologue(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk,
-                                          int32_t kv_dtype, int32_t with_key_norm);
+                                          int32_t kv_dtype, int32_t with_key_norm, int32_t q_dtype);
 
 /* Bytes of workspace nori_icl_attention uses for these sizes (0 when it never splits). */
 int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk);

@@ -88,7 +88,7 @@ struct Plan {
 // split, into context ranges that spread them over the slots the full rounds leave idle, and a
 // second kernel merges their partials. A split is taken when the rounds it saves outweigh
 // the partials' HBM traffic.
-Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
+Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int q_dtype) {
     Plan p;
     p.short_ctx = short_context(nq, nk);
     p.dp = (d + 15) / 16 * 16;
@@ -100,11 +100,12 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
     if (p.nw != 2 && has_5_waves(p.dp)) {
         if (padded(5) * 5 < padded(p.nw) * 4) p.nw = 5;
     }
-    // resident-context workgroups for contexts of up to 256 keys read by more than 160 queries
-    // per (b, h), where their 320-row tiles pad the queries no more than the ring's tiles and
-    // there are at least two units per CU: each unit stages its whole context once (320 x 256
-    // keys, 2048 (b, h) units, d 64: 308 -> 274 us)
-    if (!p.short_ctx && nk <= kResidentKeys && nq > 5 * QPW && has_resident(p.dp) && padded(10) <= padded(p.nw)) {
+    // resident-context workgroups for fp16 queries and contexts of up to 256 keys read by more
+    // than 160 queries per (b, h), where their 320-row tiles pad the queries no more than the
+    // ring's tiles and there are at least two units per CU: each unit stages its whole context
+    // once (320 x 256 keys, 2048 (b, h) units, d 64: 308 -> 274 us)
+    if (!p.short_ctx && q_dtype == NORI_F16 && nk <= kResidentKeys && nq > 5 * QPW && has_resident(p.dp) &&
+        padded(10) <= padded(p.nw)) {
         const int nqt = (int)((nq + 10 * QPW - 1) / (10 * QPW));
         if (bg * heads * (int64_t)nqt >= 2 * (int64_t)device_cu_count()) {
             p.nw = 10;
@@ -149,9 +150,10 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk) {
 
 // Whether a launch of this shape runs the q/k prologue: the short-context kernel always, a
 // resident-context launch when the key norm (if any) applies to an f16 cache.
-bool takes_prologue(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int kv_dtype, const void* k_weight) {
+bool takes_prologue(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int kv_dtype, const void* k_weight,
+                    int q_dtype) {
     if (short_context(nq, nk)) return true;
-    return make_plan(bg, nq, heads, d, nk).nw == 10 && (!k_weight || kv_dtype == NORI_F16);
+    return make_plan(bg, nq, heads, d, nk, q_dtype).nw == 10 && (!k_weight || kv_dtype == NORI_F16);
 }
 
 int64_t workspace_bytes(const Plan& p, int d) {
@@ -162,15 +164,17 @@ int64_t workspace_bytes(const Plan& p, int d) {
 }  // namespace
 
 extern "C" int32_t nori_icl_attention_takes_prologue(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk,
-                                                     int32_t kv_dtype, int32_t with_key_norm) {
+                                                     int32_t kv_dtype, int32_t with_key_norm, int32_t q_dtype) {
     if (bg <= 0 || nq <= 0 || heads <= 0 || d < 4 || d > 128 || d % 4 || nk <= 0) return 0;
     static const char one = 0;
-    return takes_prologue(bg, nq, heads, d, nk, kv_dtype, with_key_norm ? &one : nullptr) ? 1 : 0;
+    return takes_prologue(bg, nq, heads, d, nk, kv_dtype, with_key_norm ? &one : nullptr, q_dtype) ? 1 : 0;
 }
 
 extern "C" int64_t nori_icl_attention_workspace_size(int64_t bg, int64_t nq, int32_t heads, int32_t d, int64_t nk) {
     if (bg <= 0 || nq <= 0 || heads <= 0 || d < 4 || d > 128 || d % 4 || nk <= 0) return 0;
-    return workspace_bytes(make_plan(bg, nq, heads, d, nk), d);
+    // the ring kernels' plan: resident-context launches (fp16 queries) never split, so this
+    // bounds the workspace whatever the query dtype
+    return workspace_bytes(make_plan(bg, nq, heads, d, nk, NORI_F32), d);
 }
 
 namespace {
@@ -200,7 +204,8 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
         prologue.wdt = pro->weight_dtype;
         prologue.eps = pro->eps;
         prologue.qmult = pro->q_mult;
-        if (bg > 0 && nq > 0 && heads > 0 && d >= 4 && nk > 0 && !takes_prologue(bg, nq, heads, d, nk, kv_dtype, pro->k_weight))
+        if (bg > 0 && nq > 0 && heads > 0 && d >= 4 && nk > 0 &&
+            !takes_prologue(bg, nq, heads, d, nk, kv_dtype, pro->k_weight, q_dtype))
             return fail(NORI_ERR_UNSUPPORTED,
                         "icl_attention: the q/k prologue runs only on the short-context kernel (few queries over few "
                         "keys) and on resident-context launches (%lld x %lld here)",
@@ -240,7 +245,7 @@ int run_attention(const void* q, int q_dtype, int64_t bg, int64_t nq, int32_t he
     if (kv_dtype == NORI_I8 && (sc_half_stride < kv_heads || sc_row_stride < sc_half_stride + kv_heads))
         return fail(NORI_ERR_UNSUPPORTED, "icl_attention: scale rows must be [K heads | V heads] within one row stride");
 
-    const Plan plan = make_plan(bg, nq, heads, d, nk);
+    const Plan plan = make_plan(bg, nq, heads, d, nk, q_dtype);
     Args args;
     args.q = q; args.q_dtype = q_dtype; args.nq = nq; args.heads = heads; args.d = d;
     args.q_bg = q_bg_stride; args.q_row = q_row_stride; args.q_head = q_head_stride;

@@ -195,6 +195,22 @@ __device__ __forceinline__ float quad_sum(float v) {
     return v;
 }
 
+// w[a][b] = element idx(a, b) of the gain vector p (dtype dt; d elements; indices at or past d
+// read element d - 1), converted to fp32 behind one dtype branch: the per-element branches of
+// load_as_f32 in unrolled loops cost more than the loads
+template <int A, int B, typename Idx>
+__device__ __forceinline__ void gains_of(const void* p, int dt, int d, Idx idx, float (&w)[A][B]) {
+    auto fill = [&](auto load) {
+#pragma unroll
+        for (int a = 0; a < A; ++a)
+#pragma unroll
+            for (int b = 0; b < B; ++b) w[a][b] = load(min(idx(a, b), d - 1));
+    };
+    if (dt == NORI_F32) fill([&](int i) { return reinterpret_cast<const float*>(p)[i]; });
+    else if (dt == NORI_F16) fill([&](int i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]); });
+    else fill([&](int i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]); });
+}
+
 __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
     if (dt == NORI_F32) return reinterpret_cast<const float*>(p)[i];
     if (dt == NORI_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
@@ -397,10 +413,13 @@ icl_attention_kernel(const Args a) {
         // wait instead of costing one memory round trip each.
         const int64_t qbase = b * a.q_bg + min<int64_t>(qi, a.nq - 1) * a.q_row + (int64_t)h * a.q_head;
         float qv[G::KSTEPS][8];
+        // Resident-context launches take fp16 queries only (the launch planner sends the others
+        // to the ring kernels): a workgroup there runs its code once, so the query dtypes it
+        // does not take would only cost it instruction fetches.
         if (a.flags & kQVec8) {
             // one 16-byte load per 8-element chunk (a chunk past the head is zero)
             const uint16_t* q16 = reinterpret_cast<const uint16_t*>(a.q);
-            const bool bf = a.q_dtype == NORI_BF16;
+            const bool bf = !resident(NW) && a.q_dtype == NORI_BF16;
 #pragma unroll
             for (int ks = 0; ks < G::KSTEPS; ++ks) {
                 const int dd = 16 * ks + 8 * hh;
@@ -423,15 +442,15 @@ icl_attention_kernel(const Args a) {
                     }
                 }
             };
-            if (a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
+            if (resident(NW) || a.q_dtype == NORI_F16) fill([&](int64_t i) { return f16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
             else if (a.q_dtype == NORI_BF16) fill([&](int64_t i) { return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.q)[i]); });
             else fill([&](int64_t i) { return reinterpret_cast<const float*>(a.q)[i]; });
         }
         if constexpr (resident(NW)) {
             if (a.pqw) {
                 // the query row's RMS norm with its gain, T(T(q * rsqrt(mean(q^2) + eps)) * w),
-                // then T(q * qmult), T rounding to the query dtype as the separate passes do;
-                // the row's other half is in lane ^ 32
+                // then T(q * qmult), T rounding to fp16 (the query dtype) as the separate passes
+                // do; the row's other half is in lane ^ 32
                 float ss = 0.0f;
 #pragma unroll
                 for (int ks = 0; ks < G::KSTEPS; ++ks)
@@ -439,15 +458,18 @@ icl_attention_kernel(const Args a) {
                     for (int j = 0; j < 8; ++j) ss = fmaf(qv[ks][j], qv[ks][j], ss);
                 ss += other_half(ss);
                 const float inv = rsqrtf(ss / (float)d + a.peps);
+                // the gains of this lane's elements behind one dtype branch (per-element dtype
+                // branches in these unrolled loops cost a short-lived workgroup more than its
+                // arithmetic does), then the fp16 roundings
+                float wq[G::KSTEPS][8];
+                gains_of(a.pqw, a.pwdt, d, [&](int ks, int j) { return 16 * ks + 8 * hh + j; }, wq);
 #pragma unroll
                 for (int ks = 0; ks < G::KSTEPS; ++ks)
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const int dd = 16 * ks + 8 * hh + j;
-                        if (dd < d) {
-                            const float w = load_as_f32(a.pqw, a.pwdt, dd);
-                            float v = round_to_dtype(round_to_dtype(qv[ks][j] * inv, a.q_dtype) * w, a.q_dtype);
-                            if (a.pqmult != 1.0f) v = round_to_dtype(v * a.pqmult, a.q_dtype);
+                        if (16 * ks + 8 * hh + j < d) {
+                            float v = round_to<NORI_F16>(round_to<NORI_F16>(qv[ks][j] * inv) * wq[ks][j]);
+                            if (a.pqmult != 1.0f) v = round_to<NORI_F16>(v * a.pqmult);
                             qv[ks][j] = v;
                         }
                     }
@@ -789,6 +811,8 @@ icl_attention_kernel(const Args a) {
                 // as the separate pass rounds it: 4 lanes per row, DP / 4 elements each
                 constexpr int EPL = DP / 4;
                 const int part = tid & 3;
+                float wk[EPL / 4][4];  // this lane's gains, the same for every row it normalizes
+                gains_of(a.pkw, a.pwdt, d, [&](int e, int i) { return part * EPL + 4 * e + i; }, wk);
                 for (int r = tid >> 2; r < klen; r += THREADS / 4) {
                     _Float16* row = Ks + r * G::KPITCH + part * EPL;
                     float v[EPL];
@@ -809,10 +833,8 @@ icl_attention_kernel(const Args a) {
                         if (part * EPL + e < d) {  // d is a multiple of 4
                             f16x4 x;
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const float w = load_as_f32(a.pkw, a.pwdt, part * EPL + e + i);
-                                x[i] = (_Float16)round_to<NORI_F16>(round_to<NORI_F16>(v[e + i] * inv) * w);
-                            }
+                            for (int i = 0; i < 4; ++i)
+                                x[i] = (_Float16)round_to<NORI_F16>(round_to<NORI_F16>(v[e + i] * inv) * wk[e / 4][i]);
                             *reinterpret_cast<f16x4*>(row + e) = x;
                         }
                     }

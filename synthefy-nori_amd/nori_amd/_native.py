@@ -63,7 +63,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         ],
     ),
     "nori_icl_attention_workspace_size": (_i64, [_i64, _i64, _i32, _i32, _i64]),
-    "nori_icl_attention_takes_prologue": (_i32, [_i64, _i64, _i32, _i32, _i64, _i32, _i32]),
+    "nori_icl_attention_takes_prologue": (_i32, [_i64, _i64, _i32, _i32, _i64, _i32, _i32, _i32]),
     "nori_icl_attention_noalloc": (
         ctypes.c_int,
         [

@@ -39,13 +39,14 @@ def workspace_bytes(bg: int, nq: int, heads: int, d: int, nk: int) -> int:
     return int(nat.lib().nori_icl_attention_workspace_size(bg, nq, heads, d, nk))
 
 
-def takes_prologue(bg: int, nq: int, heads: int, d: int, nk: int, kv_dtype: torch.dtype, key_norm: bool) -> bool:
+def takes_prologue(bg: int, nq: int, heads: int, d: int, nk: int, kv_dtype: torch.dtype, key_norm: bool,
+                   q_dtype: torch.dtype = torch.float16) -> bool:
     """Whether ``icl_attention(..., qk_prologue=...)`` runs for these sizes: on the short-context
-    kernel (few queries over few keys) and on resident-context launches (up to 256 keys read by
-    many queries; a key norm there needs an fp16 cache) -- the launch planner's answer
-    (``nori_icl_attention_takes_prologue``)."""
+    kernel (few queries over few keys) and on resident-context launches (fp16 queries, up to 256
+    keys read by many queries; a key norm there needs an fp16 cache) -- the launch planner's
+    answer (``nori_icl_attention_takes_prologue``)."""
     return bool(nat.lib().nori_icl_attention_takes_prologue(bg, nq, heads, d, nk, nat.dtype_code(kv_dtype),
-                                                            1 if key_norm else 0))
+                                                            1 if key_norm else 0, nat.dtype_code(q_dtype)))
 
 
 def short_context(nq: int, nk: int) -> bool:

@@ -465,7 +465,7 @@ class MultiheadAttention(nn.Module):
             return None
         n_keys = int(kv.shape[1])
         bg, nq, heads, d = (int(n) for n in q.shape)
-        if not takes_prologue(bg, nq, heads, d, n_keys, kv.dtype, key_norm=True):
+        if not takes_prologue(bg, nq, heads, d, n_keys, kv.dtype, key_norm=True, q_dtype=q.dtype):
             return None
         q_mult = 1.0
         if self.qassmax is not None and n_keys > 1:  # QASSMaxScaling.forward's factor, in q's dtype

@@ -224,7 +224,8 @@ def test_qk_prologue_only_on_the_short_context_path():
             None, nat.NORI_F16, 0, 0, 0, None, 0, None, 0, ctypes.addressof(pro), None,
         )
         assert rc == (nat.NORI_ERR_INVALID if short_context(nq, nk) else nat.NORI_ERR_UNSUPPORTED), (nq, nk, rc)
-        assert lib.nori_icl_attention_takes_prologue(1, nq, 2, 64, nk, nat.NORI_F16, 0) == int(short_context(nq, nk))
+        assert lib.nori_icl_attention_takes_prologue(1, nq, 2, 64, nk, nat.NORI_F16, 0, nat.NORI_F16) == int(
+            short_context(nq, nk))
     keyed = nat.QKPrologue(None, 1, nat.NORI_F32, 1e-6, 1.0)  # any non-null gain pointer
     rc = lib.nori_icl_attention_qk(
         None, nat.NORI_F16, 1, 4, 2, 64, 0, 0, 0, None, nat.NORI_I8, None, 6, 2, 0, 0, 128, 0, 0, 0, 0.125,

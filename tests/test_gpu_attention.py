@@ -460,6 +460,8 @@ def test_qk_prologue_on_resident_context_launches(cuda, d, nk, key_norm):
     assert takes_prologue(bg, nq, heads, d, nk, torch.float16, key_norm)
     assert takes_prologue(bg, nq, heads, d, nk, torch.int8, False) and not takes_prologue(bg, nq, heads, d, nk, torch.int8, True)
     assert not takes_prologue(2, nq, heads, d, nk, torch.float16, key_norm)  # too few units: the ring kernel
+    # resident-context launches take fp16 queries only: other query dtypes go to the ring kernel
+    assert not takes_prologue(bg, nq, heads, d, nk, torch.float16, key_norm, q_dtype=torch.bfloat16)
     fused = nori_amd.icl_attention(q, kv, qk_prologue={"q_weight": qw, "k_weight": kw, "eps": 1e-6, "q_mult": mult})
     qn = rms_norm(q, d, qw, 1e-6) * torch.tensor(mult, dtype=torch.float16, device=cuda)
     kvn = kv.clone()
