@@ -52,7 +52,9 @@ typedef enum {
 /* Flags of nori_icl_attention. */
 #define NORI_ATTN_MERGE 1u /* merge into running (out fp32, lse) instead of overwriting them */
 
-/* Version of this ABI (bumped on any signature change). */
+/* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
+ * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm and the MFMA probe added). */
+#define NORI_ABI_VERSION 2
 int nori_abi_version(void);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
@@ -370,6 +372,27 @@ int nori_linear_f16(const void* x, int64_t n_outer, int64_t n_mid, int64_t n_inn
                     int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, const void* weight,
                     int64_t w_row_stride, int32_t n, void* y, int64_t y_outer_stride, int64_t y_mid_stride,
                     int64_t y_row_stride, void* stream);
+
+/*
+ * The output projection of an attention sublayer, the deep-norm residual update and the next
+ * sublayer's RMSNorm in one pass (reference model/two_phase.py:198, 209, 220-225, 264, 271-272:
+ * `x = x + alpha * out_proj(attn)` then `norm(x)` with an RMSNorm without weight,
+ * model/layer.py:251-253, whose result the next projection takes as fp16 under autocast):
+ *   u = fp16(a W^T) (as nori_linear_f16), x = x + fp16(fp32(u) * alpha) in fp32 (in place),
+ *   y = fp16(x * rsqrt(mean(x^2) + eps)).
+ * Bit for bit nori_linear_f16 followed by nori_residual_add_rms_norm (fp16 update and output).
+ * a: n_outer * n_mid * n_inner rows of k fp16 elements on the three-level grid of
+ * nori_linear_f16; weight: k rows of k elements (output width = k), w_row_stride apart; x: the
+ * fp32 stream rows and y: the fp16 output rows, on the same grid with their own strides. k is
+ * 128 or 256; a and weight rows 16-byte aligned, x rows 16-byte aligned, y rows 8-byte
+ * aligned; a, x and y must not overlap.
+ */
+int nori_linear_f16_residual_rms_norm(const void* a, int64_t n_outer, int64_t n_mid, int64_t n_inner, int32_t k,
+                                      int64_t a_outer_stride, int64_t a_mid_stride, int64_t a_row_stride,
+                                      const void* weight, int64_t w_row_stride, float alpha, float* x,
+                                      int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, float eps,
+                                      void* y, int64_t y_outer_stride, int64_t y_mid_stride, int64_t y_row_stride,
+                                      void* stream);
 
 /* ---- measurement (no counterpart in the reference) ----
  *

@@ -64,13 +64,6 @@ combine_splits_kernel(const Args a) {
     if (a.lse && dq == 0) a.lse[row] = lse_out;
 }
 
-int device_cu_count() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
-    return cus;
-}
-
 struct Plan {
     bool short_ctx;  // the VALU kernel for few queries over few keys (no tiles, no split)
     int dp;          // head width padded to the logit MFMA granule (16)
@@ -107,7 +100,7 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int q_dtype
     if (!p.short_ctx && q_dtype == NORI_F16 && nk <= kResidentKeys && nq > 5 * QPW && has_resident(p.dp) &&
         padded(10) <= padded(p.nw)) {
         const int nqt = (int)((nq + 10 * QPW - 1) / (10 * QPW));
-        if (bg * heads * (int64_t)nqt >= 2 * (int64_t)device_cu_count()) {
+        if (bg * heads * (int64_t)nqt >= 2 * (int64_t)device_cus()) {
             p.nw = 10;
             p.nqt = nqt;
             p.nunits = bg * heads * (int64_t)nqt;
@@ -121,7 +114,7 @@ Plan make_plan(int64_t bg, int64_t nq, int heads, int d, int64_t nk, int q_dtype
     p.nunits = bg * heads * (int64_t)p.nqt;
     const int KB = block_keys(p.nw);
     const int64_t nkb = (nk + KB - 1) / KB;
-    const int64_t slots = (int64_t)device_cu_count() * std::max(1, resident_workgroups(p.dp, p.mode, p.nw));
+    const int64_t slots = (int64_t)device_cus() * std::max(1, resident_workgroups(p.dp, p.mode, p.nw));
     const int64_t full = p.nunits / slots, tail = p.nunits % slots;
     // seconds per block of one workgroup at ~40 % of the dense MFMA peak shared by all slots
     const double t_blk = (double)p.nw * QPW * KB * p.dp * 4.0 / (1.0e15 / (double)slots);

@@ -305,10 +305,8 @@ bool launch_quantize_wave(const void* src, int64_t n_outer, int64_t n_inner, int
     if ((int64_t)kWaveWaves * kChunk * d * dtype_size(DT) > 65536) return false;
     const int64_t cpo = (n_inner + kChunk - 1) / kChunk;
     const int64_t chunks = cpo * n_outer;
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     // enough waves to keep HBM busy, few enough that each walks several chunks
-    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>((chunks + kWaveWaves - 1) / kWaveWaves, (int64_t)cus * 8));
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>((chunks + kWaveWaves - 1) / kWaveWaves, (int64_t)device_cus() * 8));
 #define NORI_QW(DV)                                                                                           \
     case DV:                                                                                                  \
         hipLaunchKernelGGL((quantize_wave_kernel<DT, DV>), dim3((unsigned)grid), dim3(kWaveWaves * 64), 0, stream, \

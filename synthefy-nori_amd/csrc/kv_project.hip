@@ -350,13 +350,6 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
     }
 }
 
-int device_cus() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
-    return cus;
-}
-
 template <int NR, int KS, int MT>
 int launch_with(const ProjArgs& a, size_t lds, hipStream_t stream) {
     const dim3 grid((unsigned)(a.streams * a.ngroups));

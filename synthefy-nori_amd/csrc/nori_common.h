@@ -26,6 +26,14 @@ inline int dtype_size(int dt) {
     }
 }
 
+// Compute units of the current device (256 on MI355X; that when the query fails).
+inline int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+    return cus;
+}
+
 inline const char* dtype_name(int dt) {
     switch (dt) {
         case NORI_F32: return "float32";

@@ -29,6 +29,6 @@ int launch_status(const char* what) {
 
 }  // namespace nori
 
-extern "C" int nori_abi_version(void) { return 1; }
+extern "C" int nori_abi_version(void) { return NORI_ABI_VERSION; }
 
 extern "C" const char* nori_last_error(void) { return g_error; }

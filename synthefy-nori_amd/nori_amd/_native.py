@@ -19,6 +19,7 @@ NORI_F32, NORI_F16, NORI_BF16, NORI_I8 = range(4)
 SCALE_DIV_TRUE, SCALE_DIV_RECIP = 0, 1
 ATTN_MERGE = 1
 NOALLOC_SCRATCH_BYTES = 32 << 20  # NORI_NOALLOC_SCRATCH_BYTES
+ABI_VERSION = 2  # NORI_ABI_VERSION: the signatures below
 
 _DTYPE_CODES = {
     torch.float32: NORI_F32,
@@ -90,6 +91,11 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "nori_linear_f16": (
         ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _vp],
     ),
+    "nori_linear_f16_residual_rms_norm": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _f32, _vp, _i64, _i64, _i64, _f32, _vp, _i64, _i64,
+         _i64, _vp],
+    ),
     "nori_mfma_f16_probe": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _vp]),
     "nori_mfma_f16_probe_flop": (_i64, [_i64]),
 }
@@ -111,6 +117,10 @@ def lib() -> ctypes.CDLL:
                 "(or python synthefy-nori_amd/nori_amd/build.py) first"
             )
         handle = ctypes.CDLL(LIBRARY)
+        handle.nori_abi_version.restype = ctypes.c_int
+        found = handle.nori_abi_version()
+        if found != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY} has ABI version {found}, this package binds version {ABI_VERSION}; rebuild it")
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = restype

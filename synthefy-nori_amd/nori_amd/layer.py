@@ -583,27 +583,36 @@ class MultiheadAttention(nn.Module):
             else:
                 atten_out = self._sdpa(q, k, v, attn_mask)
         else:
-            assert x_kv is not None, "kv combined attention requires kv input"
-            n_kv = int(x_kv.shape[-2])
-            use_linear = self._is_linear_projection_used(x.device)
-            # the projections read x and x_kv as they lie: a strided view such as the column
-            # attention's [table, group, row] transpose of the cells goes through the projection
-            # kernel without the copy its flattening would make (the result is contiguous)
-            if use_linear:
-                w_q, w_kv, _ = self._linear_weights(x.device)
-                q = proj_linear(x, w_q).view(BS, F, self.num_heads, self.head_dim)
-            else:
-                q = torch.einsum("... s, h d s -> ... h d", x.reshape(BS, F, -1), self.qkv_proj_weight[0])
-            kv_w = self.qkv_proj_weight[1:]
-            if copy_first_head_kv:
-                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w[:, :1])
-            elif use_linear:
-                kv = proj_linear(x_kv, w_kv).view(BS, n_kv, 2, self.num_heads, self.head_dim)
-            else:
-                kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w)
-            atten_out = self.attend_projected(q, kv, attn_mask)
+            atten_out = self.attend(x, x_kv, copy_first_head_kv, attn_mask)
         out = self.project_out(atten_out.reshape(BS, F, self.num_heads, self.head_dim))
         return out.reshape(B, S, *out.shape[1:]), None, None
+
+    def attend(self, x: torch.Tensor, x_kv: torch.Tensor | None, copy_first_head_kv: bool = False,
+               attn_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """The separate-Q/KV form of ``forward`` up to the output projection: x [B, S, F, E]
+        attends over x_kv [B, S, N, E]; returns the attention output [B * S, F, H, D] (what
+        ``project_out`` takes)."""
+        assert x_kv is not None, "kv combined attention requires kv input"
+        B, S, F, _ = x.shape
+        BS = B * S
+        n_kv = int(x_kv.shape[-2])
+        use_linear = self._is_linear_projection_used(x.device)
+        # the projections read x and x_kv as they lie: a strided view such as the column
+        # attention's [table, group, row] transpose of the cells goes through the projection
+        # kernel without the copy its flattening would make (the result is contiguous)
+        if use_linear:
+            w_q, w_kv, _ = self._linear_weights(x.device)
+            q = proj_linear(x, w_q).view(BS, F, self.num_heads, self.head_dim)
+        else:
+            q = torch.einsum("... s, h d s -> ... h d", x.reshape(BS, F, -1), self.qkv_proj_weight[0])
+        kv_w = self.qkv_proj_weight[1:]
+        if copy_first_head_kv:
+            kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w[:, :1])
+        elif use_linear:
+            kv = proj_linear(x_kv, w_kv).view(BS, n_kv, 2, self.num_heads, self.head_dim)
+        else:
+            kv = torch.einsum("... s, j h d s -> ... j h d", x_kv.reshape(BS, n_kv, -1), kv_w)
+        return self.attend_projected(q, kv, attn_mask)
 
     def attend_projected(self, q: torch.Tensor, kv: torch.Tensor, attn_mask: torch.Tensor | None = None) -> torch.Tensor:
         """The separate-Q/KV attention after its projections (layer.py:1114-1162 less the

@@ -20,7 +20,7 @@ import torch
 
 from . import _native as nat
 
-__all__ = ["linear", "takes_kernel"]
+__all__ = ["linear", "linear_residual_norm", "takes_kernel"]
 
 _WIDTHS = (128,)  # inner widths routed to the kernel (it also takes 256, where the library GEMM was faster)
 _MAX_N = 256      # output widths up to this (past it the library GEMM was as fast or faster)
@@ -42,13 +42,13 @@ def _row_levels(t: torch.Tensor) -> list[tuple[int, int]] | None:
     return merged if len(merged) <= 3 else None
 
 
-def _common_grid(x: torch.Tensor, y: torch.Tensor) -> tuple[tuple[int, ...], tuple[int, ...], tuple[int, ...]] | None:
-    """((n_outer, n_mid, n_inner), x strides, y strides): one three-level row grid addressing the
-    rows of x and of y (same leading shape) in the same order, or None. The grid's levels are
-    the union of both tensors' level boundaries; a tensor level that spans several grid levels
-    gives each of them its stride times the rows inside it."""
-    per = [_row_levels(x), _row_levels(y)]
-    if per[0] is None or per[1] is None:
+def _common_grid(*tensors: torch.Tensor) -> tuple | None:
+    """((n_outer, n_mid, n_inner), strides of each tensor ...): one three-level row grid
+    addressing the rows of every tensor (same leading shape) in the same order, or None. The
+    grid's levels are the union of the tensors' level boundaries; a tensor level that spans
+    several grid levels gives each of them its stride times the rows inside it."""
+    per = [_row_levels(t) for t in tensors]
+    if any(levels is None for levels in per):
         return None
     bounds = set()
     for levels in per:
@@ -79,7 +79,7 @@ def _common_grid(x: torch.Tensor, y: torch.Tensor) -> tuple[tuple[int, ...], tup
         strides.append(st)
     pad = 3 - len(counts)
     grid = tuple([1] * pad + counts[::-1])
-    return grid, tuple([0] * pad + strides[0][::-1]), tuple([0] * pad + strides[1][::-1])
+    return (grid,) + tuple(tuple([0] * pad + st[::-1]) for st in strides)
 
 
 def takes_kernel(x: torch.Tensor, weight: torch.Tensor, *, any_width: bool = False) -> bool:
@@ -131,5 +131,44 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = Non
             ctypes.c_void_p(out.data_ptr()), yo, ym, yr, nat.stream_of(x.device),
         ),
         "linear_f16",
+    )
+    return out
+
+
+def linear_residual_norm(a: torch.Tensor, weight: torch.Tensor, stream: torch.Tensor, alpha: float, eps: float,
+                         out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``stream += alpha * F.linear(a, weight)`` in place, then the RMSNorm (no weight, ``eps``)
+    of the updated stream rows in fp16, in one kernel (``nori_linear_f16_residual_rms_norm``):
+    bit for bit ``linear`` followed by the fused residual + norm pass. ``a`` [..., K] fp16,
+    ``weight`` [K, K] fp16 (K 128 or 256), ``stream`` [..., K] fp32 with ``a``'s leading shape
+    (any row strides: e.g. the [table, row, group] cells beside an attention output in
+    [table, group, row] order), ``out`` the same shape in fp16 (new and laid out like
+    ``stream`` when None). Returns the normalized rows, or None where the kernel does not take
+    the operands (nothing is then written)."""
+    k = int(a.shape[-1])
+    if not (a.is_cuda and a.dtype == torch.float16 and weight.dtype == torch.float16 and stream.dtype == torch.float32
+            and k in (128, 256) and tuple(weight.shape) == (k, k) and tuple(stream.shape) == tuple(a.shape)
+            and stream.device == a.device and weight.device == a.device):
+        return None
+    if a.stride(-1) != 1 or stream.stride(-1) != 1 or weight.stride(-1) != 1:
+        return None
+    if out is None:
+        out = torch.empty_like(stream, dtype=torch.float16)
+    elif tuple(out.shape) != tuple(a.shape) or out.dtype != torch.float16 or out.stride(-1) != 1:
+        return None
+    common = _common_grid(a, stream, out)
+    if common is None:
+        return None
+    (no, nm, ni), sa, sx, sy = common
+    if (a.data_ptr() % 16 or any(st % 8 for st in sa) or weight.data_ptr() % 16 or weight.stride(0) % 8
+            or stream.data_ptr() % 16 or any(st % 4 for st in sx) or out.data_ptr() % 8 or any(st % 4 for st in sy)):
+        return None
+    nat.check(
+        nat.lib().nori_linear_f16_residual_rms_norm(
+            ctypes.c_void_p(a.data_ptr()), no, nm, ni, k, *sa, ctypes.c_void_p(weight.data_ptr()), int(weight.stride(0)),
+            float(alpha), ctypes.c_void_p(stream.data_ptr()), *sx, float(eps), ctypes.c_void_p(out.data_ptr()), *sy,
+            nat.stream_of(a.device),
+        ),
+        "linear_f16_residual_rms_norm",
     )
     return out

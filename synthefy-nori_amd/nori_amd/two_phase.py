@@ -36,7 +36,7 @@ from torch import nn
 from .layer import MultiheadAttention, SwiGLUMLP
 from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, residual_add_norm
 from .projection import linear as proj_linear
-from .projection import takes_kernel
+from .projection import linear_residual_norm, takes_kernel
 
 __all__ = [
     "CellLayer2P",
@@ -72,6 +72,33 @@ def _accumulate(stream: torch.Tensor, update: torch.Tensor, alpha: float, then: 
         return None
     dt = operand_dtype(stream) if operand else stream.dtype
     return residual_add_norm(stream, update.reshape(stream.shape), alpha, then, out_dtype=dt, out=out)
+
+
+def _linear_accumulate(a: torch.Tensor, weight: torch.Tensor, stream: torch.Tensor, alpha: float, then: RMSNorm | None,
+                       project, *, operand: bool = True, out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``_accumulate(stream, project(), alpha, then, ...)`` where ``project()`` is ``F.linear(a,
+    weight)`` under fp16 autocast: ``a`` [..., K] with ``stream``'s leading shape (any row
+    strides), ``weight`` [K, K] in the projection dtype. When the next norm is formed in the
+    fp16 operand dtype, the projection, the residual update and the norm run as one kernel
+    (``linear_residual_norm``: u never reaches memory) wherever it takes the operands."""
+    if (then is not None and operand and a.is_cuda and then.weight is None
+            and tuple(then.normalized_shape) == (int(stream.shape[-1]),)
+            and operand_dtype(stream) == torch.float16 and weight.dtype == torch.float16):
+        y = linear_residual_norm(a, weight, stream, alpha, then.eps, out=out)
+        if y is not None:
+            return y
+    return _accumulate(stream, project(), alpha, then, operand=operand, out=out)
+
+
+def _attend_accumulate(attn: MultiheadAttention, atten: torch.Tensor, stream: torch.Tensor, alpha: float,
+                       then: RMSNorm | None = None, *, operand: bool = True) -> torch.Tensor | None:
+    """``stream += alpha * attn.project_out(atten)`` (then the next norm, as ``_accumulate``):
+    ``atten`` the attention output [..., H, D] with ``stream``'s leading shape, any row strides."""
+    a = atten.reshape(*atten.shape[:-2], -1)
+    w_o = attn._linear_weights(atten.device)[2] if atten.is_cuda else None
+    if w_o is None:
+        return _accumulate(stream, attn.project_out(atten), alpha, then, operand=operand)
+    return _linear_accumulate(a, w_o, stream, alpha, then, lambda: attn.project_out(atten), operand=operand)
 
 
 def _row_vectors(targets: torch.Tensor) -> torch.Tensor:
@@ -136,6 +163,15 @@ class FullColumnAttention(nn.Module):
         columns = normed_cells.transpose(1, 2)  # [batch, groups, rows, width]
         return _over_keys(self.sequence_attentions[0], columns, columns[:, :, :eval_pos]).transpose(1, 2)
 
+    def attend(self, normed_cells: torch.Tensor, eval_pos: int) -> torch.Tensor:
+        """``forward`` before the output projection: the attention output [batch, rows, groups,
+        H, D] as a view of the [batch, groups, rows] result (rows in the cells' order)."""
+        b, n, g, _ = normed_cells.shape
+        attn = self.sequence_attentions[0]
+        columns = normed_cells.transpose(1, 2)
+        out = attn.attend(columns, columns[:, :, :eval_pos])  # [batch * groups, rows, H, D]
+        return out.view(b, g, n, attn.num_heads, attn.head_dim).transpose(1, 2)
+
 
 class DecoupledFeatureAttention(nn.Module):
     """Holds the feature attention inside a row (two_phase.py:122-138): attention 0 lets the
@@ -170,6 +206,25 @@ class DecoupledFeatureAttention(nn.Module):
         """``tokens`` [batch, rows, groups + K, width]: the normalized cells, then the normalized
         target tokens of each row. Returns (cell update [batch, rows, groups, width], target
         update [batch, rows, K, width])."""
+        b, r, _, width = tokens.shape
+        cell_out, readout = self.attend(tokens, n_cells)
+        cells_out = self.feature_attentions[0].project_out(cell_out)
+        return cells_out, self.target_mix(readout).view(b, r, self.target_tokens, width)
+
+    def mix_weight(self, dtype: torch.dtype, device) -> torch.Tensor:
+        """``target_mix``'s weight in ``dtype`` (the projection dtype), cached until it changes."""
+        p = self.target_mix.weight
+        key = (dtype, device, p.data_ptr(), p._version)
+        cached = getattr(self, "_mix", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                cached = self._mix = (key, p.to(device=device, dtype=dtype).contiguous())
+        return cached[1]
+
+    def attend(self, tokens: torch.Tensor, n_cells: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """``forward`` before the cells' output projection and ``target_mix``: (the cell
+        attention's output [batch, rows, groups, H, D], the target read-out [batch, rows,
+        K * width] that ``target_mix`` takes)."""
         b, r, t, width = tokens.shape
         a0, a1 = self.feature_attentions
         h, d = a0.num_heads, a0.head_dim
@@ -193,10 +248,9 @@ class DecoupledFeatureAttention(nn.Module):
         all_kv = proj[:, :, 0:2]                # every token of the row: K then V
         target_q = proj[:, n_cells:, 5]
         cell_kv = proj[:, :n_cells, 3:5]        # the cells only
-        cells_out = a0.project_out(a0.attend_projected(cell_q, all_kv))
+        cell_out = a0.attend_projected(cell_q, all_kv).view(b, r, n_cells, h, d)
         readout = a1.project_out(a1.attend_projected(target_q, cell_kv))
-        target_update = self.target_mix(readout.reshape(b * r, -1)).view(b, r, self.target_tokens, width)
-        return cells_out.view(b, r, n_cells, width), target_update
+        return cell_out, readout.reshape(b, r, -1)
 
 
 class CellLayer2P(nn.Module):
@@ -244,9 +298,10 @@ class CellLayer2P(nn.Module):
         return the cells through ``cell_norms[1]`` (the cell MLP's operand)."""
         if normed is None:
             normed = projection_operand(self.cell_norms[0], cells)
-        update = self.column_attention(normed, eval_pos)
+        atten = self.column_attention.attend(normed, eval_pos)
         del normed
-        return _accumulate(cells, update, self.deepnorm_alpha, self.cell_norms[1] if then else None)
+        return _attend_accumulate(self.column_attention.sequence_attentions[0], atten, cells, self.deepnorm_alpha,
+                                  self.cell_norms[1] if then else None)
 
     def row_operand(self, rows: torch.Tensor) -> torch.Tensor:
         """The normalized row vectors the target-stream row attention reads, [batch, 1, n, width]."""
@@ -258,8 +313,9 @@ class CellLayer2P(nn.Module):
         rows' normalized vectors: ``context``, or the first ``eval_pos`` of ``normed``. ``then``:
         return the rows through ``target_norms[1]`` (the target MLP's operand)."""
         keys = normed[:, :, :eval_pos] if context is None else context
-        update = _over_keys(self.sequence_attentions[0], normed, keys)
-        return _accumulate(rows, update.squeeze(1), self.deepnorm_alpha, self.target_norms[1] if then else None)
+        attn = self.sequence_attentions[0]
+        atten = attn.attend(normed, keys).view(*rows.shape[:-1], attn.num_heads, attn.head_dim)
+        return _attend_accumulate(attn, atten, rows, self.deepnorm_alpha, self.target_norms[1] if then else None)
 
     def row_local_steps(self, cells: torch.Tensor, targets: torch.Tensor, cell_operand: torch.Tensor | None = None,
                         row_operand: torch.Tensor | None = None,
@@ -286,19 +342,16 @@ class CellLayer2P(nn.Module):
         _accumulate(cells, cell_update, alpha, self.cell_norms[2], out=tokens[:, :, :g])
         _accumulate(targets, row_update, alpha, self.target_norms[2], out=tokens[:, :, g:])
         del cell_update, row_update
-        cell_update, target_update = self.feature_attention(tokens, g)
+        fa = self.feature_attention
+        cell_out, readout = fa.attend(tokens, g)
         del tokens
-        if then is None:
-            _accumulate(cells, cell_update, alpha)
-            _accumulate(targets, target_update, alpha)
-            return None
-        cell_norm, row_norm, operand = then
-        cell_next = _accumulate(cells, cell_update, alpha, cell_norm, operand=operand)
-        if row_norm is None:
-            _accumulate(targets, target_update, alpha)
-            return cell_next, None
-        row_next = _accumulate(rows, target_update.reshape(rows.shape), alpha, row_norm, operand=operand)
-        return cell_next, row_next
+        cell_norm, row_norm, operand = (None, None, True) if then is None else then
+        cell_next = _attend_accumulate(fa.feature_attentions[0], cell_out, cells, alpha, cell_norm, operand=operand)
+        mix = fa.mix_weight(readout.dtype, readout.device) if readout.is_cuda else None
+        row_next = _linear_accumulate(readout, mix, rows, alpha, row_norm, lambda: fa.target_mix(readout),
+                                      operand=operand) if mix is not None else \
+            _accumulate(rows, fa.target_mix(readout), alpha, row_norm, operand=operand)
+        return None if then is None else (cell_next, row_next)
 
 
 class RowLayer2P(nn.Module):
@@ -332,8 +385,9 @@ class RowLayer2P(nn.Module):
         vectors: ``context``, or the first ``eval_pos`` of ``normed``. ``then``: return the rows
         through ``readback_norm`` (the read-back query)."""
         keys = normed[:, :, :eval_pos] if context is None else context
-        update = _over_keys(self.sequence_attentions[0], normed, keys).squeeze(1)
-        return _accumulate(rows, update, self.deepnorm_alpha, self.readback_norm if then else None)
+        attn = self.sequence_attentions[0]
+        atten = attn.attend(normed, keys).view(*rows.shape[:-1], attn.num_heads, attn.head_dim)
+        return _attend_accumulate(attn, atten, rows, self.deepnorm_alpha, self.readback_norm if then else None)
 
     def readback_steps(self, rows: torch.Tensor, cell_memory: torch.Tensor, query: torch.Tensor | None = None,
                        then: RMSNorm | None = None, operand: bool = True) -> torch.Tensor | None:
@@ -344,9 +398,10 @@ class RowLayer2P(nn.Module):
         alpha = self.deepnorm_alpha
         if query is None:
             query = projection_operand(self.readback_norm, rows)
-        update = _over_keys(self.feature_attentions[0], query.unsqueeze(2), cell_memory).squeeze(2)
+        attn = self.feature_attentions[0]
+        atten = attn.attend(query.unsqueeze(2), cell_memory).view(*rows.shape[:-1], attn.num_heads, attn.head_dim)
         del query
-        mlp_in = _accumulate(rows, update, alpha, self.mlp_norm)
+        mlp_in = _attend_accumulate(attn, atten, rows, alpha, self.mlp_norm)
         return _accumulate(rows, self.mlp[0](mlp_in), alpha, then, operand=operand)
 
 

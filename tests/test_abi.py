@@ -46,6 +46,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_kv_project_quantize_int8",
             "nori_kv_project_quantize_int8_workspace_size",
             "nori_linear_f16",
+            "nori_linear_f16_residual_rms_norm",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
         ]
@@ -59,7 +60,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
     assert set(declared_symbols()) == set(_native.SIGNATURES)
-    assert _native.lib().nori_abi_version() == 1
+    assert _native.lib().nori_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_argument_errors_map_to_reference_exceptions():
@@ -159,6 +160,16 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(lin); bad[3] = 0
     assert lib.nori_linear_f16(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_linear_f16(*lin) == nat.NORI_ERR_INVALID  # null pointers
+    # projection + residual + norm: width 128 or 256 (output width = inner width), aligned rows
+    lrn = [None, 1, 1, 4096, 128, 0, 0, 128, None, 128, 0.5, None, 0, 0, 128, 1e-5, None, 0, 0, 128, None]
+    bad = list(lrn); bad[4] = 64
+    assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"width 64" in lib.nori_last_error()
+    bad = list(lrn); bad[4] = -1
+    assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_ERR_INVALID
+    bad = list(lrn); bad[3] = 0
+    assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_linear_f16_residual_rms_norm(*lrn) == nat.NORI_ERR_INVALID  # null pointers
     # the MFMA rate probe (measurement only): operands, a sink and iterations are required
     assert lib.nori_mfma_f16_probe(None, 0, 1, None, 0, None) == nat.NORI_ERR_INVALID
     assert b"mfma_f16_probe" in lib.nori_last_error()

@@ -139,3 +139,132 @@ def test_falls_back_where_the_kernel_does_not_apply(cuda):
     assert not projection.takes_kernel(odd_k, torch.randn(64, 96, device=cuda).to(torch.float16))
     assert not projection.takes_kernel(fp32, w.float())
     assert torch.equal(projection.linear(small, w), torch.nn.functional.linear(small, w))
+
+
+# ---------------------------------------------------------------- projection + residual + norm
+# ``projection.linear_residual_norm`` (nori_linear_f16_residual_rms_norm) replaces the output
+# projection of an attention sublayer followed by the deep-norm residual update and the next
+# RMSNorm (reference two_phase.py:198, 209, 220-225, 264, 271-272; layer.py:251-253). Bars:
+#   * bit-exact (stream and normalized rows) against the projection kernel followed by the
+#     fused residual + norm kernel, which the norm tests pin to torch;
+#   * the stream bit-exact against torch's own expression ``x + alpha * u`` on the same u, the
+#     normalized rows within one fp16 ulp of ``F.rms_norm`` (the order of the fp32 sum of
+#     squares differs).
+
+ALPHA = 0.20412415  # (12 + 12) ** -0.5, a deep-norm alpha
+
+
+def separate_passes(a, w, x, alpha, eps):
+    from nori_amd.norm import RMSNorm, residual_add_norm
+
+    k = a.shape[-1]
+    u = kernel_linear(a.contiguous().view(-1, k), w).view(a.shape)
+    xr = x.clone()
+    y = residual_add_norm(xr, u, alpha, RMSNorm(k, eps=eps), out_dtype=torch.float16)
+    return u, xr, y
+
+
+@pytest.mark.parametrize("k", [128, 256])
+@pytest.mark.parametrize("rows", [256, 4097, 70_001])
+def test_residual_norm_equals_the_separate_passes(cuda, k, rows):
+    g = torch.Generator(device=cuda).manual_seed(rows + k)
+    a = torch.randn(rows, k, generator=g, device=cuda).to(torch.float16)
+    w = (torch.randn(k, k, generator=g, device=cuda) / k ** 0.5).to(torch.float16)
+    x = torch.randn(rows, k, generator=g, device=cuda) * 3.0
+    u, x_ref, y_ref = separate_passes(a, w, x, ALPHA, 1e-5)
+    xs = x.clone()
+    y = projection.linear_residual_norm(a, w, xs, ALPHA, 1e-5)
+    assert y is not None and y.dtype == torch.float16 and y.shape == (rows, k)
+    assert torch.equal(xs, x_ref)
+    assert torch.equal(y, y_ref)
+    # torch's expression on the same u: fp16 u * alpha rounded to fp16, added to the fp32 stream
+    assert torch.equal(xs, x + ALPHA * u)
+    ref = torch.nn.functional.rms_norm(x + ALPHA * u, (k,), None, 1e-5)
+    ulp = torch.clamp(ref.abs(), min=2.0 ** -14).log2().floor().exp2() * 2.0 ** -10
+    assert bool(((y.float() - ref).abs() <= ulp).all())
+
+
+def test_residual_norm_rows_in_another_order(cuda):
+    # the column attention: its output in [table, group, row] order, the cell stream in
+    # [table, row, group] order, the normalized cells written in the stream's layout
+    g = torch.Generator(device=cuda).manual_seed(3)
+    b, n, gr, k = 5, 700, 4, 128
+    cells = torch.randn(b, n, gr, k, generator=g, device=cuda) * 2.0
+    atten = torch.randn(b, gr, n, k, generator=g, device=cuda).to(torch.float16)
+    w = (torch.randn(k, k, generator=g, device=cuda) / 11.3).to(torch.float16)
+    a = atten.transpose(1, 2)
+    _, x_ref, y_ref = separate_passes(a, w, cells, ALPHA, 1e-5)
+    xs = cells.clone()
+    y = projection.linear_residual_norm(a, w, xs, ALPHA, 1e-5)
+    assert y.is_contiguous() and y.shape == cells.shape
+    assert torch.equal(xs, x_ref) and torch.equal(y, y_ref)
+    # the same through a transposed view of the stream: the output follows the stream's layout
+    xs = cells.clone()
+    yt = projection.linear_residual_norm(atten, w, xs.transpose(1, 2), ALPHA, 1e-5)
+    assert torch.equal(xs, x_ref) and torch.equal(yt.transpose(1, 2), y_ref)
+
+
+def test_residual_norm_into_a_slice(cuda):
+    g = torch.Generator(device=cuda).manual_seed(4)
+    rows, k = 3000, 128
+    a = torch.randn(rows, 4, k, generator=g, device=cuda).to(torch.float16)
+    w = (torch.randn(k, k, generator=g, device=cuda) / 11.3).to(torch.float16)
+    x = torch.randn(rows, 4, k, generator=g, device=cuda)
+    buf = torch.full((rows, 6, k), 7.0, dtype=torch.float16, device=cuda)
+    _, x_ref, y_ref = separate_passes(a, w, x, ALPHA, 1e-6)
+    xs = x.clone()
+    assert projection.linear_residual_norm(a, w, xs, ALPHA, 1e-6, out=buf[:, :4]) is not None
+    assert torch.equal(xs, x_ref) and torch.equal(buf[:, :4], y_ref)
+    assert bool((buf[:, 4:] == 7.0).all())
+
+
+def test_residual_norm_declines_what_it_does_not_take(cuda):
+    g = torch.Generator(device=cuda).manual_seed(5)
+    a = torch.randn(4096, 128, generator=g, device=cuda).to(torch.float16)
+    w = torch.randn(128, 128, generator=g, device=cuda).to(torch.float16)
+    x = torch.randn(4096, 128, generator=g, device=cuda)
+    before = x.clone()
+    assert projection.linear_residual_norm(a, w[:64], x, ALPHA, 1e-5) is None        # output width != inner
+    assert projection.linear_residual_norm(a.float(), w.float(), x, ALPHA, 1e-5) is None  # not fp16
+    assert projection.linear_residual_norm(a[:, :96], w[:96, :96], x[:, :96], ALPHA, 1e-5) is None
+    assert projection.linear_residual_norm(a, w, x.half(), ALPHA, 1e-5) is None       # stream not fp32
+    assert torch.equal(x, before)
+
+
+def test_two_phase_steps_take_the_fused_pass(cuda, monkeypatch):
+    """A cell layer and a row layer under fp16 autocast: every attention update whose next norm
+    is an fp16 operand goes through the fused kernel, and the result matches the separate
+    projection + residual + norm passes to within the fp16 roundings of the updates (at these
+    row counts the separate projection is the library GEMM, which sums in another order)."""
+    from nori_amd import two_phase
+
+    torch.manual_seed(0)
+    layer = two_phase.CellLayer2P(128, 2, 256, target_tokens=2, target_heads=4, target_hidden_dim=682,
+                                  deepnorm_alpha=ALPHA, device=cuda, dtype=torch.float32).eval()
+    row_layer = two_phase.RowLayer2P(256, 4, 682, deepnorm_alpha=ALPHA, device=cuda, dtype=torch.float32).eval()
+    g = torch.Generator(device=cuda).manual_seed(6)
+    cells = torch.randn(3, 96, 4, 128, generator=g, device=cuda)
+    targets = torch.randn(3, 96, 2, 128, generator=g, device=cuda)
+    memory = torch.randn(3, 96, 4, 256, generator=g, device=cuda).to(torch.float16)
+    calls = []
+    fused = projection.linear_residual_norm
+
+    def spy(a, *args, **kw):
+        y = fused(a, *args, **kw)
+        calls.append((int(a.shape[-1]), y is not None))
+        return y
+
+    def run(take):
+        monkeypatch.setattr(two_phase, "linear_residual_norm", spy if take else (lambda *a, **k: None))
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+            c, t = layer(cells, targets, 64)
+            r = row_layer(t.reshape(3, 96, 256), 64, memory)
+        return c, t, r
+
+    c1, t1, r1 = run(True)
+    assert calls and all(took for _, took in calls)
+    assert sorted(set(k for k, _ in calls)) == [128, 256]
+    c0, t0, r0 = run(False)
+    for got, ref in ((c1, c0), (t1, t0), (r1, r0)):
+        scale = ref.abs().amax()
+        assert float((got - ref).abs().amax()) <= 2e-3 * float(scale)
