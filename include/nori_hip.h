@@ -53,7 +53,8 @@ typedef enum {
 #define NORI_ATTN_MERGE 1u /* merge into running (out fp32, lse) instead of overwriting them */
 
 /* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
- * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm and the MFMA probe added). */
+ * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens and the
+ * MFMA probe added). */
 #define NORI_ABI_VERSION 2
 int nori_abi_version(void);
 
@@ -393,6 +394,29 @@ int nori_linear_f16_residual_rms_norm(const void* a, int64_t n_outer, int64_t n_
                                       int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, float eps,
                                       void* y, int64_t y_outer_stride, int64_t y_mid_stride, int64_t y_row_stride,
                                       void* stream);
+
+/*
+ * The fp16 cell tokens of the two-phase model's cell embedding under fp16 autocast: what
+ * MaskEmbEncoder.forward (reference model/encoders.py:432-585) hands its fusion network's
+ * first Linear, from the cell values x [tables, rows, groups, features] (fp32): per value the
+ * scientific-notation RBF embedding (encoders.py:118-276: float64 mantissa/exponent split and
+ * Gaussian kernels, the gate of the sign/exponent embeddings, LayerNorm, output Linear) in
+ * channels [0, n_rbf), the prompt-quantile PLE coordinates (encoders.py:309-429) in
+ * [n_rbf, n_rbf + n_bins), or the mask embedding where x is NaN. gate_table: fp16
+ * [40][2][n_kernels], sigmoid(gamma) then tanh(beta) of the gate MLP for the row
+ * 20 (x < 0) + 10 (exponent < 0) + exponent digit; centers [n_kernels], sigma [1], ln_weight,
+ * ln_bias [n_kernels] fp32 (may be NULL: 1, 0); w_out fp16 [n_rbf][n_kernels], b_out fp16
+ * [n_rbf] (may be NULL); edges fp32 [tables][groups][features][n_bins + 1]; mask_embedding
+ * fp32 [n_rbf + n_bins] (NULL: NaN cells keep the embedding of 0); out fp16
+ * [tables * rows * groups * features][n_rbf + n_bins]. Built for n_kernels 16 or 32,
+ * n_rbf 96, n_bins 32. The LayerNorm's and the output projection's fp32 sums are in the
+ * kernel's order; every other op rounds as torch's does.
+ */
+int nori_cell_tokens(const float* x, int64_t tables, int64_t rows, int32_t groups, int32_t features,
+                     int32_t n_kernels, const float* centers, const float* sigma, const void* gate_table,
+                     const float* ln_weight, const float* ln_bias, float ln_eps, const void* w_out, const void* b_out,
+                     int32_t n_rbf, const float* edges, int32_t n_bins, const float* mask_embedding, void* out,
+                     void* stream);
 
 /* ---- measurement (no counterpart in the reference) ----
  *

@@ -27,12 +27,14 @@ numeric embedding is not part of the nori models and raises ``NotImplementedErro
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any
 
 import torch
 import torch.nn as nn
 from torch.nn.init import orthogonal_
 
+from . import _native as nat
 from .norm import layer_norm
 
 __all__ = [
@@ -231,6 +233,27 @@ class RBFembedding(nn.Module):
         m = mag / (10.0 ** e.to(xw.dtype))
         return torch.where(zero, torch.zeros_like(m), m), e
 
+    def gate_table(self, device: torch.device) -> torch.Tensor:
+        """[40, 2, n_kernels]: sigmoid(gamma) and tanh(beta) of the gate for every row the gate
+        MLP can see -- row 20 s + 10 t + d for sign s of x, sign t of the exponent and exponent
+        digit d (one exponent digit) -- through the module's own embeddings, gate MLP and
+        activations under the current autocast state; cached until a weight or that state
+        changes."""
+        params = [self.sign_embedding.weight, self.exp_sign_embedding.weight, self.exp_digit_embedding.weight]
+        params += [p for p in self.gate_mlp.parameters()]
+        state = (torch.is_autocast_enabled("cuda"), torch.get_autocast_dtype("cuda"))
+        key = (device, state) + tuple((p.data_ptr(), p._version) for p in params)
+        cached = getattr(self, "_gate_table", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                r = torch.arange(40, device=device)
+                parts = [self.sign_embedding(r // 20), self.exp_sign_embedding((r // 10) % 2), self.exp_digit_embedding(r % 10)]
+                gb = self.gate_mlp(torch.cat(parts, dim=-1).to(self.dtype))
+                gamma, beta = torch.split(gb, self.n_kernels, dim=-1)
+                table = torch.stack((torch.sigmoid(gamma), torch.tanh(beta)), dim=1).contiguous()
+            cached = self._gate_table = (key, table)
+        return cached[1]
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x.squeeze(-1)
         rows = x.shape[0]
@@ -421,6 +444,10 @@ class MaskEmbEncoder(nn.Module):
         assert not absent, f"Missing encoder inputs: {absent}"
         x = torch.cat([input[k] for k in self.in_keys], dim=-1)
         b, s, g, _ = x.shape
+        h = self._tokens_on_device(x, input) if x.is_cuda else None
+        if h is not None:
+            input[self.out_key] = self._fusion_on_device(h).view(b, s, g, -1)
+            return input
         x = x.unsqueeze(-1)
         missing = torch.isnan(x)
         x = x.masked_fill(missing, 0.0)
@@ -435,6 +462,53 @@ class MaskEmbEncoder(nn.Module):
         h = emb.flatten(3)
         input[self.out_key] = (self._fusion_on_device(h) if h.is_cuda else self.fusion_network(h)).view(b, s, g, -1)
         return input
+
+    def _tokens_on_device(self, x: torch.Tensor, input: dict[str, Any]) -> torch.Tensor | None:
+        """The fusion network's fp16 operand [b, s, g, features * E] straight from the cell
+        values under fp16 autocast (``nori_cell_tokens``: masked fill, RBF embedding, PLE
+        coordinates and the mask embedding in one pass; the values torch's ops give, up to the
+        order of the LayerNorm's and the output projection's fp32 sums), or None where the
+        kernel does not take the configuration."""
+        rbf = self.numeric_mlp
+        if not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.float16
+                and isinstance(rbf, RBFembedding) and rbf.gate_mlp is not None and rbf.exponent_digits == 1
+                and not rbf.use_original_features and rbf.n_kernels in (16, 32) and self.prompt_quantile_ple_bins == 32
+                and rbf.out_layer.out_features == 96 and self.embedding_dim == 128 and x.dtype == torch.float32
+                and (self.nan_to_zero or self.mask_embedding.numel() == 128)):
+            return None
+        reference = input.get(PromptQuantilePLEEncoder.reference_key)
+        if not isinstance(reference, dict):
+            return None
+        edges = reference["edges"]
+        b, s, g, f = x.shape
+        if tuple(edges.shape) != (b, g, f, 33) or edges.device != x.device:
+            return None
+        dev = x.device
+        key = (dev,) + tuple((p.data_ptr(), p._version) for p in rbf.out_layer.parameters())
+        cached = getattr(self, "_out16", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                bias = rbf.out_layer.bias
+                cached = self._out16 = (key, rbf.out_layer.weight.to(dev, torch.float16).contiguous(),
+                                        None if bias is None else bias.to(dev, torch.float16).contiguous())
+        w16, b16 = cached[1:]
+        table = rbf.gate_table(dev)
+        x = x.contiguous()
+        edges = edges.to(torch.float32).contiguous()
+        ln_w = None if rbf.norm.weight is None else rbf.norm.weight.float().contiguous()
+        ln_b = None if rbf.norm.bias is None else rbf.norm.bias.float().contiguous()
+        mask = None if self.nan_to_zero else self.mask_embedding.float().contiguous()
+        h = torch.empty((b, s, g, f * self.embedding_dim), dtype=torch.float16, device=dev)
+        ptr = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+        nat.check(
+            nat.lib().nori_cell_tokens(
+                ptr(x), b, s, g, f, rbf.n_kernels, ptr(rbf.centers.float().contiguous()), ptr(rbf.sigma.float().reshape(1)),
+                ptr(table), ptr(ln_w), ptr(ln_b), float(rbf.norm.eps), ptr(w16), ptr(b16), 96, ptr(edges), 32, ptr(mask),
+                ptr(h), nat.stream_of(dev),
+            ),
+            "cell_tokens",
+        )
+        return h
 
     def _fusion_on_device(self, h: torch.Tensor) -> torch.Tensor:
         """fusion_network (Linear -> LayerNorm -> ReLU -> Linear -> LayerNorm) with the norms on

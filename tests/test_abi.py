@@ -47,6 +47,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_kv_project_quantize_int8_workspace_size",
             "nori_linear_f16",
             "nori_linear_f16_residual_rms_norm",
+            "nori_cell_tokens",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
         ]
@@ -170,6 +171,18 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(lrn); bad[3] = 0
     assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_linear_f16_residual_rms_norm(*lrn) == nat.NORI_ERR_INVALID  # null pointers
+    # cell tokens: 16 or 32 RBF kernels, 96 RBF outputs, 32 PLE bins
+    ct = [None, 2, 64, 4, 2, 16, None, None, None, None, None, 1e-5, None, None, 96, None, 32, None, None, None]
+    bad = list(ct); bad[5] = 24
+    assert lib.nori_cell_tokens(*bad) == nat.NORI_ERR_UNSUPPORTED
+    assert b"24 kernels" in lib.nori_last_error()
+    bad = list(ct); bad[16] = 16
+    assert lib.nori_cell_tokens(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(ct); bad[3] = 0
+    assert lib.nori_cell_tokens(*bad) == nat.NORI_ERR_INVALID
+    bad = list(ct); bad[2] = 0
+    assert lib.nori_cell_tokens(*bad) == nat.NORI_OK  # no rows: nothing to do
+    assert lib.nori_cell_tokens(*ct) == nat.NORI_ERR_INVALID  # null pointers
     # the MFMA rate probe (measurement only): operands, a sink and iterations are required
     assert lib.nori_mfma_f16_probe(None, 0, 1, None, 0, None) == nat.NORI_ERR_INVALID
     assert b"mfma_f16_probe" in lib.nori_last_error()
