@@ -53,8 +53,8 @@ typedef enum {
 #define NORI_ATTN_MERGE 1u /* merge into running (out fp32, lse) instead of overwriting them */
 
 /* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
- * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens and the
- * MFMA probe added). */
+ * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens,
+ * nori_layer_norm_cells and the MFMA probe added). */
 #define NORI_ABI_VERSION 2
 int nori_abi_version(void);
 
@@ -394,6 +394,26 @@ int nori_linear_f16_residual_rms_norm(const void* a, int64_t n_outer, int64_t n_
                                       int64_t x_outer_stride, int64_t x_mid_stride, int64_t x_row_stride, float eps,
                                       void* y, int64_t y_outer_stride, int64_t y_mid_stride, int64_t y_row_stride,
                                       void* stream);
+
+/*
+ * The cell encoder's last LayerNorm followed by the two additions of the two-phase forward
+ * (reference model/transformer.py:370-562: the feature positional embedding of the cell's
+ * group, then the target-aware row bias, :1080-1132), over cells x [tables, rows, groups,
+ * cols] (fp16 or fp32 rows x_row_stride apart; the fusion network's last Linear output):
+ *   v = LayerNorm(x) * weight + bias                       (as nori_layer_norm, fp32)
+ *   v = v + pos[group]                                     (pos fp32 [groups][cols], or NULL)
+ *   rb = ctx[table][row] for row < eval_pos, else 0         (ctx fp32 [tables][eval_pos][cols])
+ *   with alpha: gate = sigmoid(sum(v * rb) * inv_sqrt_e),
+ *               v = (v + (1 - alpha) rb) + alpha (rb * gate)
+ *   without alpha: v = v + rb;  no ctx: no row bias.
+ * y: fp32 [tables * rows * groups][cols], contiguous. cols 64, 128 or 256. Each op rounds as
+ * torch's does; the norm's statistics and the gate's dot product are summed in the kernel's
+ * order.
+ */
+int nori_layer_norm_cells(const void* x, int x_dtype, int64_t tables, int64_t rows, int64_t groups, int32_t cols,
+                          int64_t x_row_stride, const float* weight, const float* bias, float eps, const float* pos,
+                          const float* ctx, int64_t eval_pos, const float* alpha, float inv_sqrt_e, float* y,
+                          void* stream);
 
 /*
  * The fp16 cell tokens of the two-phase model's cell embedding under fp16 autocast: what

@@ -446,7 +446,7 @@ class MaskEmbEncoder(nn.Module):
         b, s, g, _ = x.shape
         h = self._tokens_on_device(x, input) if x.is_cuda else None
         if h is not None:
-            input[self.out_key] = self._fusion_on_device(h).view(b, s, g, -1)
+            input[self.out_key] = self._fusion_on_device(h, input).view(b, s, g, -1)
             return input
         x = x.unsqueeze(-1)
         missing = torch.isnan(x)
@@ -460,7 +460,7 @@ class MaskEmbEncoder(nn.Module):
         if not self.nan_to_zero:
             emb = torch.where(missing, self.mask_embedding.expand_as(emb), emb)
         h = emb.flatten(3)
-        input[self.out_key] = (self._fusion_on_device(h) if h.is_cuda else self.fusion_network(h)).view(b, s, g, -1)
+        input[self.out_key] = (self._fusion_on_device(h, input) if h.is_cuda else self.fusion_network(h)).view(b, s, g, -1)
         return input
 
     def _tokens_on_device(self, x: torch.Tensor, input: dict[str, Any]) -> torch.Tensor | None:
@@ -510,7 +510,13 @@ class MaskEmbEncoder(nn.Module):
         )
         return h
 
-    def _fusion_on_device(self, h: torch.Tensor) -> torch.Tensor:
+    # A caller that applies the last LayerNorm itself (fused with what follows it) sets this key
+    # in the input dict; the encoder then leaves the norm out, and returns it under
+    # ``last_norm_key`` as (module, output dtype).
+    defer_last_norm_key = "_defer_last_norm"
+    last_norm_key = "_last_norm"
+
+    def _fusion_on_device(self, h: torch.Tensor, input: dict[str, Any] | None = None) -> torch.Tensor:
         """fusion_network (Linear -> LayerNorm -> ReLU -> Linear -> LayerNorm) with the norms on
         the HIP kernel: the first writes the ReLU'd operand of the second Linear in the dtype it
         computes in, the second the fp32 (autocast) or input-dtype output torch's would."""
@@ -519,7 +525,11 @@ class MaskEmbEncoder(nn.Module):
         h = layer_norm(h, ln1.weight, ln1.bias, ln1.eps, relu=True, out_dtype=_operand_dtype(h.dtype))
         h = lin2(h)
         autocast = torch.is_autocast_enabled("cuda")
-        return layer_norm(h, ln2.weight, ln2.bias, ln2.eps, out_dtype=torch.float32 if autocast else h.dtype)
+        out_dtype = torch.float32 if autocast else h.dtype
+        if input is not None and input.get(self.defer_last_norm_key):
+            input[self.last_norm_key] = (ln2, out_dtype)
+            return h
+        return layer_norm(h, ln2.weight, ln2.bias, ln2.eps, out_dtype=out_dtype)
 
 
 class NanEncoder(nn.Module):

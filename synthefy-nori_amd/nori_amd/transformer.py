@@ -30,6 +30,7 @@ not part of this package (it raises); the dense models run through the cache ent
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Any, Callable, Literal
@@ -38,10 +39,18 @@ import torch
 import torch.nn as nn
 from torch.amp import autocast
 
-from .encoders import PromptQuantilePLEEncoder, get_cls_y_encoder, get_reg_y_encoder, get_x_encoder, preprocesss_4_x
+from . import _native as nat
+from .encoders import (
+    MaskEmbEncoder,
+    PromptQuantilePLEEncoder,
+    get_cls_y_encoder,
+    get_reg_y_encoder,
+    get_x_encoder,
+    preprocesss_4_x,
+)
 from .layer import EncoderBaseLayer, LayerStack
 from .two_phase import TwoPhaseEncoder
-from .norm import RMSNorm
+from .norm import RMSNorm, layer_norm
 
 __all__ = ["ContextCache", "FeaturesTransformer"]
 
@@ -392,6 +401,48 @@ class FeaturesTransformer(nn.Module):
             return x + (1.0 - alpha) * row_bias + alpha * (row_bias * gate)
         return x + row_bias
 
+    def _finish_cells(self, cells: torch.Tensor, last_norm, pos: torch.Tensor | None, y: torch.Tensor,
+                      eval_pos: int) -> torch.Tensor:
+        """The cell tokens the two-phase encoder takes: the cell encoder's output (``last_norm``:
+        its last LayerNorm still to apply, as (module, output dtype)), the feature positional
+        embedding and the target-aware row bias (:467-470, 1080-1132). On the GPU the three are
+        one pass (``nori_layer_norm_cells``) where it takes the configuration."""
+        scale = float(getattr(self, "target_aware_scale", 1.0))
+        target_aware = self.use_target_aware_embedding and eval_pos > 0 and abs(scale) >= 1e-8
+        if last_norm is not None:
+            ln, out_dtype = last_norm
+            b, s, g, e = cells.shape
+            fused = (
+                out_dtype == torch.float32 and cells.dtype in (torch.float16, torch.float32) and e in (64, 128, 256)
+                and (pos is None or tuple(pos.shape) == (g, e)) and (not target_aware or scale == 1.0)
+                and (not target_aware or self.reg_target_aware_embedding is not None)
+                and cells.stride(-1) == 1 and cells.is_contiguous()
+            )
+            if fused:
+                ctx = alpha = None
+                if target_aware:
+                    ctx = self.reg_target_aware_embedding(y[:, :eval_pos].unsqueeze(-1).to(out_dtype)).to(out_dtype)
+                    ctx = ctx.contiguous()
+                    if self.use_column_specific_y_aware and self.column_y_aware_alpha is not None:
+                        alpha = torch.sigmoid(self.column_y_aware_alpha).to(out_dtype).reshape(1)
+                out = torch.empty((b, s, g, e), dtype=torch.float32, device=cells.device)
+                pos32 = None if pos is None else pos.to(torch.float32).contiguous()
+                w = None if ln.weight is None else ln.weight.float().contiguous()
+                bias = None if ln.bias is None else ln.bias.float().contiguous()
+                ptr = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+                nat.check(
+                    nat.lib().nori_layer_norm_cells(
+                        ptr(cells), nat.dtype_code(cells.dtype), b, s, g, e, e, ptr(w), ptr(bias), float(ln.eps),
+                        ptr(pos32), ptr(ctx), eval_pos if ctx is not None else 0, ptr(alpha), 1.0 / self.embed_dim ** 0.5,
+                        ptr(out), nat.stream_of(cells.device),
+                    ),
+                    "layer_norm_cells",
+                )
+                return out
+            cells = layer_norm(cells, ln.weight, ln.bias, ln.eps, out_dtype=out_dtype)
+        cells = self.apply_feature_positional_embeddings(cells, pos)
+        return self.apply_target_aware_embedding(cells, y.clone(), task_type="reg", eval_pos=eval_pos)
+
     def process_4_x(self, data: dict):
         """Originally non-finite cells become NaN again after preprocessing (:1134-1139)."""
         data["data"] = torch.where(data["mask"].to(torch.bool), float("nan"), data["data"])
@@ -441,16 +492,17 @@ class FeaturesTransformer(nn.Module):
         seq_len = x.shape[1]
         x_dict, n_pad = self._build_x_preprocess_inputs(x, eval_pos)
         pre = self.process_4_x(self.x_preprocess(x_dict))
-        cells = self.encoder_x(pre)["data"]
-        cells = self.apply_feature_positional_embeddings(
-            cells, self.make_feature_positional_embeddings(cells.shape[2], device=cells.device, dtype=cells.dtype)
-        )
+        pre[MaskEmbEncoder.defer_last_norm_key] = x.is_cuda
+        encoded = self.encoder_x(pre)
+        cells, last_norm = encoded["data"], encoded.pop(MaskEmbEncoder.last_norm_key, None)
+        out_dtype = cells.dtype if last_norm is None else last_norm[1]
+        pos = self.make_feature_positional_embeddings(cells.shape[2], device=cells.device, dtype=out_dtype)
         if y.shape[1] < seq_len:
             y = torch.cat((y, torch.full((y.shape[0], seq_len - y.shape[1]), float("nan"), device=y.device, dtype=y.dtype)), 1)
-        cells = self.apply_target_aware_embedding(cells, y.clone(), task_type="reg", eval_pos=eval_pos)
+        cells = self._finish_cells(cells, last_norm, pos, y, eval_pos)
         positions = torch.arange(seq_len, device=y.device).view(1, -1)
         y_masked = torch.where(positions >= eval_pos, torch.tensor(float("nan"), device=y.device, dtype=y.dtype), y)
-        row_states, cell_states = self.transformer_encoder(cells, y_masked, eval_pos)
+        row_states, cell_states = self.transformer_encoder(cells, y_masked, eval_pos, inplace=True)
         if return_embeddings:
             return row_states
         reg_output = self.reg_y_decoder(row_states[:, eval_pos:])

@@ -468,9 +468,12 @@ class TwoPhaseEncoder(nn.Module):
         if not 0 < eval_pos <= n_rows:
             raise ValueError("two-phase encoder requires a non-empty context prefix")
 
-    def forward(self, cells: torch.Tensor, y: torch.Tensor, eval_pos: int, **_: object) -> tuple[torch.Tensor, torch.Tensor]:
+    def forward(self, cells: torch.Tensor, y: torch.Tensor, eval_pos: int, inplace: bool = False,
+                **_: object) -> tuple[torch.Tensor, torch.Tensor]:
+        """``inplace``: the cell stream is updated in ``cells`` itself (a caller's own temporary)
+        instead of in a copy."""
         self._require_context(eval_pos, cells.shape[1])
-        cells = cells.clone()  # the streams are updated in place
+        cells = cells if inplace else cells.clone()  # the streams are updated in place
         targets = self.target_encoder(y).to(cells.dtype).contiguous()
         rows = _row_vectors(targets)
         # every residual update hands the next sublayer its normalized stream (one pass)

@@ -48,6 +48,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_linear_f16",
             "nori_linear_f16_residual_rms_norm",
             "nori_cell_tokens",
+            "nori_layer_norm_cells",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
         ]
@@ -171,6 +172,17 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(lrn); bad[3] = 0
     assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_linear_f16_residual_rms_norm(*lrn) == nat.NORI_ERR_INVALID  # null pointers
+    # the cells' last LayerNorm with the positional and target-aware additions
+    lc = [None, nat.NORI_F16, 2, 64, 4, 128, 128, None, None, 1e-5, None, None, 32, None, 0.088, None, None]
+    bad = list(lc); bad[5] = 96
+    assert lib.nori_layer_norm_cells(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(lc); bad[1] = nat.NORI_BF16
+    assert lib.nori_layer_norm_cells(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(lc); bad[12] = 65
+    assert lib.nori_layer_norm_cells(*bad) == nat.NORI_ERR_INVALID
+    bad = list(lc); bad[2] = 0
+    assert lib.nori_layer_norm_cells(*bad) == nat.NORI_OK  # no tables: nothing to do
+    assert lib.nori_layer_norm_cells(*lc) == nat.NORI_ERR_INVALID  # null pointers
     # cell tokens: 16 or 32 RBF kernels, 96 RBF outputs, 32 PLE bins
     ct = [None, 2, 64, 4, 2, 16, None, None, None, None, None, 1e-5, None, None, 96, None, 32, None, None, None]
     bad = list(ct); bad[5] = 24

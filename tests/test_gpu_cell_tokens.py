@@ -139,3 +139,64 @@ def test_fp32_and_unsupported_configurations_take_the_torch_ops(cuda):
     enc.numeric_mlp.n_kernels = 8
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
         assert enc._tokens_on_device(x, inp) is None
+
+
+# ---------------------------------------------------------------- the cells' last norm + additions
+# ``nori_layer_norm_cells`` replaces the cell encoder's last LayerNorm, the feature positional
+# embedding and the target-aware row bias of the two-phase forward (reference
+# transformer.py:467-470, 1080-1132). Bars: query rows (no row bias) bit-exact against the
+# separate norm kernel + torch's ops; context rows within a few fp32 ulps (the gate's dot
+# product is summed in another order).
+
+TWO_PHASE = dict(
+    preprocess_config_x=dict(num_features=2, nan_handling_enabled=True, normalize_on_train_only=True, normalize_x=True,
+                             remove_outliers=False, normalize_by_used_features=True, prompt_quantile_ple_bins=32),
+    encoder_config_x=dict(num_features=2, embedding_size=128, mask_embedding_size=128, encoder_use_bias=True,
+                          numeric_embed_type="RBF",
+                          RBF_config=dict(token_embed_dim=8, n_kernels=16, sigma=0.5, use_learn_sigma=False,
+                                          use_learn_embeddings=False, use_original_features=False),
+                          prompt_quantile_ple_bins=32),
+    encoder_config_y=dict(num_inputs=1, embedding_size=128, nan_handling_y_encoder=True, max_num_classes=10),
+    decoder_config=dict(num_reg_quantiles=999, regression_loss="pinball"),
+    nlayers=2, nhead=2, embed_dim=128, hid_dim=384, features_per_group=2, dropout=0.0, pre_norm=True,
+    activation="swiglu", norm_type="rmsnorm", deepnorm_alpha=4 ** -0.5, feature_positional_embedding_type="subortho",
+    use_target_aware_embedding=True, use_column_specific_y_aware=True, use_qassmax=True, qass_mode="log_only",
+    omit_feature_decoder=True, two_phase_config=dict(target_tokens=2, row_layers=1, row_heads=4, row_hidden_dim=256),
+)
+
+
+@pytest.mark.parametrize("autocast", [True, False])
+@pytest.mark.parametrize("gated", [True, False])
+def test_layer_norm_cells_match_the_separate_ops(cuda, autocast, gated):
+    import nori_amd
+
+    torch.manual_seed(3)
+    model = nori_amd.FeaturesTransformer(**TWO_PHASE).eval().to(cuda)
+    with torch.no_grad():
+        model.column_y_aware_alpha.fill_(0.3)
+        model.reg_target_aware_embedding.weight.normal_(0.0, 0.5)
+        model.reg_target_aware_embedding.bias.normal_(0.0, 0.5)
+    if not gated:
+        model.use_column_specific_y_aware = False
+    ln = model.encoder_x[0].fusion_network[4]
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.2)
+        ln.bias.normal_(0.0, 0.2)
+    b, s, g, ep = 3, 200, 4, 150
+    gen = torch.Generator(device=cuda).manual_seed(9)
+    h = torch.randn(b, s, g, 128, generator=gen, device=cuda) * 2.0 + 0.5
+    y = torch.randn(b, s, generator=gen, device=cuda)
+    y[:, ep:] = float("nan")
+    dt = torch.float32
+    h = h.half() if autocast else h
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+        pos = model.make_feature_positional_embeddings(g, device=cuda, dtype=dt)
+        fused = model._finish_cells(h, (ln, dt), pos, y, ep)
+        cells = layer_norm(h, ln.weight, ln.bias, ln.eps, out_dtype=dt)
+        ref = model._finish_cells(cells, None, pos, y, ep)
+    assert fused.dtype == torch.float32 and fused.shape == (b, s, g, 128)
+    assert torch.equal(fused[:, ep:], ref[:, ep:])
+    if not gated:
+        assert torch.equal(fused, ref)
+    d = (fused[:, :ep] - ref[:, :ep]).abs()
+    assert float(d.max()) <= 8 * 2.0 ** -24 * float(ref[:, :ep].abs().max())
