@@ -54,7 +54,7 @@ typedef enum {
 
 /* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
  * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens,
- * nori_layer_norm_cells and the MFMA probe added). */
+ * nori_layer_norm_cells, nori_swiglu_mlp_residual_rms_norm and the MFMA probe added). */
 #define NORI_ABI_VERSION 2
 int nori_abi_version(void);
 
@@ -228,6 +228,23 @@ int nori_silu_mul(const void* gu, int dtype, int64_t rows, int32_t hidden, int64
 int nori_swiglu_mlp(const void* x, int dtype, int64_t rows, int32_t width, int64_t x_row_stride,
                     const void* w_gate_up, const void* w_down, int32_t hidden, void* y, int64_t y_row_stride,
                     void* stream);
+
+/*
+ * nori_swiglu_mlp followed by the deep-norm residual update of an fp32 stream and the next
+ * sublayer's RMSNorm without weight, in one kernel (reference model/two_phase.py:209,
+ * 220-225, 271-272 with layer.py:251-253 and 261-274): per row r, u = the MLP's fp16 output
+ * (never written), stream[r] = stream[r] + fp16(fp32(u) * alpha) in place, and each group of
+ * norm_width columns k is normalized, fp16(s * rsqrt(mean(s^2) + eps)), into output group
+ * q = r * (width / norm_width) + k at element (q / y_group) * y_group_stride +
+ * (q % y_group) * y_row_stride of y (fp16). Bit for bit nori_swiglu_mlp then
+ * nori_residual_add_rms_norm. Built for width 128 (norm_width 128) and 256 (norm_width 128
+ * or 256); stream rows stream_row_stride apart, 16-byte aligned; y 8-byte aligned.
+ */
+int nori_swiglu_mlp_residual_rms_norm(const void* x, int dtype, int64_t rows, int32_t width, int64_t x_row_stride,
+                                      const void* w_gate_up, const void* w_down, int32_t hidden, float alpha,
+                                      float* stream_rows, int64_t stream_row_stride, int32_t norm_width, float eps,
+                                      void* y, int64_t y_group, int64_t y_group_stride, int64_t y_row_stride,
+                                      void* stream);
 
 /*
  * QASS "full" query scaling in one pass (replaces QASSMaxScaling.forward's gate branch,

@@ -19,6 +19,14 @@
 // staging costs about a third of the kernel's time (measured by leaving it out), the gate's
 // VALU work about an eighth.
 //
+// nori_swiglu_mlp_residual_rms_norm ends the kernel with the deep-norm residual update of an
+// fp32 stream and the next sublayer's RMSNorm (no weight) instead of writing y: per row
+// x = x + f16(f16(y) * alpha) in place, then f16(x * rsqrt(mean(x^2) + eps)) over norm
+// groups of NW columns (the whole row, or 128-column tokens of a wider row) -- bit for bit
+// nori_swiglu_mlp followed by nori_residual_add_rms_norm: the sum of squares runs in that
+// kernel's order (an fma chain over each 4-column chunk, then pairwise over the chunk index
+// bits from the highest; a lane here holds every chunk of its half-row, chunk 8 t + 2 j + hh).
+//
 // Rounding: the projections sum in fp32 and round to fp16 as hipBLASLt's fp16 GEMMs do, but in
 // their own order, so a value can differ from the unfused sequence's by one fp16 ulp where the
 // fp32 sum sits at a rounding boundary. silu(g) = g * rcp(1 + 2^(-g log2 e)) with the hardware
@@ -26,6 +34,9 @@
 // to fp16; the product of two fp16 values is exact in fp32, so f16(s * u) is one packed fp16
 // multiply.
 #include "nori_common.h"
+
+// the residual epilogue rounds every op separately, as torch does
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -77,10 +88,22 @@ __device__ __forceinline__ uint32_t gate_pair(float g0, float g1, float u0, floa
     return __builtin_bit_cast(uint32_t, sh * uh);
 }
 
-template <int E>
+// The residual epilogue's operands (NW > 0): the fp32 stream (row r at xs + r * xs_row, updated
+// in place) and the normalized output, norm group q = r * (E / NW) + k at
+// (q / y_group) * y_group_stride + (q % y_group) * y_row_stride elements from y.
+struct ResEpi {
+    float* xs;
+    int64_t xs_row;
+    float alpha, eps;
+    int64_t y_group, y_group_stride, y_row_stride;
+};
+
+// NW: 0 writes y = the MLP's output (rows ys apart); else the residual epilogue with norm
+// groups of NW columns.
+template <int E, int NW>
 __global__ void __launch_bounds__(MlpGeom<E>::THREADS)
 swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, const uint16_t* __restrict__ wgu,
-                  const uint16_t* __restrict__ wd, int hp, uint16_t* __restrict__ y, int64_t ys) {
+                  const uint16_t* __restrict__ wd, int hp, uint16_t* __restrict__ y, int64_t ys, const ResEpi ep) {
     using G = MlpGeom<E>;
     __shared__ __attribute__((aligned(16))) _Float16 ring[2 * G::BUF];
 
@@ -185,7 +208,63 @@ swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, cons
 
     // ---- y[row][e .. e+3] from Y^T: element 4j + i of tile t is e = 32t + 8j + 4hh + i
     const int64_t row = r0 + l32;
-    if (row < rows) {
+    if constexpr (NW > 0) {
+        static_assert(E % NW == 0 && NW % 32 == 0, "norm groups of whole tiles");
+        constexpr int TT = NW / 32;  // tiles per norm group
+        const bool ok = row < rows;
+        float* xr = ep.xs + (ok ? row : 0) * ep.xs_row;
+        float part[G::OT][4];
+#pragma unroll
+        for (int t = 0; t < G::OT; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 32 * t + 8 * j + 4 * hh;
+                const f32x4 xv = ok ? *reinterpret_cast<const f32x4*>(xr + e) : f32x4{0.f, 0.f, 0.f, 0.f};
+                float p = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float u = round_to<NORI_F16>(yt[t][4 * j + i]);
+                    const float v = xv[i] + round_to<NORI_F16>(u * ep.alpha);
+                    yt[t][4 * j + i] = v;
+                    p = fmaf(v, v, p);
+                }
+                if (ok) *reinterpret_cast<f32x4*>(xr + e) = f32x4{yt[t][4 * j], yt[t][4 * j + 1], yt[t][4 * j + 2], yt[t][4 * j + 3]};
+                part[t][j] = p;
+            }
+#pragma unroll
+        for (int k = 0; k < E / NW; ++k) {
+            // chunk 8 t' + 2 j + hh of the group (t' = t - k TT): pairs over (t', j) from the
+            // highest bit in the lane, then over hh (lane bit 5)
+            float q[4 * TT];
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) q[4 * t + j] = part[k * TT + t][j];
+#pragma unroll
+            for (int st = 2 * TT; st >= 1; st >>= 1) {
+#pragma unroll
+                for (int i = 0; i < st; ++i) q[i] = q[i] + q[i + st];
+            }
+            float tot = q[0];
+            tot = tot + __shfl_xor(tot, 32);
+            const float inv = rsqrtf(tot / (float)NW + ep.eps);
+            if (ok) {
+                const int64_t qr = row * (E / NW) + k;
+                uint16_t* yr = y + (qr / ep.y_group) * ep.y_group_stride + (qr % ep.y_group) * ep.y_row_stride;
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x16& v = yt[k * TT + t];
+                        uint16_t h[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) h[i] = f32_to_f16(v[4 * j + i] * inv);
+                        *reinterpret_cast<u32x2*>(yr + 32 * t + 8 * j + 4 * hh) =
+                            u32x2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+                    }
+            }
+        }
+    } else if (row < rows) {
         uint16_t* yr = y + row * ys;
 #pragma unroll
         for (int t = 0; t < G::OT; ++t)
@@ -198,13 +277,14 @@ swiglu_mlp_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t xs, cons
     }
 }
 
-template <int E>
+template <int E, int NW = 0>
 void launch(const uint16_t* x, int64_t rows, int64_t xs, const uint16_t* wgu, const uint16_t* wd, int hp, uint16_t* y,
-            int64_t ys, hipStream_t stream) {
+            int64_t ys, hipStream_t stream, const ResEpi& ep = ResEpi{}) {
     using G = MlpGeom<E>;
     const int64_t per = G::NW * 32;
     const dim3 grid((unsigned)((rows + per - 1) / per));
-    hipLaunchKernelGGL((swiglu_mlp_kernel<E>), grid, dim3(G::THREADS), 0, stream, x, rows, xs, wgu, wd, hp, y, ys);
+    hipLaunchKernelGGL((swiglu_mlp_kernel<E, NW>), grid, dim3(G::THREADS), 0, stream, x, rows, xs, wgu, wd, hp, y, ys,
+                       ep);
 }
 
 }  // namespace
@@ -237,4 +317,41 @@ extern "C" int nori_swiglu_mlp(const void* x, int dtype, int64_t rows, int32_t w
         default: launch<352>(xp, rows, x_row_stride, gp, dp, hidden, yp, y_row_stride, stream); break;
     }
     return launch_status("swiglu_mlp");
+}
+
+extern "C" int nori_swiglu_mlp_residual_rms_norm(const void* x, int dtype, int64_t rows, int32_t width,
+                                                 int64_t x_row_stride, const void* w_gate_up, const void* w_down,
+                                                 int32_t hidden, float alpha, float* stream_rows,
+                                                 int64_t stream_row_stride, int32_t norm_width, float eps, void* y,
+                                                 int64_t y_group, int64_t y_group_stride, int64_t y_row_stride,
+                                                 void* stream_v) {
+    clear_error();
+    if (dtype != NORI_F16)
+        return fail(NORI_ERR_UNSUPPORTED, "swiglu_mlp_residual_rms_norm: unsupported dtype %s (float16 only)", dtype_name(dtype));
+    if (!((width == 128 && norm_width == 128) || (width == 256 && (norm_width == 128 || norm_width == 256))))
+        return fail(NORI_ERR_UNSUPPORTED, "swiglu_mlp_residual_rms_norm: width %d with norm width %d (128/128, 256/128 "
+                    "and 256/256 are built)", width, norm_width);
+    if (rows < 0 || rows > 0x7fffffffLL || hidden <= 0 || hidden % 32 != 0 || y_group <= 0)
+        return fail(NORI_ERR_INVALID, "swiglu_mlp_residual_rms_norm: bad shape (%lld rows, hidden %d, y_group %lld)",
+                    (long long)rows, hidden, (long long)y_group);
+    if (x_row_stride < width || x_row_stride % 8 || stream_row_stride < width || stream_row_stride % 4 ||
+        y_group_stride % 4 || y_row_stride % 4)
+        return fail(NORI_ERR_INVALID, "swiglu_mlp_residual_rms_norm: row strides must be multiples of 8 (x) or 4");
+    if (rows == 0) return NORI_OK;
+    if (!x || !w_gate_up || !w_down || !stream_rows || !y)
+        return fail(NORI_ERR_INVALID, "swiglu_mlp_residual_rms_norm: null pointer");
+    if ((uintptr_t)x % 16 || (uintptr_t)w_gate_up % 16 || (uintptr_t)w_down % 16 || (uintptr_t)stream_rows % 16 ||
+        (uintptr_t)y % 8)
+        return fail(NORI_ERR_INVALID, "swiglu_mlp_residual_rms_norm: x, the weights and the stream must be 16-byte "
+                    "aligned, y 8-byte aligned");
+    const ResEpi ep{stream_rows, stream_row_stride, alpha, eps, y_group, y_group_stride, y_row_stride};
+    hipStream_t stream = (hipStream_t)stream_v;
+    auto xp = reinterpret_cast<const uint16_t*>(x);
+    auto gp = reinterpret_cast<const uint16_t*>(w_gate_up);
+    auto dp = reinterpret_cast<const uint16_t*>(w_down);
+    auto yp = reinterpret_cast<uint16_t*>(y);
+    if (width == 128) launch<128, 128>(xp, rows, x_row_stride, gp, dp, hidden, yp, 0, stream, ep);
+    else if (norm_width == 128) launch<256, 128>(xp, rows, x_row_stride, gp, dp, hidden, yp, 0, stream, ep);
+    else launch<256, 256>(xp, rows, x_row_stride, gp, dp, hidden, yp, 0, stream, ep);
+    return launch_status("swiglu_mlp_residual_rms_norm");
 }

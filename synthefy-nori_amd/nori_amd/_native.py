@@ -91,6 +91,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "nori_linear_f16": (
         ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _vp],
     ),
+    "nori_swiglu_mlp_residual_rms_norm": (
+        ctypes.c_int,
+        [_vp, _i32, _i64, _i32, _i64, _vp, _vp, _i32, _f32, _vp, _i64, _i32, _f32, _vp, _i64, _i64, _i64, _vp],
+    ),
     "nori_layer_norm_cells": (
         ctypes.c_int,
         [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _vp, _f32, _vp, _vp],

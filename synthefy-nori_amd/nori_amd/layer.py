@@ -156,15 +156,7 @@ class SwiGLUMLP(nn.Module):
         # silu(g) * u with torch's rounding in the projection dtype, then the down projection.
         # The hidden width is padded to a multiple of 8 with zero gate/up rows and zero down
         # columns, so every row is 16-byte aligned; the padding contributes exact zeros.
-        width = x.shape[-1]
-        if (
-            self.fused
-            and self._projection_dtype() == torch.float16
-            and self.w_gate.bias is None
-            and self.w_down.bias is None
-            and width == self.w_down.out_features
-            and width in FUSED_MLP_WIDTHS
-        ):
+        if self.fuses(x):
             # the whole sublayer in one kernel: its operand as the projections would take it
             # (autocast casts to fp16), the hidden activations kept on the CU
             gate_up, _, down, hidden = self._stacked_weights(x, multiple=32)
@@ -172,6 +164,14 @@ class SwiGLUMLP(nn.Module):
         gate_up, gate_up_bias, down, hidden = self._stacked_weights(x)
         gu = nn.functional.linear(x, gate_up, gate_up_bias)
         return nn.functional.linear(silu_mul(gu, hidden), down, self.w_down.bias)
+
+    def fuses(self, x: torch.Tensor) -> bool:
+        """Whether ``forward(x)`` runs as the one fused SwiGLU kernel."""
+        return (
+            x.is_cuda and self.fused and self._projection_dtype() == torch.float16 and self.w_gate.bias is None
+            and self.w_down.bias is None and x.shape[-1] == self.w_down.out_features
+            and x.shape[-1] in FUSED_MLP_WIDTHS
+        )
 
     def _projection_dtype(self) -> torch.dtype:
         return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.w_gate.weight.dtype

@@ -367,6 +367,47 @@ def swiglu_mlp(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, hidde
     return out.view(*x.shape[:-1], width)
 
 
+def swiglu_mlp_residual_norm(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, hidden: int,
+                             stream: torch.Tensor, alpha: float, eps: float, norm_width: int,
+                             out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``stream += alpha * swiglu_mlp(x, ...)`` in place, then the RMSNorm (no weight, ``eps``)
+    of every ``norm_width`` columns of the updated stream rows in fp16, in one kernel
+    (``nori_swiglu_mlp_residual_rms_norm``), bit for bit ``swiglu_mlp`` followed by
+    ``residual_add_norm``. x [..., width] fp16; stream fp32, contiguous, holding x's rows of
+    width columns (its last axis ``norm_width``); ``out`` fp16 in stream's shape (any two-level
+    row layout ``residual_add_norm`` takes, e.g. a slice of a token buffer), new and contiguous
+    when None. Returns the normalized rows, or None where the kernel does not take the operands
+    (nothing is then written)."""
+    width = int(x.shape[-1])
+    if not (x.is_cuda and x.dtype == torch.float16 and stream.dtype == torch.float32 and stream.is_contiguous()
+            and stream.device == x.device and stream.numel() == x.numel() and stream.shape[-1] == norm_width
+            and (width, norm_width) in ((128, 128), (256, 128), (256, 256))
+            and gate_up.shape == (2 * hidden, width) and down.shape == (width, hidden)):
+        return None
+    x2 = x.reshape(-1, width)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16 or stream.data_ptr() % 16:
+        return None
+    rows = x2.shape[0]
+    groups = rows * (width // norm_width)
+    if out is None:
+        out = torch.empty(stream.shape, dtype=torch.float16, device=x.device)
+    if out.dtype != torch.float16 or out.numel() != stream.numel() or out.shape[-1] != norm_width:
+        return None
+    layout = _grouped_rows(out, norm_width)
+    if layout is None or layout[0] != groups or out.data_ptr() % 8:
+        return None
+    _, group, gstride, rstride = layout
+    nat.check(
+        nat.lib().nori_swiglu_mlp_residual_rms_norm(
+            x2.data_ptr(), nat.NORI_F16, rows, width, x2.stride(0), gate_up.contiguous().data_ptr(),
+            down.contiguous().data_ptr(), hidden, float(alpha), stream.data_ptr(), width, norm_width, float(eps),
+            out.data_ptr(), group, gstride, rstride, nat.stream_of(x.device),
+        ),
+        "swiglu_mlp_residual_rms_norm",
+    )
+    return out
+
+
 QASS_GATE_HIDDEN = 64
 
 

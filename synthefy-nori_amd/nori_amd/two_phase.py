@@ -34,7 +34,7 @@ import torch
 from torch import nn
 
 from .layer import MultiheadAttention, SwiGLUMLP
-from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, residual_add_norm
+from .norm import RMSNorm, operand_dtype, projection_operand, residual_add, residual_add_norm, swiglu_mlp_residual_norm
 from .projection import linear as proj_linear
 from .projection import linear_residual_norm, takes_kernel
 
@@ -99,6 +99,23 @@ def _attend_accumulate(attn: MultiheadAttention, atten: torch.Tensor, stream: to
     if w_o is None:
         return _accumulate(stream, attn.project_out(atten), alpha, then, operand=operand)
     return _linear_accumulate(a, w_o, stream, alpha, then, lambda: attn.project_out(atten), operand=operand)
+
+
+def _mlp_accumulate(mlp: SwiGLUMLP, x: torch.Tensor, stream: torch.Tensor, alpha: float, then: RMSNorm | None,
+                    *, operand: bool = True, out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``_accumulate(stream, mlp(x), alpha, then, ...)``: with the next norm formed in the fp16
+    operand dtype, the fused SwiGLU kernel applies the residual update and the norm itself
+    (``swiglu_mlp_residual_norm``: the MLP output never reaches memory) wherever it takes the
+    operands. ``stream`` holds x's rows (its last axis the norm's width)."""
+    if (then is not None and operand and x.is_cuda and then.weight is None and mlp.fuses(x)
+            and tuple(then.normalized_shape) == (int(stream.shape[-1]),)
+            and operand_dtype(stream) == torch.float16):
+        gate_up, _, down, hidden = mlp._stacked_weights(x, multiple=32)
+        y = swiglu_mlp_residual_norm(x.to(torch.float16), gate_up, down, hidden, stream, alpha, then.eps,
+                                     int(stream.shape[-1]), out=out)
+        if y is not None:
+            return y
+    return _accumulate(stream, mlp(x), alpha, then, operand=operand, out=out)
 
 
 def _row_vectors(targets: torch.Tensor) -> torch.Tensor:
@@ -331,17 +348,14 @@ class CellLayer2P(nn.Module):
             cell_operand = projection_operand(self.cell_norms[1], cells)
         if row_operand is None:
             row_operand = projection_operand(self.target_norms[1], rows)
-        cell_update = self.mlp[0](cell_operand)
-        del cell_operand
-        row_update = self.mlp[1](row_operand)
-        del row_operand
         # the two MLP updates, each with the feature attention's norm of its stream written
         # token by token into the attention's operand buffer
         b, n, g, w = cells.shape
         tokens = torch.empty((b, n, g + self.target_tokens, w), dtype=operand_dtype(cells), device=cells.device)
-        _accumulate(cells, cell_update, alpha, self.cell_norms[2], out=tokens[:, :, :g])
-        _accumulate(targets, row_update, alpha, self.target_norms[2], out=tokens[:, :, g:])
-        del cell_update, row_update
+        _mlp_accumulate(self.mlp[0], cell_operand, cells, alpha, self.cell_norms[2], out=tokens[:, :, :g])
+        del cell_operand
+        _mlp_accumulate(self.mlp[1], row_operand, targets, alpha, self.target_norms[2], out=tokens[:, :, g:])
+        del row_operand
         fa = self.feature_attention
         cell_out, readout = fa.attend(tokens, g)
         del tokens
@@ -402,7 +416,7 @@ class RowLayer2P(nn.Module):
         atten = attn.attend(query.unsqueeze(2), cell_memory).view(*rows.shape[:-1], attn.num_heads, attn.head_dim)
         del query
         mlp_in = _attend_accumulate(attn, atten, rows, alpha, self.mlp_norm)
-        return _accumulate(rows, self.mlp[0](mlp_in), alpha, then, operand=operand)
+        return _mlp_accumulate(self.mlp[0], mlp_in, rows, alpha, then, operand=operand)
 
 
 class TwoPhaseEncoder(nn.Module):

@@ -49,6 +49,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_linear_f16_residual_rms_norm",
             "nori_cell_tokens",
             "nori_layer_norm_cells",
+            "nori_swiglu_mlp_residual_rms_norm",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
         ]
@@ -172,6 +173,17 @@ def test_argument_errors_map_to_reference_exceptions():
     bad = list(lrn); bad[3] = 0
     assert lib.nori_linear_f16_residual_rms_norm(*bad) == nat.NORI_OK  # no rows: nothing to do
     assert lib.nori_linear_f16_residual_rms_norm(*lrn) == nat.NORI_ERR_INVALID  # null pointers
+    # SwiGLU + residual + norm: widths 128/128, 256/128, 256/256
+    sr = [None, nat.NORI_F16, 64, 128, 128, None, None, 256, 0.3, None, 128, 128, 1e-5, None, 1, 128, 128, None]
+    bad = list(sr); bad[11] = 64
+    assert lib.nori_swiglu_mlp_residual_rms_norm(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(sr); bad[1] = nat.NORI_BF16
+    assert lib.nori_swiglu_mlp_residual_rms_norm(*bad) == nat.NORI_ERR_UNSUPPORTED
+    bad = list(sr); bad[7] = 100
+    assert lib.nori_swiglu_mlp_residual_rms_norm(*bad) == nat.NORI_ERR_INVALID
+    bad = list(sr); bad[2] = 0
+    assert lib.nori_swiglu_mlp_residual_rms_norm(*bad) == nat.NORI_OK
+    assert lib.nori_swiglu_mlp_residual_rms_norm(*sr) == nat.NORI_ERR_INVALID  # null pointers
     # the cells' last LayerNorm with the positional and target-aware additions
     lc = [None, nat.NORI_F16, 2, 64, 4, 128, 128, None, None, 1e-5, None, None, 32, None, 0.088, None, None]
     bad = list(lc); bad[5] = 96

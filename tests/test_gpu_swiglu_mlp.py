@@ -150,3 +150,69 @@ def test_module_takes_the_fused_kernel_under_autocast():
     wide = nl.SwiGLUMLP(96, 288, 96, has_bias=False, device=DEV, dtype=torch.float32)
     with torch.inference_mode(), torch.autocast("cuda", dtype=torch.float16):
         assert wide(torch.randn(10, 96, device=DEV)).shape == (10, 96)
+
+
+# ---------------------------------------------------------------- with the residual update + norm
+# nori_swiglu_mlp_residual_rms_norm: the MLP, then stream += alpha * y and the next RMSNorm
+# (reference two_phase.py:209, 220-225, 271-272): bit for bit swiglu_mlp followed by the fused
+# residual + norm kernel (which the norm tests pin to torch), for every width / norm-width pair
+# it is built for, ragged row counts and an output that is a slice of a token buffer.
+
+ALPHA = 18 ** -0.5
+
+
+@pytest.mark.parametrize("width,norm_width,hidden", [(128, 128, 256), (256, 128, 682), (256, 256, 1024)])
+@pytest.mark.parametrize("rows", [1, 77, 5000])
+def test_residual_norm_epilogue_equals_the_separate_kernels(width, norm_width, hidden, rows):
+    from nori_amd.norm import RMSNorm, residual_add_norm, swiglu_mlp_residual_norm
+
+    gate_up, down, hp = _weights(width, hidden, seed=width + hidden + rows)
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    x = torch.randn(rows, width, generator=g, device=DEV).half()
+    stream = torch.randn(rows, width // norm_width, norm_width, generator=g, device=DEV) * 2.0
+    u = swiglu_mlp(x, gate_up, down, hp)
+    ref_stream = stream.clone()
+    ref = residual_add_norm(ref_stream, u.view(stream.shape), ALPHA, RMSNorm(norm_width, eps=1e-5),
+                            out_dtype=torch.float16)
+    got_stream = stream.clone()
+    got = swiglu_mlp_residual_norm(x, gate_up, down, hp, got_stream, ALPHA, 1e-5, norm_width)
+    assert got is not None and got.shape == stream.shape and got.dtype == torch.float16
+    assert torch.equal(got_stream, ref_stream)
+    assert torch.equal(got, ref)
+
+
+def test_residual_norm_epilogue_into_token_slices():
+    # the two-phase cell layer: the cells' MLP into the first 4 token slots of each row, the
+    # target row MLP (width 256, two 128-wide tokens) into the last 2
+    from nori_amd.norm import RMSNorm, residual_add_norm, swiglu_mlp_residual_norm
+
+    b, n, gr = 3, 700, 4
+    g = torch.Generator(device=DEV).manual_seed(5)
+    tokens = torch.full((b, n, gr + 2, 128), 7.0, dtype=torch.float16, device=DEV)
+    ref_tokens = tokens.clone()
+    cells = torch.randn(b, n, gr, 128, generator=g, device=DEV)
+    targets = torch.randn(b, n, 2, 128, generator=g, device=DEV)
+    xc = torch.randn(b, n, gr, 128, generator=g, device=DEV).half()
+    xt = torch.randn(b, n, 256, generator=g, device=DEV).half()
+    wc = _weights(128, 256, seed=1)
+    wt = _weights(256, 682, seed=2)
+    rc, rt = cells.clone(), targets.clone()
+    residual_add_norm(rc, swiglu_mlp(xc, *wc).view(rc.shape), ALPHA, RMSNorm(128, eps=1e-5), out=ref_tokens[:, :, :gr])
+    residual_add_norm(rt, swiglu_mlp(xt, *wt).view(rt.shape), ALPHA, RMSNorm(128, eps=1e-5), out=ref_tokens[:, :, gr:])
+    assert swiglu_mlp_residual_norm(xc, *wc, cells, ALPHA, 1e-5, 128, out=tokens[:, :, :gr]) is not None
+    assert swiglu_mlp_residual_norm(xt, *wt, targets, ALPHA, 1e-5, 128, out=tokens[:, :, gr:]) is not None
+    assert torch.equal(cells, rc) and torch.equal(targets, rt)
+    assert torch.equal(tokens, ref_tokens)
+
+
+def test_residual_norm_epilogue_declines_what_it_does_not_take():
+    from nori_amd.norm import swiglu_mlp_residual_norm
+
+    gate_up, down, hp = _weights(352, 1056, seed=3)
+    x = torch.randn(64, 352, device=DEV).half()
+    stream = torch.randn(64, 352, device=DEV)
+    assert swiglu_mlp_residual_norm(x, gate_up, down, hp, stream, ALPHA, 1e-5, 352) is None  # width 352
+    gate_up, down, hp = _weights(128, 256, seed=4)
+    x = torch.randn(64, 128, device=DEV).half()
+    assert swiglu_mlp_residual_norm(x, gate_up, down, hp, torch.randn(64, 128, device=DEV).half(), ALPHA, 1e-5,
+                                    128) is None  # fp16 stream
