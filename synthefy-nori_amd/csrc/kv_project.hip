@@ -228,7 +228,7 @@ __device__ __forceinline__ void row_coords(int64_t o0, int64_t i0, int off, int6
 }
 
 template <int NR, int KS, int MT>
-__global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const ProjArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) kv_project_quantize_kernel(const ProjArgs a) {
     extern __shared__ __attribute__((aligned(16))) _Float16 wt[];  // [hg*dp][xp]
 
     // work: XCD-aware numbering, the head groups of a stream consecutive within one XCD
@@ -249,14 +249,16 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
     __syncthreads();
 
     const _Float16* wa = wt + (lane & 15) * a.xp + 8 * g;  // A operand rows of tile 0 of head 0
-    for (int64_t rb = stream; rb < a.nblocks; rb += a.streams) {
+    // columns of the last tile past d are the heads' zero padding rows: left out of the absmax
+    bool pad_ok[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pad_ok[q] = 16 * (MT - 1) + 4 * g + q < a.d;
+
+    // ---- operand rows of block rb for this wavefront -> B operands; their code and scale row
+    // offsets. Lanes of rows past the last read the last row and store nothing.
+    auto load_rows = [&](int64_t rb, f16x8 (&xf)[NR][KS], int64_t (&c_off)[NR], int64_t (&s_off)[NR]) {
         const int64_t r0 = rb * a.bm;
         const int64_t o0 = r0 / a.grid.n_inner, i0 = r0 - o0 * a.grid.n_inner;
-
-        // ---- operand rows of this wavefront -> B operands; their code and scale row offsets.
-        // Lanes of rows past the last read the last row and store nothing.
-        f16x8 xf[NR][KS];
-        int64_t c_off[NR], s_off[NR];
 #pragma unroll
         for (int nt = 0; nt < NR; ++nt) {
             const int off0 = (wave * NR + nt) * 16 + (lane & 15);
@@ -270,7 +272,10 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
             for (int ks = 0; ks < KS; ++ks)
                 xf[nt][ks] = ks < a.ksteps ? *reinterpret_cast<const f16x8*>(xrow + 32 * ks) : f16x8{};
         }
+    };
 
+    // ---- every head of the group on one block's operand rows
+    auto do_heads = [&](const f16x8 (&xf)[NR][KS], const int64_t (&c_off)[NR], const int64_t (&s_off)[NR]) {
         for (int hh = 0; hh < ghe; ++hh) {
             // ---- projection of the head: MT column tiles x NR row tiles
             f32x4 acc[MT][NR];
@@ -309,11 +314,17 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         hv[m][q] = f32_to_f16(acc[m][nt][q]);
-                        if (16 * m + 4 * g + q < a.d) key = max(key, abs_key<NORI_F16>(hv[m][q]));
+                        const uint32_t k = abs_key<NORI_F16>(hv[m][q]);
+                        key = max(key, m < MT - 1 || pad_ok[q] ? k : 0u);
                     }
                 }
-                key = max(key, (uint32_t)__shfl_xor((int)key, 16));
-                key = max(key, (uint32_t)__shfl_xor((int)key, 32));
+                // the row's 4 lanes (lane ^ 16, lane ^ 32): lane swaps on the VALU
+                {
+                    const auto s16 = __builtin_amdgcn_permlane16_swap(key, key, false, false);
+                    key = max(s16[0], s16[1]);
+                    const auto s32 = __builtin_amdgcn_permlane32_swap(key, key, false, false);
+                    key = max(s32[0], s32[1]);
+                }
                 const VectorScale vs = make_scale<NORI_F16>(key, a.scale_div);
                 uint32_t words[MT];
 #pragma unroll
@@ -347,6 +358,26 @@ __global__ void __launch_bounds__(kThreads) kv_project_quantize_kernel(const Pro
                 }
             }
         }
+    };
+
+    // blocks stream, stream + streams, ...: the next block's operand rows load while this
+    // block's heads compute (two register sets, used in turn)
+    int64_t rb = stream;
+    if (rb >= a.nblocks) return;
+    f16x8 xa[NR][KS], xb[NR][KS];
+    int64_t ca[NR], sa[NR], cb[NR], sb[NR];
+    load_rows(rb, xa, ca, sa);
+    for (;;) {
+        int64_t nb = rb + a.streams;
+        if (nb < a.nblocks) load_rows(nb, xb, cb, sb);
+        do_heads(xa, ca, sa);
+        if (nb >= a.nblocks) break;
+        rb = nb;
+        nb = rb + a.streams;
+        if (nb < a.nblocks) load_rows(nb, xa, ca, sa);
+        do_heads(xb, cb, sb);
+        if (nb >= a.nblocks) break;
+        rb = nb;
     }
 }
 
@@ -380,7 +411,7 @@ int padded_tiles(int d) {
 
 // operand steps the kernel holds in registers (KS >= ksteps; the steps past ksteps are zero)
 int padded_steps(int ksteps) {
-    for (int k : {4, 8, 12, 16, 24}) if (ksteps <= k) return k;
+    for (int k : {4, 8, 11, 12, 16, 24}) if (ksteps <= k) return k;
     return 32;
 }
 
@@ -394,6 +425,7 @@ int launch(ProjArgs& a, int kpad, size_t lds, hipStream_t stream) {
     switch (kpad) {
         case 4: return launch_mt<2, 4>(a, lds, stream);
         case 8: return launch_mt<2, 8>(a, lds, stream);
+        case 11: return launch_mt<2, 11>(a, lds, stream);
         case 12: return launch_mt<2, 12>(a, lds, stream);
         case 16: return launch_mt<2, 16>(a, lds, stream);
         case 24: return launch_mt<1, 24>(a, lds, stream);
