@@ -54,8 +54,9 @@ typedef enum {
 
 /* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
  * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens,
- * nori_layer_norm_cells, nori_swiglu_mlp_residual_rms_norm and the MFMA probe added). */
-#define NORI_ABI_VERSION 2
+ * nori_layer_norm_cells, nori_swiglu_mlp_residual_rms_norm and the MFMA probe added; 3:
+ * nori_quant_f16_scale_probe added). */
+#define NORI_ABI_VERSION 3
 int nori_abi_version(void);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
@@ -471,6 +472,15 @@ int nori_cell_tokens(const float* x, int64_t tables, int64_t rows, int32_t group
 int nori_mfma_f16_probe(const void* operands, int64_t n_vec, int32_t iters, float* sink, int64_t sink_len,
                         void* stream);
 int64_t nori_mfma_f16_probe_flop(int64_t iters);
+
+/* The scale and reciprocal the fused cache write (nori_kv_project_quantize_int8) derives from an
+ * f16 head vector's absmax, without a division: s = f16(|absmax| * RN(1/127)) and
+ * y = rcp(s) refined by one Newton step, for n f16 absmax values (their sign is ignored) into
+ * s[n] and y[n] (fp32). A check hook with no counterpart in the reference: it lets a test hold
+ * s to f16(|absmax| / 127) (quantize_int8, src/synthefy_nori/model/kv_cache_scaling.py:29-37)
+ * and y to the correctly rounded 1/s over every f16 value, the premise of the fused write's
+ * exact quotients. n at most 2^30. */
+int nori_quant_f16_scale_probe(const uint16_t* absmax, int64_t n, float* s, float* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,10 +16,10 @@
 //   one wavefront per row normalizes it and writes f16(xn) to a workspace row padded with
 //   zeros to a multiple of 32 -- the cast the autocast path makes before its GEMM, with the
 //   norm folded in.
-// * projection + quantizer: persistent workgroups of 4 wavefronts, two per CU. A workgroup
+// * projection + quantizer: persistent workgroups of 8 wavefronts, two per CU. A workgroup
 //   owns a group of `hg` cache heads: their weight rows, each head padded with zero rows to
-//   16 * MT, stay in LDS as f16 for the whole launch. It walks blocks of 4 * 16 * NR rows;
-//   each wavefront loads its 16 * NR operand rows straight into v_mfma_f32_16x16x32_f16 B
+//   16 * MT, stay in LDS as f16 for the whole launch. It walks blocks of 8 * 16 * NR rows
+//   (NR = 1); each wavefront loads its 16 * NR operand rows straight into v_mfma_f32_16x16x32_f16 B
 //   operands (lane n + 16*(k/8) holds row n, elements 8*(k/8)..+8 of every 32-wide step).
 //   Per head, the MFMAs compute the transposed projection W_j . x^T, whose result layout gives
 //   every lane four consecutive K/V columns of one row: the head's absmax is a per-lane max and
@@ -39,7 +39,7 @@ namespace {
 using namespace nori;
 using namespace nori::quant;
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kWgPerCu = 2;  // resident workgroups per CU when the weight tile fits half the LDS
 constexpr size_t kLds = 160 * 1024;
@@ -325,7 +325,7 @@ __global__ void __launch_bounds__(kThreads, 2) kv_project_quantize_kernel(const 
                     const auto s32 = __builtin_amdgcn_permlane32_swap(key, key, false, false);
                     key = max(s32[0], s32[1]);
                 }
-                const VectorScale vs = make_scale<NORI_F16>(key, a.scale_div);
+                const VectorScale vs = make_scale_f16_fast(key);  // both scale_div modes
                 uint32_t words[MT];
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
@@ -415,19 +415,19 @@ int padded_steps(int ksteps) {
     return 32;
 }
 
-// 16 * NR rows per wavefront
+// 16 rows per wavefront (one row tile: eight wavefronts, four per SIMD across the two
+// workgroups of a CU, hide the per-head chain better than four wavefronts of two tiles)
 int launch(ProjArgs& a, int kpad, size_t lds, hipStream_t stream) {
-    const int nr = kpad <= 16 ? 2 : 1;
-    a.bm = kWaves * 16 * nr;
+    a.bm = kWaves * 16;
     a.nblocks = (a.grid.rows + a.bm - 1) / a.bm;
     const int64_t slots = (int64_t)device_cus() * (lds <= kLds / kWgPerCu ? kWgPerCu : 1);
     a.streams = (int)std::max<int64_t>(1, std::min<int64_t>(a.nblocks, slots / a.ngroups));
     switch (kpad) {
-        case 4: return launch_mt<2, 4>(a, lds, stream);
-        case 8: return launch_mt<2, 8>(a, lds, stream);
-        case 11: return launch_mt<2, 11>(a, lds, stream);
-        case 12: return launch_mt<2, 12>(a, lds, stream);
-        case 16: return launch_mt<2, 16>(a, lds, stream);
+        case 4: return launch_mt<1, 4>(a, lds, stream);
+        case 8: return launch_mt<1, 8>(a, lds, stream);
+        case 11: return launch_mt<1, 11>(a, lds, stream);
+        case 12: return launch_mt<1, 12>(a, lds, stream);
+        case 16: return launch_mt<1, 16>(a, lds, stream);
         case 24: return launch_mt<1, 24>(a, lds, stream);
         default: return launch_mt<1, 32>(a, lds, stream);
     }
@@ -528,4 +528,27 @@ extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t
     a.ngroups = (a.nheads + hg_max - 1) / hg_max;
     a.hg = (a.nheads + a.ngroups - 1) / a.ngroups;
     return launch(a, kpad, (size_t)a.hg * head_bytes, stream);
+}
+
+namespace {
+
+__global__ void __launch_bounds__(256) f16_scale_probe_kernel(const uint16_t* absmax, int64_t n, float* s, float* y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const VectorScale vs = make_scale_f16_fast(abs_key<NORI_F16>(absmax[i]));
+    s[i] = vs.s;
+    y[i] = vs.y;
+}
+
+}  // namespace
+
+extern "C" int nori_quant_f16_scale_probe(const uint16_t* absmax, int64_t n, float* s, float* y, void* stream) {
+    clear_error();
+    if (n < 0 || n > ((int64_t)1 << 30))
+        return fail(NORI_ERR_INVALID, "quant_f16_scale_probe: n=%lld outside [0, 2^30]", (long long)n);
+    if (n == 0) return NORI_OK;
+    if (!absmax || !s || !y) return fail(NORI_ERR_INVALID, "quant_f16_scale_probe: null pointer");
+    hipLaunchKernelGGL(f16_scale_probe_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       absmax, n, s, y);
+    return launch_status("quant_f16_scale_probe");
 }

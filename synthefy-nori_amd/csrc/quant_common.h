@@ -39,6 +39,15 @@ __device__ __forceinline__ uint32_t abs_key(typename Storage<DT>::T b) {
     else return (uint32_t)b & 0x7fffu;
 }
 
+// Scales the fast quotient and packing take. Outside [2^-96, 2^96] the residual fma(-q0, s, t)
+// may be subnormal and inexact. An f16 scale must also be normal (>= 2^-14): a subnormal one is
+// rounded with a relative error up to 1/2, so |t/s| can pass 127 (absmax 190 * 2^-24 gives
+// s = 2^-24 and quotients up to 190), and only the exact path clamps.
+template <int DT>
+__device__ __forceinline__ bool fast_scale(float s) {
+    return s >= (DT == NORI_F16 ? 0x1p-14f : 0x1p-96f) && s <= 0x1p96f;
+}
+
 struct VectorScale {
     float s;     // scale in T, widened to fp32
     float y;     // RN(1/s)
@@ -56,8 +65,22 @@ __device__ __forceinline__ VectorScale make_scale(uint32_t max_key, int scale_di
     VectorScale vs;
     vs.s = s;
     vs.y = 1.0f / s;
-    // Outside [2^-96, 2^96] the residual fma(-q0, s, t) may be subnormal and inexact.
-    vs.fast = s >= 0x1p-96f && s <= 0x1p96f;
+    vs.fast = fast_scale<DT>(s);
+    return vs;
+}
+
+// The scale of an f16 vector from its absmax key, without a division: f16(m * RN(1/127)) equals
+// f16(m / 127) for every f16 m (an exhaustive check over the f16 values: the exact quotient m/127
+// is never within the products' rounding error of an f16 rounding boundary), so both scale_div
+// modes give it; y = RN(1/s) from the hardware reciprocal and one Newton step (equal to the
+// correctly rounded reciprocal for every positive f16 s: nori_quant_f16_scale_probe).
+__device__ __forceinline__ VectorScale make_scale_f16_fast(uint32_t max_key) {
+    const float m = bits_to_f32<NORI_F16>((uint16_t)max_key);
+    VectorScale vs;
+    vs.s = round_to<NORI_F16>(m * (1.0f / 127.0f));
+    const float y0 = __builtin_amdgcn_rcpf(vs.s);
+    vs.y = fmaf(fmaf(-vs.s, y0, 1.0f), y0, y0);
+    vs.fast = fast_scale<NORI_F16>(vs.s);
     return vs;
 }
 
@@ -84,7 +107,8 @@ __device__ __forceinline__ int code_of(float t, const VectorScale& vs) {
 // word (element 0 in the low byte): rint(RN_T(q)) without a float -> int conversion. For fp16,
 // adding 1536 in fp16 rounds to an integer (the spacing in [1024, 2048) is 1, ties to even)
 // and leaves the code in the low byte of the result; |t| <= amax bounds |q| by 127 * (1 + 2^-11)
-// for fp16 and fp32 sources, so only bf16 (scale rounded to 8 bits) needs a clamp.
+// for fp16 (normal scales: fast_scale) and fp32 sources, so only bf16 (scale rounded to 8 bits)
+// needs a clamp.
 template <int DT>
 __device__ __forceinline__ uint32_t pack_codes_fast(const float (&q)[4]) {
     if constexpr (DT == NORI_F16) {

@@ -19,7 +19,7 @@ NORI_F32, NORI_F16, NORI_BF16, NORI_I8 = range(4)
 SCALE_DIV_TRUE, SCALE_DIV_RECIP = 0, 1
 ATTN_MERGE = 1
 NOALLOC_SCRATCH_BYTES = 32 << 20  # NORI_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 2  # NORI_ABI_VERSION: the signatures below
+ABI_VERSION = 3  # NORI_ABI_VERSION: the signatures below
 
 _DTYPE_CODES = {
     torch.float32: NORI_F32,
@@ -110,6 +110,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     ),
     "nori_mfma_f16_probe": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _vp]),
     "nori_mfma_f16_probe_flop": (_i64, [_i64]),
+    "nori_quant_f16_scale_probe": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -52,6 +52,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_swiglu_mlp_residual_rms_norm",
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
+            "nori_quant_f16_scale_probe",
         ]
     )
 
@@ -63,7 +64,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
     assert set(declared_symbols()) == set(_native.SIGNATURES)
-    assert _native.lib().nori_abi_version() == _native.ABI_VERSION == 2
+    assert _native.lib().nori_abi_version() == _native.ABI_VERSION == 3
 
 
 def test_argument_errors_map_to_reference_exceptions():
@@ -210,6 +211,10 @@ def test_argument_errors_map_to_reference_exceptions():
     # the MFMA rate probe (measurement only): operands, a sink and iterations are required
     assert lib.nori_mfma_f16_probe(None, 0, 1, None, 0, None) == nat.NORI_ERR_INVALID
     assert b"mfma_f16_probe" in lib.nori_last_error()
+    # the scale probe: no values is no work; values need device pointers
+    assert lib.nori_quant_f16_scale_probe(None, 0, None, None, None) == nat.NORI_OK
+    assert lib.nori_quant_f16_scale_probe(None, 4, None, None, None) == nat.NORI_ERR_INVALID
+    assert lib.nori_quant_f16_scale_probe(None, -1, None, None, None) == nat.NORI_ERR_INVALID
     # empty inputs are a no-op, not an error
     assert lib.nori_kv_quantize_int8(None, nat.NORI_F16, 0, 5, 8, 0, 8, None, 0, 8, None, 0, 1, 1, None) == nat.NORI_OK
     assert lib.nori_rms_norm(None, nat.NORI_F16, 0, 128, 128, None, nat.NORI_F16, 1e-5, None, 128, None) == nat.NORI_OK

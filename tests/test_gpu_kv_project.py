@@ -164,6 +164,63 @@ def test_special_rows(cuda):
     assert torch.equal(one_q, codes[2:]) and torch.equal(one_s, scales[2:])
 
 
+def test_scale_and_reciprocal_over_every_f16_value(cuda):
+    """The fused write's scale and reciprocal (nori_quant_f16_scale_probe) for all 65536 f16 bit
+    patterns: s = f16(|m| / 127), the reference's scale (numpy's correctly rounded fp32 quotient,
+    then f16), and y = the correctly rounded 1/s wherever the fast quotient uses it."""
+    from nori_amd import _native as nat
+
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(cuda)
+    s = torch.empty(65536, device=cuda)
+    y = torch.empty(65536, device=cuda)
+    nat.check(nat.lib().nori_quant_f16_scale_probe(bits.data_ptr(), 65536, s.data_ptr(), y.data_ptr(),
+                                                   nat.stream_of(cuda)), "quant_f16_scale_probe")
+    m = np.abs(np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        s_ref = (m / np.float32(127)).astype(np.float16).astype(np.float32)
+        y_ref = np.float32(1) / s_ref
+    s, y = s.cpu().numpy(), y.cpu().numpy()
+    nan = np.isnan(s_ref)
+    assert np.array_equal(np.isnan(s), nan) and np.array_equal(s[~nan], s_ref[~nan])
+    fast = (s_ref >= 2.0 ** -96) & (s_ref <= 2.0 ** 96)
+    # every nonzero finite scale (absmax below 63.5 f16 subnormal steps gives scale 0)
+    assert np.array_equal(fast, np.isfinite(s_ref) & (s_ref > 0)) and fast.sum() > 60000
+    assert np.array_equal(y[fast].view(np.uint32), y_ref[fast].view(np.uint32))
+
+
+def test_every_f16_scale_codes_equal_the_exact_quantizer(cuda):
+    """Identity weights make the K/V the operand values themselves (kv = x exactly), so each head
+    vector's absmax can be chosen: every positive finite f16 value once, the other 43 values
+    uniform in [-absmax, absmax] in f16. The fused write's codes and scales, and the HIP
+    quantizer's on the same K/V, equal the reference expression on the same device (absmax below
+    127 * 2^-14 gives a subnormal f16 scale, and quotients past 127 that only clamping brings
+    back: absmax 128 * 2^-24 has scale 2^-24 and code 127, not -128)."""
+    heads, d, embed = 8, 44, 352
+    amax = torch.arange(1, 0x7C00, dtype=torch.int32).to(torch.int16).view(torch.float16).float()
+    nv = amax.numel() + (-amax.numel()) % 8
+    amax = torch.cat((amax, torch.ones(nv - amax.numel())))
+    g = torch.Generator().manual_seed(5)
+    vecs = (torch.rand(nv, d, generator=g) * 2 - 1) * amax[:, None]
+    vecs[:, 0] = amax * torch.where(torch.rand(nv, generator=g) < 0.5, -1.0, 1.0)
+    vecs = torch.gather(vecs, 1, torch.argsort(torch.rand(nv, d, generator=g), dim=1)).half()
+    x = vecs.view(nv // 8, embed).to(cuda)
+    w = torch.cat((torch.eye(embed), torch.eye(embed))).to(cuda)
+    codes, scales = nori_amd.project_quantize_kv(x, w, heads, d)
+    kv = torch.cat((x, x), dim=-1).view(nv // 8, 2, heads, d)
+    ref_q, ref_s = torch_quantize(kv)
+    bad = (codes != ref_q).any(-1).flatten().nonzero().flatten().cpu()
+    if bad.numel():
+        v = bad[:4]
+        flat = kv.reshape(-1, d).cpu()
+        detail = [(float(flat[i].abs().max()), float(scales.flatten()[i]), float(ref_s.flatten()[i]),
+                   codes.reshape(-1, d)[i].cpu().tolist(), ref_q.reshape(-1, d)[i].cpu().tolist(),
+                   flat[i].tolist()) for i in v.tolist()]
+        raise AssertionError(f"{bad.numel()} head vectors differ; first: {detail}")
+    assert torch.equal(scales, ref_s)
+    hip_q, hip_s = nori_amd.quantize_int8(kv)
+    assert torch.equal(hip_q, ref_q) and torch.equal(hip_s.view_as(ref_s), ref_s)
+
+
 def test_large_row_count(cuda):
     # nori-30m's cross-cache write for one layer at a 64k context: 33 groups x 65536 rows of
     # E = 352 into 2 x 8 heads of 44; compared with the autocast path on a row sample
