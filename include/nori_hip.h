@@ -55,7 +55,7 @@ typedef enum {
 /* Version of this ABI (bumped on any signature change; 2: nori_icl_attention_takes_prologue takes
  * the query dtype; nori_linear_f16, nori_linear_f16_residual_rms_norm, nori_cell_tokens,
  * nori_layer_norm_cells, nori_swiglu_mlp_residual_rms_norm and the MFMA probe added; 3:
- * nori_quant_f16_scale_probe added). */
+ * nori_quant_f16_scale_probe and nori_kv_project_quantize_int8_workspace_bytes added). */
 #define NORI_ABI_VERSION 3
 int nori_abi_version(void);
 
@@ -321,7 +321,10 @@ int nori_icl_attention_qk(const void* q, int q_dtype, int64_t bg, int64_t nq, in
  * Rows of x and weight must be 16-byte aligned and a whole number of 16-byte chunks; code
  * rows 4-byte aligned; d a multiple of 4 up to 128; embed at most 1024. The fp16 K/V are never
  * written.
- * workspace: see nori_kv_project_quantize_int8_workspace_size.
+ * workspace: see nori_kv_project_quantize_int8_workspace_bytes. fp32 x with fp16 weight rows,
+ * embed a multiple of 8 up to 384 and d up to 64 (nori-30m: 352, 44) take one pass with no
+ * workspace (each row read and normalized once, every head in one workgroup); other cases
+ * write the f16 operand rows to the workspace first.
  * The projection's fp32 sums run in MFMA order, not the library GEMM's, so a K/V value can
  * differ from torch's fp16 F.linear in its last bit and its code by one.
  */
@@ -337,6 +340,11 @@ int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t n_outer, i
  * norm, embed a multiple of 32). Written and read within the call's stream order. */
 int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_outer, int64_t n_inner, int32_t embed,
                                                      int32_t norm);
+/* The workspace one nori_kv_project_quantize_int8 call with these arguments needs: 0 where it
+ * takes the one pass (fp32 x, fp16 weight, embed a multiple of 8 up to 384, d up to 64), else
+ * nori_kv_project_quantize_int8_workspace_size. */
+int64_t nori_kv_project_quantize_int8_workspace_bytes(int x_dtype, int64_t n_outer, int64_t n_inner, int32_t embed,
+                                                      int32_t norm, int weight_dtype, int32_t d);
 
 /*
  * 1 when nori_icl_attention_qk takes a prologue for these sizes, cache dtype and query dtype

@@ -438,6 +438,226 @@ bool direct_operands(int x_dtype, int32_t embed, int32_t norm) {
     return x_dtype == NORI_F16 && !norm && embed % 32 == 0;
 }
 
+// ------------------------------------------------------------------ one pass from fp32 rows
+// Every head of a row block in one workgroup: each fp32 row is read and normalized once, in
+// the registers that feed the MFMAs, and the f16 weights stream through LDS one head at a time
+// (two tile buffers: the next head's tile loads while this head computes). No operand-row pass
+// and no workspace; each 704-byte code row is written by one workgroup.
+struct RowsArgs {
+    const float* x; Grid grid; int64_t x_outer, x_row;  // fp32 rows (elements)
+    int norm; float eps;
+    const _Float16* w; int64_t w_stride;  // f16 W [nheads * d, embed] (row stride in elements)
+    int embed, nheads, d;
+    int8_t* codes; int64_t codes_outer, codes_row;
+    float* scales; int64_t scales_outer, scales_row;
+    int64_t nblocks;  // blocks of kWaves * 16 rows
+};
+
+template <int KS, int MT>
+__global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) {
+    constexpr int XP = 32 * KS + 8;  // LDS pitch of a weight row (f16): +16 bytes spreads the 16-row reads
+    constexpr int DP = 16 * MT;      // weight rows per head tile, zero past d
+    constexpr int CPR = 4 * KS;      // 16-byte chunks of a padded weight row
+    constexpr int TILE = DP * XP;    // f16 per tile buffer
+    constexpr int WCH = (DP * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
+    extern __shared__ __attribute__((aligned(16))) _Float16 wt[];  // [2][DP][XP]
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4;  // result lanes hold columns 4g..4g+3 of each 16-column tile
+
+    // head h's weight rows, f16, zero past d and past embed, as 16-byte chunks of this thread
+    auto load_tile = [&](int h, uint4 (&wr)[WCH]) {
+#pragma unroll
+        for (int u = 0; u < WCH; ++u) {
+            const int c = tid + kThreads * u;
+            const int row = c / CPR, col = c - row * CPR;
+            const bool valid = c < DP * CPR && row < a.d && col * 8 < a.embed;
+            wr[u] = valid ? *reinterpret_cast<const uint4*>(a.w + (int64_t)(h * a.d + row) * a.w_stride + col * 8)
+                          : uint4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_tile = [&](int buf, const uint4 (&wr)[WCH]) {
+#pragma unroll
+        for (int u = 0; u < WCH; ++u) {
+            const int c = tid + kThreads * u;
+            const int row = c / CPR, col = c - row * CPR;
+            if (c < DP * CPR) *reinterpret_cast<uint4*>(wt + buf * TILE + row * XP + col * 8) = wr[u];
+        }
+    };
+
+    int64_t rb = blockIdx.x;
+    if (rb >= a.nblocks) return;  // whole workgroup
+    uint4 wr[WCH];
+    load_tile(0, wr);
+    store_tile(0, wr);
+    __syncthreads();
+    int buf = 0;  // the buffer holding the current head's tile
+
+    const _Float16* wa = wt + (lane & 15) * XP + 8 * g;  // A operand rows of tile 0
+    bool pad_ok[4];  // columns of the last tile past d are zero padding: left out of the absmax
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pad_ok[q] = 16 * (MT - 1) + 4 * g + q < a.d;
+
+    for (; rb < a.nblocks; rb += gridDim.x) {
+        // ---- this wavefront's 16 rows: lane n + 16 g holds row n's elements 32 ks + 8 g + [0, 8)
+        const int64_t r = rb * (kWaves * 16) + wave * 16 + (lane & 15);
+        const bool valid = r < a.grid.rows;
+        const int64_t rr = valid ? r : a.grid.rows - 1;  // rows past the last read the last, store nothing
+        const int64_t o = rr / a.grid.n_inner, i = rr - o * a.grid.n_inner;
+        const float* xrow = a.x + o * a.x_outer + i * a.x_row + 8 * g;
+        const int64_t c_off = valid ? o * a.codes_outer + i * a.codes_row : -1;
+        const int64_t s_off = valid ? o * a.scales_outer + i * a.scales_row : -1;
+        f16x8 xf[KS];
+        {
+            f32x4 v[KS][2];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const bool in = 32 * ks + 8 * g < a.embed;  // embed is a multiple of 8
+                v[ks][0] = in ? *reinterpret_cast<const f32x4*>(xrow + 32 * ks) : f32x4{0.f, 0.f, 0.f, 0.f};
+                v[ks][1] = in ? *reinterpret_cast<const f32x4*>(xrow + 32 * ks + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            float inv = 1.0f;
+            if (a.norm) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ss = fmaf(v[ks][h][e], v[ks][h][e], ss);
+                // the row's four lanes (lane ^ 16, lane ^ 32)
+                const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+                ss = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+                const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+                ss = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+                inv = rsqrtf(ss / (float)a.embed + a.eps);
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                f16x8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (_Float16)pin_f32(v[ks][e >> 2][e & 3] * inv);
+                xf[ks] = h;
+            }
+        }
+
+        for (int hd = 0; hd < a.nheads; ++hd) {
+            // the next tile: this block's next head, or the next block's first
+            const bool more = hd + 1 < a.nheads || rb + gridDim.x < a.nblocks;
+            if (more) load_tile(hd + 1 < a.nheads ? hd + 1 : 0, wr);
+
+            f32x4 acc[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const _Float16* wh = wa + buf * TILE;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(wh + 16 * m * XP + 32 * ks);
+                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xf[ks], acc[m], 0, 0, 0);
+                }
+            }
+
+            // ---- quantize: lane holds columns 16m + 4g + [0, 4) of row (lane & 15)
+            uint16_t hv[MT][4];
+            uint32_t key = 0;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    hv[m][q] = f32_to_f16(acc[m][q]);
+                    const uint32_t k = abs_key<NORI_F16>(hv[m][q]);
+                    key = max(key, m < MT - 1 || pad_ok[q] ? k : 0u);
+                }
+            }
+            {
+                const auto s16 = __builtin_amdgcn_permlane16_swap(key, key, false, false);
+                key = max(s16[0], s16[1]);
+                const auto s32 = __builtin_amdgcn_permlane32_swap(key, key, false, false);
+                key = max(s32[0], s32[1]);
+            }
+            const VectorScale vs = make_scale_f16_fast(key);  // both scale_div modes
+            uint32_t words[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float q[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // the correctly rounded quotient t/s (Markstein)
+                    const float t = f16_to_f32(hv[m][e]);
+                    const float q0 = t * vs.y;
+                    q[e] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
+                }
+                words[m] = pack_codes_fast<NORI_F16>(q);
+            }
+            // scales outside the fast quotient's range: recode exactly, on a wave-uniform branch
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!vs.fast) != 0, 0)) {
+                if (!vs.fast) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+                        words[m] = pack4(code_of<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][1]), vs),
+                                         code_of<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][3]), vs));
+                }
+            }
+            if (c_off >= 0) {
+                int8_t* crow = a.codes + c_off + (int64_t)hd * a.d;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (16 * m + 4 * g < a.d) *reinterpret_cast<uint32_t*>(crow + 16 * m + 4 * g) = words[m];
+                if (g == 0) a.scales[s_off + hd] = vs.s;
+            }
+
+            if (more) store_tile(buf ^ 1, wr);
+            __syncthreads();  // the next tile is in place; every wave is done with this one
+            buf ^= 1;
+        }
+    }
+}
+
+template <int KS, int MT>
+int launch_rows_with(const RowsArgs& a, hipStream_t stream) {
+    const size_t lds = (size_t)2 * 16 * MT * (32 * KS + 8) * 2;
+    if (hipFuncSetAttribute((const void*)kv_rows_kernel<KS, MT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+        hipSuccess)
+        return fail(NORI_ERR_RUNTIME, "kv_project_quantize_int8: cannot reserve %zu bytes of LDS", lds);
+    const int64_t slots = (int64_t)device_cus() * kWgPerCu;
+    const dim3 grid((unsigned)std::min<int64_t>(a.nblocks, slots));
+    hipLaunchKernelGGL((kv_rows_kernel<KS, MT>), grid, dim3(kThreads), lds, stream, a);
+    return launch_status("kv_project_quantize_int8 (one pass)");
+}
+
+// The one-pass kernel takes fp32 rows with f16 weights, embed a multiple of 8 up to 384 (the
+// row's fp32 values are held in registers while the norm is taken) and two head tiles within
+// half the LDS (two workgroups per CU).
+bool one_pass(int x_dtype, int weight_dtype, int32_t embed, int32_t d) {
+    if (x_dtype != NORI_F32 || weight_dtype != NORI_F16 || embed % 8 || embed > 384 || d > 64) return false;
+    const int kpad = padded_steps((embed + 31) / 32);
+    const int mt = padded_tiles(d);
+    return (size_t)2 * 16 * mt * (32 * kpad + 8) * 2 <= kLds / kWgPerCu;
+}
+
+int launch_rows(RowsArgs& a, hipStream_t stream) {
+    a.nblocks = (a.grid.rows + kWaves * 16 - 1) / (kWaves * 16);
+    const int kpad = padded_steps((a.embed + 31) / 32);
+    const int mt = padded_tiles(a.d);
+#define NORI_ROWS_MT(KS_)                                          \
+    switch (mt) {                                                  \
+        case 1: return launch_rows_with<KS_, 1>(a, stream);        \
+        case 2: return launch_rows_with<KS_, 2>(a, stream);        \
+        case 3: return launch_rows_with<KS_, 3>(a, stream);        \
+        default: return launch_rows_with<KS_, 4>(a, stream);       \
+    }
+    switch (kpad) {
+        case 4: NORI_ROWS_MT(4)
+        case 8: NORI_ROWS_MT(8)
+        case 11: NORI_ROWS_MT(11)
+        default: NORI_ROWS_MT(12)
+    }
+#undef NORI_ROWS_MT
+}
+
+
 }  // namespace
 
 extern "C" int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int64_t n_outer, int64_t n_inner,
@@ -445,6 +665,13 @@ extern "C" int64_t nori_kv_project_quantize_int8_workspace_size(int x_dtype, int
     if (n_outer <= 0 || n_inner <= 0 || embed <= 0 || direct_operands(x_dtype, embed, norm)) return 0;
     if (n_inner > INT64_MAX / n_outer) return 0;
     return n_outer * n_inner * (int64_t)((embed + 31) / 32 * 32) * 2;
+}
+
+extern "C" int64_t nori_kv_project_quantize_int8_workspace_bytes(int x_dtype, int64_t n_outer, int64_t n_inner,
+                                                                int32_t embed, int32_t norm, int weight_dtype,
+                                                                int32_t d) {
+    if (one_pass(x_dtype, weight_dtype, embed, d)) return 0;
+    return nori_kv_project_quantize_int8_workspace_size(x_dtype, n_outer, n_inner, embed, norm);
 }
 
 extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t n_outer, int64_t n_inner,
@@ -483,14 +710,24 @@ extern "C" int nori_kv_project_quantize_int8(const void* x, int x_dtype, int64_t
                     "kv_project_quantize_int8: x and weight rows must be 16-byte aligned whole 16-byte chunks");
     if ((uintptr_t)codes % 4 || codes_row_stride % 4 || codes_outer_stride % 4)
         return fail(NORI_ERR_UNSUPPORTED, "kv_project_quantize_int8: code rows must be 4-byte aligned");
+    const Grid grid{n_outer * n_inner, n_inner};
+    hipStream_t stream = (hipStream_t)stream_v;
+    if (one_pass(x_dtype, weight_dtype, embed, d)) {
+        RowsArgs r;
+        r.x = reinterpret_cast<const float*>(x); r.grid = grid; r.x_outer = x_outer_stride; r.x_row = x_row_stride;
+        r.norm = norm; r.eps = eps;
+        r.w = reinterpret_cast<const _Float16*>(weight); r.w_stride = w_row_stride;
+        r.embed = embed; r.nheads = 2 * kv_heads; r.d = d;
+        r.codes = codes; r.codes_outer = codes_outer_stride; r.codes_row = codes_row_stride;
+        r.scales = scales; r.scales_outer = scales_outer_stride; r.scales_row = scales_row_stride;
+        return launch_rows(r, stream);
+    }
     const int64_t ws_need = nori_kv_project_quantize_int8_workspace_size(x_dtype, n_outer, n_inner, embed, norm);
     if (ws_need > 0 && (!workspace || workspace_bytes < ws_need || (uintptr_t)workspace % 16))
         return fail(NORI_ERR_INVALID, "kv_project_quantize_int8: needs a 16-byte aligned workspace of %lld bytes",
                     (long long)ws_need);
 
-    const Grid grid{n_outer * n_inner, n_inner};
     const int ksteps = (embed + 31) / 32;
-    hipStream_t stream = (hipStream_t)stream_v;
 
     ProjArgs a;
     a.grid = grid;

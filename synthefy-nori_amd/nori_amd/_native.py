@@ -88,6 +88,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
          _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _vp],
     ),
     "nori_kv_project_quantize_int8_workspace_size": (_i64, [_i32, _i64, _i64, _i32, _i32]),
+    "nori_kv_project_quantize_int8_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
     "nori_linear_f16": (
         ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i64, _i64, _vp],
     ),

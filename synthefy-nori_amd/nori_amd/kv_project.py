@@ -97,6 +97,10 @@ def project_quantize_kv(
         )
     if x.numel() == 0:
         return codes, scales
+    if x.dtype == torch.float32 and weight.dtype != torch.float16:
+        # the kernel takes its weights as f16 (the autocast cast, round to nearest); as f16
+        # they stream through the one-pass kernel's LDS at half the bytes
+        weight = weight.to(torch.float16)
     _launch(x, weight, kv_heads, head_dim, norm_eps, codes, scales, device)
     return codes, scales
 
@@ -121,8 +125,8 @@ def _launch(x, weight, kv_heads, head_dim, norm_eps, codes, scales, device) -> N
     n_outer, n_inner, x_outer, x_row = x_layout
     norm = int(norm_eps is not None)
     lib = nat.lib()
-    ws_bytes = int(lib.nori_kv_project_quantize_int8_workspace_size(
-        nat.dtype_code(x.dtype), n_outer, n_inner, x.shape[-1], norm))
+    ws_bytes = int(lib.nori_kv_project_quantize_int8_workspace_bytes(
+        nat.dtype_code(x.dtype), n_outer, n_inner, x.shape[-1], norm, nat.dtype_code(weight.dtype), head_dim))
     # the f16 operand rows (torch's caching allocator keeps the buffer for the next slice)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
     nat.check(

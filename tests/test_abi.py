@@ -53,6 +53,7 @@ def test_header_declares_the_expected_entry_points():
             "nori_mfma_f16_probe",
             "nori_mfma_f16_probe_flop",
             "nori_quant_f16_scale_probe",
+            "nori_kv_project_quantize_int8_workspace_bytes",
         ]
     )
 
