@@ -204,8 +204,9 @@ def build_workload(torch, layers, dev):
 
 def cache_write(torch, dev, codes, scales, reps=5):
     """One layer's cross-cache write at this workload, from the layer's fp32 context rows
-    [1, 65536, 33, 352]: the fused path (operand-row pass + projection/quantizer kernel,
-    nori_amd.project_quantize_kv) against the unfused one it replaces (HIP RMSNorm, torch's
+    [1, 65536, 33, 352]: the fused path (nori_amd.project_quantize_kv: one pass from the fp32
+    rows, or the operand-row pass + projection/quantizer kernel where the one pass does not
+    apply) against the unfused one it replaces (HIP RMSNorm, torch's
     fp16-autocast F.linear, HIP quantizer), each timed with HIP events on the launch stream.
     Both write `codes` / `scales` [33, 65536, 2, 8, 44]."""
     import nori_amd
@@ -243,13 +244,19 @@ def cache_write(torch, dev, codes, scales, reps=5):
     fused_ms, unfused_ms = avg_ms(fused), avg_ms(unfused)
     rows = GROUPS * CONTEXT_ROWS
     n_kv = rows * 2 * HEADS * HEAD_DIM
-    # algorithmic HBM bytes of the fused pair: x read, f16 operand rows written and read,
-    # codes + scales written
-    fused_bytes = rows * EMBED * 4 + 2 * rows * EMBED * 2 + n_kv + 4 * rows * 2 * HEADS
+    # one pass (no workspace) from the fp32 rows, or the operand-row pass + projection kernel
+    one_pass = nori_amd._native.lib().nori_kv_project_quantize_int8_workspace_bytes(
+        nori_amd._native.dtype_code(torch.float32), GROUPS, CONTEXT_ROWS, EMBED, 1,
+        nori_amd._native.dtype_code(torch.float16), HEAD_DIM) == 0
+    # algorithmic HBM bytes: x read, codes + scales written (and for the two-kernel path the
+    # f16 operand rows written and read)
+    fused_bytes = rows * EMBED * 4 + n_kv + 4 * rows * 2 * HEADS + (0 if one_pass else 2 * rows * EMBED * 2)
     del x, xt
     return {
         "what": "one layer's int8 cross-cache write from fp32 context rows: RMSNorm -> K/V projection "
         "(fp16 operands, fp32 sums) -> exact int8 quantizer, 33 x 65536 rows, embed 352 -> 2 x 8 x 44",
+        "fused_path": "one pass from the fp32 rows (kv_rows_kernel)" if one_pass
+        else "operand-row pass + projection/quantizer kernel",
         "fused_ms": round(fused_ms, 4),
         "unfused_ms": round(unfused_ms, 4),
         "speedup": round(unfused_ms / fused_ms, 3),
