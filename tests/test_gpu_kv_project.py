@@ -188,13 +188,15 @@ def test_scale_and_reciprocal_over_every_f16_value(cuda):
     assert np.array_equal(y[fast].view(np.uint32), y_ref[fast].view(np.uint32))
 
 
-def test_every_f16_scale_codes_equal_the_exact_quantizer(cuda):
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_every_f16_scale_codes_equal_the_exact_quantizer(cuda, xdt):
     """Identity weights make the K/V the operand values themselves (kv = x exactly), so each head
     vector's absmax can be chosen: every positive finite f16 value once, the other 43 values
     uniform in [-absmax, absmax] in f16. The fused write's codes and scales, and the HIP
     quantizer's on the same K/V, equal the reference expression on the same device (absmax below
     127 * 2^-14 gives a subnormal f16 scale, and quotients past 127 that only clamping brings
-    back: absmax 128 * 2^-24 has scale 2^-24 and code 127, not -128)."""
+    back: absmax 128 * 2^-24 has scale 2^-24 and code 127, not -128). fp16 rows feed the MFMAs
+    as they are; fp32 rows (the same values) take the one-pass kernel."""
     heads, d, embed = 8, 44, 352
     amax = torch.arange(1, 0x7C00, dtype=torch.int32).to(torch.int16).view(torch.float16).float()
     nv = amax.numel() + (-amax.numel()) % 8
@@ -205,7 +207,7 @@ def test_every_f16_scale_codes_equal_the_exact_quantizer(cuda):
     vecs = torch.gather(vecs, 1, torch.argsort(torch.rand(nv, d, generator=g), dim=1)).half()
     x = vecs.view(nv // 8, embed).to(cuda)
     w = torch.cat((torch.eye(embed), torch.eye(embed))).to(cuda)
-    codes, scales = nori_amd.project_quantize_kv(x, w, heads, d)
+    codes, scales = nori_amd.project_quantize_kv(x.to(xdt), w, heads, d)
     kv = torch.cat((x, x), dim=-1).view(nv // 8, 2, heads, d)
     ref_q, ref_s = torch_quantize(kv)
     bad = (codes != ref_q).any(-1).flatten().nonzero().flatten().cpu()
@@ -219,6 +221,26 @@ def test_every_f16_scale_codes_equal_the_exact_quantizer(cuda):
     assert torch.equal(scales, ref_s)
     hip_q, hip_s = nori_amd.quantize_int8(kv)
     assert torch.equal(hip_q, ref_q) and torch.equal(hip_s.view_as(ref_s), ref_s)
+
+
+def test_one_pass_equals_the_operand_path_on_the_same_operands(cuda):
+    """fp32 rows take the one-pass kernel (no workspace); without the norm its operands are
+    f16(x), what fp16 rows feed the two-kernel path as they are, and its MFMA order is the
+    same, so codes and scales agree bit for bit (ragged row count, a row slice view)."""
+    from nori_amd import _native as nat
+
+    lib = nat.lib()
+    f32, f16 = nat.dtype_code(torch.float32), nat.dtype_code(torch.float16)
+    assert lib.nori_kv_project_quantize_int8_workspace_bytes(f32, 3, 1000, 352, 1, f16, 44) == 0
+    assert lib.nori_kv_project_quantize_int8_workspace_bytes(f32, 3, 1000, 352, 1, f32, 44) > 0
+    assert lib.nori_kv_project_quantize_int8_workspace_bytes(f16, 3, 1000, 352, 1, f16, 44) > 0
+    assert lib.nori_kv_project_quantize_int8_workspace_bytes(f32, 3, 1000, 392, 1, f16, 44) > 0  # embed > 384
+    g = torch.Generator(device=cuda).manual_seed(11)
+    x = torch.randn(3, 1000, 352, generator=g, device=cuda)[:, 3:]
+    w = torch.randn(704, 352, generator=g, device=cuda) * 352 ** -0.5
+    one_q, one_s = nori_amd.project_quantize_kv(x, w, 8, 44)
+    op_q, op_s = nori_amd.project_quantize_kv(x.half(), w.half(), 8, 44)
+    assert torch.equal(one_q, op_q) and torch.equal(one_s, op_s)
 
 
 def test_large_row_count(cuda):
