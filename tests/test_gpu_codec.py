@@ -101,6 +101,34 @@ def test_special_vectors_match_torch(cuda, dtype):
     assert torch.equal(codes.cpu(), torch.from_numpy(o_q))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_every_absmax_matches_torch(cuda, dtype):
+    """Each vector's absmax swept over the dtype's positive finite values -- every bf16 value
+    (subnormal scales included), and for fp32 sixteen random significands at every exponent
+    from 2^-149 to 2^127 -- with the other 15 values uniform in [-absmax, absmax]: codes and
+    scales equal the reference expression on the same device and the oracle. (The fp16 sweep,
+    every f16 absmax, is in tests/test_gpu_kv_project.py beside the fused write's.)"""
+    g = torch.Generator().manual_seed(21)
+    if dtype == torch.bfloat16:
+        amax = (torch.arange(1, 0x7F80, dtype=torch.int32) << 16).view(torch.float32)
+    else:
+        e = torch.arange(-149, 128, dtype=torch.float64).repeat_interleave(16)
+        m = 1.0 + torch.rand(e.numel(), generator=g, dtype=torch.float64)
+        amax = (m * torch.pow(2.0, e)).clamp(max=3.4e38).float()
+        amax = amax[torch.isfinite(amax) & (amax > 0)]
+    d = 16
+    vecs = (torch.rand(amax.numel(), d, generator=g, dtype=torch.float64) * 2 - 1) * amax.double()[:, None]
+    vecs[:, 0] = amax.double() * torch.where(torch.rand(amax.numel(), generator=g) < 0.5, -1.0, 1.0).double()
+    vecs = torch.gather(vecs, 1, torch.argsort(torch.rand(amax.numel(), d, generator=g), dim=1))
+    t = vecs.to(dtype).to(cuda)
+    assert torch.equal(t.abs().amax(-1).float().cpu(), amax.to(dtype).float())
+    codes, scales = nori_amd.quantize_int8(t)
+    ref_q, ref_s = torch_reference(t)
+    assert_bits_equal(codes, scales, ref_q, ref_s)
+    o_q, o_s = oracle_quantize(t)
+    assert_bits_equal(codes, scales, o_q, o_s)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_dequantize_bit_exact(cuda, dtype):
     t = outlier_cache((2, 97, 2, 3, 44), torch.float32, cuda, seed=5)
