@@ -441,8 +441,11 @@ bool direct_operands(int x_dtype, int32_t embed, int32_t norm) {
 // ------------------------------------------------------------------ one pass from fp32 rows
 // Every head of a row block in one workgroup: each fp32 row is read and normalized once, in
 // the registers that feed the MFMAs, and the f16 weights stream through LDS one head at a time
-// (two tile buffers: the next head's tile loads while this head computes). No operand-row pass
-// and no workspace; each 704-byte code row is written by one workgroup.
+// (two tile buffers: the next head's tile loads while this head computes, one barrier per
+// head). The barrier would keep every wave of the CU in the same phase -- all multiplying,
+// then all quantizing -- so the odd waves run half a head behind: each quantizes head h - 1
+// before multiplying head h, and the MFMA and quantizer work of the two halves overlap. No
+// operand-row pass and no workspace; each 704-byte code row is written by one workgroup.
 struct RowsArgs {
     const float* x; Grid grid; int64_t x_outer, x_row;  // fp32 rows (elements)
     int norm; float eps;
@@ -498,6 +501,62 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
 #pragma unroll
     for (int q = 0; q < 4; ++q) pad_ok[q] = 16 * (MT - 1) + 4 * g + q < a.d;
 
+    // quantize + store one head's 16 rows: lane holds columns 16m + 4g + [0, 4) of row (lane & 15)
+    auto quant = [&](const f32x4 (&acc)[MT], int hd, int64_t c_off, int64_t s_off) {
+        uint16_t hv[MT][4];
+        uint32_t key = 0;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hv[m][q] = f32_to_f16(acc[m][q]);
+                const uint32_t k = abs_key<NORI_F16>(hv[m][q]);
+                key = max(key, m < MT - 1 || pad_ok[q] ? k : 0u);
+            }
+        }
+        {
+            const auto s16 = __builtin_amdgcn_permlane16_swap(key, key, false, false);
+            key = max(s16[0], s16[1]);
+            const auto s32 = __builtin_amdgcn_permlane32_swap(key, key, false, false);
+            key = max(s32[0], s32[1]);
+        }
+        const VectorScale vs = make_scale_f16_fast(key);  // both scale_div modes
+        uint32_t words[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float q[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // the correctly rounded quotient t/s (Markstein)
+                const float t = f16_to_f32(hv[m][e]);
+                const float q0 = t * vs.y;
+                q[e] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
+            }
+            words[m] = pack_codes_fast<NORI_F16>(q);
+        }
+        // scales outside the fast quotient's range: recode exactly, on a wave-uniform branch
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(!vs.fast) != 0, 0)) {
+            if (!vs.fast) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                words[m] = pack4(code_of<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][1]), vs),
+                             code_of<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][3]), vs));
+            }
+        }
+        if (c_off >= 0) {
+            int8_t* crow = a.codes + c_off + (int64_t)hd * a.d;
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (16 * m + 4 * g < a.d) *reinterpret_cast<uint32_t*>(crow + 16 * m + 4 * g) = words[m];
+            if (g == 0) a.scales[s_off + hd] = vs.s;
+        }
+    };
+    // odd waves run half a head behind: they quantize head h - 1 while the even waves multiply head h
+    const bool lag = wave & 1;
+    f32x4 prev[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) prev[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
     for (; rb < a.nblocks; rb += gridDim.x) {
         // ---- this wavefront's 16 rows: lane n + 16 g holds row n's elements 32 ks + 8 g + [0, 8)
         const int64_t r = rb * (kWaves * 16) + wave * 16 + (lane & 15);
@@ -546,6 +605,7 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
             const bool more = hd + 1 < a.nheads || rb + gridDim.x < a.nblocks;
             if (more) load_tile(hd + 1 < a.nheads ? hd + 1 : 0, wr);
 
+            if (lag && hd > 0) quant(prev, hd - 1, c_off, s_off);
             f32x4 acc[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -559,59 +619,17 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
                 }
             }
 
-            // ---- quantize: lane holds columns 16m + 4g + [0, 4) of row (lane & 15)
-            uint16_t hv[MT][4];
-            uint32_t key = 0;
+            if (!lag) quant(acc, hd, c_off, s_off);
+            else {
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    hv[m][q] = f32_to_f16(acc[m][q]);
-                    const uint32_t k = abs_key<NORI_F16>(hv[m][q]);
-                    key = max(key, m < MT - 1 || pad_ok[q] ? k : 0u);
-                }
-            }
-            {
-                const auto s16 = __builtin_amdgcn_permlane16_swap(key, key, false, false);
-                key = max(s16[0], s16[1]);
-                const auto s32 = __builtin_amdgcn_permlane32_swap(key, key, false, false);
-                key = max(s32[0], s32[1]);
-            }
-            const VectorScale vs = make_scale_f16_fast(key);  // both scale_div modes
-            uint32_t words[MT];
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                float q[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // the correctly rounded quotient t/s (Markstein)
-                    const float t = f16_to_f32(hv[m][e]);
-                    const float q0 = t * vs.y;
-                    q[e] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
-                }
-                words[m] = pack_codes_fast<NORI_F16>(q);
-            }
-            // scales outside the fast quotient's range: recode exactly, on a wave-uniform branch
-            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!vs.fast) != 0, 0)) {
-                if (!vs.fast) {
-#pragma unroll
-                    for (int m = 0; m < MT; ++m)
-                        words[m] = pack4(code_of<NORI_F16>(f16_to_f32(hv[m][0]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][1]), vs),
-                                         code_of<NORI_F16>(f16_to_f32(hv[m][2]), vs), code_of<NORI_F16>(f16_to_f32(hv[m][3]), vs));
-                }
-            }
-            if (c_off >= 0) {
-                int8_t* crow = a.codes + c_off + (int64_t)hd * a.d;
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-                    if (16 * m + 4 * g < a.d) *reinterpret_cast<uint32_t*>(crow + 16 * m + 4 * g) = words[m];
-                if (g == 0) a.scales[s_off + hd] = vs.s;
+                for (int m = 0; m < MT; ++m) prev[m] = acc[m];
             }
 
             if (more) store_tile(buf ^ 1, wr);
             __syncthreads();  // the next tile is in place; every wave is done with this one
             buf ^= 1;
         }
+        if (lag) quant(prev, a.nheads - 1, c_off, s_off);
     }
 }
 
