@@ -468,24 +468,29 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4;  // result lanes hold columns 4g..4g+3 of each 16-column tile
 
+    // this thread's 16-byte chunks of a head tile: their weight offset within a head's rows (-1:
+    // zero padding past d or past embed) and their LDS offset, the same for every head
+    int64_t w_off[WCH];
+    int l_off[WCH];
+#pragma unroll
+    for (int u = 0; u < WCH; ++u) {
+        const int c = tid + kThreads * u;
+        const int row = c / CPR, col = c - row * CPR;
+        w_off[u] = c < DP * CPR && row < a.d && col * 8 < a.embed ? (int64_t)row * a.w_stride + col * 8 : -1;
+        l_off[u] = c < DP * CPR ? row * XP + col * 8 : -1;
+    }
+    const int64_t head_stride = (int64_t)a.d * a.w_stride;
     // head h's weight rows, f16, zero past d and past embed, as 16-byte chunks of this thread
     auto load_tile = [&](int h, uint4 (&wr)[WCH]) {
+        const _Float16* wh = a.w + h * head_stride;
 #pragma unroll
-        for (int u = 0; u < WCH; ++u) {
-            const int c = tid + kThreads * u;
-            const int row = c / CPR, col = c - row * CPR;
-            const bool valid = c < DP * CPR && row < a.d && col * 8 < a.embed;
-            wr[u] = valid ? *reinterpret_cast<const uint4*>(a.w + (int64_t)(h * a.d + row) * a.w_stride + col * 8)
-                          : uint4{0u, 0u, 0u, 0u};
-        }
+        for (int u = 0; u < WCH; ++u)
+            wr[u] = w_off[u] >= 0 ? *reinterpret_cast<const uint4*>(wh + w_off[u]) : uint4{0u, 0u, 0u, 0u};
     };
     auto store_tile = [&](int buf, const uint4 (&wr)[WCH]) {
 #pragma unroll
-        for (int u = 0; u < WCH; ++u) {
-            const int c = tid + kThreads * u;
-            const int row = c / CPR, col = c - row * CPR;
-            if (c < DP * CPR) *reinterpret_cast<uint4*>(wt + buf * TILE + row * XP + col * 8) = wr[u];
-        }
+        for (int u = 0; u < WCH; ++u)
+            if (l_off[u] >= 0) *reinterpret_cast<uint4*>(wt + buf * TILE + l_off[u]) = wr[u];
     };
 
     int64_t rb = blockIdx.x;
