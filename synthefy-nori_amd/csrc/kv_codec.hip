@@ -143,7 +143,8 @@ quantize_direct_kernel(const void* __restrict__ src_v, int64_t n_outer, int64_t 
 // and the wave stores them with 16-byte stores. No workgroup barrier: the region is
 // private to the wave and LDS operations of a wave complete in order.
 //
-// Fast-path codes: with q the exact quotient RN(t/s) (Markstein, above), the code is
+// Fast-path codes: with q the exact quotient RN(t/s) (Markstein, above; for fp16, whose fast
+// scales are normal, the product RN(t * RN(1/s)), which has the same code), the code is
 // rint(RN_T(q)). For fp16 that is one packed add: RN16(q) + 1536 in fp16 rounds to an
 // integer half-to-even (the fp16 spacing in [1024, 2048) is 1), and the low byte of
 // 1536 + k is k in two's complement. fp32 and bf16 do the same with 1.5 * 2^23 in fp32.
@@ -257,8 +258,11 @@ quantize_wave_kernel(const uint8_t* __restrict__ src, int64_t n_outer, int64_t n
                 for (int i = 0; i < 4; ++i) {
                     const float t = elem_of<DT>(x, 4 * j + i);
                     const float q0 = t * vs.y;
-                    const float r = fmaf(-q0, vs.s, t);
-                    q[i] = fmaf(r, vs.y, q0);
+                    if constexpr (DT == NORI_F16) {
+                        q[i] = q0;  // a normal fp16 scale: the product's code is the quotient's
+                    } else {
+                        q[i] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);  // the correctly rounded t/s (Markstein)
+                    }
                 }
                 c[j] = pack_codes_fast<DT>(q);
             }

@@ -332,10 +332,8 @@ __global__ void __launch_bounds__(kThreads, 2) kv_project_quantize_kernel(const 
                     float q[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        // the correctly rounded quotient t/s (Markstein)
-                        const float t = f16_to_f32(hv[m][i]);
-                        const float q0 = t * vs.y;
-                        q[i] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
+                        // t * RN(1/s): with a normal fp16 scale its code is the quotient's
+                        q[i] = f16_to_f32(hv[m][i]) * vs.y;
                     }
                     words[m] = pack_codes_fast<NORI_F16>(q);
                 }
@@ -532,10 +530,8 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
             float q[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                // the correctly rounded quotient t/s (Markstein)
-                const float t = f16_to_f32(hv[m][e]);
-                const float q0 = t * vs.y;
-                q[e] = fmaf(fmaf(-q0, vs.s, t), vs.y, q0);
+                // t * RN(1/s): with a normal fp16 scale its code is the quotient's
+                q[e] = f16_to_f32(hv[m][e]) * vs.y;
             }
             words[m] = pack_codes_fast<NORI_F16>(q);
         }

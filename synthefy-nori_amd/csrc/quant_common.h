@@ -39,6 +39,9 @@ __device__ __forceinline__ uint32_t abs_key(typename Storage<DT>::T b) {
     else return (uint32_t)b & 0x7fffu;
 }
 
+// For an fp16 source with a normal scale the code of the plain product RN(t * y) already equals
+// the code of RN(t/s) for every element a vector can hold (an exhaustive check over the
+// (s, t) pairs: tests/exact_quotient_check.c), so the fp16 kernels skip Markstein's correction.
 // Scales the fast quotient and packing take. Outside [2^-96, 2^96] the residual fma(-q0, s, t)
 // may be subnormal and inexact. An f16 scale must also be normal (>= 2^-14): a subnormal one is
 // rounded with a relative error up to 1/2, so |t/s| can pass 127 (absmax 190 * 2^-24 gives

@@ -14,6 +14,9 @@
  * between the two quotients. fp32 sources are checked on random pairs.
  * Prints "<dtype> pairs=<n> code_mismatch=<k> quotient_mismatch=<j>" per dtype, where
  * quotient_mismatch counts pairs with |t/s| >= 1/4 whose two quotients differ in any bit.
+ * For fp16 it also checks the plain product: with a normal fp16 scale (s >= 2^-14, the fp16
+ * kernels' fast domain) the code of RN(t*y) alone must equal the code of RN(t/s)
+ * ("product_mismatch=<m>"), so the fp16 kernels may skip the correction.
  */
 #include <math.h>
 #include <stdint.h>
@@ -62,6 +65,8 @@ static int code_from(float q, int dt) {
     return (int)k;
 }
 
+static long long product_mismatch = 0;
+
 static void check_pair(float t, float s, float y, int dt, long long* pairs, long long* cm, long long* qm) {
     volatile float tv = t, sv = s;
     float exact = tv / sv;
@@ -74,6 +79,7 @@ static void check_pair(float t, float s, float y, int dt, long long* pairs, long
      * s >= 2^-96 the residual is a multiple of 2^-143 and exact. */
     if (fabsf(exact) >= 0.25f && f2u(q) != f2u(exact)) (*qm)++;
     if (code_from(q, dt) != code_from(exact, dt)) (*cm)++;
+    if (dt == 1 && s >= 0x1p-14f && code_from(q0, dt) != code_from(exact, dt)) product_mismatch++;
 }
 
 /* The kernel's fast-path predicate (kv_codec.hip, make_scale). */
@@ -99,6 +105,7 @@ static void run16(int dt) {
         }
     }
     printf("%s pairs=%lld code_mismatch=%lld quotient_mismatch=%lld\n", dt == 2 ? "bf16" : "f16", pairs, cm, qm);
+    if (dt == 1) printf("f16 product_mismatch=%lld\n", product_mismatch);
 }
 
 static uint64_t rng = 0x9e3779b97f4a7c15ull;
