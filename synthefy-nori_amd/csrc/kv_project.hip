@@ -640,7 +640,13 @@ int launch_rows_with(const RowsArgs& a, hipStream_t stream) {
     if (hipFuncSetAttribute((const void*)kv_rows_kernel<KS, MT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
         hipSuccess)
         return fail(NORI_ERR_RUNTIME, "kv_project_quantize_int8: cannot reserve %zu bytes of LDS", lds);
-    const int64_t slots = (int64_t)device_cus() * kWgPerCu;
+    // one round of resident workgroups (registers hold one per CU at nori-30m's shape), each
+    // walking its share of the row blocks
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kv_rows_kernel<KS, MT>, kThreads, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    const int64_t slots = (int64_t)device_cus() * per_cu;
     const dim3 grid((unsigned)std::min<int64_t>(a.nblocks, slots));
     hipLaunchKernelGGL((kv_rows_kernel<KS, MT>), grid, dim3(kThreads), lds, stream, a);
     return launch_status("kv_project_quantize_int8 (one pass)");
