@@ -441,8 +441,9 @@ bool direct_operands(int x_dtype, int32_t embed, int32_t norm) {
 // the registers that feed the MFMAs, and the f16 weights stream through LDS one head at a time
 // (two tile buffers: the next head's tile loads while this head computes, one barrier per
 // head). The barrier would keep every wave of the CU in the same phase -- all multiplying,
-// then all quantizing -- so the odd waves run half a head behind: each quantizes head h - 1
-// before multiplying head h, and the MFMA and quantizer work of the two halves overlap. No
+// then all quantizing -- so half the waves (one of the two on each SIMD) run half a head
+// behind: each quantizes head h - 1 before multiplying head h, and the MFMA and quantizer work
+// of the two halves overlap. No
 // operand-row pass and no workspace; each 704-byte code row is written by one workgroup.
 struct RowsArgs {
     const float* x; Grid grid; int64_t x_outer, x_row;  // fp32 rows (elements)
@@ -552,8 +553,9 @@ __global__ void __launch_bounds__(kThreads, 2) kv_rows_kernel(const RowsArgs a) 
             if (g == 0) a.scales[s_off + hd] = vs.s;
         }
     };
-    // odd waves run half a head behind: they quantize head h - 1 while the even waves multiply head h
-    const bool lag = wave & 1;
+    // half the waves run half a head behind: they quantize head h - 1 while the others multiply head h
+    // (waves 4-7: wave w shares a SIMD with wave w ^ 4, so each SIMD holds one of each)
+    const bool lag = (wave >> 2) & 1;
     f32x4 prev[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) prev[m] = f32x4{0.f, 0.f, 0.f, 0.f};
